@@ -1,0 +1,159 @@
+"""Benchmark of the pjrtx hot path on one MI355X.
+
+A step is one PJRT execute of the workload's compiled StableHLO program on
+device-resident inputs (synthetic, seeded). Default workload: BASELINE
+configs[1] — two-output max/index argmax over bf16 logits [64,128256] plus
+f16 sum/max/min of the logits cast to f16 (one fused kernel). `--config c1`
+runs configs[0] (f32 elementwise chain + row sum, [4096,4096]).
+
+Prints one JSON line: whole-job HBM GB/s over algorithmic bytes, the
+dominant kernel's roofline (HIP-event timed on the plugin's stream), and the
+CPU oracle timed on this host as a reported baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+
+WORKLOADS = {
+    "c2": dict(
+        workload="argmax2_f16reduce_64x128256_bf16",
+        desc="two-output argmax over logits [64,128256] bf16 + f16 sum/max/min of logits.astype(f16)",
+        # read logits once + outputs (bf16 values, i32 indices, 3x f16)
+        bytes=64 * 128256 * 2 + 64 * (2 + 4 + 3 * 2),
+        dtype="bf16",
+    ),
+    "c1": dict(
+        workload="f32_chain_rowsum_4096x4096",
+        desc="sum(tanh(x*y+0.5)*x - max(y,0), axis=1), x,y [4096,4096] f32",
+        bytes=2 * 4096 * 4096 * 4 + 4096 * 4,
+        dtype="f32",
+    ),
+}
+
+
+def make(config: str):
+    import numpy as np
+    from oracle import ops  # input makers only; the timed path never calls the oracle
+    from pjrtx_amd import programs
+    if config == "c2":
+        text = programs.c2_argmax_f16_reductions(64, 128256)
+        inputs = [ops.c2_inputs(64, 128256, seed=0)]
+        dtypes = ["bf16"]
+    else:
+        text = programs.c1_elementwise_rowsum(4096, 4096)
+        inputs = list(ops.c1_inputs(4096, 4096, seed=0))
+        dtypes = [None, None]
+    return text, inputs, dtypes
+
+
+def cpu_baseline(config: str, inputs, budget_s: float = 10.0) -> dict:
+    """The numpy oracle on this host's cores over the same workload, repeated
+    for about `budget_s` seconds (a reported baseline, not the target)."""
+    from oracle import ops
+    fn = (lambda: ops.c2_reference(inputs[0])) if config == "c2" else (lambda: ops.c1_rowsum(*inputs))
+    fn()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 1000:
+            break
+    per = el / n
+    gbps = WORKLOADS[config]["bytes"] / per / 1e9
+    return {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"full workload x{n} calls of the numpy oracle ({per * 1e3:.1f} ms/call, single-threaded numpy)"}
+
+
+def traffic_from_profiles(config: str):
+    p = ROOT / "profiles" / f"{WORKLOADS[config]['workload']}_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); "
+              "multi-GPU sharding is design-only", file=sys.stderr)
+        return 2
+
+    from pjrtx_amd.pjrt import Client
+    W = WORKLOADS[a.config]
+    text, inputs, dtypes = make(a.config)
+    client = Client()
+    exe = client.compile(text)
+    bufs = [client.buffer(x, dt) for x, dt in zip(inputs, dtypes)]
+    for b in bufs:
+        b.block_until_ready()
+
+    for _ in range(a.warmup):
+        outs = exe.execute_buffers(bufs)
+    outs[-1].block_until_ready()
+    del outs
+
+    t0 = time.perf_counter()
+    last = None
+    for _ in range(a.steps):
+        last = exe.execute_buffers(bufs)
+    last[-1].block_until_ready()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / a.steps
+    value = W["bytes"] / (ms_per_step / 1e3) / 1e9
+
+    # Dominant kernel: per-step HIP-event timing on the plugin's stream.
+    step_ms = exe.time_steps(bufs, iters=max(50, a.steps))
+    names = exe.step_names()
+    k = max(range(len(step_ms)), key=lambda i: step_ms[i])
+    kernel_ms = step_ms[k]
+    achieved = W["bytes"] / (kernel_ms / 1e3) / 1e9
+
+    line = {
+        "metric": "fused-op HBM GB/s (% peak)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": W["dtype"],
+        "data": "synthetic (seeded numpy inputs, resident in HBM before timing)",
+        "config": {"workload": W["workload"], "desc": W["desc"], "algorithmic_bytes": W["bytes"],
+                   "pct_hbm_peak_end_to_end": round(100 * value / HBM_PEAK_GBPS, 2),
+                   "kernels_per_step": len(step_ms)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profiles(a.config),
+                     "kernel": names[k], "kernel_us": round(kernel_ms * 1e3, 3)},
+    }
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(a.config, inputs)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,95 @@
+/*
+ * pjrtx_hip.h — the thin C ABI between the pjrtx runtime and HIP.
+ *
+ * The reference's Zig runtime reaches its device backend through a private
+ * C ABI over MLX (`pjrtx_mlx_metal_*`, reference:
+ * src/backend/mlx_metal/api.h:198-477) and a generated-kernel runner
+ * (`pjrtx_metalcpp_*`, reference: src/backend/mlx_metal/metalcpp_api.cc:
+ * 1165-1335). This header is the HIP replacement: plain pointers, sizes and
+ * integer status codes, no C++ or torch types, so that a Zig, Python
+ * (ctypes) or C caller can bind it unchanged. Every function returns 0 on
+ * success; on failure it returns a PJRT_Error_Code value and the message is
+ * available from pjrtx_hip_last_error() on the same thread.
+ *
+ * The PJRT entry point (GetPjrtApi) is declared in pjrt_c_api.h; the plugin
+ * itself is built on the functions below.
+ */
+#ifndef PJRTX_AMD_PJRTX_HIP_H_
+#define PJRTX_AMD_PJRTX_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PJRTX_HIP_API __attribute__((visibility("default")))
+
+/* Thread-local message of the last failing call. */
+PJRTX_HIP_API const char* pjrtx_hip_last_error(void);
+
+/* ---------------------------------------------------------------- devices */
+
+/* Number of visible HIP devices (0 when none). Replaces
+ * pjrtx_mlx_metal_copy_devices (api.h:198, api.cc:1753). */
+PJRTX_HIP_API int pjrtx_hip_device_count(int* count);
+
+/* Device memory from the per-device caching allocator. Replaces the buffer
+ * creation / destroy entries of api.h (pjrtx_mlx_metal_buffer_from_host_typed
+ * api.cc:1781-1852, pjrtx_mlx_metal_buffer_destroy). */
+PJRTX_HIP_API int pjrtx_hip_malloc(int device, size_t bytes, void** ptr);
+PJRTX_HIP_API int pjrtx_hip_free(int device, void* ptr);
+
+/* Stream-ordered copies on the device's single stream; each returns after
+ * the copy completed. Replace buffer_from_host_typed (api.cc:1781-1852) and
+ * pjrtx_mlx_metal_buffer_copy_to_host (api.cc:5685-5731). */
+PJRTX_HIP_API int pjrtx_hip_copy_h2d(int device, void* dst, const void* src, size_t bytes);
+PJRTX_HIP_API int pjrtx_hip_copy_d2h(int device, void* dst, const void* src, size_t bytes);
+PJRTX_HIP_API int pjrtx_hip_synchronize(int device);
+
+/* --------------------------------------------------- compiler (host only) */
+
+/* Parses a StableHLO text module, runs the fusion planner and code
+ * generator, and writes a JSON description of the plan to `out` (at most
+ * `cap` bytes; `*needed` gets the full size). Needs no GPU. Replaces the
+ * compile-time half of pjrtx_metalcpp_executable_program_create
+ * (metalcpp_api.cc:1296) together with the Zig planner
+ * (program_build.zig:10-207). */
+PJRTX_HIP_API int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed);
+
+/* As pjrtx_plan_json, and also compiles the generated fusion kernels with
+ * hiprtc for `arch` (e.g. "gfx950"); `code_size` gets the code-object size.
+ * Needs no GPU. Replaces the MSL pipeline compile (metalcpp_api.cc:459-540). */
+PJRTX_HIP_API int pjrtx_compile_check(const char* text, size_t len, const char* arch, size_t* code_size);
+
+/* Writes the full hiprtc translation unit of the plan's generated kernels
+ * (device header + bodies) to `out`, for inspection. Needs no GPU. */
+PJRTX_HIP_API int pjrtx_kernel_source(const char* text, size_t len, char* out, size_t cap, size_t* needed);
+
+/* ------------------------------------------------------ executable timing */
+
+struct PJRT_LoadedExecutable;
+struct PJRT_Buffer;
+
+/* Replays each step of a compiled executable `iters` times between two
+ * hipEvents on the device stream and writes the mean milliseconds per
+ * launch of each step to ms[0..steps). Used by the benchmark's roofline
+ * figure. Replaces PJRTX_METALCPP_EXECUTABLE_STEP_PROFILE
+ * (metalcpp_api.cc:399-416). */
+PJRTX_HIP_API int pjrtx_executable_time_steps(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
+                                size_t num_args, int iters, double* ms, size_t cap, size_t* steps);
+
+/* Kernel names of the executable's steps, '\n'-separated ("-" for steps
+ * that are not generated kernels). */
+PJRTX_HIP_API int pjrtx_executable_step_names(struct PJRT_LoadedExecutable* exe, char* out, size_t cap, size_t* needed);
+
+/* Counters of the executable: executions, kernel launches, library calls,
+ * released intermediate values. */
+PJRTX_HIP_API int pjrtx_executable_stats(struct PJRT_LoadedExecutable* exe, int64_t out[4]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PJRTX_AMD_PJRTX_HIP_H_ */

@@ -1,0 +1,930 @@
+// Kernel source generation for fusion groups.
+//
+// Each loop / reduce step becomes one `extern "C" __global__` function built
+// from the hand-written skeletons below plus the group's expression DAG,
+// evaluated per element at an index that view ops (broadcast_in_dim,
+// reshape, transpose, slice, reverse, iota) remap arithmetically instead of
+// materializing. Counterpart of the reference's MSL fusion writer
+// (reference: executable_metal_graph_fusion_request_record.zig:11-211,
+// executable_metal_graph_fusion_expression.zig:56-152 broadcast/slice index
+// maps, executable_metal_graph_fusion_request_writer.zig:7-55).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <set>
+#include <sstream>
+
+#include "planner.h"
+
+namespace pjrtx {
+namespace {
+
+std::string hex_u32(uint32_t v) { return strformat("0x%08xu", v); }
+
+// C literal for the element `i` of a constant op, in compute type.
+std::string literal_expr(const Program& prog, const Op& op, size_t i) {
+  const TensorType& t = prog.type(op.results[0]);
+  const size_t esz = dtype_size(t.dtype);
+  const size_t idx = op.splat ? 0 : i;
+  const uint8_t* p = op.literal.data() + idx * esz;
+  switch (t.dtype) {
+    case DType::kF32: {
+      uint32_t u;
+      std::memcpy(&u, p, 4);
+      return "__builtin_bit_cast(float, " + hex_u32(u) + ")";
+    }
+    case DType::kBF16: {
+      uint16_t b;
+      std::memcpy(&b, p, 2);
+      return "__builtin_bit_cast(float, " + hex_u32(static_cast<uint32_t>(b) << 16) + ")";
+    }
+    case DType::kF16: {
+      uint16_t h;
+      std::memcpy(&h, p, 2);
+      float f = f16_bits_to_f32(h);
+      uint32_t u;
+      std::memcpy(&u, &f, 4);
+      return "__builtin_bit_cast(float, " + hex_u32(u) + ")";
+    }
+    case DType::kF64: {
+      uint64_t u;
+      std::memcpy(&u, p, 8);
+      return strformat("__builtin_bit_cast(double, 0x%016llxull)", static_cast<unsigned long long>(u));
+    }
+    case DType::kPred: return p[0] ? "true" : "false";
+    case DType::kS8: return strformat("((int8_t)%d)", static_cast<int>(*reinterpret_cast<const int8_t*>(p)));
+    case DType::kU8: return strformat("((uint8_t)%u)", static_cast<unsigned>(p[0]));
+    case DType::kS16: { int16_t v; std::memcpy(&v, p, 2); return strformat("((int16_t)%d)", v); }
+    case DType::kU16: { uint16_t v; std::memcpy(&v, p, 2); return strformat("((uint16_t)%u)", v); }
+    case DType::kS32: { int32_t v; std::memcpy(&v, p, 4); return strformat("((int32_t)%d)", v); }
+    case DType::kU32: { uint32_t v; std::memcpy(&v, p, 4); return strformat("((uint32_t)%uu)", v); }
+    case DType::kS64: { int64_t v; std::memcpy(&v, p, 8); return strformat("((int64_t)%lldll)", static_cast<long long>(v)); }
+    case DType::kU64: { uint64_t v; std::memcpy(&v, p, 8); return strformat("((uint64_t)%lluull)", static_cast<unsigned long long>(v)); }
+    default: fail(Code::kUnimplemented, "literal of unsupported type");
+  }
+}
+
+std::string load_expr(DType t, const std::string& ptr, const std::string& idx) {
+  switch (t) {
+    case DType::kBF16: return "bf16_to_f32(" + ptr + "[" + idx + "])";
+    case DType::kF16: return "f16_to_f32(" + ptr + "[" + idx + "])";
+    case DType::kPred: return "(" + ptr + "[" + idx + "] != 0)";
+    default: return ptr + "[" + idx + "]";
+  }
+}
+
+std::string from_storage(DType t, const std::string& s) {
+  switch (t) {
+    case DType::kBF16: return "bf16_to_f32(" + s + ")";
+    case DType::kF16: return "f16_to_f32(" + s + ")";
+    case DType::kPred: return "(" + s + " != 0)";
+    default: return s;
+  }
+}
+
+std::string to_storage(DType t, const std::string& c) {
+  switch (t) {
+    case DType::kBF16: return "f32_to_bf16(" + c + ")";
+    case DType::kF16: return "f32_to_f16(" + c + ")";
+    case DType::kPred: return "(uint8_t)(" + c + ")";
+    default: return c;
+  }
+}
+
+// Rounds a float computation to the narrow float type of its result.
+std::string round_to(DType t, const std::string& e) {
+  if (t == DType::kBF16) return "round_bf16(" + e + ")";
+  if (t == DType::kF16) return "round_f16(" + e + ")";
+  return e;
+}
+
+const char* unsigned_of(DType t) {
+  switch (t) {
+    case DType::kS8: case DType::kU8: return "uint8_t";
+    case DType::kS16: case DType::kU16: return "uint16_t";
+    case DType::kS32: case DType::kU32: return "uint32_t";
+    default: return "uint64_t";
+  }
+}
+
+// An index into a value of a given shape: a linear expression, per-dim
+// expressions, or both. `identity` marks the kernel's own root position,
+// where vector-preloaded inputs can be used.
+struct Idx {
+  std::string key;
+  Dims shape;
+  std::string lin;
+  std::vector<std::string> multi;
+  bool identity = false;
+};
+
+class Writer {
+ public:
+  Writer(const Program& prog, const std::map<int, std::string>& ptr_of, const std::string& idx_t)
+      : prog_(prog), ptr_of_(ptr_of), idx_t_(idx_t) {}
+
+  std::ostringstream body;              // per-element statements
+  std::map<int, std::string> preload;   // value -> preload array name (root identity)
+
+  int add_index(Idx idx) {
+    idxs_.push_back(std::move(idx));
+    return static_cast<int>(idxs_.size()) - 1;
+  }
+  void seed(int v, int idx, const std::string& var) { memo_[memo_key(v, idx)] = var; }
+
+  std::string lin_of(int id) {
+    Idx& I = idxs_[id];
+    if (!I.lin.empty()) return I.lin;
+    if (I.shape.empty()) return I.lin = "0";
+    std::string e;
+    int64_t stride = 1;
+    for (int d = static_cast<int>(I.shape.size()) - 1; d >= 0; --d) {
+      if (I.shape[d] != 1) {
+        std::string term = stride == 1 ? "(" + I.multi[d] + ")" : "(" + I.multi[d] + ")*" + std::to_string(stride) + "u";
+        e = e.empty() ? term : term + " + " + e;
+      }
+      stride *= I.shape[d];
+    }
+    if (e.empty()) e = "0";
+    std::string var = tmp();
+    body << "const " << idx_t_ << " " << var << " = " << e << ";\n";
+    return idxs_[id].lin = var;
+  }
+
+  const std::vector<std::string>& multi_of(int id) {
+    Idx& I = idxs_[id];
+    if (!I.multi.empty() || I.shape.empty()) return I.multi;
+    const std::string lin = lin_of(id);
+    std::vector<std::string> m(I.shape.size());
+    std::string rest = lin;
+    for (int d = static_cast<int>(I.shape.size()) - 1; d >= 0; --d) {
+      const int64_t D = I.shape[d];
+      if (D == 1) {
+        m[d] = "0";
+        continue;
+      }
+      if (d == 0) {
+        m[d] = rest;
+        break;
+      }
+      std::string dv = tmp(), q = tmp();
+      body << "const " << idx_t_ << " " << dv << " = " << rest << " % " << D << "u;\n";
+      body << "const " << idx_t_ << " " << q << " = " << rest << " / " << D << "u;\n";
+      m[d] = dv;
+      rest = q;
+    }
+    idxs_[id].multi = m;
+    return idxs_[id].multi;
+  }
+
+  // Returns an expression (usually a variable) holding value v at index `id`.
+  std::string value(int v, int id);
+
+ private:
+  const Program& prog_;
+  const std::map<int, std::string>& ptr_of_;
+  std::string idx_t_;
+  std::vector<Idx> idxs_;
+  std::map<std::string, std::string> memo_;
+  int tmp_ = 0;
+
+  std::string tmp() { return "t" + std::to_string(tmp_++); }
+  std::string memo_key(int v, int id) { return std::to_string(v) + "@" + idxs_[id].key; }
+  std::string define(DType t, const std::string& e) {
+    std::string var = tmp();
+    body << "const " << dtype_compute_ctype(t) << " " << var << " = " << e << ";\n";
+    return var;
+  }
+  int scalar_index() {
+    Idx s;
+    s.key = "S";
+    s.lin = "0";
+    return add_index(s);
+  }
+  std::string emit_op(const Op& op, int v, int id);
+};
+
+std::string Writer::value(int v, int id) {
+  const std::string key = memo_key(v, id);
+  auto m = memo_.find(key);
+  if (m != memo_.end()) return m->second;
+  std::string out;
+  auto p = ptr_of_.find(v);
+  const DType t = prog_.type(v).dtype;
+  if (p != ptr_of_.end()) {
+    auto pre = preload.find(v);
+    if (idxs_[id].identity && pre != preload.end()) {
+      out = define(t, from_storage(t, pre->second + "[j]"));
+    } else {
+      out = define(t, load_expr(t, p->second, lin_of(id)));
+    }
+  } else {
+    // Find the producing op.
+    int oi = -1;
+    for (size_t i = 0; i < prog_.ops.size() && oi < 0; ++i)
+      for (int r : prog_.ops[i].results)
+        if (r == v) oi = static_cast<int>(i);
+    PJRTX_CHECK(oi >= 0, Code::kInternal, "fusion value without producer or input");
+    out = emit_op(prog_.ops[oi], v, id);
+  }
+  memo_[key] = out;
+  return out;
+}
+
+std::string Writer::emit_op(const Op& op, int v, int id) {
+  const TensorType& rt = prog_.type(v);
+  const DType R = rt.dtype;
+  auto operand_at_same = [&](int k) {
+    const int u = op.operands[k];
+    // Rank-0 operands of elementwise ops (select predicate, clamp bounds).
+    if (prog_.type(u).rank() == 0 && rt.rank() > 0) return value(u, scalar_index());
+    return value(u, id);
+  };
+  switch (op.kind) {
+    case OpKind::kConstant: {
+      if (op.splat || rt.elements() == 1) return literal_expr(prog_, op, 0);
+      fail(Code::kInternal, "non-splat constant inside a fusion");
+    }
+    case OpKind::kIota: {
+      const auto& m = multi_of(id);
+      const std::string e = rt.rank() == 0 ? "0" : m[op.dim];
+      if (dtype_is_float(R)) return define(R, round_to(R, "(float)(" + e + ")"));
+      return define(R, std::string("(") + dtype_compute_ctype(R) + ")(" + e + ")");
+    }
+    case OpKind::kReshape: {
+      Idx I;
+      I.key = idxs_[id].key + "|r" + dims_str(prog_.type(op.operands[0]).dims);
+      I.shape = prog_.type(op.operands[0]).dims;
+      I.lin = lin_of(id);
+      I.identity = idxs_[id].identity;
+      return value(op.operands[0], add_index(I));
+    }
+    case OpKind::kBroadcastInDim: {
+      const Dims& od = prog_.type(op.operands[0]).dims;
+      Idx I;
+      I.key = "b" + std::to_string(v) + "(" + idxs_[id].key + ")";
+      I.shape = od;
+      if (od.empty()) {
+        I.lin = "0";
+      } else {
+        const auto& m = multi_of(id);
+        for (size_t k = 0; k < od.size(); ++k)
+          I.multi.push_back((od[k] == 1 && rt.dims[op.dims[k]] != 1) ? std::string("0") : m[op.dims[k]]);
+      }
+      return value(op.operands[0], add_index(I));
+    }
+    case OpKind::kTranspose: {
+      const Dims& od = prog_.type(op.operands[0]).dims;
+      const auto& m = multi_of(id);
+      Idx I;
+      I.key = "t" + std::to_string(v) + "(" + idxs_[id].key + ")";
+      I.shape = od;
+      I.multi.resize(od.size());
+      for (size_t k = 0; k < op.dims.size(); ++k) I.multi[op.dims[k]] = m[k];
+      return value(op.operands[0], add_index(I));
+    }
+    case OpKind::kSlice: {
+      const Dims& od = prog_.type(op.operands[0]).dims;
+      const auto& m = multi_of(id);
+      Idx I;
+      I.key = "s" + std::to_string(v) + "(" + idxs_[id].key + ")";
+      I.shape = od;
+      for (size_t k = 0; k < od.size(); ++k) {
+        std::string e = m[k];
+        const int64_t st = op.strides.empty() ? 1 : op.strides[k];
+        if (st != 1) e = "(" + e + ")*" + std::to_string(st) + "u";
+        if (op.start[k] != 0) e = "(" + e + " + " + std::to_string(op.start[k]) + "u)";
+        I.multi.push_back(e);
+      }
+      return value(op.operands[0], add_index(I));
+    }
+    case OpKind::kReverse: {
+      const Dims& od = prog_.type(op.operands[0]).dims;
+      const auto& m = multi_of(id);
+      Idx I;
+      I.key = "v" + std::to_string(v) + "(" + idxs_[id].key + ")";
+      I.shape = od;
+      I.multi = m;
+      for (int64_t d : op.dims) I.multi[d] = "(" + std::to_string(od[d] - 1) + "u - " + m[d] + ")";
+      return value(op.operands[0], add_index(I));
+    }
+    default:
+      break;
+  }
+  PJRTX_CHECK(op_is_elementwise(op.kind), Code::kUnimplemented,
+              std::string("cannot fuse op ") + op.name);
+  std::vector<std::string> a;
+  for (size_t k = 0; k < op.operands.size(); ++k) a.push_back(operand_at_same(static_cast<int>(k)));
+  const DType A = prog_.type(op.operands[0]).dtype;
+  const bool fa = dtype_is_float(A);
+  const bool dbl = A == DType::kF64;
+  const char* ct = dtype_compute_ctype(R);
+  const char* act = dtype_compute_ctype(A);
+  auto fl = [&](const std::string& e) { return define(R, round_to(R, e)); };
+  auto fn1 = [&](const char* f32fn, const char* f64fn) {
+    return fl(std::string(dbl ? f64fn : f32fn) + "(" + a[0] + ")");
+  };
+  switch (op.kind) {
+    case OpKind::kAdd:
+      if (R == DType::kPred) return define(R, a[0] + " || " + a[1]);
+      return fa ? fl(a[0] + " + " + a[1]) : define(R, std::string("(") + ct + ")(" + a[0] + " + " + a[1] + ")");
+    case OpKind::kSubtract:
+      return fa ? fl(a[0] + " - " + a[1]) : define(R, std::string("(") + ct + ")(" + a[0] + " - " + a[1] + ")");
+    case OpKind::kMultiply:
+      if (R == DType::kPred) return define(R, a[0] + " && " + a[1]);
+      return fa ? fl(a[0] + " * " + a[1]) : define(R, std::string("(") + ct + ")(" + a[0] + " * " + a[1] + ")");
+    case OpKind::kDivide:
+      if (fa) return fl(a[0] + " / " + a[1]);
+      return define(R, std::string(dtype_is_signed_int(R) ? "div_s<" : "div_u<") + ct + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kRemainder:
+      if (fa) return fl(std::string(dbl ? "fmod(" : "fmodf(") + a[0] + ", " + a[1] + ")");
+      return define(R, std::string(dtype_is_signed_int(R) ? "rem_s<" : "rem_u<") + ct + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kPower:
+      if (fa) return fl(std::string(dbl ? "pow(" : "powf(") + a[0] + ", " + a[1] + ")");
+      return define(R, std::string("ipow<") + ct + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kMaximum:
+      if (fa) return fl(std::string(dbl ? "max_d(" : "max_f(") + a[0] + ", " + a[1] + ")");
+      if (R == DType::kPred) return define(R, a[0] + " || " + a[1]);
+      return define(R, std::string("max_i<") + ct + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kMinimum:
+      if (fa) return fl(std::string(dbl ? "min_d(" : "min_f(") + a[0] + ", " + a[1] + ")");
+      if (R == DType::kPred) return define(R, a[0] + " && " + a[1]);
+      return define(R, std::string("min_i<") + ct + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kAnd:
+      return define(R, R == DType::kPred ? a[0] + " && " + a[1] : std::string("(") + ct + ")(" + a[0] + " & " + a[1] + ")");
+    case OpKind::kOr:
+      return define(R, R == DType::kPred ? a[0] + " || " + a[1] : std::string("(") + ct + ")(" + a[0] + " | " + a[1] + ")");
+    case OpKind::kXor:
+      return define(R, R == DType::kPred ? a[0] + " != " + a[1] : std::string("(") + ct + ")(" + a[0] + " ^ " + a[1] + ")");
+    case OpKind::kNot:
+      return define(R, R == DType::kPred ? "!" + a[0] : std::string("(") + ct + ")(~" + a[0] + ")");
+    case OpKind::kShiftLeft:
+      return define(R, std::string("shl<") + ct + ", " + unsigned_of(R) + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kShiftRightLogical:
+      return define(R, std::string("shr_logical<") + ct + ", " + unsigned_of(R) + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kShiftRightArithmetic:
+      return define(R, std::string("shr_arith<") + ct + ", " + unsigned_of(R) + ">(" + a[0] + ", " + a[1] + ")");
+    case OpKind::kAtan2: return fl(std::string(dbl ? "atan2(" : "atan2f(") + a[0] + ", " + a[1] + ")");
+    case OpKind::kCompare: {
+      static const char* ops[] = {"==", "!=", "<", "<=", ">", ">="};
+      const char* o = ops[static_cast<int>(op.cmp_dir)];
+      if (op.cmp_type == CmpType::kTotalOrder && fa)
+        return define(R, "total_order_key(" + a[0] + ") " + o + " total_order_key(" + a[1] + ")");
+      (void)act;
+      return define(R, a[0] + " " + o + " " + a[1]);
+    }
+    case OpKind::kSelect: return define(R, a[0] + " ? " + a[1] + " : " + a[2]);
+    case OpKind::kClamp: {
+      // clamp(min, x, max)
+      const DType X = prog_.type(op.operands[1]).dtype;
+      if (dtype_is_float(X)) {
+        const bool d = X == DType::kF64;
+        return fl(std::string(d ? "min_d(max_d(" : "min_f(max_f(") + a[1] + ", " + a[0] + "), " + a[2] + ")");
+      }
+      return define(R, std::string("min_i<") + ct + ">(max_i<" + ct + ">(" + a[1] + ", " + a[0] + "), " + a[2] + ")");
+    }
+    case OpKind::kAbs:
+      if (fa) return fn1("fabsf", "fabs");
+      return define(R, std::string("(") + ct + ")(" + a[0] + " < 0 ? -" + a[0] + " : " + a[0] + ")");
+    case OpKind::kNegate:
+      return fa ? fl("-" + a[0]) : define(R, std::string("(") + ct + ")(-" + a[0] + ")");
+    case OpKind::kExp: return R == DType::kF32 || dbl ? fn1("expf", "exp") : fn1("__expf", "exp");
+    case OpKind::kExpm1: return fn1("expm1f", "expm1");
+    case OpKind::kLog: return fn1("logf", "log");
+    case OpKind::kLog1p: return fn1("log1pf", "log1p");
+    case OpKind::kLogistic:
+      return dbl ? fl("1.0 / (1.0 + exp(-" + a[0] + "))") : fl("1.0f / (1.0f + expf(-" + a[0] + "))");
+    case OpKind::kSqrt: return fn1("sqrtf", "sqrt");
+    case OpKind::kRsqrt: return dbl ? fl("1.0 / sqrt(" + a[0] + ")") : fl("1.0f / sqrtf(" + a[0] + ")");
+    case OpKind::kCbrt: return fn1("cbrtf", "cbrt");
+    case OpKind::kTanh: return fn1("tanhf", "tanh");
+    case OpKind::kSine: return fn1("sinf", "sin");
+    case OpKind::kCosine: return fn1("cosf", "cos");
+    case OpKind::kTan: return fn1("tanf", "tan");
+    case OpKind::kFloor: return fa ? fn1("floorf", "floor") : define(R, a[0]);
+    case OpKind::kCeil: return fa ? fn1("ceilf", "ceil") : define(R, a[0]);
+    case OpKind::kRoundAfz: return fn1("roundf", "round");
+    case OpKind::kRoundEven: return fn1("rintf", "rint");
+    case OpKind::kSign:
+      if (fa) return fl(std::string(dbl ? "sign_d(" : "sign_f(") + a[0] + ")");
+      return define(R, std::string("sign_i<") + ct + ">(" + a[0] + ")");
+    case OpKind::kIsFinite: return define(R, "__builtin_isfinite(" + a[0] + ")");
+    case OpKind::kPopcnt:
+      return define(R, std::string("(") + ct + ")" + (dtype_size(A) == 8 ? "__popcll((uint64_t)" : "__popc((uint32_t)(") +
+                           std::string(unsigned_of(A)) + ")" + a[0] + (dtype_size(A) == 8 ? ")" : "))"));
+    case OpKind::kClz: {
+      const size_t bits = dtype_size(A) * 8;
+      if (bits == 64) return define(R, std::string("(") + ct + ")__clzll((int64_t)" + a[0] + ")");
+      return define(R, std::string("(") + ct + ")(__clz((int32_t)(uint32_t)(" + unsigned_of(A) + ")" + a[0] + ") - " +
+                           std::to_string(32 - bits) + ")");
+    }
+    case OpKind::kConvert: {
+      const std::string x = a[0];
+      if (R == DType::kPred) return define(R, x + " != 0");
+      if (dtype_is_float(R)) {
+        if (R == DType::kF64) return define(R, "(double)" + x);
+        return fl("(float)" + x);
+      }
+      if (fa) {
+        const std::string xf = dbl ? "(float)" + x : x;
+        switch (R) {
+          case DType::kS32: return define(R, "f2i32(" + xf + ")");
+          case DType::kU32: return define(R, "f2u32(" + xf + ")");
+          case DType::kS64: return define(R, "f2i64(" + xf + ")");
+          case DType::kS8: return define(R, "f2i<int8_t>(" + xf + ", -128.0f, 127.0f)");
+          case DType::kU8: return define(R, "f2i<uint8_t>(" + xf + ", 0.0f, 255.0f)");
+          case DType::kS16: return define(R, "f2i<int16_t>(" + xf + ", -32768.0f, 32767.0f)");
+          case DType::kU16: return define(R, "f2i<uint16_t>(" + xf + ", 0.0f, 65535.0f)");
+          default: return define(R, std::string("(") + ct + ")(" + xf + ")");
+        }
+      }
+      return define(R, std::string("(") + ct + ")(" + x + ")");
+    }
+    case OpKind::kBitcastConvert: {
+      PJRTX_CHECK(dtype_size(A) == dtype_size(R), Code::kUnimplemented, "bitcast_convert between widths");
+      const std::string s = to_storage(A, a[0]);
+      return define(R, from_storage(R, std::string("__builtin_bit_cast(") + dtype_storage_ctype(R) + ", (" +
+                                           dtype_storage_ctype(A) + ")(" + s + "))"));
+    }
+    default:
+      fail(Code::kUnimplemented, std::string("cannot fuse op ") + op.name);
+  }
+}
+
+// ----------------------------------------------------------------------------
+
+struct Accum {
+  ReducerKind kind;
+  DType vt;            // value dtype (result 0)
+  DType it;            // index dtype (argmax result 1)
+  std::string acc_t;   // accumulator C type
+  std::string v, i;    // accumulator variable names (i for argmax)
+};
+
+std::string acc_ctype(ReducerKind k, DType t) {
+  if (k == ReducerKind::kAnd || k == ReducerKind::kOr) return "uint32_t";
+  if (t == DType::kF64) return "double";
+  if (dtype_is_float(t)) return "float";
+  if (t == DType::kPred) return "uint32_t";
+  return dtype_compute_ctype(t);
+}
+
+std::string identity_of(ReducerKind k, DType t, const std::string& ct) {
+  const bool f = dtype_is_float(t);
+  switch (k) {
+    case ReducerKind::kSum: return "(" + ct + ")0";
+    case ReducerKind::kProd: return "(" + ct + ")1";
+    case ReducerKind::kAnd: return "1u";
+    case ReducerKind::kOr: return "0u";
+    case ReducerKind::kMax:
+    case ReducerKind::kArgMax:
+      if (f) return t == DType::kF64 ? "-__builtin_inf()" : "-__builtin_inff()";
+      return dtype_is_signed_int(t) ? "(" + ct + ")((" + ct + ")1 << (sizeof(" + ct + ")*8-1))" : "(" + ct + ")0";
+    case ReducerKind::kMin:
+    case ReducerKind::kArgMin:
+      if (f) return t == DType::kF64 ? "__builtin_inf()" : "__builtin_inff()";
+      return dtype_is_signed_int(t) ? "(" + ct + ")(~((" + ct + ")1 << (sizeof(" + ct + ")*8-1)))" : "(" + ct + ")~(" + ct + ")0";
+  }
+  return "0";
+}
+
+// a = combine(a, b) for single-value reducers.
+std::string combine_stmt(ReducerKind k, DType t, const std::string& a, const std::string& b) {
+  const bool f = dtype_is_float(t);
+  const bool d = t == DType::kF64;
+  switch (k) {
+    case ReducerKind::kSum: return a + " += " + b + ";";
+    case ReducerKind::kProd: return a + " *= " + b + ";";
+    case ReducerKind::kAnd: return a + " = " + a + " & (uint32_t)(" + b + ");";
+    case ReducerKind::kOr: return a + " = " + a + " | (uint32_t)(" + b + ");";
+    case ReducerKind::kMax:
+      return a + " = " + (f ? (d ? "max_d(" : "max_f(") : "max_i(") + a + ", " + b + ");";
+    case ReducerKind::kMin:
+      return a + " = " + (f ? (d ? "min_d(" : "min_f(") : "min_i(") + a + ", " + b + ");";
+    default: return "";
+  }
+}
+
+std::string arg_better(ReducerKind k) { return k == ReducerKind::kArgMax ? "argmax_better" : "argmin_better"; }
+
+class KernelGen {
+ public:
+  KernelGen(const Program& prog, std::ostringstream& out) : prog_(prog), out_(out) {}
+  void loop(Step& s);
+  void reduce(Step& s);
+
+ private:
+  const Program& prog_;
+  std::ostringstream& out_;
+
+  std::string idx_type(const Step& s) {
+    int64_t m = 0;
+    for (int v : s.inputs) m = std::max(m, prog_.type(v).elements());
+    for (int v : s.outputs) m = std::max(m, prog_.type(v).elements());
+    if (s.kind == StepKind::kReduce) m = std::max(m, num_elements(s.reduce_operand_shape));
+    if (s.kind == StepKind::kLoop) m = std::max(m, num_elements(s.loop_shape));
+    return m < (int64_t(1) << 31) ? "uint32_t" : "uint64_t";
+  }
+  void signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch);
+};
+
+void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch) {
+  out_ << "extern \"C\" __global__ void __launch_bounds__(256) " << s.name << "(";
+  int k = 0;
+  for (int v : s.inputs) {
+    const DType t = prog_.type(v).dtype;
+    out_ << (k ? ", " : "") << "const " << dtype_storage_ctype(t) << "* __restrict__ in" << k;
+    (*ptr_of)[v] = "in" + std::to_string(k);
+    ++k;
+  }
+  int o = 0;
+  for (int v : s.outputs) {
+    const DType t = prog_.type(v).dtype;
+    out_ << (k + o ? ", " : "") << dtype_storage_ctype(t) << "* __restrict__ out" << o;
+    ++o;
+  }
+  if (with_scratch) out_ << ", unsigned char* __restrict__ scratch, uint32_t* __restrict__ counters";
+  out_ << ") {\n";
+}
+
+void KernelGen::loop(Step& s) {
+  std::map<int, std::string> ptr_of;
+  signature(s, &ptr_of, false);
+  const std::string it = idx_type(s);
+  const int64_t n = num_elements(s.loop_shape);
+  const int vec = s.vec;
+  out_ << "typedef " << it << " idx_t;\n";
+  out_ << "const idx_t n = " << n << "u;\n";
+  out_ << "const idx_t base = ((idx_t)blockIdx.x * 256u + threadIdx.x) * " << vec << "u;\n";
+  out_ << "if (base >= n) return;\n";
+  out_ << "const bool full = base + " << vec << "u <= n;\n";
+  Writer w(prog_, ptr_of, it);
+  // Inputs with the root's element count are read at the root linear index
+  // through a reshape chain at most: preload them as vectors.
+  for (int v : s.inputs) {
+    if (prog_.type(v).elements() != n) continue;
+    const DType t = prog_.type(v).dtype;
+    std::string name = "pre_" + ptr_of[v];
+    out_ << dtype_storage_ctype(t) << " " << name << "[" << vec << "];\n";
+    out_ << "ldv<" << dtype_storage_ctype(t) << ", " << vec << ">(" << name << ", " << ptr_of[v] << ", base, n, full);\n";
+    w.preload[v] = name;
+  }
+  for (size_t o = 0; o < s.outputs.size(); ++o) {
+    out_ << dtype_storage_ctype(prog_.type(s.outputs[o]).dtype) << " res" << o << "[" << vec << "];\n";
+  }
+  Idx root;
+  root.key = "R";
+  root.shape = s.loop_shape;
+  root.lin = "lin";
+  root.identity = true;
+  const int rid = w.add_index(root);
+  w.multi_of(rid);  // unused digits are dropped by the compiler
+  std::vector<std::string> vals;
+  for (int v : s.outputs) vals.push_back(w.value(v, rid));
+  out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
+  out_ << "const idx_t lin = full ? base + j : ((base + j < n) ? base + j : n - 1u);\n";
+  out_ << w.body.str();
+  for (size_t o = 0; o < s.outputs.size(); ++o)
+    out_ << "res" << o << "[j] = " << to_storage(prog_.type(s.outputs[o]).dtype, vals[o]) << ";\n";
+  out_ << "}\n";
+  for (size_t o = 0; o < s.outputs.size(); ++o) {
+    const DType t = prog_.type(s.outputs[o]).dtype;
+    out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", base, res" << o << ", n, full);\n";
+  }
+  out_ << "}\n\n";
+}
+
+void KernelGen::reduce(Step& s) {
+  std::map<int, std::string> ptr_of;
+  const bool split = s.row_schedule && s.splits > 1;
+  signature(s, &ptr_of, split);
+  const std::string it = idx_type(s);
+  out_ << "typedef " << it << " idx_t;\n";
+  const Dims& shape = s.reduce_operand_shape;
+  const int rank = static_cast<int>(shape.size());
+  auto is_red = [&](int d) {
+    return std::binary_search(s.reduce_dims.begin(), s.reduce_dims.end(), static_cast<int64_t>(d));
+  };
+  Dims kept_dims, red_dims;
+  for (int d = 0; d < rank; ++d) (is_red(d) ? red_dims : kept_dims).push_back(shape[d]);
+
+  // Accumulators.
+  std::vector<Accum> accs;
+  for (size_t r = 0; r < s.reduces.size(); ++r) {
+    const ReduceSpec& rs = s.reduces[r];
+    Accum a;
+    a.kind = rs.kind;
+    a.vt = prog_.type(rs.results[0]).dtype;
+    a.it = rs.results.size() > 1 ? prog_.type(rs.results[1]).dtype : DType::kInvalid;
+    a.acc_t = acc_ctype(rs.kind, a.vt);
+    a.v = "acc" + std::to_string(r);
+    a.i = "aci" + std::to_string(r);
+    accs.push_back(a);
+  }
+  const bool arg = [&] {
+    for (auto& a : accs)
+      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) return true;
+    return false;
+  }();
+  (void)arg;
+
+  Writer w(prog_, ptr_of, it);
+  // Root index over the reduce operand shape.
+  Idx root;
+  root.key = "R";
+  root.shape = shape;
+  root.lin = "lin";
+  root.identity = s.row_schedule;
+  root.multi.resize(rank);
+  const int vec = s.vec;
+
+  std::ostringstream head;  // before the element loop
+  if (s.row_schedule) {
+    head << "const idx_t row = (idx_t)blockIdx.x / " << s.splits << "u;\n";
+    head << "const idx_t split = (idx_t)blockIdx.x - row * " << s.splits << "u;\n";
+    head << "const idx_t c0 = split * " << s.chunk << "u;\n";
+    head << "const idx_t c1 = (c0 + " << s.chunk << "u < " << s.row_len << "u) ? c0 + " << s.chunk << "u : "
+         << s.row_len << "u;\n";
+    // kept digits from row, reduced digits from col
+    std::string rest = "row";
+    for (int d = rank - 1, k = static_cast<int>(kept_dims.size()) - 1; d >= 0; --d) {
+      if (is_red(d)) continue;
+      if (k == 0) {
+        root.multi[d] = rest;
+      } else {
+        head << "const idx_t kd" << d << " = " << rest << " % " << shape[d] << "u;\n";
+        head << "const idx_t kq" << d << " = " << rest << " / " << shape[d] << "u;\n";
+        root.multi[d] = "kd" + std::to_string(d);
+        rest = "kq" + std::to_string(d);
+      }
+      --k;
+    }
+  } else {
+    head << "const idx_t row = (idx_t)blockIdx.x * 256u + threadIdx.x;\n";
+    head << "if (row >= " << s.rows << "u) return;\n";
+    std::string rest = "row";
+    for (int d = rank - 1, k = static_cast<int>(kept_dims.size()) - 1; d >= 0; --d) {
+      if (is_red(d)) continue;
+      if (k == 0) {
+        root.multi[d] = rest;
+      } else {
+        head << "const idx_t kd" << d << " = " << rest << " % " << shape[d] << "u;\n";
+        head << "const idx_t kq" << d << " = " << rest << " / " << shape[d] << "u;\n";
+        root.multi[d] = "kd" + std::to_string(d);
+        rest = "kq" + std::to_string(d);
+      }
+      --k;
+    }
+  }
+  // Reduced digits from `col` (emitted inside the element loop).
+  std::ostringstream col_digits;
+  {
+    std::string rest = "col";
+    for (int d = rank - 1, k = static_cast<int>(red_dims.size()) - 1; d >= 0; --d) {
+      if (!is_red(d)) continue;
+      if (k == 0) {
+        root.multi[d] = rest;
+      } else {
+        col_digits << "const idx_t rd" << d << " = " << rest << " % " << shape[d] << "u;\n";
+        col_digits << "const idx_t rq" << d << " = " << rest << " / " << shape[d] << "u;\n";
+        root.multi[d] = "rd" + std::to_string(d);
+        rest = "rq" + std::to_string(d);
+      }
+      --k;
+    }
+  }
+  if (kept_dims.empty()) {
+    // nothing: all dims reduced
+  }
+  const int rid = w.add_index(root);
+  // Values of every reduce operand at the root.
+  std::vector<std::vector<std::string>> xs(s.reduces.size());
+  // Preloads (row schedule only).
+  std::ostringstream pre;
+  if (s.row_schedule) {
+    const int64_t n_all = num_elements(shape);
+    for (int v : s.inputs) {
+      if (prog_.type(v).elements() != n_all) continue;
+      const DType t = prog_.type(v).dtype;
+      std::string name = "pre_" + ptr_of[v];
+      pre << dtype_storage_ctype(t) << " " << name << "[" << vec << "];\n";
+      pre << "ldv<" << dtype_storage_ctype(t) << ", " << vec << ">(" << name << ", " << ptr_of[v]
+          << ", lbase, row * " << s.row_len << "u + c1, full);\n";
+      w.preload[v] = name;
+    }
+  }
+  for (size_t r = 0; r < s.reduces.size(); ++r)
+    for (int v : s.reduces[r].inputs) xs[r].push_back(w.value(v, rid));
+  std::string elem_body = w.body.str();
+
+  out_ << head.str();
+  for (auto& a : accs) {
+    out_ << a.acc_t << " " << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
+    if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
+      out_ << "int64_t " << a.i << " = 0x7fffffffffffffffll;\n";
+  }
+  auto combine_elem = [&](std::ostream& o) {
+    for (size_t r = 0; r < accs.size(); ++r) {
+      const Accum& a = accs[r];
+      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
+        o << "if (" << arg_better(a.kind) << "((float)" << xs[r][0] << ", (int64_t)" << xs[r][1] << ", " << a.v << ", "
+          << a.i << ")) { " << a.v << " = " << xs[r][0] << "; " << a.i << " = (int64_t)" << xs[r][1] << "; }\n";
+      } else {
+        o << combine_stmt(a.kind, a.vt, a.v, "(" + a.acc_t + ")(" + xs[r][0] + ")") << "\n";
+      }
+    }
+  };
+  if (s.row_schedule) {
+    out_ << "for (idx_t c = c0 + threadIdx.x * " << vec << "u; c < c1; c += " << 256 * vec << "u) {\n";
+    out_ << "const idx_t lbase = row * " << s.row_len << "u + c;\n";
+    out_ << "const bool full = c + " << vec << "u <= c1;\n";
+    out_ << pre.str();
+    out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
+    out_ << "if (full || c + j < c1) {\n";
+    out_ << "const idx_t col = c + j;\nconst idx_t lin = lbase + j;\n";
+    out_ << col_digits.str() << elem_body;
+    combine_elem(out_);
+    out_ << "}\n}\n}\n";
+    // Shared slots for the cross-wave step of the block reductions.
+    for (auto& a : accs) {
+      out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[4];\n";
+      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << "__shared__ int64_t sm_" << a.i << "[4];\n";
+    }
+    // Block reduction: 64-lane xor butterfly, then the 4 wave results are
+    // combined in wave order by thread 0 (fixed order: deterministic).
+    auto block_reduce = [&]() {
+      for (auto& a : accs) {
+        const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
+        out_ << "#pragma unroll\nfor (int m = 32; m >= 1; m >>= 1) {\n";
+        if (am) {
+          out_ << "const float ov = wave_shfl_xor(" << a.v << ", m);\n";
+          out_ << "const int64_t oi = wave_shfl_xor(" << a.i << ", m);\n";
+          out_ << "if (" << arg_better(a.kind) << "(ov, oi, " << a.v << ", " << a.i << ")) { " << a.v << " = ov; " << a.i
+               << " = oi; }\n";
+        } else {
+          out_ << "const " << a.acc_t << " o = wave_shfl_xor(" << a.v << ", m);\n";
+          out_ << combine_stmt(a.kind, a.vt, a.v, "o") << "\n";
+        }
+        out_ << "}\n";
+      }
+      out_ << "if ((threadIdx.x & 63) == 0) {\n";
+      for (auto& a : accs) {
+        out_ << "sm_" << a.v << "[threadIdx.x >> 6] = " << a.v << ";\n";
+        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
+          out_ << "sm_" << a.i << "[threadIdx.x >> 6] = " << a.i << ";\n";
+      }
+      out_ << "}\n__syncthreads();\n";
+      out_ << "if (threadIdx.x == 0) {\n";
+      for (auto& a : accs) {
+        const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
+        out_ << a.v << " = sm_" << a.v << "[0];\n";
+        if (am) out_ << a.i << " = sm_" << a.i << "[0];\n";
+        out_ << "for (int k = 1; k < 4; ++k) {\n";
+        if (am) {
+          out_ << "if (" << arg_better(a.kind) << "(sm_" << a.v << "[k], sm_" << a.i << "[k], " << a.v << ", " << a.i
+               << ")) { " << a.v << " = sm_" << a.v << "[k]; " << a.i << " = sm_" << a.i << "[k]; }\n";
+        } else {
+          out_ << combine_stmt(a.kind, a.vt, a.v, "sm_" + a.v + "[k]") << "\n";
+        }
+        out_ << "}\n";
+      }
+      out_ << "}\n";
+    };
+    block_reduce();
+    if (split) {
+      // Partials in scratch: per reducer a [rows*splits] array of 8-byte
+      // slots (argmax: value slots then index slots). The workgroup that
+      // arrives last for a row combines the row's partials with all of its
+      // threads (thread t reads split t) in the same fixed tree.
+      size_t off = 0;
+      const int64_t slots = s.rows * s.splits;
+      std::vector<size_t> offs;
+      for (auto& a : accs) {
+        offs.push_back(off);
+        off += static_cast<size_t>(slots) * 8;
+        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) off += static_cast<size_t>(slots) * 8;
+      }
+      out_ << "__shared__ uint32_t sm_last;\n";
+      out_ << "if (threadIdx.x == 0) {\n";
+      for (size_t r = 0; r < accs.size(); ++r) {
+        const Accum& a = accs[r];
+        out_ << "{ uint64_t* slot = reinterpret_cast<uint64_t*>(scratch + " << offs[r] << "u);\n";
+        out_ << "uint64_t bits = 0; __builtin_memcpy(&bits, &" << a.v << ", sizeof(" << a.v << "));\n";
+        out_ << "__hip_atomic_store(&slot[row * " << s.splits << "u + split], bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
+          out_ << "__hip_atomic_store(&slot[" << slots << "u + row * " << s.splits << "u + split], (uint64_t)" << a.i
+               << ", __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+        }
+        out_ << "}\n";
+      }
+      out_ << "__threadfence();\n";
+      out_ << "sm_last = (atomicAdd(&counters[row], 1u) == " << s.splits - 1 << "u) ? 1u : 0u;\n";
+      out_ << "}\n__syncthreads();\n";
+      out_ << "if (sm_last == 0u) return;\n";
+      out_ << "__threadfence();\n";
+      for (size_t r = 0; r < accs.size(); ++r) {
+        const Accum& a = accs[r];
+        const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
+        out_ << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
+        if (am) out_ << a.i << " = 0x7fffffffffffffffll;\n";
+        out_ << "if (threadIdx.x < " << s.splits << "u) {\n";
+        out_ << "uint64_t* slot = reinterpret_cast<uint64_t*>(scratch + " << offs[r] << "u);\n";
+        out_ << "const uint64_t bits = __hip_atomic_load(&slot[row * " << s.splits
+             << "u + threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+        out_ << "__builtin_memcpy(&" << a.v << ", &bits, sizeof(" << a.v << "));\n";
+        if (am) {
+          out_ << a.i << " = (int64_t)__hip_atomic_load(&slot[" << slots << "u + row * " << s.splits
+               << "u + threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+        }
+        out_ << "}\n";
+      }
+      block_reduce();
+      out_ << "if (threadIdx.x == 0) __hip_atomic_store(&counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+    }
+    out_ << "if (threadIdx.x != 0) return;\n";
+  } else {
+    // Column schedule: one thread per output, serial walk of reduced elements.
+    out_ << "for (idx_t col = 0; col < " << s.row_len << "u; ++col) {\n";
+    out_ << col_digits.str();
+    // linear index of the full multi-index
+    std::string lin;
+    {
+      int64_t stride = 1;
+      for (int d = rank - 1; d >= 0; --d) {
+        if (shape[d] != 1) {
+          std::string term = stride == 1 ? "(" + root.multi[d] + ")" : "(" + root.multi[d] + ")*" + std::to_string(stride) + "u";
+          lin = lin.empty() ? term : term + " + " + lin;
+        }
+        stride *= shape[d];
+      }
+      if (lin.empty()) lin = "0";
+    }
+    out_ << "const idx_t lin = " << lin << ";\n";
+    out_ << elem_body;
+    combine_elem(out_);
+    out_ << "}\n";
+  }
+  // Final: fold in the init values, evaluate the epilogue, store.
+  Writer e(prog_, ptr_of, it);
+  Idx oroot;
+  oroot.key = "O";
+  oroot.shape = kept_dims;
+  oroot.lin = "row";
+  const int oid = e.add_index(oroot);
+  e.multi_of(oid);
+  Idx sidx;
+  sidx.key = "S";
+  sidx.lin = "0";
+  const int scal = e.add_index(sidx);
+  std::ostringstream fin;
+  for (size_t r = 0; r < accs.size(); ++r) {
+    const Accum& a = accs[r];
+    const ReduceSpec& rs = s.reduces[r];
+    const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
+    std::string init0 = e.value(rs.inits[0], scal);
+    if (am) {
+      std::string init1 = e.value(rs.inits[1], scal);
+      fin << "if (" << arg_better(a.kind) << "((float)" << init0 << ", (int64_t)" << init1 << ", " << a.v << ", " << a.i
+          << ")) { " << a.v << " = " << init0 << "; " << a.i << " = (int64_t)" << init1 << "; }\n";
+    } else {
+      fin << combine_stmt(a.kind, a.vt, a.v, "(" + a.acc_t + ")(" + init0 + ")") << "\n";
+    }
+    // Seed the reduce results at the output index.
+    const DType vt = a.vt;
+    std::string rv = "fin" + std::to_string(r);
+    if (a.kind == ReducerKind::kAnd || a.kind == ReducerKind::kOr) {
+      fin << "const " << dtype_compute_ctype(vt) << " " << rv << " = (" << dtype_compute_ctype(vt) << ")" << a.v << ";\n";
+    } else if (dtype_is_float(vt)) {
+      fin << "const " << dtype_compute_ctype(vt) << " " << rv << " = " << round_to(vt, a.v) << ";\n";
+    } else {
+      fin << "const " << dtype_compute_ctype(vt) << " " << rv << " = (" << dtype_compute_ctype(vt) << ")" << a.v << ";\n";
+    }
+    e.seed(rs.results[0], oid, rv);
+    if (am) {
+      std::string ri = "fni" + std::to_string(r);
+      fin << "const " << dtype_compute_ctype(a.it) << " " << ri << " = (" << dtype_compute_ctype(a.it) << ")" << a.i << ";\n";
+      e.seed(rs.results[1], oid, ri);
+    }
+  }
+  std::vector<std::string> outs;
+  for (int v : s.outputs) outs.push_back(e.value(v, oid));
+  out_ << "{\n" << fin.str() << e.body.str();
+  for (size_t o = 0; o < s.outputs.size(); ++o)
+    out_ << "out" << o << "[row] = " << to_storage(prog_.type(s.outputs[o]).dtype, outs[o]) << ";\n";
+  out_ << "}\n}\n\n";
+}
+
+}  // namespace
+
+std::string generate_kernels(const Program& prog, Plan& plan) {
+  std::ostringstream out;
+  KernelGen gen(prog, out);
+  for (Step& s : plan.steps) {
+    if (s.kind == StepKind::kLoop) gen.loop(s);
+    else if (s.kind == StepKind::kReduce) gen.reduce(s);
+  }
+  return out.str();
+}
+
+}  // namespace pjrtx

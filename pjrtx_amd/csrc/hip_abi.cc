@@ -1,0 +1,179 @@
+// pjrtx_hip_* C ABI (declared in include/pjrtx_hip.h).
+#include <cstring>
+#include <map>
+#include <mutex>
+
+#include "../../include/pjrt_c_api.h"
+#include "../../include/pjrtx_hip.h"
+#include "pjrt_handles.h"
+#include "runtime.h"
+
+using namespace pjrtx;
+
+namespace {
+thread_local std::string g_last_error;
+
+template <typename Fn>
+int guarded(Fn&& fn) {
+  try {
+    fn();
+    return 0;
+  } catch (const Error& e) {
+    g_last_error = e.what();
+    return static_cast<int>(e.code);
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return static_cast<int>(Code::kInternal);
+  }
+}
+
+std::mutex g_mu;
+std::map<int, std::unique_ptr<Device>> g_abi_devices;
+std::map<void*, MemRef> g_abi_allocs;
+
+Device* abi_device(int ordinal) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_abi_devices.find(ordinal);
+  if (it != g_abi_devices.end()) return it->second.get();
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || ordinal < 0 || ordinal >= n) {
+    (void)hipGetLastError();
+    fail(Code::kFailedPrecondition, strformat("no HIP device %d", ordinal));
+  }
+  auto d = std::make_unique<Device>(ordinal);
+  Device* raw = d.get();
+  g_abi_devices[ordinal] = std::move(d);
+  return raw;
+}
+
+void copy_out(const std::string& s, char* out, size_t cap, size_t* needed) {
+  if (needed) *needed = s.size() + 1;
+  if (out && cap) {
+    const size_t n = std::min(cap - 1, s.size());
+    std::memcpy(out, s.data(), n);
+    out[n] = '\0';
+  }
+}
+}  // namespace
+
+extern "C" {
+
+const char* pjrtx_hip_last_error(void) { return g_last_error.c_str(); }
+
+int pjrtx_hip_device_count(int* count) {
+  return guarded([&] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    *count = n;
+  });
+}
+
+int pjrtx_hip_malloc(int device, size_t bytes, void** ptr) {
+  return guarded([&] {
+    MemRef m = abi_device(device)->allocate(bytes);
+    std::lock_guard<std::mutex> lk(g_mu);
+    *ptr = m->ptr;
+    if (m->ptr) g_abi_allocs[m->ptr] = m;
+  });
+}
+
+int pjrtx_hip_free(int device, void* ptr) {
+  return guarded([&] {
+    (void)device;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_abi_allocs.find(ptr);
+    PJRTX_CHECK(it != g_abi_allocs.end(), Code::kInvalidArgument, "pjrtx_hip_free: unknown pointer");
+    g_abi_allocs.erase(it);
+  });
+}
+
+int pjrtx_hip_copy_h2d(int device, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    Device* d = abi_device(device);
+    d->make_current();
+    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, d->stream()), "hipMemcpyAsync(H2D)");
+    hip_check(hipStreamSynchronize(d->stream()), "hipStreamSynchronize");
+  });
+}
+
+int pjrtx_hip_copy_d2h(int device, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    Device* d = abi_device(device);
+    d->make_current();
+    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, d->stream()), "hipMemcpyAsync(D2H)");
+    hip_check(hipStreamSynchronize(d->stream()), "hipStreamSynchronize");
+  });
+}
+
+int pjrtx_hip_synchronize(int device) {
+  return guarded([&] {
+    Device* d = abi_device(device);
+    hip_check(hipStreamSynchronize(d->stream()), "hipStreamSynchronize");
+  });
+}
+
+int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
+  return guarded([&] {
+    Program prog = parse_stablehlo(std::string(text, len));
+    Plan plan = make_plan(prog);
+    copy_out(plan.describe(prog), out, cap, needed);
+  });
+}
+
+int pjrtx_compile_check(const char* text, size_t len, const char* arch, size_t* code_size) {
+  return guarded([&] {
+    Program prog = parse_stablehlo(std::string(text, len));
+    Plan plan = make_plan(prog);
+    size_t n = 0;
+    if (plan.num_fusion_kernels > 0) n = compile_kernels(plan.kernel_source, arch ? arch : "gfx950").size();
+    if (code_size) *code_size = n;
+  });
+}
+
+int pjrtx_kernel_source(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
+  return guarded([&] {
+    Program prog = parse_stablehlo(std::string(text, len));
+    Plan plan = make_plan(prog);
+    copy_out(kernel_translation_unit(plan.kernel_source), out, cap, needed);
+  });
+}
+
+int pjrtx_executable_time_steps(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* args, size_t num_args, int iters,
+                                double* ms, size_t cap, size_t* steps) {
+  return guarded([&] {
+    PJRTX_CHECK(exe && iters > 0, Code::kInvalidArgument, "time_steps: bad arguments");
+    std::vector<BufferRef> in;
+    for (size_t i = 0; i < num_args; ++i) in.push_back(args[i]->buf);
+    Device* dev = in.empty() ? exe->devices.at(0)->dev : in[0]->dev;
+    std::vector<double> t = exe->exe->time_steps(dev, in, iters);
+    if (steps) *steps = t.size();
+    for (size_t i = 0; i < t.size() && i < cap; ++i) ms[i] = t[i];
+  });
+}
+
+int pjrtx_executable_step_names(PJRT_LoadedExecutable* exe, char* out, size_t cap, size_t* needed) {
+  return guarded([&] {
+    std::string s;
+    for (const Step& st : exe->exe->plan().steps) {
+      std::string n = st.name;
+      if (n.empty()) n = st.kind == StepKind::kLibrary ? std::string("lib:") + lib_kind_name(st.lib) : "-";
+      s += n + "\n";
+    }
+    copy_out(s, out, cap, needed);
+  });
+}
+
+int pjrtx_executable_stats(PJRT_LoadedExecutable* exe, int64_t out[4]) {
+  return guarded([&] {
+    ExecStats s = exe->exe->stats();
+    out[0] = s.executions;
+    out[1] = s.kernel_launches;
+    out[2] = s.library_calls;
+    out[3] = s.released_values;
+  });
+}
+
+}  // extern "C"

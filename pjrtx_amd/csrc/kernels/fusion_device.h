@@ -1,0 +1,240 @@
+// Device-side building blocks for the per-fusion-group kernels that the
+// planner generates at PJRT compile time (compiled with hiprtc for gfx950).
+//
+// The generated kernel for a fusion group is this header plus one
+// expression body: the hand-written parts here are the memory access
+// (16-byte vector loads/stores), the XLA element semantics of every
+// StableHLO elementwise op, and the 64-lane wavefront + LDS reductions.
+// It replaces the reference's generated MSL helpers
+// (reference: src/backend/mlx_metal/executable_metal_graph_map_rules.zig:41-234,
+// executable_metal_graph_reduction.zig:57-323).
+//
+// Element policy: f16/bf16 values are carried in float registers and rounded
+// back to their type after every op whose result has that type, which keeps
+// the per-op rounding of a bf16/f16 program.
+#pragma once
+
+typedef unsigned char uint8_t;
+typedef signed char int8_t;
+typedef unsigned short uint16_t;
+typedef short int16_t;
+typedef unsigned int uint32_t;
+typedef int int32_t;
+typedef unsigned long long uint64_t;
+typedef long long int64_t;
+
+#define PJRTX_DEV static __device__ __forceinline__
+
+// ---------------------------------------------------------------- conversions
+
+PJRTX_DEV float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+PJRTX_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+PJRTX_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+PJRTX_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+PJRTX_DEV uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+PJRTX_DEV float round_f16(float f) { return (float)(_Float16)f; }
+
+// Storage <-> compute for each element kind.
+PJRTX_DEV float ld_f32(const float* p, uint32_t i) { return p[i]; }
+PJRTX_DEV float ld_bf16(const uint16_t* p, uint32_t i) { return bf16_to_f32(p[i]); }
+PJRTX_DEV float ld_f16(const uint16_t* p, uint32_t i) { return f16_to_f32(p[i]); }
+
+// ------------------------------------------------------------ vector accesses
+// Loads N consecutive storage elements starting at `base` (multiple of N).
+// `full` is false only for the last partial vector of a tensor, which is read
+// element by element up to `n`.
+
+template <typename S, int N>
+struct VecBytes {
+  static constexpr int kBytes = (int)sizeof(S) * N;
+};
+
+template <typename S, int N>
+PJRTX_DEV void ldv(S (&dst)[N], const S* __restrict__ src, uint32_t base, uint32_t n, bool full) {
+  if (full) {
+    constexpr int kBytes = (int)sizeof(S) * N;
+    if constexpr (kBytes % 16 == 0) {
+      typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int c = 0; c < kBytes / 16; ++c) {
+        v4 v = *reinterpret_cast<const v4*>(reinterpret_cast<const char*>(src + base) + 16 * c);
+        *reinterpret_cast<v4*>(reinterpret_cast<char*>(dst) + 16 * c) = v;
+      }
+    } else if constexpr (kBytes == 8) {
+      typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<v2*>(dst) = *reinterpret_cast<const v2*>(src + base);
+    } else if constexpr (kBytes == 4) {
+      *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src + base);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) dst[j] = src[base + j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) dst[j] = (base + j < n) ? src[base + j] : src[n - 1];
+  }
+}
+
+template <typename S, int N>
+PJRTX_DEV void stv(S* __restrict__ dst, uint32_t base, const S (&src)[N], uint32_t n, bool full) {
+  if (full) {
+    constexpr int kBytes = (int)sizeof(S) * N;
+    if constexpr (kBytes % 16 == 0) {
+      typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int c = 0; c < kBytes / 16; ++c) {
+        *reinterpret_cast<v4*>(reinterpret_cast<char*>(dst + base) + 16 * c) =
+            *reinterpret_cast<const v4*>(reinterpret_cast<const char*>(src) + 16 * c);
+      }
+    } else if constexpr (kBytes == 8) {
+      typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<v2*>(dst + base) = *reinterpret_cast<const v2*>(src);
+    } else if constexpr (kBytes == 4) {
+      *reinterpret_cast<uint32_t*>(dst + base) = *reinterpret_cast<const uint32_t*>(src);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) dst[base + j] = src[j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (base + j < n) dst[base + j] = src[j];
+  }
+}
+
+// -------------------------------------------------- XLA elementwise semantics
+
+PJRTX_DEV bool isnan_f(float x) { return x != x; }
+PJRTX_DEV bool isnan_d(double x) { return x != x; }
+
+// maximum/minimum propagate NaN (XLA semantics), unlike fmaxf/fminf.
+PJRTX_DEV float max_f(float a, float b) { return (isnan_f(a) || a >= b) ? a : b; }
+PJRTX_DEV float min_f(float a, float b) { return (isnan_f(a) || a <= b) ? a : b; }
+PJRTX_DEV double max_d(double a, double b) { return (isnan_d(a) || a >= b) ? a : b; }
+PJRTX_DEV double min_d(double a, double b) { return (isnan_d(a) || a <= b) ? a : b; }
+template <typename T> PJRTX_DEV T max_i(T a, T b) { return a > b ? a : b; }
+template <typename T> PJRTX_DEV T min_i(T a, T b) { return a < b ? a : b; }
+
+PJRTX_DEV float sign_f(float x) { return isnan_f(x) ? x : (x > 0.f ? 1.f : (x < 0.f ? -1.f : x)); }
+PJRTX_DEV double sign_d(double x) { return isnan_d(x) ? x : (x > 0.0 ? 1.0 : (x < 0.0 ? -1.0 : x)); }
+template <typename T> PJRTX_DEV T sign_i(T x) { return (T)((x > 0) - (x < 0)); }
+
+PJRTX_DEV float logistic_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+PJRTX_DEV float rsqrt_f(float x) { return 1.0f / sqrtf(x); }
+PJRTX_DEV float is_finite_f(float x) { return __builtin_isfinite(x); }
+
+// Integer division / remainder with XLA's defined results for x/0 and
+// INT_MIN/-1 (x/0 = -1, x%0 = x, INT_MIN/-1 = INT_MIN, INT_MIN%-1 = 0).
+template <typename T> PJRTX_DEV T div_s(T a, T b) {
+  if (b == 0) return (T)-1;
+  if (b == (T)-1 && a == (T)((T)1 << (sizeof(T) * 8 - 1))) return a;
+  return a / b;
+}
+template <typename T> PJRTX_DEV T rem_s(T a, T b) {
+  if (b == 0) return a;
+  if (b == (T)-1) return 0;
+  return a % b;
+}
+template <typename T> PJRTX_DEV T div_u(T a, T b) { return b == 0 ? (T)~(T)0 : a / b; }
+template <typename T> PJRTX_DEV T rem_u(T a, T b) { return b == 0 ? a : a % b; }
+
+// Shifts: amounts >= bit width give 0 (left/logical) or the sign fill.
+template <typename T, typename U> PJRTX_DEV T shl(T a, T b) {
+  return ((U)b >= sizeof(T) * 8) ? (T)0 : (T)((U)a << (U)b);
+}
+template <typename T, typename U> PJRTX_DEV T shr_logical(T a, T b) {
+  return ((U)b >= sizeof(T) * 8) ? (T)0 : (T)((U)a >> (U)b);
+}
+template <typename T, typename U> PJRTX_DEV T shr_arith(T a, T b) {
+  const U bits = sizeof(T) * 8;
+  return ((U)b >= bits) ? (T)(a < 0 ? -1 : 0) : (T)(a >> b);
+}
+
+template <typename T> PJRTX_DEV T ipow(T base, T exp) {
+  if (exp < 0) return (base == 1) ? (T)1 : (base == (T)-1 ? ((exp & 1) ? (T)-1 : (T)1) : (T)0);
+  T r = 1;
+  while (exp) {
+    if (exp & 1) r *= base;
+    base *= base;
+    exp >>= 1;
+  }
+  return r;
+}
+
+// float -> integer converts saturate and map NaN to 0 (XLA semantics).
+template <typename T> PJRTX_DEV T f2i(float x, float lo, float hi) {
+  if (isnan_f(x)) return (T)0;
+  if (x <= lo) return (T)lo;
+  if (x >= hi) return (T)hi;
+  return (T)x;
+}
+PJRTX_DEV int32_t f2i32(float x) {
+  if (isnan_f(x)) return 0;
+  if (x <= -2147483648.0f) return (-2147483647 - 1);
+  if (x >= 2147483648.0f) return 2147483647;
+  return (int32_t)x;
+}
+PJRTX_DEV uint32_t f2u32(float x) {
+  if (isnan_f(x) || x <= 0.0f) return 0u;
+  if (x >= 4294967296.0f) return 4294967295u;
+  return (uint32_t)x;
+}
+PJRTX_DEV int64_t f2i64(float x) {
+  if (isnan_f(x)) return 0;
+  if (x <= -9223372036854775808.0f) return (-9223372036854775807LL - 1);
+  if (x >= 9223372036854775808.0f) return 9223372036854775807LL;
+  return (int64_t)x;
+}
+
+// Float total order key (for TOTALORDER comparisons).
+// Negative floats get their magnitude bits flipped so that signed integer
+// order equals -NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN.
+PJRTX_DEV int32_t total_order_key(float x) {
+  int32_t i = __builtin_bit_cast(int32_t, x);
+  return i < 0 ? (i ^ 0x7fffffff) : i;
+}
+
+// ------------------------------------------------------------ argmax order
+// (value, index) pairs ordered so that NaN wins over any number, larger
+// values win, and ties go to the lower index. This is the order JAX's argmax
+// comparator defines; it is total on distinct indices, so any combine tree
+// gives the same winner.
+PJRTX_DEV bool argmax_better(float va, int64_t ia, float vb, int64_t ib) {
+  const bool na = isnan_f(va), nb = isnan_f(vb);
+  if (na != nb) return na;
+  if (!na && va != vb) return va > vb;
+  return ia < ib;
+}
+PJRTX_DEV bool argmin_better(float va, int64_t ia, float vb, int64_t ib) {
+  const bool na = isnan_f(va), nb = isnan_f(vb);
+  if (na != nb) return na;
+  if (!na && va != vb) return va < vb;
+  return ia < ib;
+}
+
+// ------------------------------------------------------ wavefront reductions
+// 64-lane wavefronts: xor-butterfly over lane offsets 32..1. Every lane ends
+// with the same value, combined in a fixed order (deterministic).
+
+template <typename T>
+PJRTX_DEV T wave_shfl_xor(T v, int mask) {
+  if constexpr (sizeof(T) == 8) {
+    uint64_t u = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    lo = (uint32_t)__shfl_xor((int)lo, mask, 64);
+    hi = (uint32_t)__shfl_xor((int)hi, mask, 64);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __shfl_xor(__builtin_bit_cast(int, v), mask, 64));
+  } else {
+    return (T)__shfl_xor((int)v, mask, 64);
+  }
+}

@@ -1,0 +1,598 @@
+// Fusion planner implementation. See planner.h for the contract.
+#include "planner.h"
+
+#include <algorithm>
+#include <functional>
+#include <queue>
+#include <sstream>
+
+namespace pjrtx {
+
+const char* reducer_name(ReducerKind k) {
+  switch (k) {
+    case ReducerKind::kSum: return "sum";
+    case ReducerKind::kProd: return "prod";
+    case ReducerKind::kMax: return "max";
+    case ReducerKind::kMin: return "min";
+    case ReducerKind::kAnd: return "and";
+    case ReducerKind::kOr: return "or";
+    case ReducerKind::kArgMax: return "argmax";
+    case ReducerKind::kArgMin: return "argmin";
+  }
+  return "?";
+}
+
+const char* lib_kind_name(LibKind k) {
+  switch (k) {
+    case LibKind::kCopy: return "copy";
+    case LibKind::kDot: return "dot_general";
+    case LibKind::kGather: return "gather";
+    case LibKind::kScatter: return "scatter";
+    case LibKind::kDynamicSlice: return "dynamic_slice";
+    case LibKind::kDynamicUpdateSlice: return "dynamic_update_slice";
+    case LibKind::kConcatenate: return "concatenate";
+    case LibKind::kPad: return "pad";
+  }
+  return "?";
+}
+
+ReducerKind classify_reducer(const Program& prog, const Op& op) {
+  PJRTX_CHECK(op.regions.size() == 1, Code::kInvalidArgument, "reduce needs exactly one region");
+  const Region& r = op.regions[0];
+  const size_t n = op.results.size();
+  if (n == 2) {
+    // (values, indices) with a compare of the two value block arguments.
+    const int v_acc = r.params[0], v_x = r.params[2];
+    bool has_select = false;
+    int dir = 0;  // +1 argmax, -1 argmin
+    for (const Op& b : r.ops) {
+      if (b.kind == OpKind::kSelect) has_select = true;
+      if (b.kind == OpKind::kCompare && b.operands.size() == 2) {
+        const bool vv = (b.operands[0] == v_acc && b.operands[1] == v_x) ||
+                        (b.operands[0] == v_x && b.operands[1] == v_acc);
+        if (vv && (b.cmp_dir == CmpDir::kGT || b.cmp_dir == CmpDir::kGE)) dir = dir ? dir : 1;
+        if (vv && (b.cmp_dir == CmpDir::kLT || b.cmp_dir == CmpDir::kLE)) dir = dir ? dir : -1;
+      }
+    }
+    const DType vt = prog.type(op.results[0]).dtype;
+    const DType it = prog.type(op.results[1]).dtype;
+    PJRTX_CHECK(has_select && dir != 0 && dtype_is_float(vt) &&
+                    (it == DType::kS32 || it == DType::kS64 || it == DType::kU32),
+                Code::kUnimplemented,
+                "two-result reduce is supported only as argmax/argmin over float values with "
+                "s32/s64/u32 indices");
+    return dir > 0 ? ReducerKind::kArgMax : ReducerKind::kArgMin;
+  }
+  PJRTX_CHECK(n == 1, Code::kUnimplemented, "reduce with more than two results is not supported");
+  // Single-result: body must be one binary op of the two block args.
+  int kind_op = -1;
+  for (size_t i = 0; i < r.ops.size(); ++i) {
+    if (r.ops[i].kind != OpKind::kReturn) {
+      PJRTX_CHECK(kind_op < 0, Code::kUnimplemented, "reduce region with more than one op is not supported");
+      kind_op = static_cast<int>(i);
+    }
+  }
+  PJRTX_CHECK(kind_op >= 0, Code::kUnimplemented, "empty reduce region");
+  const Op& b = r.ops[kind_op];
+  const DType t = prog.type(op.results[0]).dtype;
+  switch (b.kind) {
+    case OpKind::kAdd: return t == DType::kPred ? ReducerKind::kOr : ReducerKind::kSum;
+    case OpKind::kMultiply: return t == DType::kPred ? ReducerKind::kAnd : ReducerKind::kProd;
+    case OpKind::kMaximum: return ReducerKind::kMax;
+    case OpKind::kMinimum: return ReducerKind::kMin;
+    case OpKind::kAnd: return ReducerKind::kAnd;
+    case OpKind::kOr: return ReducerKind::kOr;
+    default:
+      fail(Code::kUnimplemented, std::string("unsupported reduce region op ") + op_kind_name(b.kind));
+  }
+}
+
+namespace {
+
+bool is_splat_constant(const Program& prog, const Op& op) {
+  return op.kind == OpKind::kConstant && (op.splat || prog.type(op.results[0]).elements() == 1);
+}
+
+bool is_library(OpKind k) {
+  return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
+         k == OpKind::kDynamicSlice || k == OpKind::kDynamicUpdateSlice ||
+         k == OpKind::kConcatenate || k == OpKind::kPad;
+}
+
+LibKind lib_kind_of(OpKind k) {
+  switch (k) {
+    case OpKind::kDotGeneral: return LibKind::kDot;
+    case OpKind::kGather: return LibKind::kGather;
+    case OpKind::kScatter: return LibKind::kScatter;
+    case OpKind::kDynamicSlice: return LibKind::kDynamicSlice;
+    case OpKind::kDynamicUpdateSlice: return LibKind::kDynamicUpdateSlice;
+    case OpKind::kConcatenate: return LibKind::kConcatenate;
+    case OpKind::kPad: return LibKind::kPad;
+    default: return LibKind::kCopy;
+  }
+}
+
+class Planner {
+ public:
+  Planner(const Program& prog, const PlanOptions& opts) : prog_(prog), opts_(opts) {}
+  Plan run();
+
+ private:
+  const Program& prog_;
+  const PlanOptions& opts_;
+  Plan plan_;
+  std::map<int, int>& producer_ = plan_.producer;
+  std::map<int, std::vector<int>> users_;  // value -> ops using it
+  std::set<int> outputs_;
+  std::set<int>& mat_ = plan_.materialized;
+
+  bool fusible_op(const Op& op) const {
+    return op_is_elementwise(op.kind) || op_is_view(op.kind) || is_splat_constant(prog_, op);
+  }
+  void decide_materialization();
+  // Collects the fused ops reachable backward from `roots` without crossing
+  // materialized values. Fills ops (sorted) and inputs.
+  void closure(const std::vector<int>& roots, std::vector<int>* ops, std::vector<int>* inputs) const;
+  void build_steps(std::vector<Step>* steps);
+  void merge_siblings(std::vector<Step>* steps);
+  void merge_epilogues(std::vector<Step>* steps);
+  void schedule(std::vector<Step>* steps);
+  void liveness();
+  void shape_reduce(Step* s);
+  void shape_loop(Step* s);
+};
+
+void Planner::decide_materialization() {
+  for (int p : prog_.params) mat_.insert(p);
+  for (int r : prog_.results) outputs_.insert(r);
+  for (size_t i = 0; i < prog_.ops.size(); ++i) {
+    const Op& op = prog_.ops[i];
+    for (int v : op.results) producer_[v] = static_cast<int>(i);
+    for (int v : op.operands) users_[v].push_back(static_cast<int>(i));
+  }
+  std::map<int, int> cost;  // inlined op count of a non-materialized value
+  for (size_t i = 0; i < prog_.ops.size(); ++i) {
+    const Op& op = prog_.ops[i];
+    if (op.kind == OpKind::kReturn) {
+      for (int v : op.operands) mat_.insert(v);
+      continue;
+    }
+    if (op.kind == OpKind::kConstant) {
+      if (!is_splat_constant(prog_, op)) {
+        mat_.insert(op.results[0]);
+        plan_.constants.push_back(op.results[0]);
+      }
+      cost[op.results[0]] = 0;
+      continue;
+    }
+    if (op.kind == OpKind::kReduce) {
+      const size_t n = op.results.size();
+      for (size_t k = 0; k < n; ++k) {
+        // Init values are scalars: literals when splat constants, else read.
+        int init = op.operands[n + k];
+        auto pi = producer_.find(init);
+        const bool lit = pi != producer_.end() && is_splat_constant(prog_, prog_.ops[pi->second]);
+        if (!lit) mat_.insert(init);
+      }
+      for (int v : op.results) mat_.insert(v);
+      continue;
+    }
+    if (is_library(op.kind)) {
+      for (int v : op.operands) mat_.insert(v);
+      for (int v : op.results) mat_.insert(v);
+      continue;
+    }
+    PJRTX_CHECK(fusible_op(op), Code::kUnimplemented,
+                std::string("op not supported by the HIP backend: ") + op.name);
+    // Elementwise / view op.
+    int c = op_is_view(op.kind) ? 0 : 1;
+    for (int v : op.operands) {
+      if (!mat_.count(v)) c += cost[v];
+    }
+    if (op.kind == OpKind::kBroadcastInDim && !op.operands.empty()) {
+      const int u = op.operands[0];
+      const bool expands = prog_.type(op.results[0]).elements() > prog_.type(u).elements();
+      if (expands && !mat_.count(u) && cost[u] > 8 && prog_.type(u).elements() > 1) {
+        // Avoid recomputing an expensive value once per broadcast element.
+        mat_.insert(u);
+        c -= cost[u];
+      }
+    }
+    cost[op.results[0]] = c;
+  }
+  // Multi-use values whose recompute would be expensive are materialized.
+  for (size_t i = 0; i < prog_.ops.size(); ++i) {
+    const Op& op = prog_.ops[i];
+    if (!fusible_op(op) || op.results.empty()) continue;
+    const int v = op.results[0];
+    if (mat_.count(v) || is_splat_constant(prog_, op)) continue;
+    const size_t nusers = users_[v].size();
+    if (nusers > 1 && cost[v] > opts_.recompute_limit) mat_.insert(v);
+  }
+}
+
+void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops,
+                      std::vector<int>* inputs) const {
+  std::set<int> seen_ops, seen_inputs;
+  std::function<void(int, bool)> visit = [&](int v, bool is_root) {
+    if (!is_root && mat_.count(v)) {
+      if (seen_inputs.insert(v).second) inputs->push_back(v);
+      return;
+    }
+    auto pi = producer_.find(v);
+    if (pi == producer_.end()) {  // parameter
+      if (seen_inputs.insert(v).second) inputs->push_back(v);
+      return;
+    }
+    const int oi = pi->second;
+    if (!seen_ops.insert(oi).second) return;
+    const Op& op = prog_.ops[oi];
+    for (int u : op.operands) visit(u, false);
+  };
+  for (int r : roots) visit(r, true);
+  ops->assign(seen_ops.begin(), seen_ops.end());  // std::set is sorted: program order
+}
+
+void Planner::build_steps(std::vector<Step>* steps) {
+  for (size_t i = 0; i < prog_.ops.size(); ++i) {
+    const Op& op = prog_.ops[i];
+    if (op.kind == OpKind::kReturn || op.kind == OpKind::kConstant && !is_splat_constant(prog_, op)) continue;
+    if (op.kind == OpKind::kReduce) {
+      Step s;
+      s.kind = StepKind::kReduce;
+      ReduceSpec rs;
+      rs.op_index = static_cast<int>(i);
+      rs.kind = classify_reducer(prog_, op);
+      const size_t n = op.results.size();
+      rs.inputs.assign(op.operands.begin(), op.operands.begin() + n);
+      rs.inits.assign(op.operands.begin() + n, op.operands.end());
+      rs.results = op.results;
+      s.reduces.push_back(rs);
+      s.reduce_operand_shape = prog_.type(rs.inputs[0]).dims;
+      s.reduce_dims = op.dims;
+      std::sort(s.reduce_dims.begin(), s.reduce_dims.end());
+      std::vector<int> roots = rs.inputs;
+      std::vector<int> init_inputs;
+      for (int v : rs.inits) roots.push_back(v);
+      closure(roots, &s.ops, &s.inputs);
+      s.outputs = op.results;
+      steps->push_back(std::move(s));
+      continue;
+    }
+    if (is_library(op.kind)) {
+      Step s;
+      s.kind = StepKind::kLibrary;
+      s.lib = lib_kind_of(op.kind);
+      s.lib_op = static_cast<int>(i);
+      s.inputs = op.operands;
+      s.outputs = op.results;
+      steps->push_back(std::move(s));
+      continue;
+    }
+    // Fusible op: a loop step only if its result is materialized.
+    if (op.results.empty() || !mat_.count(op.results[0])) continue;
+    const int v = op.results[0];
+    Step s;
+    if (op.kind == OpKind::kReshape && mat_.count(op.operands[0])) {
+      s.kind = StepKind::kAlias;
+      s.inputs = op.operands;
+      s.outputs = {v};
+      s.lib_op = static_cast<int>(i);
+      steps->push_back(std::move(s));
+      continue;
+    }
+    s.kind = StepKind::kLoop;
+    closure({v}, &s.ops, &s.inputs);
+    s.outputs = {v};
+    s.loop_shape = prog_.type(v).dims;
+    steps->push_back(std::move(s));
+  }
+}
+
+// Producers of each materialized value, for dependency tests.
+static std::map<int, int> value_to_step(const std::vector<Step>& steps) {
+  std::map<int, int> m;
+  for (size_t i = 0; i < steps.size(); ++i)
+    for (int v : steps[i].outputs) m[v] = static_cast<int>(i);
+  return m;
+}
+
+static bool depends_on(const std::vector<Step>& steps, const std::map<int, int>& v2s, int from, int target) {
+  // true if step `from` (transitively) reads an output of step `target`.
+  std::vector<int> stack = {from};
+  std::set<int> seen;
+  while (!stack.empty()) {
+    int s = stack.back();
+    stack.pop_back();
+    if (!seen.insert(s).second) continue;
+    for (int v : steps[s].inputs) {
+      auto it = v2s.find(v);
+      if (it == v2s.end()) continue;
+      if (it->second == target) return true;
+      stack.push_back(it->second);
+    }
+  }
+  return false;
+}
+
+void Planner::merge_siblings(std::vector<Step>* steps) {
+  bool changed = true;
+  while (changed) {
+    changed = false;
+    auto v2s = value_to_step(*steps);
+    for (size_t a = 0; a < steps->size() && !changed; ++a) {
+      Step& A = (*steps)[a];
+      if (A.kind != StepKind::kReduce) continue;
+      for (size_t b = a + 1; b < steps->size() && !changed; ++b) {
+        Step& B = (*steps)[b];
+        if (B.kind != StepKind::kReduce) continue;
+        if (A.reduce_operand_shape != B.reduce_operand_shape || A.reduce_dims != B.reduce_dims) continue;
+        if (depends_on(*steps, v2s, static_cast<int>(a), static_cast<int>(b)) ||
+            depends_on(*steps, v2s, static_cast<int>(b), static_cast<int>(a)))
+          continue;
+        // Merge B into A.
+        for (auto& r : B.reduces) A.reduces.push_back(r);
+        std::set<int> ops(A.ops.begin(), A.ops.end());
+        ops.insert(B.ops.begin(), B.ops.end());
+        A.ops.assign(ops.begin(), ops.end());
+        for (int v : B.inputs)
+          if (std::find(A.inputs.begin(), A.inputs.end(), v) == A.inputs.end()) A.inputs.push_back(v);
+        for (int v : B.outputs) A.outputs.push_back(v);
+        steps->erase(steps->begin() + b);
+        changed = true;
+      }
+    }
+  }
+}
+
+void Planner::merge_epilogues(std::vector<Step>* steps) {
+  bool changed = true;
+  while (changed) {
+    changed = false;
+    auto v2s = value_to_step(*steps);
+    for (size_t g = 0; g < steps->size() && !changed; ++g) {
+      Step& G = (*steps)[g];
+      if (G.kind != StepKind::kLoop || G.outputs.size() != 1) continue;
+      // Which reduce step feeds G?
+      int rs = -1;
+      bool ok = true;
+      for (int v : G.inputs) {
+        auto it = v2s.find(v);
+        const bool scalar = prog_.type(v).elements() == 1;
+        if (it != v2s.end() && (*steps)[it->second].kind == StepKind::kReduce) {
+          if (rs >= 0 && rs != it->second) ok = false;
+          rs = it->second;
+        } else if (!scalar) {
+          ok = false;
+        }
+      }
+      if (!ok || rs < 0) continue;
+      Step& R = (*steps)[rs];
+      Dims out_dims;
+      for (size_t d = 0; d < R.reduce_operand_shape.size(); ++d)
+        if (!std::binary_search(R.reduce_dims.begin(), R.reduce_dims.end(), static_cast<int64_t>(d)))
+          out_dims.push_back(R.reduce_operand_shape[d]);
+      if (G.loop_shape != out_dims) continue;
+      // Every access to an R output must be at the output index: no view op
+      // may sit between an R output and G's root, except over literals.
+      bool identity_only = true;
+      for (int oi : G.ops) {
+        const Op& op = prog_.ops[oi];
+        if (!op_is_view(op.kind) || op.kind == OpKind::kIota) continue;
+        for (int u : op.operands) {
+          auto pi = producer_.find(u);
+          const bool literal = pi != producer_.end() && is_splat_constant(prog_, prog_.ops[pi->second]);
+          if (!literal) identity_only = false;
+        }
+      }
+      if (!identity_only) continue;
+      // Merge G into R as epilogue.
+      std::set<int> eops(R.epilogue_ops.begin(), R.epilogue_ops.end());
+      eops.insert(G.ops.begin(), G.ops.end());
+      R.epilogue_ops.assign(eops.begin(), eops.end());
+      for (int v : G.inputs) {
+        if (v2s.count(v) && v2s[v] == rs) continue;
+        if (std::find(R.inputs.begin(), R.inputs.end(), v) == R.inputs.end()) R.inputs.push_back(v);
+      }
+      R.outputs.push_back(G.outputs[0]);
+      steps->erase(steps->begin() + g);
+      changed = true;
+    }
+  }
+  // Raw reduce results that only feed epilogues no longer need a buffer.
+  std::map<int, int> readers;
+  for (const Step& s : *steps)
+    for (int v : s.inputs) readers[v]++;
+  for (Step& s : *steps) {
+    if (s.kind != StepKind::kReduce || s.epilogue_ops.empty()) continue;
+    std::vector<int> keep;
+    for (int v : s.outputs) {
+      const bool raw = std::any_of(s.reduces.begin(), s.reduces.end(), [&](const ReduceSpec& r) {
+        return std::find(r.results.begin(), r.results.end(), v) != r.results.end();
+      });
+      if (raw && !outputs_.count(v) && readers[v] == 0) {
+        mat_.erase(v);
+        continue;
+      }
+      keep.push_back(v);
+    }
+    s.outputs = keep;
+  }
+}
+
+void Planner::schedule(std::vector<Step>* steps) {
+  auto v2s = value_to_step(*steps);
+  const size_t n = steps->size();
+  std::vector<std::set<int>> deps(n);
+  std::vector<std::vector<int>> rdeps(n);
+  for (size_t i = 0; i < n; ++i) {
+    for (int v : (*steps)[i].inputs) {
+      auto it = v2s.find(v);
+      if (it != v2s.end() && it->second != static_cast<int>(i) && deps[i].insert(it->second).second)
+        rdeps[it->second].push_back(static_cast<int>(i));
+    }
+  }
+  std::priority_queue<int, std::vector<int>, std::greater<int>> ready;
+  std::vector<size_t> indeg(n);
+  for (size_t i = 0; i < n; ++i) {
+    indeg[i] = deps[i].size();
+    if (!indeg[i]) ready.push(static_cast<int>(i));
+  }
+  std::vector<Step> out;
+  while (!ready.empty()) {
+    int i = ready.top();
+    ready.pop();
+    out.push_back(std::move((*steps)[i]));
+    for (int j : rdeps[i])
+      if (--indeg[j] == 0) ready.push(j);
+  }
+  PJRTX_CHECK(out.size() == n, Code::kInternal, "fusion planner produced a cyclic schedule");
+  *steps = std::move(out);
+}
+
+void Planner::liveness() {
+  std::set<int> persistent(prog_.params.begin(), prog_.params.end());
+  for (int c : plan_.constants) persistent.insert(c);
+  std::map<int, int> last_use;
+  for (size_t i = 0; i < plan_.steps.size(); ++i)
+    for (int v : plan_.steps[i].inputs) last_use[v] = static_cast<int>(i);
+  for (auto& [v, i] : last_use) {
+    if (persistent.count(v) || outputs_.count(v)) continue;
+    plan_.steps[i].release_after.push_back(v);
+  }
+}
+
+void Planner::shape_loop(Step* s) {
+  const int64_t n = num_elements(s->loop_shape);
+  // 16-byte accesses for the narrowest element touched at the root index.
+  size_t min_size = dtype_size(prog_.type(s->outputs[0]).dtype);
+  for (int v : s->inputs)
+    if (prog_.type(v).elements() == n) min_size = std::min(min_size, dtype_size(prog_.type(v).dtype));
+  int vec = static_cast<int>(16 / std::max<size_t>(min_size, 1));
+  vec = std::max(1, std::min(vec, 8));
+  s->vec = vec;
+  const int64_t per_block = 256 * vec;
+  s->grid = static_cast<uint32_t>(std::max<int64_t>(1, (n + per_block - 1) / per_block));
+  s->block = 256;
+}
+
+void Planner::shape_reduce(Step* s) {
+  const Dims& shape = s->reduce_operand_shape;
+  const int rank = static_cast<int>(shape.size());
+  const int nred = static_cast<int>(s->reduce_dims.size());
+  bool trailing = true;
+  for (int k = 0; k < nred; ++k)
+    if (s->reduce_dims[k] != rank - nred + k) trailing = false;
+  int64_t rows = 1, row_len = 1;
+  for (int d = 0; d < rank; ++d) {
+    if (std::binary_search(s->reduce_dims.begin(), s->reduce_dims.end(), static_cast<int64_t>(d))) row_len *= shape[d];
+    else rows *= shape[d];
+  }
+  s->rows = rows;
+  s->row_len = row_len;
+  // Row schedule needs enough work per row to fill a workgroup; otherwise a
+  // thread per output walks its reduced elements serially.
+  s->row_schedule = trailing && row_len >= 64;
+  if (!s->row_schedule) {
+    s->vec = 1;
+    s->splits = 1;
+    s->grid = static_cast<uint32_t>(std::max<int64_t>(1, (rows + 255) / 256));
+    s->block = 256;
+    return;
+  }
+  size_t min_size = 8;
+  for (const ReduceSpec& r : s->reduces)
+    for (int v : r.inputs) (void)v;
+  for (int v : s->inputs)
+    if (prog_.type(v).elements() == num_elements(shape)) min_size = std::min(min_size, dtype_size(prog_.type(v).dtype));
+  int vec = static_cast<int>(16 / std::max<size_t>(min_size, 1));
+  vec = std::max(1, std::min(vec, 8));
+  while (vec > 1 && row_len % vec != 0) vec /= 2;
+  s->vec = vec;
+  const int64_t per_iter = 256 * vec;
+  int64_t splits = (opts_.reduce_target_blocks + rows - 1) / rows;
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, row_len / (2 * per_iter)));
+  splits = std::max<int64_t>(1, std::min<int64_t>(splits, 64));
+  int64_t chunk = (row_len + splits - 1) / splits;
+  chunk = (chunk + vec - 1) / vec * vec;
+  splits = (row_len + chunk - 1) / chunk;
+  s->splits = splits;
+  s->chunk = chunk;
+  s->grid = static_cast<uint32_t>(rows * splits);
+  s->block = 256;
+  if (splits > 1) {
+    size_t per_slot = 0;
+    for (const ReduceSpec& r : s->reduces) per_slot += (r.kind == ReducerKind::kArgMax || r.kind == ReducerKind::kArgMin) ? 16 : 8;
+    s->scratch_bytes = static_cast<size_t>(rows * splits) * per_slot;
+    s->counter_bytes = static_cast<size_t>(rows) * 4;
+  }
+}
+
+Plan Planner::run() {
+  decide_materialization();
+  std::vector<Step> steps;
+  build_steps(&steps);
+  if (opts_.fuse_siblings) merge_siblings(&steps);
+  if (opts_.fuse_epilogues) merge_epilogues(&steps);
+  schedule(&steps);
+  int kernel_id = 0;
+  for (Step& s : steps) {
+    if (s.kind == StepKind::kLoop) {
+      shape_loop(&s);
+      s.name = strformat("pjrtx_fusion_loop_%d", kernel_id++);
+    } else if (s.kind == StepKind::kReduce) {
+      shape_reduce(&s);
+      s.name = strformat("pjrtx_fusion_reduce_%d", kernel_id++);
+    }
+  }
+  plan_.steps = std::move(steps);
+  plan_.num_fusion_kernels = kernel_id;
+  liveness();
+  return std::move(plan_);
+}
+
+}  // namespace
+
+std::string Plan::describe(const Program& prog) const {
+  std::ostringstream o;
+  auto list = [&](const std::vector<int>& v) {
+    std::string s = "[";
+    for (size_t i = 0; i < v.size(); ++i) s += (i ? "," : "") + std::to_string(v[i]);
+    return s + "]";
+  };
+  o << "{\"steps\":[";
+  for (size_t i = 0; i < steps.size(); ++i) {
+    const Step& s = steps[i];
+    if (i) o << ",";
+    const char* kind = s.kind == StepKind::kLoop ? "loop" : s.kind == StepKind::kReduce ? "reduce"
+                     : s.kind == StepKind::kAlias ? "alias" : "library";
+    o << "{\"kind\":\"" << kind << "\",\"name\":\"" << s.name << "\"";
+    o << ",\"inputs\":" << list(s.inputs) << ",\"outputs\":" << list(s.outputs);
+    std::vector<std::string> names;
+    o << ",\"ops\":[";
+    for (size_t k = 0; k < s.ops.size(); ++k) o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.ops[k]].kind) << "\"";
+    o << "],\"epilogue\":[";
+    for (size_t k = 0; k < s.epilogue_ops.size(); ++k) o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.epilogue_ops[k]].kind) << "\"";
+    o << "]";
+    if (s.kind == StepKind::kReduce) {
+      o << ",\"reducers\":[";
+      for (size_t k = 0; k < s.reduces.size(); ++k) o << (k ? "," : "") << "\"" << reducer_name(s.reduces[k].kind) << "\"";
+      o << "],\"row_schedule\":" << (s.row_schedule ? "true" : "false") << ",\"rows\":" << s.rows
+        << ",\"row_len\":" << s.row_len << ",\"splits\":" << s.splits << ",\"chunk\":" << s.chunk;
+    }
+    if (s.kind == StepKind::kLibrary) o << ",\"library\":\"" << lib_kind_name(s.lib) << "\"";
+    o << ",\"vec\":" << s.vec << ",\"grid\":" << s.grid << ",\"block\":" << s.block;
+    o << ",\"release_after\":" << list(s.release_after) << "}";
+  }
+  o << "],\"constants\":" << list(constants) << ",\"fusion_kernels\":" << num_fusion_kernels << "}";
+  return o.str();
+}
+
+Plan make_plan(const Program& prog, const PlanOptions& opts) {
+  Planner p(prog, opts);
+  Plan plan = p.run();
+  plan.kernel_source = generate_kernels(prog, plan);
+  return plan;
+}
+
+}  // namespace pjrtx

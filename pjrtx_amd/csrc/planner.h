@@ -1,0 +1,110 @@
+// Fusion planner: Program -> Plan (an ordered list of steps, one GPU kernel
+// launch or library call per step, with liveness releases).
+//
+// Replaces the reference's backend program model and fusion planner
+// (reference: src/backend/mlx_metal/program.zig:21-286 Program/Node/
+// FusionGroup/ScheduleItem, program_build.zig:10-207,224-263,
+// program_fusion.zig:8-70, program_schedule_build.zig:6-51,
+// program_liveness.zig:10, program_validation.zig:11) and its per-group
+// lowering (executable_metal_graph_lowering.zig:177-424). Where the reference
+// only groups contiguous view/elementwise runs and materializes every
+// reduction input, this planner also fuses:
+//   * the elementwise/view prologue of a reduction into the reduction kernel,
+//   * sibling reductions over the same operand shape (multi-output),
+//   * elementwise epilogues on a reduction's output (e.g. f32->f16 convert),
+//   * the iota index operand of a two-output argmax (synthesized, not read),
+//   * splat constants as literals (never materialized).
+#pragma once
+
+#include <map>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "ir.h"
+
+namespace pjrtx {
+
+enum class ReducerKind { kSum, kProd, kMax, kMin, kAnd, kOr, kArgMax, kArgMin };
+const char* reducer_name(ReducerKind k);
+
+// Classifies a reduce region (reference: stablehlo_operation_attrs.zig:222-245
+// reduceKindFromRegion). Two-result regions with compare+select become
+// argmax/argmin with JAX's comparator semantics; unknown regions fail closed.
+ReducerKind classify_reducer(const Program& prog, const Op& reduce_op);
+
+struct ReduceSpec {
+  int op_index = -1;
+  ReducerKind kind = ReducerKind::kSum;
+  std::vector<int> inputs;   // reduced operands (argmax: values, indices)
+  std::vector<int> inits;    // init values
+  std::vector<int> results;  // result values
+};
+
+enum class StepKind { kLoop, kReduce, kAlias, kLibrary };
+
+enum class LibKind { kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad };
+const char* lib_kind_name(LibKind k);
+
+struct Step {
+  StepKind kind = StepKind::kLoop;
+  std::string name;          // generated kernel symbol
+  std::vector<int> ops;      // fused program ops (prologue/body), topological
+  std::vector<int> inputs;   // materialized values read
+  std::vector<int> outputs;  // materialized values written
+
+  // kLoop
+  Dims loop_shape;
+  int vec = 1;
+
+  // kReduce
+  std::vector<ReduceSpec> reduces;
+  std::vector<int> epilogue_ops;
+  Dims reduce_operand_shape;
+  Dims reduce_dims;          // sorted
+  bool row_schedule = true;  // reduced dims are the trailing dims
+  int64_t rows = 1;          // row schedule: product of kept dims
+  int64_t row_len = 1;       // row schedule: product of reduced dims
+  int64_t splits = 1;        // workgroups per row
+  int64_t chunk = 0;         // elements per split
+  size_t scratch_bytes = 0;  // partial accumulators (splits > 1)
+  size_t counter_bytes = 0;  // per-row arrival counters (splits > 1)
+
+  // kLibrary / kAlias
+  LibKind lib = LibKind::kCopy;
+  int lib_op = -1;
+
+  // launch geometry of generated kernels
+  uint32_t grid = 1;
+  uint32_t block = 256;
+
+  std::vector<int> release_after;  // intermediate values dead after this step
+};
+
+struct Plan {
+  std::vector<Step> steps;
+  std::set<int> materialized;
+  std::vector<int> constants;        // materialized non-splat constant values
+  std::map<int, int> producer;       // value -> op index
+  std::string kernel_source;         // hiprtc source for all generated steps
+  int num_fusion_kernels = 0;
+  std::string describe(const Program& prog) const;  // JSON summary
+};
+
+struct PlanOptions {
+  // Multi-use elementwise values are recomputed in each consumer while their
+  // inlined cost stays at or below this many ops.
+  int recompute_limit = 24;
+  // Target number of workgroups a reduction launch should reach.
+  // (environment: PJRTX_REDUCE_TARGET_BLOCKS)
+  int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 2048);
+  bool fuse_siblings = true;
+  bool fuse_epilogues = true;
+};
+
+Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
+
+// Emits the HIP source of every generated step (codegen.cc).
+std::string generate_kernels(const Program& prog, Plan& plan);
+
+}  // namespace pjrtx

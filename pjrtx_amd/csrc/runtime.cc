@@ -1,0 +1,526 @@
+// Device runtime implementation. See runtime.h.
+#include "runtime.h"
+
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <set>
+#include <sstream>
+
+#include "fusion_device_inc.h"  // kFusionDeviceHeader (generated at build)
+
+namespace pjrtx {
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    fail(e == hipErrorOutOfMemory ? Code::kResourceExhausted : Code::kInternal,
+         strformat("%s failed: %s", what, hipGetErrorString(e)));
+  }
+}
+
+// ----------------------------------------------------------------- allocator
+
+DeviceMemory::~DeviceMemory() {
+  if (dev && ptr) dev->allocator().release(ptr, capacity);
+}
+
+Allocator::~Allocator() = default;
+
+static size_t round_capacity(size_t bytes) {
+  if (bytes <= 4096) return 4096;
+  if (bytes <= (size_t(1) << 20)) return (bytes + 4095) & ~size_t(4095);
+  return (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+}
+
+void* Allocator::alloc(size_t bytes, size_t* capacity) {
+  const size_t cap = round_capacity(bytes);
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = free_.lower_bound(cap);
+    if (it != free_.end() && it->first <= cap + cap / 4) {
+      void* p = it->second;
+      *capacity = it->first;
+      free_.erase(it);
+      in_use_ += static_cast<int64_t>(*capacity);
+      if (in_use_ > peak_) peak_ = in_use_.load();
+      num_allocs_++;
+      if (static_cast<int64_t>(bytes) > largest_) largest_ = static_cast<int64_t>(bytes);
+      return p;
+    }
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, cap);
+  if (e == hipErrorOutOfMemory) {
+    (void)hipGetLastError();
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    trim();
+    e = hipMalloc(&p, cap);
+  }
+  hip_check(e, "hipMalloc");
+  *capacity = cap;
+  reserved_ += static_cast<int64_t>(cap);
+  in_use_ += static_cast<int64_t>(cap);
+  if (in_use_ > peak_) peak_ = in_use_.load();
+  num_allocs_++;
+  if (static_cast<int64_t>(bytes) > largest_) largest_ = static_cast<int64_t>(bytes);
+  return p;
+}
+
+void Allocator::release(void* p, size_t capacity) {
+  std::lock_guard<std::mutex> lk(mu_);
+  free_.emplace(capacity, p);
+  in_use_ -= static_cast<int64_t>(capacity);
+}
+
+void Allocator::trim() {
+  std::lock_guard<std::mutex> lk(mu_);
+  for (auto& [cap, p] : free_) {
+    (void)hipFree(p);
+    reserved_ -= static_cast<int64_t>(cap);
+  }
+  free_.clear();
+}
+
+// -------------------------------------------------------------------- device
+
+Device::Device(int ordinal) : ordinal_(ordinal), alloc_(ordinal) {
+  hip_check(hipSetDevice(ordinal), "hipSetDevice");
+  hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  hipDeviceProp_t prop;
+  hip_check(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
+  arch_ = prop.gcnArchName;
+  size_t colon = arch_.find(':');
+  if (colon != std::string::npos) arch_ = arch_.substr(0, colon);
+  name_ = prop.name;
+  total_mem_ = static_cast<int64_t>(prop.totalGlobalMem);
+  cus_ = prop.multiProcessorCount;
+}
+
+Device::~Device() {
+  // Process-lifetime object; the stream is released with the process.
+}
+
+void Device::make_current() const { hip_check(hipSetDevice(ordinal_), "hipSetDevice"); }
+
+MemRef Device::allocate(size_t bytes) {
+  auto m = std::make_shared<DeviceMemory>();
+  m->dev = this;
+  m->bytes = bytes;
+  if (bytes == 0) return m;
+  make_current();
+  m->ptr = alloc_.alloc(bytes, &m->capacity);
+  return m;
+}
+
+// --------------------------------------------------------------------- event
+
+namespace {
+// Runs on_ready callbacks once their events complete. Events on one stream
+// complete in order, so a FIFO worker suffices.
+class EventWorker {
+ public:
+  static EventWorker& get() {
+    static EventWorker* w = new EventWorker();
+    return *w;
+  }
+  void push(std::shared_ptr<Event> e, std::function<void()> fn) {
+    std::lock_guard<std::mutex> lk(mu_);
+    q_.emplace_back(std::move(e), std::move(fn));
+    cv_.notify_one();
+  }
+
+ private:
+  EventWorker() { std::thread([this] { loop(); }).detach(); }
+  void loop() {
+    while (true) {
+      std::pair<std::shared_ptr<Event>, std::function<void()>> item;
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return !q_.empty(); });
+        item = std::move(q_.front());
+        q_.pop_front();
+      }
+      item.first->await();
+      item.second();
+    }
+  }
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::deque<std::pair<std::shared_ptr<Event>, std::function<void()>>> q_;
+};
+}  // namespace
+
+std::shared_ptr<Event> Event::ready() {
+  auto e = std::shared_ptr<Event>(new Event());
+  e->done_ = true;
+  return e;
+}
+
+std::shared_ptr<Event> Event::failed(Code code, const std::string& msg) {
+  auto e = std::shared_ptr<Event>(new Event());
+  e->done_ = true;
+  e->code_ = code;
+  e->msg_ = msg;
+  return e;
+}
+
+std::shared_ptr<Event> Event::record(Device* dev) {
+  auto e = std::shared_ptr<Event>(new Event());
+  dev->make_current();
+  hip_check(hipEventCreateWithFlags(&e->ev_, hipEventDisableTiming), "hipEventCreate");
+  hip_check(hipEventRecord(e->ev_, dev->stream()), "hipEventRecord");
+  e->dev_ = dev;
+  return e;
+}
+
+Event::~Event() {
+  if (ev_) (void)hipEventDestroy(ev_);
+}
+
+bool Event::is_ready() {
+  std::lock_guard<std::mutex> lk(mu_);
+  if (done_) return true;
+  hipError_t q = hipEventQuery(ev_);
+  if (q == hipSuccess) {
+    done_ = true;
+  } else if (q != hipErrorNotReady) {
+    done_ = true;
+    code_ = Code::kInternal;
+    msg_ = std::string("device work failed: ") + hipGetErrorString(q);
+  }
+  return done_;
+}
+
+void Event::await() {
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (done_) return;
+  }
+  hipError_t e = hipEventSynchronize(ev_);
+  std::lock_guard<std::mutex> lk(mu_);
+  done_ = true;
+  if (e != hipSuccess) {
+    code_ = Code::kInternal;
+    msg_ = std::string("device work failed: ") + hipGetErrorString(e);
+  }
+}
+
+void Event::on_ready(std::function<void()> fn) {
+  if (is_ready()) {
+    fn();
+    return;
+  }
+  // The worker holds a reference until it has run the callback.
+  EventWorker::get().push(shared_from_this(), std::move(fn));
+}
+
+// ------------------------------------------------------------------- buffers
+
+BufferRef buffer_from_host(Device* dev, const TensorType& t, const void* data, const int64_t* byte_strides) {
+  auto b = std::make_shared<Buffer>();
+  b->dev = dev;
+  b->type = t;
+  const size_t bytes = t.bytes();
+  b->mem = dev->allocate(bytes);
+  if (bytes) {
+    if (byte_strides) {
+      // Dense row-major is required; reject other layouts explicitly.
+      int64_t expect = static_cast<int64_t>(dtype_size(t.dtype));
+      for (int d = t.rank() - 1; d >= 0; --d) {
+        if (t.dims[d] != 1 && byte_strides[d] != expect)
+          fail(Code::kUnimplemented, "BufferFromHostBuffer: only dense row-major host layouts are supported");
+        expect *= t.dims[d];
+      }
+    }
+    dev->make_current();
+    hip_check(hipMemcpyAsync(b->mem->ptr, data, bytes, hipMemcpyHostToDevice, dev->stream()), "hipMemcpyAsync(H2D)");
+    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+  }
+  b->ready = Event::ready();
+  return b;
+}
+
+void buffer_to_host(const Buffer& b, void* dst, size_t dst_size) {
+  const size_t bytes = b.type.bytes();
+  PJRTX_CHECK(dst_size >= bytes, Code::kInvalidArgument,
+              strformat("ToHostBuffer: destination holds %zu bytes, buffer needs %zu", dst_size, bytes));
+  if (!bytes) return;
+  b.dev->make_current();
+  hip_check(hipMemcpyAsync(dst, b.mem->ptr, bytes, hipMemcpyDeviceToHost, b.dev->stream()), "hipMemcpyAsync(D2H)");
+  hip_check(hipStreamSynchronize(b.dev->stream()), "hipStreamSynchronize");
+}
+
+// ------------------------------------------------------------ kernel compile
+
+std::string kernel_translation_unit(const std::string& body) {
+  return std::string(kFusionDeviceHeader) + "\n" + body;
+}
+
+namespace {
+uint64_t fnv1a(const std::string& s, uint64_t seed) {
+  uint64_t h = seed;
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+std::string cache_dir() {
+  const char* d = std::getenv("PJRTX_KERNEL_CACHE_DIR");
+  if (d && *d) return d;
+  const char* home = std::getenv("HOME");
+  return std::string(home ? home : "/tmp") + "/.cache/pjrtx_amd";
+}
+
+std::mutex g_compile_mu;
+std::map<std::string, std::vector<char>> g_code_cache;
+}  // namespace
+
+std::vector<char> compile_kernels(const std::string& body, const std::string& arch) {
+  const std::string src = kernel_translation_unit(body);
+  const std::vector<std::string> opts = {
+      "--offload-arch=" + arch, "-O3", "-std=c++17", "-ffp-contract=fast",
+      // Packed f32 math is kept off: hand-written code relies on scalar f32.
+      "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  std::string key_src = src;
+  for (auto& o : opts) key_src += "\n//" + o;
+  const std::string key = strformat("%016llx%016llx", static_cast<unsigned long long>(fnv1a(key_src, 1469598103934665603ull)),
+                                    static_cast<unsigned long long>(fnv1a(key_src, 0x9e3779b97f4a7c15ull)));
+  std::lock_guard<std::mutex> lk(g_compile_mu);
+  auto it = g_code_cache.find(key);
+  if (it != g_code_cache.end()) return it->second;
+  const bool use_disk = !env_flag("PJRTX_NO_KERNEL_DISK_CACHE");
+  const std::string path = cache_dir() + "/" + key + ".co";
+  if (use_disk) {
+    std::ifstream f(path, std::ios::binary);
+    if (f) {
+      std::vector<char> code((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+      if (!code.empty()) {
+        g_code_cache[key] = code;
+        return code;
+      }
+    }
+  }
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "pjrtx_fusion.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    fail(Code::kInternal, "hiprtcCreateProgram failed");
+  std::vector<const char*> copts;
+  for (auto& o : opts) copts.push_back(o.c_str());
+  hiprtcResult r = hiprtcCompileProgram(prog, static_cast<int>(copts.size()), copts.data());
+  size_t log_size = 0;
+  hiprtcGetProgramLogSize(prog, &log_size);
+  std::string log(log_size, '\0');
+  if (log_size) hiprtcGetProgramLog(prog, log.data());
+  if (r != HIPRTC_SUCCESS) {
+    hiprtcDestroyProgram(&prog);
+    if (env_flag("PJRTX_DUMP_KERNELS_ON_ERROR")) std::fprintf(stderr, "%s\n", src.c_str());
+    fail(Code::kInternal, "hiprtc compile of fusion kernels failed:\n" + log.substr(0, 4000));
+  }
+  size_t code_size = 0;
+  hiprtcGetCodeSize(prog, &code_size);
+  std::vector<char> code(code_size);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  if (use_disk) {
+    std::string dir = cache_dir();
+    for (size_t pos = 1; pos != std::string::npos;) {
+      pos = dir.find('/', pos + 1);
+      ::mkdir(dir.substr(0, pos).c_str(), 0755);
+    }
+    const std::string tmp = path + strformat(".tmp%d", static_cast<int>(::getpid()));
+    std::ofstream f(tmp, std::ios::binary);
+    if (f) {
+      f.write(code.data(), static_cast<std::streamsize>(code.size()));
+      f.close();
+      std::rename(tmp.c_str(), path.c_str());
+    }
+  }
+  g_code_cache[key] = code;
+  return code;
+}
+
+// ---------------------------------------------------------------- executable
+
+Executable::Executable(Program prog, Plan plan, std::string fingerprint, std::string name)
+    : prog_(std::move(prog)), plan_(std::move(plan)), fingerprint_(std::move(fingerprint)), name_(std::move(name)) {}
+
+Executable::~Executable() {
+  for (auto& [ord, L] : loaded_) {
+    if (L->module) (void)hipModuleUnload(L->module);
+  }
+}
+
+void Executable::load(Device* dev) { loaded_for(dev); }
+
+Executable::Loaded* Executable::loaded_for(Device* dev) {
+  std::lock_guard<std::mutex> lk(mu_);
+  auto it = loaded_.find(dev->ordinal());
+  if (it != loaded_.end()) return it->second.get();
+  auto L = std::make_unique<Loaded>();
+  L->dev = dev;
+  dev->make_current();
+  if (plan_.num_fusion_kernels > 0) {
+    if (code_.empty()) code_ = compile_kernels(plan_.kernel_source, dev->arch());
+    hip_check(hipModuleLoadData(&L->module, code_.data()), "hipModuleLoadData");
+  }
+  L->funcs.resize(plan_.steps.size(), nullptr);
+  L->scratch.resize(plan_.steps.size());
+  L->counters.resize(plan_.steps.size());
+  for (size_t i = 0; i < plan_.steps.size(); ++i) {
+    const Step& s = plan_.steps[i];
+    if (s.kind == StepKind::kLoop || s.kind == StepKind::kReduce) {
+      hip_check(hipModuleGetFunction(&L->funcs[i], L->module, s.name.c_str()), "hipModuleGetFunction");
+    }
+    if (s.scratch_bytes) L->scratch[i] = dev->allocate(s.scratch_bytes);
+    if (s.counter_bytes) {
+      L->counters[i] = dev->allocate(s.counter_bytes);
+      hip_check(hipMemsetAsync(L->counters[i]->ptr, 0, s.counter_bytes, dev->stream()), "hipMemsetAsync");
+    }
+  }
+  // Resident constants: uploaded once (reference: executable_constants.zig:32-83).
+  for (int v : plan_.constants) {
+    int oi = plan_.producer.at(v);
+    const Op& op = prog_.ops[oi];
+    const TensorType& t = prog_.type(v);
+    std::vector<uint8_t> full;
+    const uint8_t* src = op.literal.data();
+    if (op.splat) {
+      const size_t esz = dtype_size(t.dtype);
+      full.resize(t.bytes());
+      for (int64_t k = 0; k < t.elements(); ++k) std::memcpy(full.data() + k * esz, op.literal.data(), esz);
+      src = full.data();
+    }
+    MemRef m = dev->allocate(t.bytes());
+    if (t.bytes()) hip_check(hipMemcpy(m->ptr, src, t.bytes(), hipMemcpyHostToDevice), "hipMemcpy(constant)");
+    L->constants[v] = m;
+  }
+  hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+  Loaded* raw = L.get();
+  loaded_[dev->ordinal()] = std::move(L);
+  return raw;
+}
+
+void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals) {
+  const Step& s = plan_.steps[si];
+  Device* dev = L->dev;
+  switch (s.kind) {
+    case StepKind::kAlias:
+      vals[s.outputs[0]] = vals[s.inputs[0]];
+      return;
+    case StepKind::kLibrary:
+      for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
+      run_library_step(dev, prog_, s, vals);
+      stats_.library_calls++;
+      return;
+    case StepKind::kLoop:
+    case StepKind::kReduce: {
+      for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
+      if (s.kind == StepKind::kLoop && num_elements(s.loop_shape) == 0) return;
+      if (s.kind == StepKind::kReduce && s.rows == 0) return;
+      std::vector<void*> ptrs;
+      ptrs.reserve(s.inputs.size() + s.outputs.size() + 2);
+      for (int v : s.inputs) ptrs.push_back(vals[v] ? vals[v]->ptr : nullptr);
+      for (int v : s.outputs) ptrs.push_back(vals[v]->ptr);
+      if (s.kind == StepKind::kReduce && s.row_schedule && s.splits > 1) {
+        ptrs.push_back(L->scratch[si]->ptr);
+        ptrs.push_back(L->counters[si]->ptr);
+      }
+      std::vector<void*> args(ptrs.size());
+      for (size_t k = 0; k < ptrs.size(); ++k) args[k] = &ptrs[k];
+      hip_check(hipModuleLaunchKernel(L->funcs[si], s.grid, 1, 1, s.block, 1, 1, 0, dev->stream(), args.data(), nullptr),
+                "hipModuleLaunchKernel");
+      stats_.kernel_launches++;
+      return;
+    }
+  }
+}
+
+std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<BufferRef>& args,
+                                           std::shared_ptr<Event>* done) {
+  PJRTX_CHECK(args.size() == prog_.params.size(), Code::kInvalidArgument,
+              strformat("execute: program takes %zu arguments, got %zu", prog_.params.size(), args.size()));
+  for (size_t i = 0; i < args.size(); ++i) {
+    const TensorType& want = prog_.type(prog_.params[i]);
+    PJRTX_CHECK(args[i] && !args[i]->deleted, Code::kInvalidArgument, strformat("execute: argument %zu is deleted", i));
+    PJRTX_CHECK(args[i]->type == want, Code::kInvalidArgument,
+                strformat("execute: argument %zu has type %s, program expects %s", i, args[i]->type.str().c_str(),
+                          want.str().c_str()));
+    PJRTX_CHECK(args[i]->dev == dev, Code::kInvalidArgument, strformat("execute: argument %zu is on another device", i));
+  }
+  Loaded* L = loaded_for(dev);
+  std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  dev->make_current();
+  std::vector<MemRef> vals(prog_.values.size());
+  for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i]->mem;
+  for (auto& [v, m] : L->constants) vals[v] = m;
+  for (size_t si = 0; si < plan_.steps.size(); ++si) {
+    run_step(L, si, vals);
+    for (int v : plan_.steps[si].release_after) {
+      vals[v].reset();
+      stats_.released_values++;
+    }
+  }
+  // Outputs: a result that is an argument, a constant or repeated gets its
+  // own copy so that every returned buffer owns distinct memory.
+  std::vector<BufferRef> outs;
+  std::set<const DeviceMemory*> seen;
+  std::set<const DeviceMemory*> borrowed;
+  for (size_t i = 0; i < args.size(); ++i) borrowed.insert(args[i]->mem.get());
+  for (auto& [v, m] : L->constants) borrowed.insert(m.get());
+  for (int r : prog_.results) {
+    MemRef m = vals[r];
+    PJRTX_CHECK(m != nullptr, Code::kInternal, "execute: result value was not produced");
+    if (borrowed.count(m.get()) || seen.count(m.get())) {
+      MemRef c = dev->allocate(m->bytes);
+      if (m->bytes)
+        hip_check(hipMemcpyAsync(c->ptr, m->ptr, m->bytes, hipMemcpyDeviceToDevice, dev->stream()), "hipMemcpyAsync(D2D)");
+      m = c;
+    }
+    seen.insert(m.get());
+    auto b = std::make_shared<Buffer>();
+    b->dev = dev;
+    b->type = prog_.type(r);
+    b->mem = m;
+    outs.push_back(b);
+  }
+  std::shared_ptr<Event> ev = Event::record(dev);
+  for (auto& b : outs) b->ready = ev;
+  if (done) *done = ev;
+  stats_.executions++;
+  return outs;
+}
+
+std::vector<double> Executable::time_steps(Device* dev, const std::vector<BufferRef>& args, int iters) {
+  Loaded* L = loaded_for(dev);
+  std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  dev->make_current();
+  std::vector<MemRef> vals(prog_.values.size());
+  for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i]->mem;
+  for (auto& [v, m] : L->constants) vals[v] = m;
+  std::vector<double> ms(plan_.steps.size(), 0.0);
+  hipEvent_t a, b;
+  hip_check(hipEventCreate(&a), "hipEventCreate");
+  hip_check(hipEventCreate(&b), "hipEventCreate");
+  for (size_t si = 0; si < plan_.steps.size(); ++si) {
+    run_step(L, si, vals);  // warm and produce outputs for later steps
+    hip_check(hipEventRecord(a, dev->stream()), "hipEventRecord");
+    for (int k = 0; k < iters; ++k) run_step(L, si, vals);
+    hip_check(hipEventRecord(b, dev->stream()), "hipEventRecord");
+    hip_check(hipEventSynchronize(b), "hipEventSynchronize");
+    float t = 0.f;
+    hip_check(hipEventElapsedTime(&t, a, b), "hipEventElapsedTime");
+    ms[si] = static_cast<double>(t) / iters;
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return ms;
+}
+
+}  // namespace pjrtx

@@ -1,0 +1,185 @@
+// Device runtime of the plugin: one HIP stream per GPU, a caching device
+// allocator, readiness events, device-resident buffers, and the executable
+// that replays a Plan as kernel launches.
+//
+// Replaces the reference's backend execute path
+// (reference: src/backend/mlx_metal/execution_call.zig:66-145,
+// execution_schedule.zig:58-197, execution_liveness.zig:16-52,
+// metalcpp_api.cc:961-1161 value-table executor) and its buffer / event
+// runtime (src/runtime/event.zig:30-95, src/runtime/execution_call.zig:39-102,
+// api.cc:1781-1852 H2D, api.cc:5685-5731 D2H).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <condition_variable>
+#include <deque>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "ir.h"
+#include "planner.h"
+
+namespace pjrtx {
+
+void hip_check(hipError_t e, const char* what);
+
+class Device;
+
+// One block from the caching allocator; returned to the cache when the last
+// reference drops. Reuse is stream-ordered because all work on a device is
+// issued to its single stream.
+struct DeviceMemory {
+  Device* dev = nullptr;
+  void* ptr = nullptr;
+  size_t bytes = 0;     // requested
+  size_t capacity = 0;  // allocated
+  ~DeviceMemory();
+};
+using MemRef = std::shared_ptr<DeviceMemory>;
+
+class Allocator {
+ public:
+  explicit Allocator(int ordinal) : ordinal_(ordinal) {}
+  ~Allocator();
+  void* alloc(size_t bytes, size_t* capacity);
+  void release(void* p, size_t capacity);
+  void trim();  // returns cached blocks to HIP (device must be idle)
+  int64_t bytes_in_use() const { return in_use_; }
+  int64_t peak_bytes_in_use() const { return peak_; }
+  int64_t bytes_reserved() const { return reserved_; }
+  int64_t num_allocs() const { return num_allocs_; }
+  int64_t largest_alloc() const { return largest_; }
+
+ private:
+  int ordinal_;
+  std::mutex mu_;
+  std::multimap<size_t, void*> free_;
+  std::atomic<int64_t> in_use_{0}, peak_{0}, reserved_{0}, num_allocs_{0}, largest_{0};
+};
+
+class Device {
+ public:
+  explicit Device(int ordinal);
+  ~Device();
+  int ordinal() const { return ordinal_; }
+  hipStream_t stream() const { return stream_; }
+  Allocator& allocator() { return alloc_; }
+  MemRef allocate(size_t bytes);
+  void make_current() const;
+  std::mutex& exec_mutex() { return exec_mu_; }
+  const std::string& arch() const { return arch_; }
+  const std::string& name() const { return name_; }
+  int64_t total_memory() const { return total_mem_; }
+  int compute_units() const { return cus_; }
+
+ private:
+  int ordinal_;
+  hipStream_t stream_ = nullptr;
+  Allocator alloc_;
+  std::mutex exec_mu_;
+  std::string arch_, name_;
+  int64_t total_mem_ = 0;
+  int cus_ = 0;
+};
+
+// Readiness of device work: pending until a recorded hipEvent completes.
+class Event : public std::enable_shared_from_this<Event> {
+ public:
+  static std::shared_ptr<Event> ready();
+  static std::shared_ptr<Event> failed(Code code, const std::string& msg);
+  static std::shared_ptr<Event> record(Device* dev);  // marks the stream's current tail
+  ~Event();
+  bool is_ready();
+  void await();  // blocks until done
+  Code error_code() const { return code_; }
+  const std::string& error_message() const { return msg_; }
+  // Calls fn once the event is done (immediately if it already is).
+  void on_ready(std::function<void()> fn);
+
+ private:
+  Event() = default;
+  std::mutex mu_;
+  hipEvent_t ev_ = nullptr;
+  Device* dev_ = nullptr;
+  bool done_ = false;
+  Code code_ = Code::kOk;
+  std::string msg_;
+};
+
+struct Buffer {
+  Device* dev = nullptr;
+  TensorType type;
+  MemRef mem;
+  std::shared_ptr<Event> ready;
+  std::atomic<bool> deleted{false};
+};
+using BufferRef = std::shared_ptr<Buffer>;
+
+BufferRef buffer_from_host(Device* dev, const TensorType& t, const void* data, const int64_t* byte_strides);
+void buffer_to_host(const Buffer& b, void* dst, size_t dst_size);
+
+// hiprtc compile of generated kernel source for the device arch, cached in
+// memory and on disk (PJRTX_KERNEL_CACHE_DIR, default ~/.cache/pjrtx_amd).
+std::vector<char> compile_kernels(const std::string& source, const std::string& arch);
+// The full translation unit hiprtc sees: device helper header + body.
+std::string kernel_translation_unit(const std::string& body);
+
+struct ExecStats {
+  int64_t executions = 0;
+  int64_t kernel_launches = 0;
+  int64_t library_calls = 0;
+  int64_t released_values = 0;
+};
+
+class Executable {
+ public:
+  Executable(Program prog, Plan plan, std::string fingerprint, std::string name);
+  ~Executable();
+  // Loads code and resident constants on `dev` (once).
+  void load(Device* dev);
+  // Runs the plan; inputs must be on `dev`. Returns one buffer per result.
+  std::vector<BufferRef> execute(Device* dev, const std::vector<BufferRef>& args,
+                                 std::shared_ptr<Event>* done);
+  // Times each step by replaying its launch `iters` times between two
+  // hipEvents on the device stream (inputs from `args`). Fills ms per step.
+  std::vector<double> time_steps(Device* dev, const std::vector<BufferRef>& args, int iters);
+
+  const Program& program() const { return prog_; }
+  const Plan& plan() const { return plan_; }
+  const std::string& fingerprint() const { return fingerprint_; }
+  const std::string& name() const { return name_; }
+  size_t code_size() const { return code_.size(); }
+  ExecStats stats() const { return stats_; }
+
+ private:
+  struct Loaded {
+    Device* dev = nullptr;
+    hipModule_t module = nullptr;
+    std::vector<hipFunction_t> funcs;       // per step (null for non-kernel)
+    std::map<int, MemRef> constants;        // value id -> resident buffer
+    std::vector<MemRef> scratch, counters;  // per step
+  };
+  Program prog_;
+  Plan plan_;
+  std::string fingerprint_, name_;
+  std::vector<char> code_;
+  std::mutex mu_;
+  std::map<int, std::unique_ptr<Loaded>> loaded_;
+  ExecStats stats_;
+
+  Loaded* loaded_for(Device* dev);
+  void run_step(Loaded* L, size_t si, std::vector<MemRef>& vals);
+};
+
+// Library steps (dot_general, gather, scatter, dynamic slices, ...).
+void run_library_step(Device* dev, const Program& prog, const Step& step,
+                      std::vector<MemRef>& vals);
+
+}  // namespace pjrtx

@@ -1,0 +1,314 @@
+"""Builder of StableHLO text modules in the form JAX prints for
+``jax.jit(f).lower(*args).as_text()``.
+
+JAX and jaxlib are not installed on these machines, so the programs that
+JAX would hand the plugin are written with this builder instead: each method
+emits the StableHLO op (pretty form, or the generic form JAX uses for
+gather/scatter) that the corresponding ``jax.numpy`` / ``jax.lax`` call lowers
+to, including JAX's conventions (f16 sums upcast to f32, argmax as a
+two-operand reduce over (values, iota) with JAX's NaN/tie comparator,
+explicit ``broadcast_in_dim`` of scalars).
+"""
+from __future__ import annotations
+
+import math
+import struct
+from dataclasses import dataclass
+
+MLIR_TYPES = {
+    "f32": "f32", "bf16": "bf16", "f16": "f16", "f64": "f64", "pred": "i1",
+    "s8": "i8", "s16": "i16", "s32": "i32", "s64": "i64",
+    "u8": "ui8", "u16": "ui16", "u32": "ui32", "u64": "ui64",
+}
+FLOATS = {"f32", "bf16", "f16", "f64"}
+
+
+def tensor_type(shape, dtype: str) -> str:
+    return "tensor<" + "".join(f"{d}x" for d in shape) + MLIR_TYPES[dtype] + ">"
+
+
+@dataclass(frozen=True)
+class T:
+    name: str
+    shape: tuple
+    dtype: str
+
+    @property
+    def type(self) -> str:
+        return tensor_type(self.shape, self.dtype)
+
+    @property
+    def rank(self) -> int:
+        return len(self.shape)
+
+
+def _fmt_float(v: float, dtype: str) -> str:
+    if math.isnan(v):
+        return {"f32": "0x7FC00000", "bf16": "0x7FC0", "f16": "0x7E00", "f64": "0x7FF8000000000000"}[dtype]
+    if math.isinf(v):
+        if dtype == "f32":
+            return "0x7F800000" if v > 0 else "0xFF800000"
+        if dtype == "bf16":
+            return "0x7F80" if v > 0 else "0xFF80"
+        if dtype == "f16":
+            return "0x7C00" if v > 0 else "0xFC00"
+        return "0x7FF0000000000000" if v > 0 else "0xFFF0000000000000"
+    if dtype == "f32":
+        v = struct.unpack("<f", struct.pack("<f", v))[0]
+    return f"{v:.6e}" if dtype != "f64" else repr(float(v))
+
+
+def _literal(value, dtype: str) -> str:
+    if dtype == "pred":
+        return "true" if value else "false"
+    if dtype in FLOATS:
+        return _fmt_float(float(value), dtype)
+    return str(int(value))
+
+
+class Builder:
+    """Accumulates one ``@main`` function; ``build()`` returns module text."""
+
+    def __init__(self, name: str = "jit_f"):
+        self.name = name
+        self.params: list[T] = []
+        self.lines: list[str] = []
+        self._n = 0
+        self._c = 0
+
+    # -------------------------------------------------------------- values
+    def _fresh(self) -> str:
+        n = f"%{self._n}"
+        self._n += 1
+        return n
+
+    def _emit(self, text: str, shape, dtype) -> T:
+        t = T(self._fresh(), tuple(shape), dtype)
+        self.lines.append(f"    {t.name} = {text}")
+        return t
+
+    def param(self, shape, dtype: str) -> T:
+        t = T(f"%arg{len(self.params)}", tuple(shape), dtype)
+        self.params.append(t)
+        return t
+
+    def constant(self, value, dtype: str, shape=()) -> T:
+        name = f"%cst_{self._c}" if dtype in FLOATS else f"%c_{self._c}"
+        self._c += 1
+        t = T(name, tuple(shape), dtype)
+        self.lines.append(f"    {name} = stablehlo.constant dense<{_literal(value, dtype)}> : {t.type}")
+        return t
+
+    def dense(self, values, dtype: str, shape) -> T:
+        flat = [_literal(v, dtype) for v in values]
+        if len(shape) == 1:
+            body = "[" + ", ".join(flat) + "]"
+        else:
+            import numpy as np
+            arr = np.array(flat, dtype=object).reshape(shape)
+
+            def rec(a):
+                if a.ndim == 1:
+                    return "[" + ", ".join(a) + "]"
+                return "[" + ", ".join(rec(x) for x in a) + "]"
+            body = rec(arr)
+        name = f"%c_{self._c}"
+        self._c += 1
+        t = T(name, tuple(shape), dtype)
+        self.lines.append(f"    {name} = stablehlo.constant dense<{body}> : {t.type}")
+        return t
+
+    def scalar_like(self, value, like: T) -> T:
+        """Scalar constant broadcast to `like`'s shape (JAX's lowering of
+        python scalars in binary ops)."""
+        c = self.constant(value, like.dtype)
+        if like.rank == 0:
+            return c
+        return self.broadcast_in_dim(c, like.shape, [])
+
+    # --------------------------------------------------------- elementwise
+    def _unary(self, op: str, x: T, dtype: str | None = None) -> T:
+        dt = dtype or x.dtype
+        if dt == x.dtype:
+            return self._emit(f"stablehlo.{op} {x.name} : {x.type}", x.shape, dt)
+        return self._emit(f"stablehlo.{op} {x.name} : ({x.type}) -> {tensor_type(x.shape, dt)}", x.shape, dt)
+
+    def _binary(self, op: str, a: T, b: T) -> T:
+        assert a.shape == b.shape and a.dtype == b.dtype, (op, a, b)
+        return self._emit(f"stablehlo.{op} {a.name}, {b.name} : {a.type}", a.shape, a.dtype)
+
+    def add(self, a, b): return self._binary("add", a, b)
+    def subtract(self, a, b): return self._binary("subtract", a, b)
+    def multiply(self, a, b): return self._binary("multiply", a, b)
+    def divide(self, a, b): return self._binary("divide", a, b)
+    def maximum(self, a, b): return self._binary("maximum", a, b)
+    def minimum(self, a, b): return self._binary("minimum", a, b)
+    def power(self, a, b): return self._binary("power", a, b)
+    def remainder(self, a, b): return self._binary("remainder", a, b)
+    def and_(self, a, b): return self._binary("and", a, b)
+    def or_(self, a, b): return self._binary("or", a, b)
+    def xor(self, a, b): return self._binary("xor", a, b)
+    def shift_left(self, a, b): return self._binary("shift_left", a, b)
+    def shift_right_arithmetic(self, a, b): return self._binary("shift_right_arithmetic", a, b)
+    def shift_right_logical(self, a, b): return self._binary("shift_right_logical", a, b)
+    def atan2(self, a, b): return self._binary("atan2", a, b)
+
+    def tanh(self, x): return self._unary("tanh", x)
+    def exp(self, x): return self._unary("exponential", x)
+    def log(self, x): return self._unary("log", x)
+    def log1p(self, x): return self._unary("log_plus_one", x)
+    def rsqrt(self, x): return self._unary("rsqrt", x)
+    def sqrt(self, x): return self._unary("sqrt", x)
+    def negate(self, x): return self._unary("negate", x)
+    def abs(self, x): return self._unary("abs", x)
+    def logistic(self, x): return self._unary("logistic", x)
+    def sine(self, x): return self._unary("sine", x)
+    def cosine(self, x): return self._unary("cosine", x)
+    def floor(self, x): return self._unary("floor", x)
+    def ceil(self, x): return self._unary("ceil", x)
+    def sign(self, x): return self._unary("sign", x)
+    def not_(self, x): return self._unary("not", x)
+    def cbrt(self, x): return self._unary("cbrt", x)
+    def round_nearest_afz(self, x): return self._unary("round_nearest_afz", x)
+    def popcnt(self, x): return self._unary("popcnt", x)
+    def clz(self, x): return self._unary("count_leading_zeros", x)
+    def is_finite(self, x): return self._unary("is_finite", x, "pred")
+
+    def convert(self, x: T, dtype: str) -> T:
+        return self._emit(f"stablehlo.convert {x.name} : ({x.type}) -> {tensor_type(x.shape, dtype)}", x.shape, dtype)
+
+    def bitcast_convert(self, x: T, dtype: str) -> T:
+        return self._emit(f"stablehlo.bitcast_convert {x.name} : ({x.type}) -> {tensor_type(x.shape, dtype)}",
+                          x.shape, dtype)
+
+    def compare(self, direction: str, a: T, b: T, kind: str | None = None) -> T:
+        kind = kind or ("FLOAT" if a.dtype in FLOATS else ("UNSIGNED" if a.dtype.startswith("u") or a.dtype == "pred"
+                                                            else "SIGNED"))
+        out = tensor_type(a.shape, "pred")
+        return self._emit(f"stablehlo.compare  {direction}, {a.name}, {b.name},  {kind} : ({a.type}, {b.type}) -> {out}",
+                          a.shape, "pred")
+
+    def select(self, p: T, a: T, b: T) -> T:
+        return self._emit(f"stablehlo.select {p.name}, {a.name}, {b.name} : {p.type}, {a.type}", a.shape, a.dtype)
+
+    def clamp(self, lo: T, x: T, hi: T) -> T:
+        if lo.shape == x.shape and hi.shape == x.shape:
+            return self._emit(f"stablehlo.clamp {lo.name}, {x.name}, {hi.name} : {x.type}", x.shape, x.dtype)
+        return self._emit(f"stablehlo.clamp {lo.name}, {x.name}, {hi.name} : ({lo.type}, {x.type}, {hi.type}) -> "
+                          f"{x.type}", x.shape, x.dtype)
+
+    # ------------------------------------------------------------- views
+    def broadcast_in_dim(self, x: T, shape, dims) -> T:
+        d = ", ".join(str(v) for v in dims)
+        return self._emit(f"stablehlo.broadcast_in_dim {x.name}, dims = [{d}] : ({x.type}) -> "
+                          f"{tensor_type(shape, x.dtype)}", shape, x.dtype)
+
+    def reshape(self, x: T, shape) -> T:
+        return self._emit(f"stablehlo.reshape {x.name} : ({x.type}) -> {tensor_type(shape, x.dtype)}", shape, x.dtype)
+
+    def transpose(self, x: T, perm) -> T:
+        shape = tuple(x.shape[p] for p in perm)
+        d = ", ".join(str(v) for v in perm)
+        return self._emit(f"stablehlo.transpose {x.name}, dims = [{d}] : ({x.type}) -> {tensor_type(shape, x.dtype)}",
+                          shape, x.dtype)
+
+    def slice(self, x: T, start, limit, strides=None) -> T:
+        strides = strides or [1] * x.rank
+        shape = tuple((l - s + st - 1) // st for s, l, st in zip(start, limit, strides))
+        rng = ", ".join(f"{s}:{l}" if st == 1 else f"{s}:{l}:{st}" for s, l, st in zip(start, limit, strides))
+        return self._emit(f"stablehlo.slice {x.name} [{rng}] : ({x.type}) -> {tensor_type(shape, x.dtype)}",
+                          shape, x.dtype)
+
+    def iota(self, shape, dim: int, dtype: str = "s32") -> T:
+        return self._emit(f"stablehlo.iota dim = {dim} : {tensor_type(shape, dtype)}", shape, dtype)
+
+    def reverse(self, x: T, dims) -> T:
+        d = ", ".join(str(v) for v in dims)
+        return self._emit(f"stablehlo.reverse {x.name}, dims = [{d}] : {x.type}", x.shape, x.dtype)
+
+    def concatenate(self, xs: list[T], dim: int) -> T:
+        shape = list(xs[0].shape)
+        shape[dim] = sum(x.shape[dim] for x in xs)
+        names = ", ".join(x.name for x in xs)
+        types = ", ".join(x.type for x in xs)
+        return self._emit(f"stablehlo.concatenate {names}, dim = {dim} : ({types}) -> "
+                          f"{tensor_type(shape, xs[0].dtype)}", shape, xs[0].dtype)
+
+    # -------------------------------------------------------- reductions
+    def reduce(self, x: T, init: T, dims, op: str) -> T:
+        """Single-operand reduce in the `applies` form (op: add/maximum/minimum/...)."""
+        shape = tuple(s for i, s in enumerate(x.shape) if i not in dims)
+        d = ", ".join(str(v) for v in dims)
+        return self._emit(f"stablehlo.reduce({x.name} init: {init.name}) applies stablehlo.{op} across dimensions = "
+                          f"[{d}] : ({x.type}, {init.type}) -> {tensor_type(shape, x.dtype)}", shape, x.dtype)
+
+    def argmax(self, x: T, axis: int, index_dtype: str = "s32", both: bool = True, kind: str = "max"):
+        """Two-operand reduce over (x, iota) with JAX's argmax/argmin
+        comparator (NaN wins, ties -> lowest index). Returns (values, indices)."""
+        idx = self.iota(x.shape, axis, index_dtype)
+        init_v = self.constant(float("-inf") if kind == "max" else float("inf"), x.dtype)
+        init_i = self.constant(0, index_dtype)
+        shape = tuple(s for i, s in enumerate(x.shape) if i != axis)
+        name = self._fresh()
+        sv, si = tensor_type((), x.dtype), tensor_type((), index_dtype)
+        cmp = "GT" if kind == "max" else "LT"
+        fk = "FLOAT"
+        ik = "SIGNED" if index_dtype.startswith("s") else "UNSIGNED"
+        pred = tensor_type((), "pred")
+        b = name[1:]
+        body = [
+            f"    {name}:2 = stablehlo.reduce({x.name} init: {init_v.name}), ({idx.name} init: {init_i.name}) across "
+            f"dimensions = [{axis}] : ({x.type}, {idx.type}, {sv}, {si}) -> ({tensor_type(shape, x.dtype)}, "
+            f"{tensor_type(shape, index_dtype)})",
+            f"     reducer(%r{b}_a: {sv}, %r{b}_c: {sv}) (%r{b}_b: {si}, %r{b}_d: {si})  {{",
+            f"      %r{b}_1 = stablehlo.compare  {cmp}, %r{b}_a, %r{b}_c,  {fk} : ({sv}, {sv}) -> {pred}",
+            f"      %r{b}_2 = stablehlo.compare  NE, %r{b}_a, %r{b}_a,  {fk} : ({sv}, {sv}) -> {pred}",
+            f"      %r{b}_3 = stablehlo.or %r{b}_1, %r{b}_2 : {pred}",
+            f"      %r{b}_4 = stablehlo.compare  EQ, %r{b}_a, %r{b}_c,  {fk} : ({sv}, {sv}) -> {pred}",
+            f"      %r{b}_5 = stablehlo.compare  LT, %r{b}_b, %r{b}_d,  {ik} : ({si}, {si}) -> {pred}",
+            f"      %r{b}_6 = stablehlo.and %r{b}_4, %r{b}_5 : {pred}",
+            f"      %r{b}_7 = stablehlo.or %r{b}_3, %r{b}_6 : {pred}",
+            f"      %r{b}_8 = stablehlo.select %r{b}_3, %r{b}_a, %r{b}_c : {pred}, {sv}",
+            f"      %r{b}_9 = stablehlo.select %r{b}_7, %r{b}_b, %r{b}_d : {pred}, {si}",
+            f"      stablehlo.return %r{b}_8, %r{b}_9 : {sv}, {si}",
+            "    }",
+        ]
+        self.lines.extend(body)
+        return T(f"{name}#0", shape, x.dtype), T(f"{name}#1", shape, index_dtype)
+
+    # JAX-level helpers --------------------------------------------------
+    def sum(self, x: T, axes) -> T:
+        """jnp.sum: f16/bf16 inputs are summed in f32 and converted back."""
+        axes = list(axes)
+        if x.dtype in ("f16", "bf16"):
+            xf = self.convert(x, "f32")
+            r = self.reduce(xf, self.constant(0.0, "f32"), axes, "add")
+            return self.convert(r, x.dtype)
+        return self.reduce(x, self.constant(0, x.dtype), axes, "add")
+
+    def max(self, x: T, axes) -> T:
+        init = self.constant(float("-inf") if x.dtype in FLOATS else -(2 ** 31), x.dtype)
+        return self.reduce(x, init, list(axes), "maximum")
+
+    def min(self, x: T, axes) -> T:
+        init = self.constant(float("inf") if x.dtype in FLOATS else 2 ** 31 - 1, x.dtype)
+        return self.reduce(x, init, list(axes), "minimum")
+
+    # ------------------------------------------------------------ output
+    def build(self, outputs: list[T]) -> str:
+        args = ", ".join(f"{p.name}: {p.type}" for p in self.params)
+        if len(outputs) == 1:
+            res = f"({outputs[0].type} {{jax.result_info = \"result\"}})"
+        else:
+            res = "(" + ", ".join(f"{o.type} {{jax.result_info = \"result[{i}]\"}}" for i, o in enumerate(outputs)) + ")"
+        ret_names = ", ".join(o.name for o in outputs)
+        ret_types = ", ".join(o.type for o in outputs)
+        return "\n".join([
+            f"module @{self.name} attributes {{mhlo.num_partitions = 1 : i32, mhlo.num_replicas = 1 : i32}} {{",
+            f"  func.func public @main({args}) -> {res} {{",
+            *self.lines,
+            f"    return {ret_names} : {ret_types}",
+            "  }",
+            "}",
+            "",
+        ])
