@@ -526,11 +526,11 @@ class KernelGen {
     if (s.kind == StepKind::kLoop) m = std::max(m, num_elements(s.loop_shape));
     return m < (int64_t(1) << 31) ? "uint32_t" : "uint64_t";
   }
-  void signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch);
+  void signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch, const char* suffix = "");
 };
 
-void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch) {
-  out_ << "extern \"C\" __global__ void __launch_bounds__(256) " << s.name << "(";
+void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch, const char* suffix) {
+  out_ << "extern \"C\" __global__ void __launch_bounds__(256) " << s.name << suffix << "(";
   int k = 0;
   for (int v : s.inputs) {
     const DType t = prog_.type(v).dtype;
@@ -544,7 +544,7 @@ void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, boo
     out_ << (k + o ? ", " : "") << dtype_storage_ctype(t) << "* __restrict__ out" << o;
     ++o;
   }
-  if (with_scratch) out_ << ", unsigned char* __restrict__ scratch, uint32_t* __restrict__ counters";
+  if (with_scratch) out_ << ", unsigned char* __restrict__ scratch";
   out_ << ") {\n";
 }
 
@@ -622,12 +622,10 @@ void KernelGen::reduce(Step& s) {
     a.i = "aci" + std::to_string(r);
     accs.push_back(a);
   }
-  const bool arg = [&] {
-    for (auto& a : accs)
-      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) return true;
-    return false;
-  }();
-  (void)arg;
+  // Argmax index accumulators are 32-bit when every index fits.
+  const bool narrow_index = num_elements(shape) < (int64_t(1) << 31);
+  const std::string ait = narrow_index ? "int32_t" : "int64_t";
+  const std::string aimax = narrow_index ? "0x7fffffff" : "0x7fffffffffffffffll";
 
   Writer w(prog_, ptr_of, it);
   // Root index over the reduce operand shape.
@@ -700,66 +698,108 @@ void KernelGen::reduce(Step& s) {
   const int rid = w.add_index(root);
   // Values of every reduce operand at the root.
   std::vector<std::vector<std::string>> xs(s.reduces.size());
-  // Preloads (row schedule only).
-  std::ostringstream pre;
+  // Preloads (row schedule only): `unroll` sub-chunks of `vec` elements per
+  // thread are all requested before any is consumed, so that each thread has
+  // several 16-byte loads in flight. The element body reads P_<input>[j],
+  // bound to the current sub-chunk's registers.
+  std::ostringstream pre_decl, pre_load;
+  const int unroll = std::max<int>(1, s.unroll);
   if (s.row_schedule) {
     const int64_t n_all = num_elements(shape);
     for (int v : s.inputs) {
       if (prog_.type(v).elements() != n_all) continue;
       const DType t = prog_.type(v).dtype;
-      std::string name = "pre_" + ptr_of[v];
-      pre << dtype_storage_ctype(t) << " " << name << "[" << vec << "];\n";
-      pre << "ldv<" << dtype_storage_ctype(t) << ", " << vec << ">(" << name << ", " << ptr_of[v]
-          << ", lbase, row * " << s.row_len << "u + c1, full);\n";
-      w.preload[v] = name;
+      const std::string st = dtype_storage_ctype(t);
+      const std::string name = "pre_" + ptr_of[v];
+      pre_decl << st << " " << name << "[" << unroll << "][" << vec << "];\n";
+      pre_load << "ldv<" << st << ", " << vec << ">(" << name << "[u], " << ptr_of[v] << ", row * " << s.row_len
+               << "u + cu, row * " << s.row_len << "u + c1, cu + " << vec << "u <= c1);\n";
+      w.preload[v] = "P_" + ptr_of[v];
     }
   }
-  for (size_t r = 0; r < s.reduces.size(); ++r)
-    for (int v : s.reduces[r].inputs) xs[r].push_back(w.value(v, rid));
+  for (size_t r = 0; r < s.reduces.size(); ++r) {
+    const ReduceSpec& rs = s.reduces[r];
+    for (int v : rs.inputs) {
+      // max/min of a float->float convert: a rounding is monotone, so the
+      // running max/min is kept on the unconverted value and rounded once in
+      // the final step (which rounds to the result type anyway).
+      const bool mm = rs.kind == ReducerKind::kMax || rs.kind == ReducerKind::kMin;
+      int src = v;
+      for (const Op& op : prog_.ops) {
+        if (!mm || op.results.empty() || op.results[0] != v || op.kind != OpKind::kConvert) continue;
+        const DType from = prog_.type(op.operands[0]).dtype, to = prog_.type(v).dtype;
+        const bool f32ish = [](DType t) { return t == DType::kF32 || t == DType::kF16 || t == DType::kBF16; }(from);
+        if (f32ish && (to == DType::kF32 || to == DType::kF16 || to == DType::kBF16)) src = op.operands[0];
+      }
+      xs[r].push_back(w.value(src, rid));
+    }
+  }
   std::string elem_body = w.body.str();
 
   out_ << head.str();
   for (auto& a : accs) {
     out_ << a.acc_t << " " << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
     if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
-      out_ << "int64_t " << a.i << " = 0x7fffffffffffffffll;\n";
+      out_ << ait << " " << a.i << " = " << aimax << ";\n";
   }
+  // In-thread update. A thread visits its elements by increasing index, so
+  // the in-order forms (argmax_take, max_seq, min_seq) give the same result
+  // as the full pair comparator with fewer instructions.
   auto combine_elem = [&](std::ostream& o) {
     for (size_t r = 0; r < accs.size(); ++r) {
       const Accum& a = accs[r];
       if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
-        o << "if (" << arg_better(a.kind) << "((float)" << xs[r][0] << ", (int64_t)" << xs[r][1] << ", " << a.v << ", "
-          << a.i << ")) { " << a.v << " = " << xs[r][0] << "; " << a.i << " = (int64_t)" << xs[r][1] << "; }\n";
+        const char* take = a.kind == ReducerKind::kArgMax ? "argmax_take" : "argmin_take";
+        o << "{ const float xv = (float)" << xs[r][0] << "; const bool bt = " << take << "(xv, " << a.v << "); " << a.v
+          << " = bt ? xv : " << a.v << "; " << a.i << " = bt ? (" << ait << ")" << xs[r][1] << " : " << a.i << "; }\n";
+      } else if ((a.kind == ReducerKind::kMax || a.kind == ReducerKind::kMin) && a.acc_t == "float") {
+        o << a.v << " = " << (a.kind == ReducerKind::kMax ? "max_seq(" : "min_seq(") << a.v << ", (float)(" << xs[r][0]
+          << "));\n";
       } else {
         o << combine_stmt(a.kind, a.vt, a.v, "(" + a.acc_t + ")(" + xs[r][0] + ")") << "\n";
       }
     }
   };
   if (s.row_schedule) {
-    out_ << "for (idx_t c = c0 + threadIdx.x * " << vec << "u; c < c1; c += " << 256 * vec << "u) {\n";
-    out_ << "const idx_t lbase = row * " << s.row_len << "u + c;\n";
-    out_ << "const bool full = c + " << vec << "u <= c1;\n";
-    out_ << pre.str();
+    const int64_t span = 256 * vec;
+    out_ << pre_decl.str();
+    out_ << "for (idx_t c = c0 + threadIdx.x * " << vec << "u; c < c1; c += " << span * unroll << "u) {\n";
+    out_ << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
+    out_ << "const idx_t cu = c + (idx_t)u * " << span << "u;\n";
+    out_ << pre_load.str();
+    out_ << "}\n";
+    out_ << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
+    out_ << "const idx_t cu = c + (idx_t)u * " << span << "u;\n";
+    for (auto& [v, pname] : w.preload) out_ << "const auto& " << pname << " = pre_" << ptr_of[v] << "[u];\n";
+    // Whole sub-chunk in range: no per-element guard.
+    out_ << "if (cu + " << vec << "u <= c1) {\n";
     out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
-    out_ << "if (full || c + j < c1) {\n";
-    out_ << "const idx_t col = c + j;\nconst idx_t lin = lbase + j;\n";
+    out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
+    out_ << col_digits.str() << elem_body;
+    combine_elem(out_);
+    out_ << "}\n";
+    out_ << "} else if (cu < c1) {\n";
+    out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
+    out_ << "if (cu + j < c1) {\n";
+    out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
     out_ << col_digits.str() << elem_body;
     combine_elem(out_);
     out_ << "}\n}\n}\n";
+    out_ << "}\n}\n";
     // Shared slots for the cross-wave step of the block reductions.
     for (auto& a : accs) {
       out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[4];\n";
-      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << "__shared__ int64_t sm_" << a.i << "[4];\n";
+      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << "__shared__ " << ait << " sm_" << a.i << "[4];\n";
     }
     // Block reduction: 64-lane xor butterfly, then the 4 wave results are
     // combined in wave order by thread 0 (fixed order: deterministic).
-    auto block_reduce = [&]() {
+    auto wave_reduce = [&]() {
       for (auto& a : accs) {
         const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
         out_ << "#pragma unroll\nfor (int m = 32; m >= 1; m >>= 1) {\n";
         if (am) {
           out_ << "const float ov = wave_shfl_xor(" << a.v << ", m);\n";
-          out_ << "const int64_t oi = wave_shfl_xor(" << a.i << ", m);\n";
+          out_ << "const " << ait << " oi = wave_shfl_xor(" << a.i << ", m);\n";
           out_ << "if (" << arg_better(a.kind) << "(ov, oi, " << a.v << ", " << a.i << ")) { " << a.v << " = ov; " << a.i
                << " = oi; }\n";
         } else {
@@ -768,6 +808,9 @@ void KernelGen::reduce(Step& s) {
         }
         out_ << "}\n";
       }
+    };
+    auto block_reduce = [&]() {
+      wave_reduce();
       out_ << "if ((threadIdx.x & 63) == 0) {\n";
       for (auto& a : accs) {
         out_ << "sm_" << a.v << "[threadIdx.x >> 6] = " << a.v << ";\n";
@@ -791,58 +834,58 @@ void KernelGen::reduce(Step& s) {
       }
       out_ << "}\n";
     };
-    block_reduce();
-    if (split) {
-      // Partials in scratch: per reducer a [rows*splits] array of 8-byte
-      // slots (argmax: value slots then index slots). The workgroup that
-      // arrives last for a row combines the row's partials with all of its
-      // threads (thread t reads split t) in the same fixed tree.
+    // Partial-slot layout in scratch: per reducer a [rows*splits] array of
+    // 8-byte slots (argmax: value slots, then index slots).
+    const int64_t slots = s.rows * s.splits;
+    std::vector<size_t> offs;
+    {
       size_t off = 0;
-      const int64_t slots = s.rows * s.splits;
-      std::vector<size_t> offs;
       for (auto& a : accs) {
         offs.push_back(off);
         off += static_cast<size_t>(slots) * 8;
         if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) off += static_cast<size_t>(slots) * 8;
       }
-      out_ << "__shared__ uint32_t sm_last;\n";
-      out_ << "if (threadIdx.x == 0) {\n";
+    }
+    block_reduce();
+    if (split) {
+      // Partials of this split go to scratch with plain stores; the
+      // `<name>_combine` kernel (launched next on the same stream) folds
+      // them. The kernel boundary publishes the stores, so no per-workgroup
+      // device-scope fence is needed.
+      out_ << "if (threadIdx.x != 0) return;\n";
       for (size_t r = 0; r < accs.size(); ++r) {
         const Accum& a = accs[r];
         out_ << "{ uint64_t* slot = reinterpret_cast<uint64_t*>(scratch + " << offs[r] << "u);\n";
         out_ << "uint64_t bits = 0; __builtin_memcpy(&bits, &" << a.v << ", sizeof(" << a.v << "));\n";
-        out_ << "__hip_atomic_store(&slot[row * " << s.splits << "u + split], bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
-        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
-          out_ << "__hip_atomic_store(&slot[" << slots << "u + row * " << s.splits << "u + split], (uint64_t)" << a.i
-               << ", __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
-        }
+        out_ << "slot[row * " << s.splits << "u + split] = bits;\n";
+        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
+          out_ << "slot[" << slots << "u + row * " << s.splits << "u + split] = (uint64_t)" << a.i << ";\n";
         out_ << "}\n";
       }
-      out_ << "__threadfence();\n";
-      out_ << "sm_last = (atomicAdd(&counters[row], 1u) == " << s.splits - 1 << "u) ? 1u : 0u;\n";
-      out_ << "}\n__syncthreads();\n";
-      out_ << "if (sm_last == 0u) return;\n";
-      out_ << "__threadfence();\n";
+      out_ << "}\n\n";
+      // Combine kernel: one wavefront per row, lane k reads split k.
+      signature(s, &ptr_of, true, "_combine");
+      out_ << "typedef " << it << " idx_t;\n";
+      out_ << "const idx_t row = (idx_t)blockIdx.x * 4u + (threadIdx.x >> 6);\n";
+      out_ << "if (row >= " << s.rows << "u) return;\n";
+      out_ << "const uint32_t lane = threadIdx.x & 63u;\n";
       for (size_t r = 0; r < accs.size(); ++r) {
         const Accum& a = accs[r];
         const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
-        out_ << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
-        if (am) out_ << a.i << " = 0x7fffffffffffffffll;\n";
-        out_ << "if (threadIdx.x < " << s.splits << "u) {\n";
-        out_ << "uint64_t* slot = reinterpret_cast<uint64_t*>(scratch + " << offs[r] << "u);\n";
-        out_ << "const uint64_t bits = __hip_atomic_load(&slot[row * " << s.splits
-             << "u + threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+        out_ << a.acc_t << " " << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
+        if (am) out_ << ait << " " << a.i << " = " << aimax << ";\n";
+        out_ << "if (lane < " << s.splits << "u) {\n";
+        out_ << "const uint64_t* slot = reinterpret_cast<const uint64_t*>(scratch + " << offs[r] << "u);\n";
+        out_ << "const uint64_t bits = slot[row * " << s.splits << "u + lane];\n";
         out_ << "__builtin_memcpy(&" << a.v << ", &bits, sizeof(" << a.v << "));\n";
-        if (am) {
-          out_ << a.i << " = (int64_t)__hip_atomic_load(&slot[" << slots << "u + row * " << s.splits
-               << "u + threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
-        }
+        if (am) out_ << a.i << " = (" << ait << ")slot[" << slots << "u + row * " << s.splits << "u + lane];\n";
         out_ << "}\n";
       }
-      block_reduce();
-      out_ << "if (threadIdx.x == 0) __hip_atomic_store(&counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+      wave_reduce();
+      out_ << "if (lane != 0) return;\n";
+    } else {
+      out_ << "if (threadIdx.x != 0) return;\n";
     }
-    out_ << "if (threadIdx.x != 0) return;\n";
   } else {
     // Column schedule: one thread per output, serial walk of reduced elements.
     out_ << "for (idx_t col = 0; col < " << s.row_len << "u; ++col) {\n";
@@ -885,8 +928,8 @@ void KernelGen::reduce(Step& s) {
     std::string init0 = e.value(rs.inits[0], scal);
     if (am) {
       std::string init1 = e.value(rs.inits[1], scal);
-      fin << "if (" << arg_better(a.kind) << "((float)" << init0 << ", (int64_t)" << init1 << ", " << a.v << ", " << a.i
-          << ")) { " << a.v << " = " << init0 << "; " << a.i << " = (int64_t)" << init1 << "; }\n";
+      fin << "if (" << arg_better(a.kind) << "((float)" << init0 << ", (" << ait << ")" << init1 << ", " << a.v << ", " << a.i
+          << ")) { " << a.v << " = " << init0 << "; " << a.i << " = (" << ait << ")" << init1 << "; }\n";
     } else {
       fin << combine_stmt(a.kind, a.vt, a.v, "(" + a.acc_t + ")(" + init0 + ")") << "\n";
     }

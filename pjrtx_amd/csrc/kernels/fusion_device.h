@@ -207,18 +207,30 @@ PJRTX_DEV int32_t total_order_key(float x) {
 // values win, and ties go to the lower index. This is the order JAX's argmax
 // comparator defines; it is total on distinct indices, so any combine tree
 // gives the same winner.
-PJRTX_DEV bool argmax_better(float va, int64_t ia, float vb, int64_t ib) {
+template <typename I>
+PJRTX_DEV bool argmax_better(float va, I ia, float vb, I ib) {
   const bool na = isnan_f(va), nb = isnan_f(vb);
   if (na != nb) return na;
   if (!na && va != vb) return va > vb;
   return ia < ib;
 }
-PJRTX_DEV bool argmin_better(float va, int64_t ia, float vb, int64_t ib) {
+template <typename I>
+PJRTX_DEV bool argmin_better(float va, I ia, float vb, I ib) {
   const bool na = isnan_f(va), nb = isnan_f(vb);
   if (na != nb) return na;
   if (!na && va != vb) return va < vb;
   return ia < ib;
 }
+
+// In-order forms used while one thread walks its elements by increasing
+// index: the newcomer x (higher index) replaces the accumulator only if it
+// is strictly better, or is the first NaN. Same winner as argmax_better for
+// that order, at a fraction of the instructions.
+PJRTX_DEV bool argmax_take(float x, float acc) { return x > acc || (isnan_f(x) && !isnan_f(acc)); }
+PJRTX_DEV bool argmin_take(float x, float acc) { return x < acc || (isnan_f(x) && !isnan_f(acc)); }
+// NaN-propagating running max/min (an accumulator that saw NaN stays NaN).
+PJRTX_DEV float max_seq(float acc, float x) { return (x > acc || isnan_f(x)) ? x : acc; }
+PJRTX_DEV float min_seq(float acc, float x) { return (x < acc || isnan_f(x)) ? x : acc; }
 
 // ------------------------------------------------------ wavefront reductions
 // 64-lane wavefronts: xor-butterfly over lane offsets 32..1. Every lane ends

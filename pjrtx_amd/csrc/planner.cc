@@ -501,8 +501,6 @@ void Planner::shape_reduce(Step* s) {
     return;
   }
   size_t min_size = 8;
-  for (const ReduceSpec& r : s->reduces)
-    for (int v : r.inputs) (void)v;
   for (int v : s->inputs)
     if (prog_.type(v).elements() == num_elements(shape)) min_size = std::min(min_size, dtype_size(prog_.type(v).dtype));
   int vec = static_cast<int>(16 / std::max<size_t>(min_size, 1));
@@ -510,21 +508,25 @@ void Planner::shape_reduce(Step* s) {
   while (vec > 1 && row_len % vec != 0) vec /= 2;
   s->vec = vec;
   const int64_t per_iter = 256 * vec;
+  // Few long rows: split each row over several workgroups so the launch
+  // reaches the target block count, keeping at least one full 256*vec span
+  // per split.
   int64_t splits = (opts_.reduce_target_blocks + rows - 1) / rows;
-  splits = std::min<int64_t>(splits, std::max<int64_t>(1, row_len / (2 * per_iter)));
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, row_len / per_iter));
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, 64));
   int64_t chunk = (row_len + splits - 1) / splits;
   chunk = (chunk + vec - 1) / vec * vec;
   splits = (row_len + chunk - 1) / chunk;
   s->splits = splits;
   s->chunk = chunk;
+  s->unroll = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(8, (chunk + per_iter - 1) / per_iter)));
   s->grid = static_cast<uint32_t>(rows * splits);
   s->block = 256;
   if (splits > 1) {
     size_t per_slot = 0;
     for (const ReduceSpec& r : s->reduces) per_slot += (r.kind == ReducerKind::kArgMax || r.kind == ReducerKind::kArgMin) ? 16 : 8;
     s->scratch_bytes = static_cast<size_t>(rows * splits) * per_slot;
-    s->counter_bytes = static_cast<size_t>(rows) * 4;
+    s->combine_grid = static_cast<uint32_t>((rows + 3) / 4);
   }
 }
 

@@ -67,8 +67,9 @@ struct Step {
   int64_t row_len = 1;       // row schedule: product of reduced dims
   int64_t splits = 1;        // workgroups per row
   int64_t chunk = 0;         // elements per split
+  int unroll = 1;            // 256*vec-element sub-chunks loaded together per thread
   size_t scratch_bytes = 0;  // partial accumulators (splits > 1)
-  size_t counter_bytes = 0;  // per-row arrival counters (splits > 1)
+  uint32_t combine_grid = 0; // splits > 1: workgroups of `<name>_combine` (4 rows each)
 
   // kLibrary / kAlias
   LibKind lib = LibKind::kCopy;
@@ -97,7 +98,7 @@ struct PlanOptions {
   int recompute_limit = 24;
   // Target number of workgroups a reduction launch should reach.
   // (environment: PJRTX_REDUCE_TARGET_BLOCKS)
-  int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 2048);
+  int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 1024);
   bool fuse_siblings = true;
   bool fuse_epilogues = true;
 };

@@ -371,18 +371,18 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
     hip_check(hipModuleLoadData(&L->module, code_.data()), "hipModuleLoadData");
   }
   L->funcs.resize(plan_.steps.size(), nullptr);
+  L->combine_funcs.resize(plan_.steps.size(), nullptr);
   L->scratch.resize(plan_.steps.size());
-  L->counters.resize(plan_.steps.size());
   for (size_t i = 0; i < plan_.steps.size(); ++i) {
     const Step& s = plan_.steps[i];
     if (s.kind == StepKind::kLoop || s.kind == StepKind::kReduce) {
       hip_check(hipModuleGetFunction(&L->funcs[i], L->module, s.name.c_str()), "hipModuleGetFunction");
     }
-    if (s.scratch_bytes) L->scratch[i] = dev->allocate(s.scratch_bytes);
-    if (s.counter_bytes) {
-      L->counters[i] = dev->allocate(s.counter_bytes);
-      hip_check(hipMemsetAsync(L->counters[i]->ptr, 0, s.counter_bytes, dev->stream()), "hipMemsetAsync");
+    if (s.combine_grid) {
+      const std::string cname = s.name + "_combine";
+      hip_check(hipModuleGetFunction(&L->combine_funcs[i], L->module, cname.c_str()), "hipModuleGetFunction");
     }
+    if (s.scratch_bytes) L->scratch[i] = dev->allocate(s.scratch_bytes);
   }
   // Resident constants: uploaded once (reference: executable_constants.zig:32-83).
   for (int v : plan_.constants) {
@@ -428,15 +428,19 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals) {
       ptrs.reserve(s.inputs.size() + s.outputs.size() + 2);
       for (int v : s.inputs) ptrs.push_back(vals[v] ? vals[v]->ptr : nullptr);
       for (int v : s.outputs) ptrs.push_back(vals[v]->ptr);
-      if (s.kind == StepKind::kReduce && s.row_schedule && s.splits > 1) {
-        ptrs.push_back(L->scratch[si]->ptr);
-        ptrs.push_back(L->counters[si]->ptr);
-      }
+      if (s.combine_grid) ptrs.push_back(L->scratch[si]->ptr);
       std::vector<void*> args(ptrs.size());
       for (size_t k = 0; k < ptrs.size(); ++k) args[k] = &ptrs[k];
       hip_check(hipModuleLaunchKernel(L->funcs[si], s.grid, 1, 1, s.block, 1, 1, 0, dev->stream(), args.data(), nullptr),
                 "hipModuleLaunchKernel");
       stats_.kernel_launches++;
+      if (s.combine_grid) {
+        // Second pass of a split reduction: same arguments, one wave per row.
+        hip_check(hipModuleLaunchKernel(L->combine_funcs[si], s.combine_grid, 1, 1, 256, 1, 1, 0, dev->stream(),
+                                        args.data(), nullptr),
+                  "hipModuleLaunchKernel(combine)");
+        stats_.kernel_launches++;
+      }
       return;
     }
   }

@@ -162,9 +162,10 @@ class Executable {
   struct Loaded {
     Device* dev = nullptr;
     hipModule_t module = nullptr;
-    std::vector<hipFunction_t> funcs;       // per step (null for non-kernel)
-    std::map<int, MemRef> constants;        // value id -> resident buffer
-    std::vector<MemRef> scratch, counters;  // per step
+    std::vector<hipFunction_t> funcs;          // per step (null for non-kernel)
+    std::vector<hipFunction_t> combine_funcs;  // split reductions: second pass
+    std::map<int, MemRef> constants;           // value id -> resident buffer
+    std::vector<MemRef> scratch;               // per step partials
   };
   Program prog_;
   Plan plan_;
