@@ -123,3 +123,182 @@ def c1_inputs(rows: int, cols: int, seed: int = 0):
 def c2_inputs(rows: int, vocab: int, seed: int = 0) -> np.ndarray:
     rng = np.random.default_rng(seed)
     return f32_to_bf16_bits(rng.standard_normal((rows, vocab), dtype=np.float32))
+
+
+# ------------------------------------------------------------------ gather
+
+def gather_stablehlo(operand, indices, offset_dims, collapsed_slice_dims, start_index_map, index_vector_dim,
+                     slice_sizes, operand_batching_dims=(), start_indices_batching_dims=()):
+    """StableHLO gather by its definition, element by element (small inputs).
+    Starts are clamped so each slice stays in bounds, the rule the reference's
+    gather kernel applies (reference: executable_metal_graph_gather.zig:61-65)."""
+    operand = np.asarray(operand)
+    indices = np.asarray(indices)
+    if index_vector_dim == indices.ndim:
+        indices = indices[..., None]
+    batch_idx_dims = [d for d in range(indices.ndim) if d != index_vector_dim]
+    window = [d for d in range(operand.ndim) if d not in collapsed_slice_dims and d not in operand_batching_dims]
+    out_rank = len(batch_idx_dims) + len(offset_dims)
+    batch_out = [d for d in range(out_rank) if d not in offset_dims]
+    shape = [0] * out_rank
+    for o, d in zip(batch_out, batch_idx_dims):
+        shape[o] = indices.shape[d]
+    for o, d in zip(offset_dims, window):
+        shape[o] = slice_sizes[d]
+    out = np.zeros(shape, dtype=operand.dtype)
+    for oi in np.ndindex(*shape):
+        bcoord = [oi[o] for o in batch_out]
+        start = [0] * operand.ndim
+        for k, od in enumerate(start_index_map):
+            sl = list(bcoord)
+            sl.insert(index_vector_dim, k)
+            start[od] = int(indices[tuple(sl)])
+        for ob, ib in zip(operand_batching_dims, start_indices_batching_dims):
+            start[ob] = bcoord[batch_idx_dims.index(ib)]
+        src = []
+        for d in range(operand.ndim):
+            s = min(max(start[d], 0), operand.shape[d] - slice_sizes[d])
+            src.append(s)
+        for o, d in zip(offset_dims, window):
+            src[d] += oi[o]
+        out[oi] = operand[tuple(src)]
+    return out
+
+
+def gather_rows(table, idx):
+    """table[idx] as jnp indexing lowers it: negative indices wrapped once,
+    then starts clamped to [0, rows-1] (row-gather special case of
+    gather_stablehlo)."""
+    idx = np.asarray(idx, dtype=np.int64)
+    n = table.shape[0]
+    idx = np.where(idx < 0, idx + n, idx)
+    return table[np.clip(idx, 0, n - 1)]
+
+
+# ----------------------------------------------------------------- scatter
+
+def scatter_stablehlo(operand, indices, updates, update_window_dims, inserted_window_dims,
+                      scatter_dims_to_operand_dims, index_vector_dim, combiner="add", input_batching_dims=(),
+                      scatter_indices_batching_dims=()):
+    """StableHLO scatter by its definition, applied sequentially in update
+    order (the order of XLA's CPU scatter loop); windows whose start is out of
+    bounds are skipped (reference dimension numbers: api.cc:3158-3236)."""
+    out = np.array(operand, copy=True)
+    indices = np.asarray(indices)
+    updates = np.asarray(updates)
+    if index_vector_dim == indices.ndim:
+        indices = indices[..., None]
+    upd_scatter = [d for d in range(updates.ndim) if d not in update_window_dims]
+    idx_batch = [d for d in range(indices.ndim) if d != index_vector_dim]
+    window = [d for d in range(out.ndim) if d not in inserted_window_dims and d not in input_batching_dims]
+    wsize = [1] * out.ndim
+    for j, d in enumerate(window):
+        wsize[d] = updates.shape[update_window_dims[j]]
+    for ui in np.ndindex(*updates.shape):
+        sc = [ui[d] for d in upd_scatter]
+        start = [0] * out.ndim
+        for k, od in enumerate(scatter_dims_to_operand_dims):
+            sl = list(sc)
+            sl.insert(index_vector_dim, k)
+            start[od] = int(indices[tuple(sl)])
+        for ob, ib in zip(input_batching_dims, scatter_indices_batching_dims):
+            start[ob] = sc[idx_batch.index(ib)]
+        if any(start[d] < 0 or start[d] > out.shape[d] - wsize[d] for d in range(out.ndim)):
+            continue
+        tgt = list(start)
+        for j, d in enumerate(window):
+            tgt[d] += ui[update_window_dims[j]]
+        tgt = tuple(tgt)
+        u = updates[ui]
+        if combiner == "add":
+            out[tgt] = out[tgt] + u
+        elif combiner == "set":
+            out[tgt] = u
+        elif combiner == "maximum":
+            out[tgt] = max(out[tgt], u)
+        elif combiner == "minimum":
+            out[tgt] = min(out[tgt], u)
+        elif combiner == "multiply":
+            out[tgt] = out[tgt] * u
+    return out
+
+
+def scatter_rows_add(operand, idx, updates):
+    """Row scatter-add in update order: np.add.at applies the additions one by
+    one in index order, in the operand's dtype (f32 adds for f32, wrapping
+    adds for int32) — the sequential loop scatter_stablehlo defines."""
+    out = np.array(operand, copy=True)
+    idx = np.asarray(idx, dtype=np.int64)
+    ok = (idx >= 0) & (idx < operand.shape[0])
+    np.add.at(out, idx[ok], updates[ok])
+    return out
+
+
+def scatter_rows_add_int(operand, idx, updates):
+    """Integer row scatter-add, vectorized: integer addition is associative,
+    so per-row sums in any order (int64, then wrapped) equal the sequential
+    loop bit for bit."""
+    idx = np.asarray(idx, dtype=np.int64)
+    ok = (idx >= 0) & (idx < operand.shape[0])
+    order = np.argsort(idx[ok], kind="stable")
+    si = idx[ok][order]
+    su = updates[ok][order].astype(np.int64)
+    out = operand.astype(np.int64)
+    if si.size:
+        starts = np.flatnonzero(np.r_[True, si[1:] != si[:-1]])
+        sums = np.add.reduceat(su, starts, axis=0)
+        out[si[starts]] += sums
+    return out.astype(operand.dtype)
+
+
+def zipf_indices(n: int, rows: int, seed: int = 0, a: float = 1.1) -> np.ndarray:
+    return ((np.random.default_rng(seed).zipf(a, n) - 1) % rows).astype(np.int32)
+
+
+# --------------------------------------------------------------------- dot
+
+def dot_general_f64(lhs, rhs, lhs_batch=(), rhs_batch=(), lhs_contract=(), rhs_contract=()):
+    """dot_general in float64; output dims (batch..., lhs free..., rhs free...)
+    (reference: api.cc:1562-1577, 3429-3492)."""
+    letters = "abcdefghijklmnopqrstuvwxyz"
+    li = [None] * lhs.ndim
+    ri = [None] * rhs.ndim
+    c = 0
+    for lb, rb in zip(lhs_batch, rhs_batch):
+        li[lb] = ri[rb] = letters[c]
+        c += 1
+    for lc, rc in zip(lhs_contract, rhs_contract):
+        li[lc] = ri[rc] = letters[c]
+        c += 1
+    lf, rf = [], []
+    for d in range(lhs.ndim):
+        if li[d] is None:
+            li[d] = letters[c]
+            lf.append(letters[c])
+            c += 1
+    for d in range(rhs.ndim):
+        if ri[d] is None:
+            ri[d] = letters[c]
+            rf.append(letters[c])
+            c += 1
+    out = "".join(letters[i] for i in range(len(lhs_batch))) + "".join(lf) + "".join(rf)
+    return np.einsum(f"{''.join(li)},{''.join(ri)}->{out}", np.asarray(lhs, np.float64), np.asarray(rhs, np.float64))
+
+
+def attention_bf16(q, k, v, causal=True):
+    """The C3 program's arithmetic for one or more heads (bf16 bits in/out):
+    scores rounded to bf16, masked, softmax in f32, P rounded to bf16,
+    context accumulated in f32 and rounded to bf16."""
+    qf, kf, vf = (bf16_bits_to_f32(t).astype(np.float64) for t in (q, k, v))
+    s = np.einsum("...qd,...kd->...qk", qf, kf)
+    s = bf16_bits_to_f32(f32_to_bf16_bits(s.astype(np.float32))).astype(np.float32)
+    if causal:
+        L = s.shape[-1]
+        mask = np.tril(np.ones((L, L), dtype=bool))
+        s = np.where(mask, s, np.float32(-np.inf))
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m, dtype=np.float32)
+    p = e / e.sum(axis=-1, keepdims=True, dtype=np.float32)
+    p = bf16_bits_to_f32(f32_to_bf16_bits(p.astype(np.float32))).astype(np.float64)
+    ctx = np.einsum("...qk,...kd->...qd", p, vf)
+    return f32_to_bf16_bits(ctx.astype(np.float32))

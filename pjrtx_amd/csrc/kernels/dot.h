@@ -1,0 +1,42 @@
+// Launchers of the dot_general kernels (kernels/dot.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.h"
+
+namespace pjrtx {
+
+// C[b][m][n] = sum_k A[b][m][k] * B[b][k][n]; A K-contiguous (row stride lda);
+// B N-contiguous ([K][N], row stride ldb) or K-contiguous ([N][K]); C row-major
+// with row stride ldc and batch stride M*ldc. Strides in elements.
+struct GemmParams {
+  int batch = 1, M = 0, N = 0, K = 0;
+  int64_t lda = 0, ldb = 0, ldc = 0;
+  int64_t a_batch_stride = 0, b_batch_stride = 0;
+};
+void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const void* B, void* C, bool f16, bool b_kmajor,
+                      int out_bytes);
+
+// Y[m][n] = sum_k X[m][k] * W[.]: M in 1..8; W [K][N] (ldw = row stride) or,
+// when K-major, [N][K]. `partials` holds ksplit*M*N floats.
+struct GemvParams {
+  int M = 1, N = 0, K = 0;
+  int64_t ldx = 0, ldw = 0, ldy = 0;
+  int kchunk = 0, ksplit = 1;
+};
+// out_kind: 0 bf16, 1 f16, 2 f32
+void launch_gemv(hipStream_t s, const GemvParams& p, const void* X, const void* W, void* Y, float* partials, bool f16,
+                 bool w_kmajor, int out_kind);
+
+// Fallback with arbitrary element strides.
+struct FmaGemmParams {
+  int64_t batch = 1, M = 0, N = 0, K = 0;
+  int64_t a_bs = 0, a_ms = 0, a_ks = 0;
+  int64_t b_bs = 0, b_ns = 0, b_ks = 0;
+};
+void launch_fma_gemm(hipStream_t s, const FmaGemmParams& p, const void* A, const void* B, void* C, DType in, DType out);
+
+}  // namespace pjrtx

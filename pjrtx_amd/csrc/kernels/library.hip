@@ -1,0 +1,239 @@
+// Precompiled library kernels: N-d box copy (slices, dynamic slices,
+// dynamic-update-slice, concatenate, pad), fill, and StableHLO gather.
+//
+// Every kernel moves data in "units": whole elements, or 16-byte vectors
+// when the innermost dimension is contiguous and aligned on both sides.
+// One thread handles one unit; consecutive threads touch consecutive units
+// along the innermost dimension, so accesses coalesce.
+//
+// Replaces the reference's slice / gather steps (reference:
+// src/backend/mlx_metal/executable_metal_graph_slice.zig:8-380 incl. the
+// clamped DUS starts at :293-299, executable_metal_graph_gather.zig:13-92
+// with clamped indices at :61-65, executable_metal_graph_structural.zig,
+// executable_metal_graph_generation.zig:8-135 concatenate).
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "common.h"
+#include "kernels/library.h"
+
+namespace pjrtx {
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int B> struct Unit;
+template <> struct Unit<1> { typedef uint8_t T; };
+template <> struct Unit<2> { typedef uint16_t T; };
+template <> struct Unit<4> { typedef uint32_t T; };
+template <> struct Unit<8> { typedef uint64_t T; };
+template <> struct Unit<16> { typedef u32x4 T; };
+
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int bytes, int is_signed) {
+  if (bytes == 8) return reinterpret_cast<const int64_t*>(p)[i];
+  if (bytes == 4) {
+    const uint32_t u = reinterpret_cast<const uint32_t*>(p)[i];
+    return is_signed ? (int64_t)(int32_t)u : (int64_t)u;
+  }
+  if (bytes == 2) {
+    const uint16_t u = reinterpret_cast<const uint16_t*>(p)[i];
+    return is_signed ? (int64_t)(int16_t)u : (int64_t)u;
+  }
+  const uint8_t u = reinterpret_cast<const uint8_t*>(p)[i];
+  return is_signed ? (int64_t)(int8_t)u : (int64_t)u;
+}
+
+__device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// Box copy in units. `p` dims/strides/offsets are in units; dyn starts are in
+// elements of the dynamically indexed tensor and are scaled by `dyn_scale`
+// (element strides in units, per dim).
+struct BoxUnits {
+  BoxCopy b;
+  int64_t total;
+  int64_t dyn_scale[kMaxRank];
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) box_copy_kernel(BoxUnits p, const T* __restrict__ src, T* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.total) return;
+  int64_t rem = i, so = p.b.src_off, d_o = p.b.dst_off;
+  for (int d = p.b.rank - 1; d >= 0; --d) {
+    const int64_t D = p.b.dims[d];
+    const int64_t c = rem % D;
+    rem /= D;
+    so += c * p.b.src_stride[d];
+    d_o += c * p.b.dst_stride[d];
+  }
+  // Dynamic starts: same value for every thread (uniform scalar loads).
+  for (int d = 0; d < p.b.rank; ++d) {
+    if (!p.b.dyn_start[d]) continue;
+    int64_t st = load_index(p.b.dyn_start[d], 0, p.b.dyn_start_bytes, p.b.dyn_start_signed);
+    st = clamp64(st, 0, p.b.dyn_limit[d] - p.b.dims[d]);
+    if (p.b.dyn_on_dst) d_o += st * p.dyn_scale[d];
+    else so += st * p.dyn_scale[d];
+  }
+  dst[d_o] = src[so];
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fill_kernel(T* __restrict__ dst, const T* __restrict__ value, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = value[0];
+}
+
+struct GatherUnits {
+  GatherParams g;
+  int64_t total;          // output units
+  int64_t unit_elems;     // elements per unit along the innermost output dim
+  int vector_inner;       // 1: innermost output dim is a full contiguous operand row
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) gather_kernel(GatherUnits p, const T* __restrict__ operand,
+                                                     const void* __restrict__ indices, T* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.total) return;
+  const GatherParams& g = p.g;
+  int64_t coord[kMaxRank];
+  int64_t rem = i;
+  for (int d = g.out_rank - 1; d >= 0; --d) {
+    const int64_t D = (d == g.out_rank - 1) ? g.out_dims[d] / p.unit_elems : g.out_dims[d];
+    coord[d] = rem % D;
+    rem /= D;
+  }
+  if (g.out_rank > 0) coord[g.out_rank - 1] *= p.unit_elems;
+  // Position of this output's index vector inside start_indices.
+  int64_t idx_base = 0;
+  int64_t batch_coord[kMaxRank];
+  for (int k = 0; k < kMaxRank; ++k) batch_coord[k] = 0;
+  for (int d = 0; d < g.out_rank; ++d) {
+    if (g.out_map[d] >= 0) {
+      idx_base += coord[d] * g.idx_stride[g.out_map[d]];
+      batch_coord[g.out_map[d]] = coord[d];
+    }
+  }
+  int64_t start[kMaxRank];
+  for (int d = 0; d < g.op_rank; ++d) start[d] = 0;
+  for (int k = 0; k < g.n_index; ++k) {
+    const int64_t off = (g.ivd < g.idx_rank) ? (int64_t)k * g.idx_stride[g.ivd] : 0;
+    start[g.start_map[k]] = load_index(indices, idx_base + off, g.idx_bytes, g.idx_signed);
+  }
+  for (int k = 0; k < g.n_batching; ++k) start[g.op_batch_dim[k]] = batch_coord[g.idx_batch_dim[k]];
+  int64_t src = 0;
+  for (int d = 0; d < g.op_rank; ++d) {
+    const int64_t s = clamp64(start[d], 0, g.op_dims[d] - g.slice[d]);
+    src += s * g.op_stride[d];
+  }
+  for (int d = 0; d < g.out_rank; ++d)
+    if (g.out_map[d] < 0) src += coord[d] * g.op_stride[-g.out_map[d] - 1];
+  out[i] = operand[src / p.unit_elems];
+}
+
+int64_t blocks_for(int64_t n) { return (n + 255) / 256; }
+
+void check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(Code::kInternal, strformat("%s launch failed: %s", what, hipGetErrorString(e)));
+}
+
+}  // namespace
+
+void launch_box_copy(hipStream_t s, const BoxCopy& in, const void* src, void* dst, int elem_bytes) {
+  BoxUnits p;
+  p.b = in;
+  int64_t total = 1;
+  for (int d = 0; d < in.rank; ++d) total *= in.dims[d];
+  if (total == 0) return;
+  for (int d = 0; d < in.rank; ++d) p.dyn_scale[d] = in.dyn_on_dst ? in.dst_stride[d] : in.src_stride[d];
+  // 16-byte units when the innermost dim is contiguous on both sides and
+  // every offset / stride stays 16-byte aligned.
+  int unit = elem_bytes;
+  const int r = in.rank;
+  if (r > 0 && in.src_stride[r - 1] == 1 && in.dst_stride[r - 1] == 1 && elem_bytes < 16) {
+    const int64_t per = 16 / elem_bytes;
+    bool ok = in.dims[r - 1] % per == 0 && in.src_off % per == 0 && in.dst_off % per == 0 &&
+              reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+    for (int d = 0; d + 1 < r && ok; ++d) ok = in.src_stride[d] % per == 0 && in.dst_stride[d] % per == 0;
+    if (ok && in.dyn_start[r - 1]) ok = false;
+    if (ok) unit = 16;
+  }
+  if (unit != elem_bytes) {
+    const int64_t per = unit / elem_bytes;
+    p.b.dims[r - 1] /= per;
+    for (int d = 0; d + 1 < r; ++d) {
+      p.b.src_stride[d] /= per;
+      p.b.dst_stride[d] /= per;
+      p.dyn_scale[d] /= per;
+    }
+    p.b.src_off /= per;
+    p.b.dst_off /= per;
+    total /= per;
+  }
+  p.total = total;
+  const dim3 grid(static_cast<unsigned>(blocks_for(total)));
+  switch (unit) {
+    case 1: hipLaunchKernelGGL(box_copy_kernel<uint8_t>, grid, dim3(256), 0, s, p, (const uint8_t*)src, (uint8_t*)dst); break;
+    case 2: hipLaunchKernelGGL(box_copy_kernel<uint16_t>, grid, dim3(256), 0, s, p, (const uint16_t*)src, (uint16_t*)dst); break;
+    case 4: hipLaunchKernelGGL(box_copy_kernel<uint32_t>, grid, dim3(256), 0, s, p, (const uint32_t*)src, (uint32_t*)dst); break;
+    case 8: hipLaunchKernelGGL(box_copy_kernel<uint64_t>, grid, dim3(256), 0, s, p, (const uint64_t*)src, (uint64_t*)dst); break;
+    case 16: hipLaunchKernelGGL(box_copy_kernel<u32x4>, grid, dim3(256), 0, s, p, (const u32x4*)src, (u32x4*)dst); break;
+    default: fail(Code::kInternal, "box copy: bad element size");
+  }
+  check_launch("box_copy");
+}
+
+void launch_fill(hipStream_t s, void* dst, const void* value, int64_t n, int elem_bytes) {
+  if (n == 0) return;
+  const dim3 grid(static_cast<unsigned>(blocks_for(n)));
+  switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(fill_kernel<uint8_t>, grid, dim3(256), 0, s, (uint8_t*)dst, (const uint8_t*)value, n); break;
+    case 2: hipLaunchKernelGGL(fill_kernel<uint16_t>, grid, dim3(256), 0, s, (uint16_t*)dst, (const uint16_t*)value, n); break;
+    case 4: hipLaunchKernelGGL(fill_kernel<uint32_t>, grid, dim3(256), 0, s, (uint32_t*)dst, (const uint32_t*)value, n); break;
+    case 8: hipLaunchKernelGGL(fill_kernel<uint64_t>, grid, dim3(256), 0, s, (uint64_t*)dst, (const uint64_t*)value, n); break;
+    default: fail(Code::kInternal, "fill: bad element size");
+  }
+  check_launch("fill");
+}
+
+void launch_gather(hipStream_t s, const GatherParams& g, const void* operand, const void* indices, void* out,
+                   int elem_bytes) {
+  GatherUnits p;
+  p.g = g;
+  int64_t total = 1;
+  for (int d = 0; d < g.out_rank; ++d) total *= g.out_dims[d];
+  if (total == 0) return;
+  p.unit_elems = 1;
+  p.vector_inner = 0;
+  // Rows of the operand's innermost dim copied whole: 16-byte units.
+  const int r = g.out_rank;
+  if (r > 0 && g.out_map[r - 1] == -(g.op_rank - 1) - 1 && g.op_stride[g.op_rank - 1] == 1 &&
+      g.slice[g.op_rank - 1] == g.op_dims[g.op_rank - 1] && elem_bytes < 16) {
+    const int64_t per = 16 / elem_bytes;
+    bool ok = g.out_dims[r - 1] % per == 0 && reinterpret_cast<uintptr_t>(operand) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    for (int d = 0; d + 1 < g.op_rank && ok; ++d) ok = g.op_stride[d] % per == 0;
+    if (ok) {
+      p.unit_elems = per;
+      p.vector_inner = 1;
+    }
+  }
+  p.total = total / p.unit_elems;
+  const dim3 grid(static_cast<unsigned>(blocks_for(p.total)));
+  if (p.unit_elems > 1) {
+    hipLaunchKernelGGL(gather_kernel<u32x4>, grid, dim3(256), 0, s, p, (const u32x4*)operand, indices, (u32x4*)out);
+  } else {
+    switch (elem_bytes) {
+      case 1: hipLaunchKernelGGL(gather_kernel<uint8_t>, grid, dim3(256), 0, s, p, (const uint8_t*)operand, indices, (uint8_t*)out); break;
+      case 2: hipLaunchKernelGGL(gather_kernel<uint16_t>, grid, dim3(256), 0, s, p, (const uint16_t*)operand, indices, (uint16_t*)out); break;
+      case 4: hipLaunchKernelGGL(gather_kernel<uint32_t>, grid, dim3(256), 0, s, p, (const uint32_t*)operand, indices, (uint32_t*)out); break;
+      case 8: hipLaunchKernelGGL(gather_kernel<uint64_t>, grid, dim3(256), 0, s, p, (const uint64_t*)operand, indices, (uint64_t*)out); break;
+      default: fail(Code::kInternal, "gather: bad element size");
+    }
+  }
+  check_launch("gather");
+}
+
+}  // namespace pjrtx

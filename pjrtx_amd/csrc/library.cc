@@ -1,13 +1,219 @@
-// Dispatch of library steps (materializing ops that are not fusion groups).
+// Dispatch of library steps: StableHLO ops that materialize their result
+// through a precompiled kernel instead of a generated fusion.
+#include "kernels/library.h"
+
+#include <cstring>
+
 #include "runtime.h"
 
 namespace pjrtx {
 
+namespace {
+
+void row_major_strides(const Dims& d, int64_t* out) {
+  int64_t s = 1;
+  for (int i = static_cast<int>(d.size()) - 1; i >= 0; --i) {
+    out[i] = s;
+    s *= d[i];
+  }
+}
+
+void check_rank(const Dims& d, const char* what) {
+  PJRTX_CHECK(d.size() <= static_cast<size_t>(kMaxRank), Code::kUnimplemented,
+              strformat("%s: rank %zu exceeds %d", what, d.size(), kMaxRank));
+}
+
+void* ptr(std::vector<MemRef>& vals, int v) { return vals[v] ? vals[v]->ptr : nullptr; }
+
+void run_dynamic_slice(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
+  const TensorType& x = prog.type(op.operands[0]);
+  const TensorType& out = prog.type(op.results[0]);
+  check_rank(x.dims, "dynamic_slice");
+  BoxCopy b;
+  b.rank = x.rank();
+  row_major_strides(x.dims, b.src_stride);
+  row_major_strides(out.dims, b.dst_stride);
+  for (int d = 0; d < b.rank; ++d) {
+    b.dims[d] = out.dims[d];
+    b.dyn_start[d] = ptr(vals, op.operands[1 + d]);
+    b.dyn_limit[d] = x.dims[d];
+  }
+  const DType it = prog.type(op.operands[1]).dtype;
+  b.dyn_start_bytes = static_cast<int>(dtype_size(it));
+  b.dyn_start_signed = dtype_is_signed_int(it);
+  b.dyn_on_dst = 0;
+  launch_box_copy(dev->stream(), b, ptr(vals, op.operands[0]), ptr(vals, op.results[0]),
+                  static_cast<int>(dtype_size(x.dtype)));
+}
+
+void run_dynamic_update_slice(Device* dev, const Program& prog, const Step& step, const Op& op,
+                              std::vector<MemRef>& vals) {
+  const TensorType& x = prog.type(op.operands[0]);
+  const TensorType& u = prog.type(op.operands[1]);
+  check_rank(x.dims, "dynamic_update_slice");
+  const int esz = static_cast<int>(dtype_size(x.dtype));
+  if (!step.in_place) {
+    // Copy the operand into the fresh output, then write the update.
+    if (x.bytes())
+      hip_check(hipMemcpyAsync(ptr(vals, op.results[0]), ptr(vals, op.operands[0]), x.bytes(), hipMemcpyDeviceToDevice,
+                               dev->stream()),
+                "hipMemcpyAsync(DUS operand)");
+  }
+  BoxCopy b;
+  b.rank = x.rank();
+  row_major_strides(u.dims, b.src_stride);
+  row_major_strides(x.dims, b.dst_stride);
+  for (int d = 0; d < b.rank; ++d) {
+    b.dims[d] = u.dims[d];
+    b.dyn_start[d] = ptr(vals, op.operands[2 + d]);
+    b.dyn_limit[d] = x.dims[d];
+  }
+  const DType it = prog.type(op.operands[2]).dtype;
+  b.dyn_start_bytes = static_cast<int>(dtype_size(it));
+  b.dyn_start_signed = dtype_is_signed_int(it);
+  b.dyn_on_dst = 1;
+  launch_box_copy(dev->stream(), b, ptr(vals, op.operands[1]), ptr(vals, op.results[0]), esz);
+}
+
+void run_concatenate(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
+  const TensorType& out = prog.type(op.results[0]);
+  check_rank(out.dims, "concatenate");
+  int64_t ost[kMaxRank];
+  row_major_strides(out.dims, ost);
+  int64_t offset = 0;
+  for (int src : op.operands) {
+    const TensorType& t = prog.type(src);
+    BoxCopy b;
+    b.rank = t.rank();
+    row_major_strides(t.dims, b.src_stride);
+    for (int d = 0; d < b.rank; ++d) {
+      b.dims[d] = t.dims[d];
+      b.dst_stride[d] = ost[d];
+    }
+    b.dst_off = offset * ost[op.dim];
+    launch_box_copy(dev->stream(), b, ptr(vals, src), ptr(vals, op.results[0]), static_cast<int>(dtype_size(t.dtype)));
+    offset += t.dims[op.dim];
+  }
+}
+
+void run_pad(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
+  const TensorType& x = prog.type(op.operands[0]);
+  const TensorType& out = prog.type(op.results[0]);
+  check_rank(out.dims, "pad");
+  for (size_t d = 0; d < x.dims.size(); ++d)
+    PJRTX_CHECK(op.pad_low[d] >= 0 && op.pad_high[d] >= 0 && op.pad_interior[d] >= 0, Code::kUnimplemented,
+                "pad with negative (cropping) padding is not supported");
+  const int esz = static_cast<int>(dtype_size(x.dtype));
+  launch_fill(dev->stream(), ptr(vals, op.results[0]), ptr(vals, op.operands[1]), out.elements(), esz);
+  int64_t ost[kMaxRank];
+  row_major_strides(out.dims, ost);
+  BoxCopy b;
+  b.rank = x.rank();
+  row_major_strides(x.dims, b.src_stride);
+  for (int d = 0; d < b.rank; ++d) {
+    b.dims[d] = x.dims[d];
+    b.dst_stride[d] = ost[d] * (op.pad_interior[d] + 1);
+    b.dst_off += op.pad_low[d] * ost[d];
+  }
+  launch_box_copy(dev->stream(), b, ptr(vals, op.operands[0]), ptr(vals, op.results[0]), esz);
+}
+
+}  // namespace
+
+// Translates StableHLO gather dimension numbers into the kernel's mapping
+// (semantics: StableHLO spec `gather`; start indices are clamped so the slice
+// stays in bounds, as reference executable_metal_graph_gather.zig:61-65).
+GatherParams make_gather_params(const Program& prog, const Op& op) {
+  const TensorType& x = prog.type(op.operands[0]);
+  const TensorType& idx = prog.type(op.operands[1]);
+  const TensorType& out = prog.type(op.results[0]);
+  check_rank(x.dims, "gather");
+  check_rank(out.dims, "gather");
+  check_rank(idx.dims, "gather");
+  GatherParams g;
+  g.out_rank = out.rank();
+  g.op_rank = x.rank();
+  g.idx_rank = idx.rank();
+  for (int d = 0; d < g.out_rank; ++d) g.out_dims[d] = out.dims[d];
+  for (int d = 0; d < g.op_rank; ++d) {
+    g.op_dims[d] = x.dims[d];
+    g.slice[d] = op.sizes.at(d);
+  }
+  row_major_strides(x.dims, g.op_stride);
+  row_major_strides(idx.dims, g.idx_stride);
+  g.ivd = static_cast<int>(op.index_vector_dim < 0 ? idx.rank() : op.index_vector_dim);
+  g.n_index = static_cast<int>(op.start_index_map.size());
+  PJRTX_CHECK(g.ivd == g.idx_rank || idx.dims[g.ivd] == g.n_index, Code::kInvalidArgument,
+              "gather: index vector length does not match start_index_map");
+  for (int k = 0; k < g.n_index; ++k) g.start_map[k] = static_cast<int>(op.start_index_map[k]);
+  g.n_batching = static_cast<int>(op.operand_batching_dims.size());
+  for (int k = 0; k < g.n_batching; ++k) {
+    g.op_batch_dim[k] = static_cast<int>(op.operand_batching_dims[k]);
+    g.idx_batch_dim[k] = static_cast<int>(op.start_indices_batching_dims[k]);
+  }
+  // Output dims: offset_dims are window dims (operand dims that are neither
+  // collapsed nor batching, in increasing order); the rest are batch dims
+  // (start_indices dims except index_vector_dim, in order).
+  std::vector<int> window_operand_dims;
+  for (int d = 0; d < g.op_rank; ++d) {
+    bool collapsed = false;
+    for (int64_t c : op.collapsed_slice_dims) collapsed |= c == d;
+    for (int64_t c : op.operand_batching_dims) collapsed |= c == d;
+    if (!collapsed) window_operand_dims.push_back(d);
+  }
+  std::vector<int> batch_idx_dims;
+  for (int d = 0; d < g.idx_rank; ++d)
+    if (d != g.ivd) batch_idx_dims.push_back(d);
+  size_t wi = 0, bi = 0;
+  for (int d = 0; d < g.out_rank; ++d) {
+    bool is_offset = false;
+    for (int64_t o : op.offset_dims) is_offset |= o == d;
+    if (is_offset) {
+      PJRTX_CHECK(wi < window_operand_dims.size(), Code::kInvalidArgument, "gather: too many offset dims");
+      g.out_map[d] = -window_operand_dims[wi++] - 1;
+    } else {
+      PJRTX_CHECK(bi < batch_idx_dims.size(), Code::kInvalidArgument, "gather: too many batch dims");
+      g.out_map[d] = batch_idx_dims[bi++];
+    }
+  }
+  g.idx_bytes = static_cast<int>(dtype_size(idx.dtype));
+  g.idx_signed = dtype_is_signed_int(idx.dtype);
+  return g;
+}
+
+void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
+void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
+
 void run_library_step(Device* dev, const Program& prog, const Step& step, std::vector<MemRef>& vals) {
-  (void)dev;
-  (void)prog;
-  (void)vals;
-  fail(Code::kUnimplemented, std::string("library op not available in this build: ") + lib_kind_name(step.lib));
+  const Op& op = prog.ops.at(step.lib_op);
+  switch (step.lib) {
+    case LibKind::kDynamicSlice:
+      run_dynamic_slice(dev, prog, op, vals);
+      return;
+    case LibKind::kDynamicUpdateSlice:
+      run_dynamic_update_slice(dev, prog, step, op, vals);
+      return;
+    case LibKind::kConcatenate:
+      run_concatenate(dev, prog, op, vals);
+      return;
+    case LibKind::kPad:
+      run_pad(dev, prog, op, vals);
+      return;
+    case LibKind::kGather: {
+      GatherParams g = make_gather_params(prog, op);
+      launch_gather(dev->stream(), g, ptr(vals, op.operands[0]), ptr(vals, op.operands[1]), ptr(vals, op.results[0]),
+                    static_cast<int>(dtype_size(prog.type(op.operands[0]).dtype)));
+      return;
+    }
+    case LibKind::kDot:
+      run_dot_general(dev, prog, op, vals);
+      return;
+    case LibKind::kScatter:
+      run_scatter(dev, prog, op, vals);
+      return;
+    default:
+      fail(Code::kUnimplemented, std::string("library op not available: ") + lib_kind_name(step.lib));
+  }
 }
 
 }  // namespace pjrtx

@@ -209,6 +209,12 @@ void Planner::decide_materialization() {
     const size_t nusers = users_[v].size();
     if (nusers > 1 && cost[v] > opts_.recompute_limit) mat_.insert(v);
   }
+  // A splat constant that needs a buffer (library operand, program output,
+  // non-literal reduce init) is uploaded once at load, like any constant.
+  for (const Op& op : prog_.ops) {
+    if (op.kind == OpKind::kConstant && is_splat_constant(prog_, op) && mat_.count(op.results[0]))
+      plan_.constants.push_back(op.results[0]);
+  }
 }
 
 void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops,
@@ -236,7 +242,7 @@ void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops,
 void Planner::build_steps(std::vector<Step>* steps) {
   for (size_t i = 0; i < prog_.ops.size(); ++i) {
     const Op& op = prog_.ops[i];
-    if (op.kind == OpKind::kReturn || op.kind == OpKind::kConstant && !is_splat_constant(prog_, op)) continue;
+    if (op.kind == OpKind::kReturn || op.kind == OpKind::kConstant) continue;  // constants: literals or resident
     if (op.kind == OpKind::kReduce) {
       Step s;
       s.kind = StepKind::kReduce;
@@ -273,7 +279,13 @@ void Planner::build_steps(std::vector<Step>* steps) {
     if (op.results.empty() || !mat_.count(op.results[0])) continue;
     const int v = op.results[0];
     Step s;
-    if (op.kind == OpKind::kReshape && mat_.count(op.operands[0])) {
+    // A broadcast that only inserts unit dims (dims increasing) keeps the
+    // row-major order: it is a reshape.
+    bool unit_broadcast = false;
+    if (op.kind == OpKind::kBroadcastInDim && prog_.type(v).elements() == prog_.type(op.operands[0]).elements()) {
+      unit_broadcast = std::is_sorted(op.dims.begin(), op.dims.end());
+    }
+    if ((op.kind == OpKind::kReshape || unit_broadcast) && mat_.count(op.operands[0])) {
       s.kind = StepKind::kAlias;
       s.inputs = op.operands;
       s.outputs = {v};
@@ -460,6 +472,24 @@ void Planner::liveness() {
     if (persistent.count(v) || outputs_.count(v)) continue;
     plan_.steps[i].release_after.push_back(v);
   }
+  // In-place dynamic_update_slice (reference: executable_metal_graph_slice.zig:
+  // 129-144): allowed when the operand is an intermediate produced by a
+  // kernel (not a view alias of another live buffer) whose last reader is
+  // this step.
+  std::set<int> aliased;
+  std::map<int, StepKind> producer_kind;
+  for (const Step& s : plan_.steps) {
+    if (s.kind == StepKind::kAlias) aliased.insert(s.inputs[0]);
+    for (int v : s.outputs) producer_kind[v] = s.kind;
+  }
+  for (size_t i = 0; i < plan_.steps.size(); ++i) {
+    Step& s = plan_.steps[i];
+    if (s.kind != StepKind::kLibrary || s.lib != LibKind::kDynamicUpdateSlice) continue;
+    const int v0 = prog_.ops[s.lib_op].operands[0];
+    const bool intermediate = !persistent.count(v0) && !outputs_.count(v0) && !aliased.count(v0) &&
+                              producer_kind.count(v0) && producer_kind[v0] != StepKind::kAlias;
+    if (intermediate && last_use[v0] == static_cast<int>(i)) s.in_place = true;
+  }
 }
 
 void Planner::shape_loop(Step* s) {
@@ -582,7 +612,8 @@ std::string Plan::describe(const Program& prog) const {
       o << "],\"row_schedule\":" << (s.row_schedule ? "true" : "false") << ",\"rows\":" << s.rows
         << ",\"row_len\":" << s.row_len << ",\"splits\":" << s.splits << ",\"chunk\":" << s.chunk;
     }
-    if (s.kind == StepKind::kLibrary) o << ",\"library\":\"" << lib_kind_name(s.lib) << "\"";
+    if (s.kind == StepKind::kLibrary)
+      o << ",\"library\":\"" << lib_kind_name(s.lib) << "\",\"in_place\":" << (s.in_place ? "true" : "false");
     o << ",\"vec\":" << s.vec << ",\"grid\":" << s.grid << ",\"block\":" << s.block;
     o << ",\"release_after\":" << list(s.release_after) << "}";
   }

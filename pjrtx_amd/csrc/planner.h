@@ -74,6 +74,9 @@ struct Step {
   // kLibrary / kAlias
   LibKind lib = LibKind::kCopy;
   int lib_op = -1;
+  // dynamic_update_slice whose operand dies here: the update is written into
+  // the operand's buffer, which becomes the result (no copy).
+  bool in_place = false;
 
   // launch geometry of generated kernels
   uint32_t grid = 1;

@@ -398,7 +398,12 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
       src = full.data();
     }
     MemRef m = dev->allocate(t.bytes());
-    if (t.bytes()) hip_check(hipMemcpy(m->ptr, src, t.bytes(), hipMemcpyHostToDevice), "hipMemcpy(constant)");
+    // Stream-ordered upload: the block may have been freed by work still
+    // queued on this stream.
+    if (t.bytes()) {
+      hip_check(hipMemcpyAsync(m->ptr, src, t.bytes(), hipMemcpyHostToDevice, dev->stream()), "hipMemcpyAsync(constant)");
+      hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    }
     L->constants[v] = m;
   }
   hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
@@ -415,7 +420,11 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals) {
       vals[s.outputs[0]] = vals[s.inputs[0]];
       return;
     case StepKind::kLibrary:
-      for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
+      if (s.in_place) {
+        vals[s.outputs[0]] = vals[prog_.ops[s.lib_op].operands[0]];
+      } else {
+        for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
+      }
       run_library_step(dev, prog_, s, vals);
       stats_.library_calls++;
       return;

@@ -234,6 +234,89 @@ class Builder:
         return self._emit(f"stablehlo.concatenate {names}, dim = {dim} : ({types}) -> "
                           f"{tensor_type(shape, xs[0].dtype)}", shape, xs[0].dtype)
 
+    # ------------------------------------------- materializing structural ops
+    def dynamic_slice(self, x: T, starts: list[T], sizes) -> T:
+        names = ", ".join([x.name] + [s.name for s in starts])
+        types = ", ".join([x.type] + [s.type for s in starts])
+        sz = ", ".join(str(v) for v in sizes)
+        return self._emit(f"stablehlo.dynamic_slice {names}, sizes = [{sz}] : ({types}) -> "
+                          f"{tensor_type(sizes, x.dtype)}", sizes, x.dtype)
+
+    def dynamic_update_slice(self, x: T, update: T, starts: list[T]) -> T:
+        names = ", ".join([x.name, update.name] + [s.name for s in starts])
+        types = ", ".join([x.type, update.type] + [s.type for s in starts])
+        return self._emit(f"stablehlo.dynamic_update_slice {names} : ({types}) -> {x.type}", x.shape, x.dtype)
+
+    def pad(self, x: T, value: T, low, high, interior) -> T:
+        shape = tuple(lo + hi + d + max(d - 1, 0) * it for d, lo, hi, it in zip(x.shape, low, high, interior))
+        f = lambda v: ", ".join(str(a) for a in v)  # noqa: E731
+        return self._emit(f"stablehlo.pad {x.name}, {value.name}, low = [{f(low)}], high = [{f(high)}], interior = "
+                          f"[{f(interior)}] : ({x.type}, {value.type}) -> {tensor_type(shape, x.dtype)}", shape, x.dtype)
+
+    def dot_general(self, a: T, b: T, batch=((), ()), contract=((), ()), out_dtype: str | None = None) -> T:
+        lb, rb = list(batch[0]), list(batch[1])
+        lc, rc = list(contract[0]), list(contract[1])
+        shape = [a.shape[d] for d in lb]
+        shape += [a.shape[d] for d in range(a.rank) if d not in lb and d not in lc]
+        shape += [b.shape[d] for d in range(b.rank) if d not in rb and d not in rc]
+        f = lambda v: ", ".join(str(x) for x in v)  # noqa: E731
+        bd = f"batching_dims = [{f(lb)}] x [{f(rb)}], " if lb else ""
+        dt = out_dtype or a.dtype
+        return self._emit(f"stablehlo.dot_general {a.name}, {b.name}, {bd}contracting_dims = [{f(lc)}] x [{f(rc)}], "
+                          f"precision = [DEFAULT, DEFAULT] : ({a.type}, {b.type}) -> {tensor_type(shape, dt)}",
+                          shape, dt)
+
+    def gather(self, x: T, idx: T, offset_dims, collapsed_slice_dims, start_index_map, index_vector_dim, slice_sizes,
+               operand_batching_dims=(), start_indices_batching_dims=()) -> T:
+        f = lambda v: ", ".join(str(a) for a in v)  # noqa: E731
+        batch_idx = [d for d in range(idx.rank) if d != index_vector_dim]
+        out_rank = len(batch_idx) + len(offset_dims)
+        window = [d for d in range(x.rank) if d not in collapsed_slice_dims and d not in operand_batching_dims]
+        shape, bi, wi = [], 0, 0
+        for o in range(out_rank):
+            if o in offset_dims:
+                shape.append(slice_sizes[window[wi]])
+                wi += 1
+            else:
+                shape.append(idx.shape[batch_idx[bi]])
+                bi += 1
+        extra = ""
+        if operand_batching_dims:
+            extra = (f", operand_batching_dims = [{f(operand_batching_dims)}], start_indices_batching_dims = "
+                     f"[{f(start_indices_batching_dims)}]")
+        dn = (f"#stablehlo.gather<offset_dims = [{f(offset_dims)}], collapsed_slice_dims = [{f(collapsed_slice_dims)}]"
+              f"{extra}, start_index_map = [{f(start_index_map)}], index_vector_dim = {index_vector_dim}>")
+        return self._emit(f"\"stablehlo.gather\"({x.name}, {idx.name}) <{{dimension_numbers = {dn}, "
+                          f"indices_are_sorted = false, slice_sizes = array<i64: {f(slice_sizes)}>}}> : "
+                          f"({x.type}, {idx.type}) -> {tensor_type(shape, x.dtype)}", shape, x.dtype)
+
+    def scatter(self, x: T, idx: T, upd: T, update_window_dims, inserted_window_dims, scatter_dims_to_operand_dims,
+                index_vector_dim, combiner: str = "add", input_batching_dims=(), scatter_indices_batching_dims=()) -> T:
+        f = lambda v: ", ".join(str(a) for a in v)  # noqa: E731
+        extra = ""
+        if input_batching_dims:
+            extra = (f", input_batching_dims = [{f(input_batching_dims)}], scatter_indices_batching_dims = "
+                     f"[{f(scatter_indices_batching_dims)}]")
+        dn = (f"#stablehlo.scatter<update_window_dims = [{f(update_window_dims)}], inserted_window_dims = "
+              f"[{f(inserted_window_dims)}]{extra}, scatter_dims_to_operand_dims = [{f(scatter_dims_to_operand_dims)}], "
+              f"index_vector_dim = {index_vector_dim}>")
+        name = self._fresh()
+        st = tensor_type((), x.dtype)
+        b = name[1:]
+        if combiner == "set":
+            body = [f"      stablehlo.return %s{b}_u : {st}"]
+        else:
+            body = [f"      %s{b}_r = stablehlo.{combiner} %s{b}_a, %s{b}_u : {st}",
+                    f"      stablehlo.return %s{b}_r : {st}"]
+        self.lines.extend([
+            f"    {name} = \"stablehlo.scatter\"({x.name}, {idx.name}, {upd.name}) <{{indices_are_sorted = false, "
+            f"scatter_dimension_numbers = {dn}, unique_indices = false}}> ({{",
+            f"    ^bb0(%s{b}_a: {st}, %s{b}_u: {st}):",
+            *body,
+            f"    }}) : ({x.type}, {idx.type}, {upd.type}) -> {x.type}",
+        ])
+        return T(name, x.shape, x.dtype)
+
     # -------------------------------------------------------- reductions
     def reduce(self, x: T, init: T, dims, op: str) -> T:
         """Single-operand reduce in the `applies` form (op: add/maximum/minimum/...)."""

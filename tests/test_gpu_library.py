@@ -1,0 +1,305 @@
+"""GPU parity of the library steps (gather, scatter, dot_general, dynamic
+slices, concatenate, pad) through the PJRT C API, against the numpy oracle
+and the reference's known answers.
+
+Tolerances: gather / slices / integer scatter bit-exact; f32 scatter-add
+bit-exact against the in-order oracle (same f32 additions in the same order);
+bf16 dot_general 2e-2 relative to the output scale (|ref| or the RMS of the
+row, whichever is larger: bf16 outputs near zero have no relative precision).
+"""
+import json
+import pathlib
+
+import numpy as np
+import pytest
+
+from oracle import ops
+from pjrtx_amd import programs
+from pjrtx_amd.hlo import Builder
+
+pytestmark = pytest.mark.gpu
+KATS = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+bf = ops.f32_to_bf16_bits
+fb = ops.bf16_bits_to_f32
+
+
+def run(client, text, *args, dtypes=None):
+    return client.compile(text)(*args, dtypes=dtypes)
+
+
+def assert_bf16_close(got_bits, want, rtol=2e-2):
+    got = fb(got_bits).astype(np.float64)
+    want = np.asarray(want, np.float64)
+    scale = np.sqrt(np.mean(want ** 2, axis=-1, keepdims=True)) + 1e-30
+    err = np.abs(got - want) / np.maximum(np.abs(want), scale)
+    assert err.max() <= rtol, f"max scaled error {err.max():.3g}"
+
+
+# ------------------------------------------------------------------ gather
+
+def test_gather_kats(client):
+    k = KATS["gather_axis0"]
+    b = Builder()
+    x = b.param((3, 2), "f32")
+    i = b.param((2, 1), "s32")
+    t = b.build([b.gather(x, i, [1], [0], [0], 1, [1, 2])])
+    (out,) = run(client, t, np.array(k["operand"], np.float32), np.array(k["indices"], np.int32)[:, None])
+    np.testing.assert_array_equal(out, k["expected"])
+    k = KATS["gather_axis1"]
+    b = Builder()
+    x = b.param((3, 2), "f32")
+    i = b.param((2, 1), "s32")
+    t = b.build([b.gather(x, i, [0], [1], [1], 1, [3, 1])])
+    (out,) = run(client, t, np.array(k["operand"], np.float32), np.array(k["indices"], np.int32)[:, None])
+    np.testing.assert_array_equal(out, k["expected"])
+    k = KATS["gather_point"]
+    b = Builder()
+    x = b.param((3, 2), "f32")
+    i = b.param((2, 2), "s32")
+    t = b.build([b.gather(x, i, [], [0, 1], [0, 1], 1, [1, 1])])
+    (out,) = run(client, t, np.array(k["operand"], np.float32), np.array(k["indices"], np.int32))
+    np.testing.assert_array_equal(out, k["expected"])
+
+
+def test_batched_gather(client):
+    x = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    idx = np.array([[2, 0], [1, 2]], np.int32)[..., None]
+    b = Builder()
+    xp = b.param((2, 3, 4), "f32")
+    ip = b.param((2, 2, 1), "s32")
+    t = b.build([b.gather(xp, ip, [2], [1], [1], 2, [1, 1, 4], operand_batching_dims=[0],
+                          start_indices_batching_dims=[0])])
+    (out,) = run(client, t, x, idx)
+    np.testing.assert_array_equal(out, ops.gather_stablehlo(x, idx, [2], [1], [1], 2, [1, 1, 4], [0], [0]))
+
+
+@pytest.mark.parametrize("vocab,dim,batch,seq", [(100, 64, 2, 7), (1000, 4096, 2, 64), (128256, 4096, 8, 2048)])
+def test_embedding_gather(client, vocab, dim, batch, seq):
+    rng = np.random.default_rng(vocab)
+    table = bf((0.02 * rng.standard_normal((vocab, dim))).astype(np.float32))
+    idx = rng.integers(0, vocab, (batch, seq)).astype(np.int32)
+    idx.flat[0] = -1  # wrapped to the last row, as jnp indexing does
+    idx.flat[-1] = vocab - 1
+    (out,) = run(client, programs.c4_embedding_gather(vocab, dim, batch, seq), table, idx, dtypes=["bf16", None])
+    np.testing.assert_array_equal(out, ops.gather_rows(table, idx))
+
+
+# ----------------------------------------------------------------- scatter
+
+@pytest.mark.parametrize("mode", ["set", "add"])
+def test_scatter_kats(client, mode):
+    combiner = "set" if mode == "set" else "add"
+    k = KATS["scatter_1d"]
+    b = Builder()
+    x, i, u = b.param((4,), "f32"), b.param((2, 1), "s32"), b.param((2,), "f32")
+    t = b.build([b.scatter(x, i, u, [], [0], [0], 1, combiner)])
+    (out,) = run(client, t, np.array(k["operand"], np.float32), np.array(k["indices"], np.int32)[:, None],
+                 np.array(k["updates"], np.float32))
+    np.testing.assert_array_equal(out, k[mode])
+    k = KATS["scatter_point"]
+    b = Builder()
+    x, i, u = b.param((3, 2), "f32"), b.param((2, 2), "s32"), b.param((2,), "f32")
+    t = b.build([b.scatter(x, i, u, [], [0, 1], [0, 1], 1, combiner)])
+    (out,) = run(client, t, np.array(k["operand"], np.float32), np.array(k["indices"], np.int32),
+                 np.array(k["updates"], np.float32))
+    np.testing.assert_array_equal(out, k[mode])
+    k = KATS["scatter_window"]
+    b = Builder()
+    x, i, u = b.param((3, 4), "f32"), b.param((2, 1), "s32"), b.param((2, 2), "f32")
+    t = b.build([b.scatter(x, i, u, [1], [0], [0], 1, combiner)])
+    (out,) = run(client, t, np.array(k["operand"], np.float32), np.array(k["indices"], np.int32)[:, None],
+                 np.array(k["updates"], np.float32))
+    np.testing.assert_array_equal(out, k[mode])
+
+
+def test_scatter_batched_kat(client):
+    k = KATS["scatter_batched"]
+    b = Builder()
+    x, i, u = b.param((2, 3, 4), "f32"), b.param((2, 2, 1), "s32"), b.param((2, 2, 4), "f32")
+    t = b.build([b.scatter(x, i, u, [2], [1], [1], 2, "set", input_batching_dims=[0],
+                           scatter_indices_batching_dims=[0])])
+    (out,) = run(client, t, np.array(k["operand"], np.float32).reshape(2, 3, 4), np.array(k["indices"], np.int32),
+                 np.array(k["updates"], np.float32).reshape(2, 2, 4))
+    np.testing.assert_array_equal(out.reshape(-1), k["set"])
+
+
+@pytest.mark.parametrize("rows,dim,n", [(16, 8, 100), (4096, 256, 65536)])
+def test_scatter_add_f32_in_update_order(client, rows, dim, n):
+    rng = np.random.default_rng(rows)
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    idx = ops.zipf_indices(n, rows, seed=rows)
+    idx[:3] = [-1, rows, rows + 5]  # out of bounds: skipped
+    upd = rng.standard_normal((n, dim)).astype(np.float32)
+    (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "f32"), x, idx, upd)
+    np.testing.assert_array_equal(out, ops.scatter_rows_add(x, idx, upd))
+
+
+def test_scatter_add_full_size_zipf(client):
+    """C4b / C4c at the BASELINE size: [65536,256] operand, 1,048,576 Zipf(1.1)
+    updates. int32 bit-exact on the whole output; f32 bit-exact on a column
+    subset (columns are independent) plus a column-sum property overall."""
+    rows, dim, n = 65536, 256, 1048576
+    rng = np.random.default_rng(4)
+    idx = ops.zipf_indices(n, rows, seed=4)
+    xi = rng.integers(-1000, 1000, (rows, dim)).astype(np.int32)
+    ui = rng.integers(-1000, 1000, (n, dim)).astype(np.int32)
+    (out_i,) = run(client, programs.c4_scatter_add(rows, dim, n, "s32"), xi, idx, ui)
+    np.testing.assert_array_equal(out_i, ops.scatter_rows_add_int(xi, idx, ui))
+    xf = np.zeros((rows, dim), np.float32)
+    uf = rng.standard_normal((n, dim), dtype=np.float32)
+    (out_f,) = run(client, programs.c4_scatter_add(rows, dim, n, "f32"), xf, idx, uf)
+    cols = [0, 1, 127, 255]
+    want = ops.scatter_rows_add(xf[:, cols], idx, uf[:, cols])
+    np.testing.assert_array_equal(out_f[:, cols], want)
+    np.testing.assert_allclose(out_f.astype(np.float64).sum(axis=0), uf.astype(np.float64).sum(axis=0),
+                               rtol=1e-4, atol=1e-2)
+
+
+def test_scatter_set_last_update_wins(client):
+    rows, dim, n = 64, 16, 4096
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    idx = rng.integers(0, rows, n).astype(np.int32)
+    upd = rng.standard_normal((n, dim)).astype(np.float32)
+    (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "f32", combiner="set"), x, idx, upd)
+    want = x.copy()
+    for j in range(n):
+        want[idx[j]] = upd[j]
+    np.testing.assert_array_equal(out, want)
+
+
+# ------------------------------------------------------------- dot_general
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_dot_kat(client, dtype):
+    k = KATS["dot_2x2"]
+    b = Builder()
+    x, y = b.param((2, 2), dtype), b.param((2, 2), dtype)
+    t = b.build([b.dot_general(x, y, contract=((1,), (0,)))])
+    lhs, rhs = np.array(k["lhs"], np.float32), np.array(k["rhs"], np.float32)
+    if dtype == "bf16":
+        out = run(client, t, bf(lhs), bf(rhs), dtypes=["bf16", "bf16"])[0]
+        out = fb(out)
+    else:
+        npd = np.float16 if dtype == "f16" else np.float32
+        out = run(client, t, lhs.astype(npd), rhs.astype(npd))[0]
+    np.testing.assert_array_equal(out.astype(np.float32), k["expected"])
+
+
+@pytest.mark.parametrize("shape", [
+    ("mk,kn", (64, 128), (128, 96)),            # NN, ragged N
+    ("mk,nk", (200, 64), (136, 64)),            # NT (rhs contract last)
+    ("bmk,bkn", (3, 130, 72), (3, 72, 40)),     # batched NN, ragged everything
+    ("bmk,bnk", (4, 256, 128), (4, 256, 128)),  # batched NT (attention scores)
+    ("mk,kn", (1, 2048), (2048, 2048)),         # GEMV (decode)
+    ("mk,kn", (4, 512), (512, 1000)),           # GEMV M=4
+    ("mk,nk", (1, 512), (300, 512)),            # GEMV K-major
+])
+def test_dot_bf16_random(client, shape):
+    spec, sa, sb = shape
+    rng = np.random.default_rng(sum(sa) + sum(sb))
+    a = bf(rng.standard_normal(sa).astype(np.float32))
+    b_ = bf(rng.standard_normal(sb).astype(np.float32))
+    lhs_s, rhs_s = spec.split(",")
+    lb = tuple(i for i, c in enumerate(lhs_s) if c == "b")
+    rb = tuple(i for i, c in enumerate(rhs_s) if c == "b")
+    lc = (lhs_s.index("k"),)
+    rc = (rhs_s.index("k"),)
+    bld = Builder()
+    x, y = bld.param(sa, "bf16"), bld.param(sb, "bf16")
+    t = bld.build([bld.dot_general(x, y, batch=(lb, rb), contract=(lc, rc))])
+    (out,) = run(client, t, a, b_, dtypes=["bf16", "bf16"])
+    want = ops.dot_general_f64(fb(a), fb(b_), lb, rb, lc, rc)
+    assert out.shape == want.shape
+    assert_bf16_close(out, want)
+
+
+def test_dot_f32_fallback_and_rank3_rank2(client):
+    # jax_op_suite attention_scores_rhs_contract_last / attention_values_rhs_second_last
+    q = ((np.arange(2 * 3 * 4 * 5, dtype=np.float32).reshape(2, 3, 4, 5) - 11) / 7)
+    kc = ((np.arange(2 * 6 * 5, dtype=np.float32).reshape(2, 6, 5) - 9) / 11)
+    b = Builder()
+    x, y = b.param(q.shape, "f32"), b.param(kc.shape, "f32")
+    t = b.build([b.dot_general(x, y, batch=((0,), (0,)), contract=((3,), (2,)))])
+    (out,) = run(client, t, q, kc)
+    np.testing.assert_allclose(out, ops.dot_general_f64(q, kc, (0,), (0,), (3,), (2,)), rtol=1e-5, atol=1e-6)
+
+
+def test_matmul_8192_sampled_rows(client):
+    """C3d at full size; rows sampled for the float64 reference."""
+    n = 8192
+    rng = np.random.default_rng(8)
+    a = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
+    b_ = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
+    (out,) = run(client, programs.c3_matmul(n, n, n), a, b_, dtypes=["bf16", "bf16"])
+    rows = np.array([0, 1, 127, 128, 4095, 8191])
+    want = fb(a[rows]).astype(np.float64) @ fb(b_).astype(np.float64)
+    assert_bf16_close(out[rows], want)
+
+
+@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 64), (2, 2, 512, 128)])
+def test_attention_small(client, b, h, s, d):
+    rng = np.random.default_rng(s)
+    q, k, v = (bf((rng.standard_normal((b, h, s, d)) / np.sqrt(d)).astype(np.float32)) for _ in range(3))
+    (out,) = run(client, programs.c3_attention(b, h, s, d), q, k, v, dtypes=["bf16"] * 3)
+    want = fb(ops.attention_bf16(q, k, v, causal=True))
+    assert_bf16_close(out, want)
+
+
+# ---------------------------------------------- dynamic slices, concat, pad
+
+def test_dynamic_slice_and_update_clamped(client):
+    x = np.arange(3 * 4, dtype=np.float32).reshape(3, 4)
+    b = Builder()
+    xp = b.param((3, 4), "f32")
+    i0, i1 = b.param((), "s32"), b.param((), "s32")
+    up = b.param((2, 2), "f32")
+    ds = b.dynamic_slice(xp, [i0, i1], [2, 2])
+    dus = b.dynamic_update_slice(xp, up, [i0, i1])
+    exe = client.compile(b.build([ds, dus]))
+    u = np.array([[100, 101], [102, 103]], np.float32)
+    for s0, s1 in [(0, 0), (1, 2), (5, -3), (-1, 3)]:
+        got_ds, got_dus = exe(x, np.array(s0, np.int32), np.array(s1, np.int32), u)
+        c0, c1 = min(max(s0, 0), 1), min(max(s1, 0), 2)  # StableHLO clamps starts
+        np.testing.assert_array_equal(got_ds, x[c0:c0 + 2, c1:c1 + 2])
+        want = x.copy()
+        want[c0:c0 + 2, c1:c1 + 2] = u
+        np.testing.assert_array_equal(got_dus, want)
+
+
+def test_kv_cache_update_in_place_chain(client):
+    # cache' = DUS(DUS(cache + 0, k0, p), k1, p+1): the second update writes in place.
+    L, H, D = 16, 2, 8
+    b = Builder()
+    cache = b.param((1, L, H, D), "bf16")
+    k0 = b.param((1, 1, H, D), "bf16")
+    pos = b.param((), "s32")
+    z = b.constant(0, "s32")
+    c1 = b.dynamic_update_slice(b.add(cache, b.scalar_like(0.0, cache)), k0, [z, pos, z, z])
+    p1 = b.add(pos, b.constant(1, "s32"))
+    c2 = b.dynamic_update_slice(c1, k0, [z, p1, z, z])
+    exe = client.compile(b.build([c2]))
+    plan = json.loads(exe.optimized_program())
+    assert any(s.get("in_place") for s in plan["steps"]), plan
+    rng = np.random.default_rng(0)
+    cv = bf(rng.standard_normal((1, L, H, D)).astype(np.float32))
+    kv = bf(rng.standard_normal((1, 1, H, D)).astype(np.float32))
+    (out,) = exe(cv, kv, np.array(5, np.int32), dtypes=["bf16", "bf16", None])
+    want = cv.copy()
+    want[:, 5] = kv[:, 0]
+    want[:, 6] = kv[:, 0]
+    np.testing.assert_array_equal(out, want)
+
+
+def test_concatenate_and_pad(client):
+    a = np.arange(6, dtype=np.float32).reshape(2, 3)
+    c = np.arange(8, dtype=np.float32).reshape(2, 4) + 100
+    b = Builder()
+    ap, cp = b.param((2, 3), "f32"), b.param((2, 4), "f32")
+    cat = b.concatenate([ap, cp], 1)
+    pad = b.pad(ap, b.constant(-1.0, "f32"), [1, 0], [0, 2], [1, 1])
+    got_cat, got_pad = run(client, b.build([cat, pad]), a, c)
+    np.testing.assert_array_equal(got_cat, np.concatenate([a, c], axis=1))
+    want = np.full((4, 7), -1.0, np.float32)
+    want[1::2, 0:5:2] = a
+    np.testing.assert_array_equal(got_pad, want)
