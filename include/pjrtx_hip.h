@@ -72,16 +72,18 @@ PJRTX_HIP_API int pjrtx_kernel_source(const char* text, size_t len, char* out, s
 struct PJRT_LoadedExecutable;
 struct PJRT_Buffer;
 
-/* Replays each step of a compiled executable `iters` times between two
- * hipEvents on the device stream and writes the mean milliseconds per
- * launch of each step to ms[0..steps). Used by the benchmark's roofline
- * figure. Replaces PJRTX_METALCPP_EXECUTABLE_STEP_PROFILE
- * (metalcpp_api.cc:399-416). */
+/* Replays each launch unit of a compiled executable `iters` times between
+ * two hipEvents on the device stream and writes the mean milliseconds per
+ * launch to ms[0..steps). A launch unit is one step, except that a split
+ * reduction is two units (its main kernel, then its combine kernel). Used by
+ * the benchmark's roofline figure. Replaces
+ * PJRTX_METALCPP_EXECUTABLE_STEP_PROFILE (metalcpp_api.cc:399-416). */
 PJRTX_HIP_API int pjrtx_executable_time_steps(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
                                 size_t num_args, int iters, double* ms, size_t cap, size_t* steps);
 
-/* Kernel names of the executable's steps, '\n'-separated ("-" for steps
- * that are not generated kernels). */
+/* Names of the executable's launch units, in the order of
+ * pjrtx_executable_time_steps, '\n'-separated: the kernel name, or
+ * "lib:<kind>" for a library step, "-" for a view that launches nothing. */
 PJRTX_HIP_API int pjrtx_executable_step_names(struct PJRT_LoadedExecutable* exe, char* out, size_t cap, size_t* needed);
 
 /* Counters of the executable: executions, kernel launches, library calls,

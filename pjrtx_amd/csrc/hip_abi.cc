@@ -157,11 +157,7 @@ int pjrtx_executable_time_steps(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* 
 int pjrtx_executable_step_names(PJRT_LoadedExecutable* exe, char* out, size_t cap, size_t* needed) {
   return guarded([&] {
     std::string s;
-    for (const Step& st : exe->exe->plan().steps) {
-      std::string n = st.name;
-      if (n.empty()) n = st.kind == StepKind::kLibrary ? std::string("lib:") + lib_kind_name(st.lib) : "-";
-      s += n + "\n";
-    }
+    for (const std::string& n : exe->exe->unit_names()) s += n + "\n";
     copy_out(s, out, cap, needed);
   });
 }

@@ -412,7 +412,7 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
   return raw;
 }
 
-void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals) {
+void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int phase) {
   const Step& s = plan_.steps[si];
   Device* dev = L->dev;
   switch (s.kind) {
@@ -430,7 +430,8 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals) {
       return;
     case StepKind::kLoop:
     case StepKind::kReduce: {
-      for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
+      if (phase != 1)
+        for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
       if (s.kind == StepKind::kLoop && num_elements(s.loop_shape) == 0) return;
       if (s.kind == StepKind::kReduce && s.rows == 0) return;
       std::vector<void*> ptrs;
@@ -440,10 +441,13 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals) {
       if (s.combine_grid) ptrs.push_back(L->scratch[si]->ptr);
       std::vector<void*> args(ptrs.size());
       for (size_t k = 0; k < ptrs.size(); ++k) args[k] = &ptrs[k];
-      hip_check(hipModuleLaunchKernel(L->funcs[si], s.grid, 1, 1, s.block, 1, 1, 0, dev->stream(), args.data(), nullptr),
-                "hipModuleLaunchKernel");
-      stats_.kernel_launches++;
-      if (s.combine_grid) {
+      if (phase != 1) {
+        hip_check(hipModuleLaunchKernel(L->funcs[si], s.grid, 1, 1, s.block, 1, 1, 0, dev->stream(), args.data(),
+                                        nullptr),
+                  "hipModuleLaunchKernel");
+        stats_.kernel_launches++;
+      }
+      if (s.combine_grid && phase != 0) {
         // Second pass of a split reduction: same arguments, one wave per row.
         hip_check(hipModuleLaunchKernel(L->combine_funcs[si], s.combine_grid, 1, 1, 256, 1, 1, 0, dev->stream(),
                                         args.data(), nullptr),
@@ -510,6 +514,21 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
   return outs;
 }
 
+std::vector<std::string> Executable::unit_names() const {
+  std::vector<std::string> out;
+  for (const Step& st : plan_.steps) {
+    if (st.kind == StepKind::kLibrary) {
+      out.push_back(std::string("lib:") + lib_kind_name(st.lib));
+    } else if (st.kind == StepKind::kAlias) {
+      out.push_back("-");
+    } else {
+      out.push_back(st.name);
+      if (st.combine_grid) out.push_back(st.name + "_combine");
+    }
+  }
+  return out;
+}
+
 std::vector<double> Executable::time_steps(Device* dev, const std::vector<BufferRef>& args, int iters) {
   Loaded* L = loaded_for(dev);
   std::lock_guard<std::mutex> lk(dev->exec_mutex());
@@ -517,19 +536,29 @@ std::vector<double> Executable::time_steps(Device* dev, const std::vector<Buffer
   std::vector<MemRef> vals(prog_.values.size());
   for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i]->mem;
   for (auto& [v, m] : L->constants) vals[v] = m;
-  std::vector<double> ms(plan_.steps.size(), 0.0);
+  std::vector<double> ms;
   hipEvent_t a, b;
   hip_check(hipEventCreate(&a), "hipEventCreate");
   hip_check(hipEventCreate(&b), "hipEventCreate");
-  for (size_t si = 0; si < plan_.steps.size(); ++si) {
-    run_step(L, si, vals);  // warm and produce outputs for later steps
+  auto timed = [&](size_t si, int phase) {
     hip_check(hipEventRecord(a, dev->stream()), "hipEventRecord");
-    for (int k = 0; k < iters; ++k) run_step(L, si, vals);
+    for (int k = 0; k < iters; ++k) run_step(L, si, vals, phase);
     hip_check(hipEventRecord(b, dev->stream()), "hipEventRecord");
     hip_check(hipEventSynchronize(b), "hipEventSynchronize");
     float t = 0.f;
     hip_check(hipEventElapsedTime(&t, a, b), "hipEventElapsedTime");
-    ms[si] = static_cast<double>(t) / iters;
+    ms.push_back(static_cast<double>(t) / iters);
+  };
+  for (size_t si = 0; si < plan_.steps.size(); ++si) {
+    const Step& st = plan_.steps[si];
+    run_step(L, si, vals);  // warm and produce outputs for later steps
+    bool split = st.kind != StepKind::kLibrary && st.kind != StepKind::kAlias && st.combine_grid;
+    if (split) {
+      timed(si, 0);
+      timed(si, 1);
+    } else {
+      timed(si, -1);
+    }
   }
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);

@@ -147,9 +147,13 @@ class Executable {
   // Runs the plan; inputs must be on `dev`. Returns one buffer per result.
   std::vector<BufferRef> execute(Device* dev, const std::vector<BufferRef>& args,
                                  std::shared_ptr<Event>* done);
-  // Times each step by replaying its launch `iters` times between two
-  // hipEvents on the device stream (inputs from `args`). Fills ms per step.
+  // Times each launch unit (a step; a split reduction counts as two units,
+  // main pass then combine pass) by replaying it `iters` times between two
+  // hipEvents on the device stream (inputs from `args`). Returns ms per unit
+  // in the order of unit_names().
   std::vector<double> time_steps(Device* dev, const std::vector<BufferRef>& args, int iters);
+  // Kernel name of each launch unit ("lib:<kind>" for library steps).
+  std::vector<std::string> unit_names() const;
 
   const Program& program() const { return prog_; }
   const Plan& plan() const { return plan_; }
@@ -176,7 +180,9 @@ class Executable {
   ExecStats stats_;
 
   Loaded* loaded_for(Device* dev);
-  void run_step(Loaded* L, size_t si, std::vector<MemRef>& vals);
+  // phase: -1 runs the whole step; 0 only the main kernel of a split
+  // reduction, 1 only its combine kernel (outputs must already exist).
+  void run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int phase = -1);
 };
 
 // Library steps (dot_general, gather, scatter, dynamic slices, ...).

@@ -496,6 +496,8 @@ class Client:
 
     def buffer(self, array: np.ndarray, dtype: str | None = None) -> Buffer:
         arr = np.ascontiguousarray(array)
+        if np.ndim(array) == 0:
+            arr = arr.reshape(())  # ascontiguousarray promotes scalars to 1-d
         name = np_dtype_name(arr, dtype)
         if name == "pred":
             arr = arr.astype(np.uint8)

@@ -25,6 +25,15 @@ def c1_elementwise_rowsum(rows: int = 4096, cols: int = 4096) -> str:
     return b.build([out])
 
 
+def stream_negate(rows: int = 8192, cols: int = 4096) -> str:
+    """out = -x over f32 [rows, cols]: a plain streaming kernel that reads and
+    writes exactly rows*cols*4 bytes each. Used to calibrate the hardware
+    byte counters (FETCH_SIZE / WRITE_SIZE) against a known size."""
+    b = Builder("jit_stream_negate")
+    x = b.param((rows, cols), "f32")
+    return b.build([b.negate(x)])
+
+
 def c2_argmax_f16_reductions(rows: int = 64, vocab: int = 128256) -> str:
     b = Builder("jit_c2")
     logits = b.param((rows, vocab), "bf16")
