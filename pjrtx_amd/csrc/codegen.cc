@@ -309,6 +309,43 @@ std::string Writer::emit_op(const Op& op, int v, int id) {
       for (int64_t d : op.dims) I.multi[d] = "(" + std::to_string(od[d] - 1) + "u - " + m[d] + ")";
       return value(op.operands[0], add_index(I));
     }
+    case OpKind::kConcatenate: {
+      // Each operand is read at the coordinate clamped into its own extent
+      // (always in bounds); the result is chosen by the range the output
+      // coordinate falls in. `m` is copied: add_index below may reallocate.
+      const std::vector<std::string> m = multi_of(id);
+      const int64_t cd = op.dim;
+      const std::string c = m[cd];
+      std::vector<std::string> vals;
+      std::vector<int64_t> ends;
+      int64_t off = 0;
+      for (size_t k = 0; k < op.operands.size(); ++k) {
+        const Dims& od = prog_.type(op.operands[k]).dims;
+        const int64_t sz = od[cd];
+        if (sz == 0) continue;
+        const std::string lo = std::to_string(off) + "u", hi = std::to_string(sz - 1) + "u";
+        std::string e;
+        if (off == 0) {
+          e = "(" + c + " < " + hi + " ? " + c + " : " + hi + ")";
+        } else {
+          e = "(" + c + " < " + lo + " ? 0u : (" + c + " - " + lo + " < " + hi + " ? " + c + " - " + lo + " : " + hi +
+              "))";
+        }
+        Idx I;
+        I.key = "c" + std::to_string(v) + "_" + std::to_string(k) + "(" + idxs_[id].key + ")";
+        I.shape = od;
+        I.multi = m;
+        I.multi[cd] = e;
+        vals.push_back(value(op.operands[k], add_index(I)));
+        off += sz;
+        ends.push_back(off);
+      }
+      PJRTX_CHECK(!vals.empty(), Code::kInternal, "concatenate with no elements inside a fusion");
+      std::string e = vals.back();
+      for (int k = static_cast<int>(vals.size()) - 2; k >= 0; --k)
+        e = "(" + c + " < " + std::to_string(ends[k]) + "u ? " + vals[k] + " : " + e + ")";
+      return define(R, e);
+    }
     default:
       break;
   }

@@ -110,6 +110,10 @@ struct Program {
   std::vector<int> params;       // value ids of entry parameters
   std::vector<Op> ops;           // entry body, topologically ordered
   std::vector<int> results;      // value ids returned by the entry
+  // Per entry parameter: the result index it is donated to
+  // (`tf.aliasing_output = N`), -2 for a donor with no fixed result
+  // (`jax.buffer_donor = true`), -1 when not donated.
+  std::vector<int> param_alias;
   int num_partitions = 1;
   int num_replicas = 1;
 

@@ -215,6 +215,7 @@ namespace {
 struct RawFunc {
   std::string name;
   std::vector<int> params;
+  std::vector<int> param_alias;  // see Program::param_alias
   std::vector<TensorType> result_types;
   std::vector<Op> ops;  // includes call ops as kind kReturn+callee marker
 };
@@ -489,6 +490,7 @@ Program Parser::run() {
   // Inline everything into main.
   RawFunc& main = funcs_["main"];
   prog_.params = main.params;
+  prog_.param_alias = main.param_alias;
   std::vector<int> results;
   inline_into("main", main.params, &results, &prog_.ops, 0);
   prog_.results = results;
@@ -543,6 +545,26 @@ void Parser::inline_into(const std::string& fname, const std::vector<int>& args,
   }
 }
 
+// Donation attributes of an entry argument, as jax.jit(donate_argnums=...)
+// lowers them: `tf.aliasing_output = N : i32` names the result that reuses
+// the argument's buffer; `jax.buffer_donor = true` donates it without one.
+static int donation_from_attrs(const std::string& attrs) {
+  size_t p = attrs.find("tf.aliasing_output");
+  if (p != std::string::npos) {
+    p = attrs.find('=', p);
+    if (p != std::string::npos) {
+      ++p;
+      while (p < attrs.size() && attrs[p] == ' ') ++p;
+      size_t q = p;
+      while (q < attrs.size() && isdigit(static_cast<unsigned char>(attrs[q]))) ++q;
+      if (q > p) return std::stoi(attrs.substr(p, q - p));
+    }
+  }
+  p = attrs.find("jax.buffer_donor");
+  if (p != std::string::npos && attrs.find("true", p) != std::string::npos) return -2;
+  return -1;
+}
+
 void Parser::parse_func() {
   ws();
   if (!try_word("func.func")) error("expected func.func");
@@ -556,10 +578,12 @@ void Parser::parse_func() {
       std::string n = ssa_name();
       expect(":");
       TensorType t = type();
-      if (peek() == '{') balanced();
+      int alias = -1;
+      if (peek() == '{') alias = donation_from_attrs(balanced());
       int id = new_value(t, n);
       bind(n, id);
       f.params.push_back(id);
+      f.param_alias.push_back(alias);
     } while (try_lit(","));
     expect(")");
   }

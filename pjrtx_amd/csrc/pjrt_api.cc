@@ -858,8 +858,28 @@ static PJRT_Error* LoadedExecutable_Execute(PJRT_LoadedExecutable_Execute_Args* 
       PJRTX_CHECK(!b->buf->deleted, Code::kInvalidArgument, strformat("Execute: argument %zu was deleted or donated", i));
       in.push_back(b->buf);
     }
+    // Donation (reference: execute.zig:40-70): an argument whose parameter
+    // carries tf.aliasing_output / jax.buffer_donor is donated unless the
+    // caller lists it as non-donatable or passes the same buffer twice.
+    const std::vector<int>& alias = prog.param_alias;
+    std::vector<bool> donate(in.size(), false);
+    for (size_t i = 0; i < in.size(); ++i) donate[i] = i < alias.size() && alias[i] != -1;
+    if (args->options && args->options->non_donatable_input_indices) {
+      for (size_t k = 0; k < args->options->num_non_donatable_input_indices; ++k) {
+        const int64_t idx = args->options->non_donatable_input_indices[k];
+        if (idx >= 0 && static_cast<size_t>(idx) < donate.size()) donate[idx] = false;
+      }
+    }
+    for (size_t i = 0; i < in.size(); ++i)
+      for (size_t j = 0; j < in.size(); ++j)
+        if (i != j && in[i].get() == in[j].get()) donate[i] = false;
     std::shared_ptr<Event> done;
-    std::vector<BufferRef> outs = le->exe->execute(d->dev, in, &done);
+    std::vector<BufferRef> outs = le->exe->execute(d->dev, in, &done, &donate);
+    for (size_t i = 0; i < in.size(); ++i) {
+      if (!donate[i]) continue;
+      in[i]->deleted = true;  // the memory now belongs to the results
+      in[i]->mem.reset();
+    }
     for (size_t i = 0; i < nout; ++i) {
       auto* pb = new PJRT_Buffer();
       pb->buf = outs[i];

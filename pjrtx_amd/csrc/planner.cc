@@ -2,6 +2,7 @@
 #include "planner.h"
 
 #include <algorithm>
+#include <cstdio>
 #include <functional>
 #include <queue>
 #include <sstream>
@@ -93,10 +94,20 @@ bool is_splat_constant(const Program& prog, const Op& op) {
   return op.kind == OpKind::kConstant && (op.splat || prog.type(op.results[0]).elements() == 1);
 }
 
-bool is_library(OpKind k) {
+// A concatenate of a few operands fuses as an index select (each operand
+// read at a clamped coordinate, the result picked by range); a long operand
+// list runs as box copies instead.
+constexpr size_t kMaxFusedConcatOperands = 8;
+
+bool fusible_concat(const Op& op) {
+  return op.kind == OpKind::kConcatenate && op.operands.size() <= kMaxFusedConcatOperands;
+}
+
+bool is_library(const Op& op) {
+  const OpKind k = op.kind;
   return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
          k == OpKind::kDynamicSlice || k == OpKind::kDynamicUpdateSlice ||
-         k == OpKind::kConcatenate || k == OpKind::kPad;
+         (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad;
 }
 
 LibKind lib_kind_of(OpKind k) {
@@ -127,12 +138,16 @@ class Planner {
   std::set<int>& mat_ = plan_.materialized;
 
   bool fusible_op(const Op& op) const {
-    return op_is_elementwise(op.kind) || op_is_view(op.kind) || is_splat_constant(prog_, op);
+    return op_is_elementwise(op.kind) || op_is_view(op.kind) || fusible_concat(op) || is_splat_constant(prog_, op);
   }
   void decide_materialization();
   // Collects the fused ops reachable backward from `roots` without crossing
   // materialized values. Fills ops (sorted) and inputs.
-  void closure(const std::vector<int>& roots, std::vector<int>* ops, std::vector<int>* inputs) const;
+  // `roots_are_outputs`: the roots are the values this step produces (their
+  // producers are fused even though the roots are materialized); otherwise
+  // a materialized root is read as an input.
+  void closure(const std::vector<int>& roots, std::vector<int>* ops, std::vector<int>* inputs,
+               bool roots_are_outputs = true) const;
   void build_steps(std::vector<Step>* steps);
   void merge_siblings(std::vector<Step>* steps);
   void merge_epilogues(std::vector<Step>* steps);
@@ -177,7 +192,7 @@ void Planner::decide_materialization() {
       for (int v : op.results) mat_.insert(v);
       continue;
     }
-    if (is_library(op.kind)) {
+    if (is_library(op)) {
       for (int v : op.operands) mat_.insert(v);
       for (int v : op.results) mat_.insert(v);
       continue;
@@ -185,7 +200,7 @@ void Planner::decide_materialization() {
     PJRTX_CHECK(fusible_op(op), Code::kUnimplemented,
                 std::string("op not supported by the HIP backend: ") + op.name);
     // Elementwise / view op.
-    int c = op_is_view(op.kind) ? 0 : 1;
+    int c = (op_is_view(op.kind) || op.kind == OpKind::kConcatenate) ? 0 : 1;
     for (int v : op.operands) {
       if (!mat_.count(v)) c += cost[v];
     }
@@ -217,8 +232,8 @@ void Planner::decide_materialization() {
   }
 }
 
-void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops,
-                      std::vector<int>* inputs) const {
+void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops, std::vector<int>* inputs,
+                      bool roots_are_outputs) const {
   std::set<int> seen_ops, seen_inputs;
   std::function<void(int, bool)> visit = [&](int v, bool is_root) {
     if (!is_root && mat_.count(v)) {
@@ -235,7 +250,7 @@ void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops,
     const Op& op = prog_.ops[oi];
     for (int u : op.operands) visit(u, false);
   };
-  for (int r : roots) visit(r, true);
+  for (int r : roots) visit(r, roots_are_outputs);
   ops->assign(seen_ops.begin(), seen_ops.end());  // std::set is sorted: program order
 }
 
@@ -260,12 +275,12 @@ void Planner::build_steps(std::vector<Step>* steps) {
       std::vector<int> roots = rs.inputs;
       std::vector<int> init_inputs;
       for (int v : rs.inits) roots.push_back(v);
-      closure(roots, &s.ops, &s.inputs);
+      closure(roots, &s.ops, &s.inputs, /*roots_are_outputs=*/false);
       s.outputs = op.results;
       steps->push_back(std::move(s));
       continue;
     }
-    if (is_library(op.kind)) {
+    if (is_library(op)) {
       Step s;
       s.kind = StepKind::kLibrary;
       s.lib = lib_kind_of(op.kind);
@@ -390,7 +405,7 @@ void Planner::merge_epilogues(std::vector<Step>* steps) {
       bool identity_only = true;
       for (int oi : G.ops) {
         const Op& op = prog_.ops[oi];
-        if (!op_is_view(op.kind) || op.kind == OpKind::kIota) continue;
+        if ((!op_is_view(op.kind) && op.kind != OpKind::kConcatenate) || op.kind == OpKind::kIota) continue;
         for (int u : op.operands) {
           auto pi = producer_.find(u);
           const bool literal = pi != producer_.end() && is_splat_constant(prog_, prog_.ops[pi->second]);
@@ -474,8 +489,12 @@ void Planner::liveness() {
   }
   // In-place dynamic_update_slice (reference: executable_metal_graph_slice.zig:
   // 129-144): allowed when the operand is an intermediate produced by a
-  // kernel (not a view alias of another live buffer) whose last reader is
-  // this step.
+  // kernel, or a donated entry argument, (not a view alias of another live
+  // buffer) whose last reader is this step.
+  std::map<int, int> donated_param;  // value id -> parameter position
+  for (size_t k = 0; k < prog_.params.size(); ++k)
+    if (k < prog_.param_alias.size() && prog_.param_alias[k] != -1)
+      donated_param[prog_.params[k]] = static_cast<int>(k);
   std::set<int> aliased;
   std::map<int, StepKind> producer_kind;
   for (const Step& s : plan_.steps) {
@@ -488,7 +507,11 @@ void Planner::liveness() {
     const int v0 = prog_.ops[s.lib_op].operands[0];
     const bool intermediate = !persistent.count(v0) && !outputs_.count(v0) && !aliased.count(v0) &&
                               producer_kind.count(v0) && producer_kind[v0] != StepKind::kAlias;
-    if (intermediate && last_use[v0] == static_cast<int>(i)) s.in_place = true;
+    const bool donated = donated_param.count(v0) && !outputs_.count(v0) && !aliased.count(v0);
+    if ((intermediate || donated) && last_use[v0] == static_cast<int>(i)) {
+      s.in_place = true;
+      if (donated) plan_.written_params.push_back(donated_param[v0]);
+    }
   }
 }
 
@@ -600,6 +623,12 @@ std::string Plan::describe(const Program& prog) const {
                      : s.kind == StepKind::kAlias ? "alias" : "library";
     o << "{\"kind\":\"" << kind << "\",\"name\":\"" << s.name << "\"";
     o << ",\"inputs\":" << list(s.inputs) << ",\"outputs\":" << list(s.outputs);
+    auto bytes_of = [&](const std::vector<int>& vs) {
+      std::string b = "[";
+      for (size_t k = 0; k < vs.size(); ++k) b += (k ? "," : "") + std::to_string(prog.type(vs[k]).bytes());
+      return b + "]";
+    };
+    o << ",\"in_bytes\":" << bytes_of(s.inputs) << ",\"out_bytes\":" << bytes_of(s.outputs);
     std::vector<std::string> names;
     o << ",\"ops\":[";
     for (size_t k = 0; k < s.ops.size(); ++k) o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.ops[k]].kind) << "\"";
@@ -617,13 +646,15 @@ std::string Plan::describe(const Program& prog) const {
     o << ",\"vec\":" << s.vec << ",\"grid\":" << s.grid << ",\"block\":" << s.block;
     o << ",\"release_after\":" << list(s.release_after) << "}";
   }
-  o << "],\"constants\":" << list(constants) << ",\"fusion_kernels\":" << num_fusion_kernels << "}";
+  o << "],\"constants\":" << list(constants) << ",\"fusion_kernels\":" << num_fusion_kernels
+    << ",\"param_alias\":" << list(prog.param_alias) << ",\"written_params\":" << list(written_params) << "}";
   return o.str();
 }
 
 Plan make_plan(const Program& prog, const PlanOptions& opts) {
   Planner p(prog, opts);
   Plan plan = p.run();
+  if (env_flag("PJRTX_PLAN_DEBUG")) std::fprintf(stderr, "pjrtx plan: %s\n", plan.describe(prog).c_str());
   plan.kernel_source = generate_kernels(prog, plan);
   return plan;
 }

@@ -89,6 +89,10 @@ struct Plan {
   std::vector<Step> steps;
   std::set<int> materialized;
   std::vector<int> constants;        // materialized non-splat constant values
+  // Entry parameter positions whose buffer a step writes in place (donated
+  // arguments only). The runtime copies such an argument first when the
+  // caller does not donate it.
+  std::vector<int> written_params;
   std::map<int, int> producer;       // value -> op index
   std::string kernel_source;         // hiprtc source for all generated steps
   int num_fusion_kernels = 0;

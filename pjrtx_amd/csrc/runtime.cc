@@ -460,7 +460,7 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
 }
 
 std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<BufferRef>& args,
-                                           std::shared_ptr<Event>* done) {
+                                           std::shared_ptr<Event>* done, const std::vector<bool>* donate) {
   PJRTX_CHECK(args.size() == prog_.params.size(), Code::kInvalidArgument,
               strformat("execute: program takes %zu arguments, got %zu", prog_.params.size(), args.size()));
   for (size_t i = 0; i < args.size(); ++i) {
@@ -476,6 +476,17 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
   dev->make_current();
   std::vector<MemRef> vals(prog_.values.size());
   for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i]->mem;
+  auto donated = [&](size_t i) { return donate && i < donate->size() && (*donate)[i]; };
+  for (int k : plan_.written_params) {
+    if (donated(k)) continue;
+    // The plan writes this parameter in place; keep the caller's buffer intact.
+    const MemRef& src = args[k]->mem;
+    MemRef c = dev->allocate(src->bytes);
+    if (src->bytes)
+      hip_check(hipMemcpyAsync(c->ptr, src->ptr, src->bytes, hipMemcpyDeviceToDevice, dev->stream()),
+                "hipMemcpyAsync(undonated argument)");
+    vals[prog_.params[k]] = c;
+  }
   for (auto& [v, m] : L->constants) vals[v] = m;
   for (size_t si = 0; si < plan_.steps.size(); ++si) {
     run_step(L, si, vals);
@@ -489,7 +500,8 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
   std::vector<BufferRef> outs;
   std::set<const DeviceMemory*> seen;
   std::set<const DeviceMemory*> borrowed;
-  for (size_t i = 0; i < args.size(); ++i) borrowed.insert(args[i]->mem.get());
+  for (size_t i = 0; i < args.size(); ++i)
+    if (!donated(i)) borrowed.insert(args[i]->mem.get());
   for (auto& [v, m] : L->constants) borrowed.insert(m.get());
   for (int r : prog_.results) {
     MemRef m = vals[r];

@@ -145,8 +145,12 @@ class Executable {
   // Loads code and resident constants on `dev` (once).
   void load(Device* dev);
   // Runs the plan; inputs must be on `dev`. Returns one buffer per result.
+  // `donate[i]` true hands argument i's memory to this execution: a step may
+  // write it in place and a result may keep it (the caller must treat the
+  // argument as deleted). A parameter the plan writes in place but whose
+  // argument is not donated is copied first.
   std::vector<BufferRef> execute(Device* dev, const std::vector<BufferRef>& args,
-                                 std::shared_ptr<Event>* done);
+                                 std::shared_ptr<Event>* done, const std::vector<bool>* donate = nullptr);
   // Times each launch unit (a step; a split reduction counts as two units,
   // main pass then combine pass) by replaying it `iters` times between two
   // hipEvents on the device stream (inputs from `args`). Returns ms per unit

@@ -55,7 +55,8 @@ def _fmt_float(v: float, dtype: str) -> str:
         return "0x7FF0000000000000" if v > 0 else "0xFFF0000000000000"
     if dtype == "f32":
         v = struct.unpack("<f", struct.pack("<f", v))[0]
-    return f"{v:.6e}" if dtype != "f64" else repr(float(v))
+        return f"{v:.9e}"  # 9 significant digits round-trip every f32
+    return repr(float(v))
 
 
 def _literal(value, dtype: str) -> str:
@@ -72,6 +73,7 @@ class Builder:
     def __init__(self, name: str = "jit_f"):
         self.name = name
         self.params: list[T] = []
+        self.donated: set[str] = set()
         self.lines: list[str] = []
         self._n = 0
         self._c = 0
@@ -87,9 +89,14 @@ class Builder:
         self.lines.append(f"    {t.name} = {text}")
         return t
 
-    def param(self, shape, dtype: str) -> T:
+    def param(self, shape, dtype: str, donate: bool = False) -> T:
+        """Entry argument. `donate=True` is jax.jit's donate_argnums: the
+        argument is marked `tf.aliasing_output = N` for the first unclaimed
+        result of the same type, else `jax.buffer_donor = true`."""
         t = T(f"%arg{len(self.params)}", tuple(shape), dtype)
         self.params.append(t)
+        if donate:
+            self.donated.add(t.name)
         return t
 
     def constant(self, value, dtype: str, shape=()) -> T:
@@ -379,7 +386,19 @@ class Builder:
 
     # ------------------------------------------------------------ output
     def build(self, outputs: list[T]) -> str:
-        args = ", ".join(f"{p.name}: {p.type}" for p in self.params)
+        claimed: set[int] = set()
+        parts = []
+        for p in self.params:
+            attr = ""
+            if p.name in self.donated:
+                match = next((i for i, o in enumerate(outputs) if i not in claimed and o.type == p.type), None)
+                if match is None:
+                    attr = " {jax.buffer_donor = true}"
+                else:
+                    claimed.add(match)
+                    attr = f" {{tf.aliasing_output = {match} : i32}}"
+            parts.append(f"{p.name}: {p.type}{attr}")
+        args = ", ".join(parts)
         if len(outputs) == 1:
             res = f"({outputs[0].type} {{jax.result_info = \"result\"}})"
         else:

@@ -113,6 +113,7 @@ LoadedDestroyArgs = _args("LoadedDestroyArgs", [("executable", c_void_p)])
 OptimizedProgramArgs = _args("OptimizedProgramArgs", [("executable", c_void_p), ("program", POINTER(Program))])
 BufferDestroyArgs = _args("BufferDestroyArgs", [("buffer", c_void_p)])
 BufferElementTypeArgs = _args("BufferElementTypeArgs", [("buffer", c_void_p), ("type", c_int)])
+BufferIsDeletedArgs = _args("BufferIsDeletedArgs", [("buffer", c_void_p), ("is_deleted", ctypes.c_bool)])
 BufferDimensionsArgs = _args("BufferDimensionsArgs", [("buffer", c_void_p), ("dims", POINTER(c_int64)),
                                                       ("num_dims", c_size_t)])
 ToHostArgs = _args("ToHostArgs", [("src", c_void_p), ("host_layout", c_void_p), ("dst", c_void_p),
@@ -358,6 +359,14 @@ class Buffer:
             self.client.p.call("Event_Destroy", d)
         return out
 
+    def is_deleted(self) -> bool:
+        """PJRT_Buffer_IsDeleted: true after Delete or after the buffer was
+        donated to an execution."""
+        a = _mk(BufferIsDeletedArgs())
+        a.buffer = self.handle
+        self.client.p.call("Buffer_IsDeleted", a)
+        return bool(a.is_deleted)
+
     def delete(self) -> None:
         if self.handle:
             a = _mk(BufferDestroyArgs())
@@ -397,7 +406,10 @@ class Executable:
         self.client.p.call("Executable_OptimizedProgram", a)
         return buf.raw[: prog.code_size].decode()
 
-    def execute_buffers(self, args: list[Buffer]) -> list[Buffer]:
+    def execute_buffers(self, args: list[Buffer], non_donatable: list[int] | None = None) -> list[Buffer]:
+        """PJRT_LoadedExecutable_Execute on one device. Arguments whose
+        parameters are marked donated (and not listed in `non_donatable`)
+        are consumed: their buffers read as deleted afterwards."""
         p = self.client.p
         arg_arr = (c_void_p * max(1, len(args)))(*[b.handle for b in args])
         arg_lists = (POINTER(c_void_p) * 1)(ctypes.cast(arg_arr, POINTER(c_void_p)))
@@ -405,6 +417,10 @@ class Executable:
         out_lists = (POINTER(c_void_p) * 1)(ctypes.cast(out_arr, POINTER(c_void_p)))
         events = (c_void_p * 1)()
         opts = _mk(ExecuteOptions())
+        if non_donatable:
+            nd = (c_int64 * len(non_donatable))(*non_donatable)
+            opts.non_donatable_input_indices = nd
+            opts.num_non_donatable_input_indices = len(non_donatable)
         a = _mk(ExecuteArgs())
         a.executable = self.handle
         a.options = ctypes.pointer(opts)

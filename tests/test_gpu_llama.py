@@ -1,0 +1,119 @@
+"""C5 llama-like decode through the plugin, checked against the numpy oracle
+(oracle/llama.py): teacher-forced logits within bf16 tolerance, greedy
+tokens, cache donation, and at full size the KV-cache property (one decode
+step equals a one-token-longer prefill)."""
+import numpy as np
+import pytest
+
+from oracle import llama as O
+from pjrtx_amd import llama_like as L
+
+pytestmark = pytest.mark.gpu
+
+# bf16 logits: the program rounds every stored activation to bf16, and
+# the GPU accumulates dots and sums in a different order from numpy. The
+# bar is 2e-2 of the logit range.
+TOL = 2e-2
+
+
+def _check_step(gpu_logits, ora_logits, gpu_tok):
+    scale = float(np.abs(ora_logits).max())
+    err = float(np.abs(gpu_logits - ora_logits).max())
+    assert err <= TOL * scale, f"logits differ by {err} (scale {scale})"
+    assert gpu_tok == int(np.argmax(gpu_logits))  # the program's argmax of its own logits
+    top = np.sort(ora_logits)[::-1]
+    if top[0] - top[1] > 2 * TOL * scale:  # a clear winner must agree
+        assert gpu_tok == int(np.argmax(ora_logits))
+
+
+def _gpu_logits(buf):
+    return O.bf16_bits_to_f32(buf.to_numpy())[0]
+
+
+@pytest.fixture(scope="module")
+def tiny(client):
+    w = L.init_weights(L.TINY, seed=0)
+    return L.LlamaRunner(client, L.TINY, w), O.weights_f32(L.TINY, w)
+
+
+def test_tiny_greedy_decode_matches_oracle(tiny):
+    runner, W = tiny
+    cfg = L.TINY
+    prompt = L.prompt_tokens(cfg, seed=1)
+    toks, _, logits = runner.generate(prompt, cfg.new_tokens, keep_logits=True)
+    ora_toks, ora_logits = O.generate(cfg, W, prompt, cfg.new_tokens, forced=toks[:-1])
+    for i in range(cfg.new_tokens):
+        _check_step(O.bf16_bits_to_f32(logits[i])[0], ora_logits[i], int(toks[i]))
+    agree = np.mean(toks == ora_toks)
+    assert agree >= 0.9, (toks, ora_toks)
+
+
+def test_tiny_cache_donation(tiny, client):
+    runner, _ = tiny
+    cfg = L.TINY
+    prompt = L.prompt_tokens(cfg, seed=2)
+    tok, _, caches = runner.start(prompt)
+    # Not donated: the caller's caches stay valid and unchanged.
+    before = [c.to_numpy() for c in caches]
+    pos = client.buffer(np.array(len(prompt), np.int32))
+    nd = list(range(len(runner.weights) + 2, len(runner.weights) + 2 + len(caches)))
+    outs_keep = runner.decode.execute_buffers(runner.weights + [tok, pos] + caches, non_donatable=nd)
+    assert not any(c.is_deleted() for c in caches)
+    for c, b in zip(caches, before):
+        np.testing.assert_array_equal(c.to_numpy(), b)
+    # Donated: same results, the inputs read as deleted afterwards.
+    outs = runner.decode.execute_buffers(runner.weights + [tok, pos] + caches)
+    assert all(c.is_deleted() for c in caches)
+    for a, b in zip(outs, outs_keep):
+        np.testing.assert_array_equal(a.to_numpy(), b.to_numpy())
+    # The new token's row was written at the position; earlier rows kept.
+    k0 = outs[2].to_numpy()
+    assert np.array_equal(k0[:, :, :len(prompt)], before[0][:, :, :len(prompt)])
+    assert np.any(k0[:, :, len(prompt)] != 0)
+
+
+def test_tiny_plan_updates_caches_in_place(client):
+    import json
+    exe = client.compile(L.decode_program(L.TINY))
+    plan = json.loads(exe.optimized_program())
+    dus = [s for s in plan["steps"] if s.get("library") == "dynamic_update_slice"]
+    assert len(dus) == 2 * L.TINY.layers and all(s["in_place"] for s in dus)
+    assert len(plan["written_params"]) == 2 * L.TINY.layers
+
+
+@pytest.fixture(scope="module")
+def full(client):
+    w = L.init_weights(L.FULL, seed=0)
+    return L.LlamaRunner(client, L.FULL, w), w
+
+
+def test_full_prefill_and_decode_match_oracle(full):
+    runner, wbits = full
+    cfg = L.FULL
+    W = O.weights_f32(cfg, wbits)
+    prompt = L.prompt_tokens(cfg, seed=1)
+    steps = 3
+    toks, timing, logits = runner.generate(prompt, steps, keep_logits=True)
+    kc, vc = O.empty_caches(cfg)
+    t, lg = O.forward(cfg, W, prompt, 0, kc, vc)
+    _check_step(O.bf16_bits_to_f32(logits[0])[0], lg, int(toks[0]))
+    for i in range(1, steps):
+        t, lg = O.forward(cfg, W, np.array([toks[i - 1]], np.int32), len(prompt) + i - 1, kc, vc)
+        _check_step(O.bf16_bits_to_f32(logits[i])[0], lg, int(toks[i]))
+
+
+def test_full_decode_step_equals_longer_prefill(full, client):
+    runner, _ = full
+    cfg = L.FULL
+    prompt = L.prompt_tokens(cfg, seed=7)
+    tok, _, caches = runner.start(prompt)
+    _, step_logits, _ = runner.step(tok, len(prompt), caches)
+    import dataclasses
+    longer = dataclasses.replace(cfg, prompt=cfg.prompt + 1)
+    exe = client.compile(L.prefill_program(longer))
+    ext = np.append(prompt, tok.to_numpy()[0]).astype(np.int32)
+    z = np.zeros(L.cache_shape(cfg), np.uint16)
+    outs = exe.execute_buffers(runner.weights + [client.buffer(ext)] +
+                               [client.buffer(z, "bf16") for _ in range(2 * cfg.layers)])
+    a, b = _gpu_logits(step_logits), _gpu_logits(outs[1])
+    assert np.abs(a - b).max() <= TOL * np.abs(b).max()
