@@ -1,14 +1,24 @@
 """Benchmark of the pjrtx hot path on one MI355X.
 
-A step is one PJRT execute of the workload's compiled StableHLO program on
-device-resident inputs (synthetic, seeded). Default workload: BASELINE
-configs[1] — two-output max/index argmax over bf16 logits [64,128256] plus
-f16 sum/max/min of the logits cast to f16 (one fused kernel). `--config c1`
-runs configs[0] (f32 elementwise chain + row sum, [4096,4096]).
+A step is one PJRT execute of a workload's compiled StableHLO program on
+device-resident inputs (synthetic, seeded). Workloads (`--config`), after
+BASELINE.json's configs:
 
-Prints one JSON line: whole-job HBM GB/s over algorithmic bytes, the
-dominant kernel's roofline (HIP-event timed on the plugin's stream), and the
-CPU oracle timed on this host as a reported baseline.
+  c2       (default, configs[1]) two-output max/index argmax over bf16
+           logits [64,128256] plus f16 sum/max/min of logits.astype(f16)
+  c1       configs[0]: f32 elementwise chain + row sum, [4096,4096]
+  c3mm     configs[2]: plain bf16 matmul [8192,8192] x [8192,8192]
+  c3attn   configs[2]: attention dot_generals [8,32,2048,128], causal mask,
+           f32 softmax, bf16 context
+  c4g      configs[3]: embedding gather, table [128256,4096] bf16, idx [8,2048]
+  c4s/c4i  configs[3]: Zipf(1.1) scatter-add of [1048576,256] updates into
+           [65536,256], f32 / int32
+  c5       configs[4]: llama-like greedy decode, tokens/s (a step is one token)
+  copy     counter calibration stream (not a bench line)
+
+Prints one JSON line: the whole-job rate, the dominant kernel's roofline
+(HIP-event timed per launch on the plugin's stream) and, unless
+--no-cpu-baseline, the numpy oracle timed on this host on a bounded sample.
 """
 from __future__ import annotations
 
@@ -18,110 +28,340 @@ import os
 import pathlib
 import sys
 import time
+from dataclasses import dataclass, field
+from typing import Callable
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}
+
+
+def host_threads() -> int:
+    n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def randn_bits(shape, seed: int, scale: float = 1.0):
+    """Seeded N(0,1)*scale as bf16 bit patterns, filled in independently
+    seeded 2^22-element blocks on a thread pool."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    out = np.empty(shape, np.uint16)
+    flat = out.reshape(-1)
+
+    def fill(blk):
+        lo = blk << 22
+        hi = min(flat.size, lo + (1 << 22))
+        w = np.random.default_rng([seed, blk]).standard_normal(hi - lo, dtype=np.float32)
+        w *= np.float32(scale)
+        u = w.view(np.uint32)
+        flat[lo:hi] = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    with ThreadPoolExecutor(min(16, host_threads())) as ex:
+        list(ex.map(fill, range((flat.size + (1 << 22) - 1) >> 22)))
+    return out
+
+
+def randn_f32(shape, seed: int):
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    out = np.empty(shape, np.float32)
+    flat = out.reshape(-1)
+
+    def fill(blk):
+        lo = blk << 22
+        hi = min(flat.size, lo + (1 << 22))
+        flat[lo:hi] = np.random.default_rng([seed, blk]).standard_normal(hi - lo, dtype=np.float32)
+
+    with ThreadPoolExecutor(min(16, host_threads())) as ex:
+        list(ex.map(fill, range((flat.size + (1 << 22) - 1) >> 22)))
+    return out
+
+
+def randint_s32(shape, seed: int, lo: int, hi: int):
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    out = np.empty(shape, np.int32)
+    flat = out.reshape(-1)
+
+    def fill(blk):
+        lo_i = blk << 22
+        hi_i = min(flat.size, lo_i + (1 << 22))
+        flat[lo_i:hi_i] = np.random.default_rng([seed, blk]).integers(lo, hi, hi_i - lo_i, dtype=np.int32)
+
+    with ThreadPoolExecutor(min(16, host_threads())) as ex:
+        list(ex.map(fill, range((flat.size + (1 << 22) - 1) >> 22)))
+    return out
+
+
+@dataclass
+class Workload:
+    workload: str
+    desc: str
+    make: Callable        # () -> (program text, inputs, dtypes)
+    bytes: int            # algorithmic HBM bytes per step
+    dtype: str
+    flops: int = 0        # per step (dot workloads)
+    cpu: Callable | None = None  # (inputs) -> (callable, fraction of one step it does, sample text)
+    meta: dict = field(default_factory=dict)
+
+
+def _c1():
+    from oracle import ops
+    from pjrtx_amd import programs
+    return programs.c1_elementwise_rowsum(4096, 4096), list(ops.c1_inputs(4096, 4096, seed=0)), [None, None]
+
+
+def _c2():
+    from oracle import ops
+    from pjrtx_amd import programs
+    return programs.c2_argmax_f16_reductions(64, 128256), [ops.c2_inputs(64, 128256, seed=0)], ["bf16"]
+
+
+def _copy():
+    from pjrtx_amd import programs
+    return programs.stream_negate(8192, 4096), [randn_f32((8192, 4096), 0)], [None]
+
+
+def _c3mm():
+    from pjrtx_amd import programs
+    s = 1.0 / 8192 ** 0.5
+    return programs.c3_matmul(8192, 8192, 8192), [randn_bits((8192, 8192), 1, s), randn_bits((8192, 8192), 2, s)], \
+        ["bf16", "bf16"]
+
+
+def _c3attn():
+    from pjrtx_amd import programs
+    shp, s = (8, 32, 2048, 128), 1.0 / 128 ** 0.5
+    return programs.c3_attention(*shp), [randn_bits(shp, 10 + i, s) for i in range(3)], ["bf16"] * 3
+
+
+def _c4g():
+    import numpy as np
+    from pjrtx_amd import programs
+    table = randn_bits((128256, 4096), 20, 0.02)
+    idx = np.random.default_rng(21).integers(0, 128256, (8, 2048)).astype(np.int32)
+    return programs.c4_embedding_gather(128256, 4096, 8, 2048), [table, idx], ["bf16", None]
+
+
+def _c4s(dtype: str):
+    import numpy as np
+    from oracle import ops
+    from pjrtx_amd import programs
+    rows, dim, n = 65536, 256, 1048576
+    idx = ops.zipf_indices(n, rows, seed=30)
+    if dtype == "f32":
+        x = np.zeros((rows, dim), np.float32)
+        upd = randn_f32((n, dim), 31)
+    else:
+        x = np.zeros((rows, dim), np.int32)
+        upd = randint_s32((n, dim), 31, -1000, 1000)
+    return programs.c4_scatter_add(rows, dim, n, dtype), [x, idx, upd], [None, None, None]
+
+
+# --------------------------------------------------------------- CPU legs
+
+def _cpu_c1(inputs):
+    from oracle import ops
+    return (lambda: ops.c1_rowsum(*inputs)), 1.0, "full workload, numpy oracle"
+
+
+def _cpu_c2(inputs):
+    from oracle import ops
+    return (lambda: ops.c2_reference(inputs[0])), 1.0, "full workload, numpy oracle"
+
+
+def _cpu_copy(inputs):
+    import numpy as np
+    return (lambda: np.negative(inputs[0])), 1.0, "full workload, numpy negate"
+
+
+def _cpu_c3mm(inputs):
+    import numpy as np
+    from oracle import ops
+    a = ops.bf16_bits_to_f32(inputs[0][:1024])
+    b = ops.bf16_bits_to_f32(inputs[1])
+    return (lambda: np.matmul(a, b)), 1024 / 8192, "1024 of 8192 output rows, numpy f32 matmul (BLAS, all host threads)"
+
+
+def _cpu_c3attn(inputs):
+    from oracle import ops
+    q, k, v = (t[0, :2] for t in inputs)
+    return (lambda: ops.attention_bf16(q, k, v)), 2 / 256, "2 of 256 (batch, head) pairs, numpy oracle"
+
+
+def _cpu_c4g(inputs):
+    from oracle import ops
+    return (lambda: ops.gather_rows(inputs[0], inputs[1])), 1.0, "full workload, numpy gather"
+
+
+def _cpu_c4s(inputs):
+    from oracle import ops
+    x, idx, upd = inputs
+    n = len(idx) // 64
+    fn = ops.scatter_rows_add if x.dtype.kind == "f" else ops.scatter_rows_add_int
+    return (lambda: fn(x, idx[:n], upd[:n])), 1 / 64, "1/64 of the updates, numpy np.add.at in update order"
+
 
 WORKLOADS = {
-    "c2": dict(
-        workload="argmax2_f16reduce_64x128256_bf16",
-        desc="two-output argmax over logits [64,128256] bf16 + f16 sum/max/min of logits.astype(f16)",
-        # read logits once + outputs (bf16 values, i32 indices, 3x f16)
-        bytes=64 * 128256 * 2 + 64 * (2 + 4 + 3 * 2),
-        # main pass reads every logit once; its partials stay in L2/MALL-sized scratch
-        kernel_bytes=64 * 128256 * 2,
-        dtype="bf16",
-    ),
-    "c1": dict(
-        workload="f32_chain_rowsum_4096x4096",
-        desc="sum(tanh(x*y+0.5)*x - max(y,0), axis=1), x,y [4096,4096] f32",
-        bytes=2 * 4096 * 4096 * 4 + 4096 * 4,
-        kernel_bytes=2 * 4096 * 4096 * 4 + 4096 * 4,
-        dtype="f32",
-    ),
+    "c2": Workload("argmax2_f16reduce_64x128256_bf16",
+                   "two-output argmax over logits [64,128256] bf16 + f16 sum/max/min of logits.astype(f16)",
+                   _c2, 64 * 128256 * 2 + 64 * (2 + 4 + 3 * 2), "bf16", cpu=_cpu_c2),
+    "c1": Workload("f32_chain_rowsum_4096x4096", "sum(tanh(x*y+0.5)*x - max(y,0), axis=1), x,y [4096,4096] f32",
+                   _c1, 2 * 4096 * 4096 * 4 + 4096 * 4, "f32", cpu=_cpu_c1),
+    "c3mm": Workload("bf16_matmul_8192x8192x8192", "bf16 [8192,8192] x [8192,8192] -> bf16, f32 accumulation",
+                     _c3mm, 3 * 8192 * 8192 * 2, "bf16", flops=2 * 8192 ** 3, cpu=_cpu_c3mm),
+    "c3attn": Workload("attention_8x32x2048x128_causal_bf16",
+                       "scores=einsum(bhqd,bhkd), causal select, f32 softmax, context=einsum(bhqk,bhkd) -> bf16",
+                       _c3attn, 2 * 2415919104 + 4294967296, "bf16", flops=2 * 274877906944, cpu=_cpu_c3attn),
+    "c4g": Workload("embedding_gather_128256x4096_bf16_idx8x2048", "table[idx], table [128256,4096] bf16",
+                    _c4g, 16384 * 4096 * 2 + 65536 + 16384 * 4096 * 2, "bf16", cpu=_cpu_c4g),
+    "c4s": Workload("scatter_add_zipf1.1_1048576x256_into_65536_f32",
+                    "operand.at[idx].add(updates), Zipf(1.1) idx, f32, deterministic update order",
+                    lambda: _c4s("f32"), 1073741824 + 4194304 + 2 * 67108864, "f32", cpu=_cpu_c4s),
+    "c4i": Workload("scatter_add_zipf1.1_1048576x256_into_65536_s32",
+                    "operand.at[idx].add(updates), Zipf(1.1) idx, int32 (bit-exact)",
+                    lambda: _c4s("s32"), 1073741824 + 4194304 + 2 * 67108864, "int32", cpu=_cpu_c4s),
     # Calibration only (not a bench line): a plain f32 stream of known size
     # whose FETCH_SIZE / WRITE_SIZE readings scale the other workloads' counters.
-    "copy": dict(
-        workload="stream_negate_8192x4096_f32",
-        desc="out = -x, x [8192,4096] f32 (counter calibration)",
-        bytes=2 * 8192 * 4096 * 4,
-        kernel_bytes=2 * 8192 * 4096 * 4,
-        dtype="f32",
-    ),
+    "copy": Workload("stream_negate_8192x4096_f32", "out = -x, x [8192,4096] f32 (counter calibration)",
+                     _copy, 2 * 8192 * 4096 * 4, "f32", cpu=_cpu_copy),
 }
 
 
-def make(config: str):
-    import numpy as np
-    from oracle import ops  # input makers only; the timed path never calls the oracle
-    from pjrtx_amd import programs
-    if config == "c2":
-        text = programs.c2_argmax_f16_reductions(64, 128256)
-        inputs = [ops.c2_inputs(64, 128256, seed=0)]
-        dtypes = ["bf16"]
-    elif config == "copy":
-        text = programs.stream_negate(8192, 4096)
-        inputs = [np.random.default_rng(0).standard_normal((8192, 4096), dtype=np.float32)]
-        dtypes = [None]
-    else:
-        text = programs.c1_elementwise_rowsum(4096, 4096)
-        inputs = list(ops.c1_inputs(4096, 4096, seed=0))
-        dtypes = [None, None]
-    return text, inputs, dtypes
-
-
-def cpu_baseline(config: str, inputs, budget_s: float = 10.0) -> dict:
-    """The numpy oracle on this host's cores over the same workload, repeated
-    for about `budget_s` seconds (a reported baseline, not the target)."""
-    import numpy as np
-    from oracle import ops
-    fn = {"c2": lambda: ops.c2_reference(inputs[0]), "c1": lambda: ops.c1_rowsum(*inputs),
-          "copy": lambda: np.negative(inputs[0])}[config]
+def cpu_baseline(W: Workload, inputs, budget_s: float = 10.0) -> dict:
+    """The numpy oracle on this host over a bounded sample of the workload,
+    repeated for about `budget_s` seconds (a reported baseline, not the
+    target), scaled to the full step."""
+    fn, frac, sample = W.cpu(inputs)
     fn()
-    n = 0
-    t0 = time.perf_counter()
+    n, t0 = 0, time.perf_counter()
     while True:
         fn()
         n += 1
         el = time.perf_counter() - t0
         if el > budget_s or n >= 1000:
             break
-    per = el / n
-    gbps = WORKLOADS[config]["bytes"] / per / 1e9
-    return {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"full workload x{n} calls of the numpy oracle ({per * 1e3:.1f} ms/call, single-threaded numpy)"}
-
-
-def traffic_from_profiles(config: str):
-    p = ROOT / "profiles" / f"{WORKLOADS[config]['workload']}_traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            return None
-    return None
+    step_s = el / n / frac
+    out = {"unit": "TFLOP/s" if W.flops else "GB/s", "cores": host_threads(), "kind": "port",
+           "sample": f"{sample}; {n} calls, {el / n * 1e3:.1f} ms/call"}
+    out["value"] = round(W.flops / step_s / 1e12, 4) if W.flops else round(W.bytes / step_s / 1e9, 3)
+    if "BLAS" not in sample:
+        out["cores"] = 1  # numpy elementwise / indexing runs on one thread
+    return out
 
 
 def launch_units(plan: dict) -> list[dict]:
     """The plan's launch units in the order pjrtx_executable_time_steps
     reports them (a split reduction is a main and a combine unit), each with
     its algorithmic bytes (inputs read once + outputs written; 0 for a
-    combine pass, which only reads the partial slots)."""
+    combine pass, which only reads the partial slots) and dot flops."""
     units = []
     for st in plan["steps"]:
         if st["kind"] == "alias":
-            units.append({"name": "-", "bytes": 0})
+            units.append({"name": "-", "bytes": 0, "flops": 0})
             continue
         name = st["name"] or ("lib:" + st.get("library", "?"))
-        units.append({"name": name, "bytes": sum(st["in_bytes"]) + sum(st["out_bytes"])})
+        units.append({"name": name, "bytes": sum(st["in_bytes"]) + sum(st["out_bytes"]),
+                      "flops": st.get("flops", 0)})
         if st["kind"] == "reduce" and st.get("splits", 1) > 1:
-            units.append({"name": name + "_combine", "bytes": 0})
+            units.append({"name": name + "_combine", "bytes": 0, "flops": 0})
     return units
 
 
-def bench_c5(a) -> int:
+def roofline(units, unit_ms, names, dtype: str) -> dict:
+    """Roofline of the dominant launch unit: HBM-bound unless its arithmetic
+    intensity is past the MFMA ridge point."""
+    k = max(range(len(unit_ms)), key=lambda i: unit_ms[i] if units[i]["bytes"] else -1)
+    u, sec = units[k], unit_ms[k] / 1e3
+    peak_tf = MFMA_PEAK_TFLOPS.get(dtype, MFMA_PEAK_TFLOPS["bf16"])
+    ridge = peak_tf * 1e12 / (HBM_PEAK_GBPS * 1e9)
+    out = {"kernel": names[k], "kernel_us": round(unit_ms[k] * 1e3, 3), "kernel_algorithmic_bytes": u["bytes"]}
+    if u["flops"] and u["flops"] / max(u["bytes"], 1) > ridge:
+        ach = u["flops"] / sec / 1e12
+        out.update({"bound": "mfma", "achieved": round(ach, 2), "peak": peak_tf, "unit": "TFLOP/s",
+                    "frac": round(ach / peak_tf, 4), "kernel_flops": u["flops"]})
+    else:
+        ach = u["bytes"] / sec / 1e9
+        out.update({"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBPS, 4)})
+        if u["flops"]:
+            out["kernel_tflops"] = round(u["flops"] / sec / 1e12, 2)
+    keys = ["bound", "achieved", "peak", "unit", "frac"]
+    return {**{kk: out[kk] for kk in keys}, "traffic": None, **{kk: v for kk, v in out.items() if kk not in keys}}
+
+
+def traffic_from_profiles(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel`, from the counter summary committed
+    under profiles/ (null when that kernel was not profiled)."""
+    p = ROOT / "profiles" / f"{workload}_traffic.json"
+    if p.exists():
+        try:
+            d = json.loads(p.read_text())
+            if d.get("kernel") == kernel:
+                return d.get("hbm_bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def bench_program(a, W: Workload) -> dict:
+    from pjrtx_amd.pjrt import Client
+    text, inputs, dtypes = W.make()
+    client = Client()
+    exe = client.compile(text)
+    bufs = [client.buffer(x, dt) for x, dt in zip(inputs, dtypes)]
+    for b in bufs:
+        b.block_until_ready()
+    outs = None
+    for _ in range(a.warmup):
+        outs = exe.execute_buffers(bufs)
+    if outs:
+        outs[-1].block_until_ready()
+    del outs
+    t0 = time.perf_counter()
+    last = None
+    for _ in range(a.steps):
+        last = exe.execute_buffers(bufs)
+    last[-1].block_until_ready()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / a.steps
+    del last
+
+    plan = json.loads(exe.optimized_program())
+    units = launch_units(plan)
+    unit_ms = exe.time_steps(bufs, iters=max(10, min(50, a.steps)))
+    names = exe.step_names()
+    assert len(units) == len(unit_ms) == len(names), (len(units), len(unit_ms), len(names))
+    rf = roofline(units, unit_ms, names, W.dtype)
+    rf["traffic"] = traffic_from_profiles(W.workload, rf["kernel"])
+    sec = ms_per_step / 1e3
+    if W.flops:
+        metric, value, unit = "dot_general TFLOP/s (% MFMA peak)", W.flops / sec / 1e12, "TFLOP/s"
+        pct = 100 * value / MFMA_PEAK_TFLOPS.get(W.dtype, 2500.0)
+    else:
+        metric, value, unit = "fused-op HBM GB/s (% peak)", W.bytes / sec / 1e9, "GB/s"
+        pct = 100 * value / HBM_PEAK_GBPS
+    line = {
+        "metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": W.dtype,
+        "data": "synthetic (seeded numpy inputs, resident in HBM before timing)",
+        "config": {"workload": W.workload, "desc": W.desc, "algorithmic_bytes": W.bytes,
+                   **({"flops": W.flops} if W.flops else {}),
+                   "pct_peak_end_to_end": round(pct, 2),
+                   "hbm_gbps_end_to_end": round(W.bytes / sec / 1e9, 2),
+                   "kernels_per_step": sum(1 for n in names if n != "-"),
+                   "kernel_us": {n: round(t * 1e3, 3) for n, t in zip(names, unit_ms) if n != "-"}},
+        "roofline": rf,
+    }
+    if not a.no_cpu_baseline and W.cpu:
+        line["cpu_baseline"] = cpu_baseline(W, inputs)
+    return line
+
+
+def bench_c5(a) -> dict:
     """C5: greedy decode of the llama-like model. A step is one decode token
     (one PJRT execute of the decode program, caches donated). Prefill of the
     512-token prompt is timed separately and reported in `config`."""
@@ -158,56 +398,38 @@ def bench_c5(a) -> int:
     ms_per_step = decode_s * 1e3 / steps
     tokens = [int(x.to_numpy()[0]) for x in toks]
 
-    # Per-launch timing of one decode step (HIP events on the plugin stream).
     plan = json.loads(runner.decode.optimized_program())
     units = launch_units(plan)
     args = runner.weights + [tok, pos_bufs[-1]] + caches
     unit_ms = runner.decode.time_steps(args, iters=20)
     names = runner.decode.step_names()
     assert len(units) == len(unit_ms) == len(names), (len(units), len(unit_ms), len(names))
-    k = max(range(len(unit_ms)), key=lambda i: unit_ms[i] if units[i]["bytes"] else -1)
-    kernel_ms = unit_ms[k]
     by_kind: dict[str, float] = {}
     for u, ms in zip(units, unit_ms):
         key = u["name"] if u["name"].startswith("lib:") else ("fusion_combine" if u["name"].endswith("_combine")
                                                                else "fusion")
         by_kind[key] = by_kind.get(key, 0.0) + ms * 1e3
     weight_bytes = 2 * L.num_params(cfg) - 2 * cfg.vocab * cfg.d_model + 2 * cfg.d_model  # one embedding row
-    kv_bytes = 2 * cfg.layers * 2 * cfg.heads * cfg.head_dim * (cfg.max_len + 1)  # cache read over max_len + new row
+    kv_bytes = 2 * cfg.layers * 2 * cfg.heads * cfg.head_dim * (cfg.max_len + 1)  # cache read + new row
     step_bytes = weight_bytes + kv_bytes
     line = {
         "metric": "llama-like decode tokens/s (greedy, batch 1)",
-        "value": round(steps / decode_s, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "value": round(steps / decode_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init bf16 weights 0.02*N(0,1) seed 0, random 512-token prompt seed 1)",
         "config": {"workload": "llama_like_decode_8L_d2048_h16x128_ffn5632_v32000_prompt512",
-                   "prefill_ms": round(prefill_s * 1e3, 3),
-                   "prefill_tokens_per_s": round(p / prefill_s, 1),
-                   "setup_s": round(setup_s, 1),
-                   "decode_step_hbm_bytes": step_bytes,
+                   "prefill_ms": round(prefill_s * 1e3, 3), "prefill_tokens_per_s": round(p / prefill_s, 1),
+                   "setup_s": round(setup_s, 1), "decode_step_hbm_bytes": step_bytes,
                    "decode_step_gbps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
                    "launch_units_per_step": sum(1 for n in names if n != "-"),
                    "gpu_us_per_step_by_kind": {kk: round(v, 2) for kk, v in sorted(by_kind.items())},
-                   "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2),
-                   "first_tokens": tokens[:8]},
-        "roofline": {"bound": "hbm", "achieved": round(units[k]["bytes"] / (kernel_ms / 1e3) / 1e9, 2),
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(units[k]["bytes"] / (kernel_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": names[k], "kernel_us": round(kernel_ms * 1e3, 3),
-                     "kernel_algorithmic_bytes": units[k]["bytes"]},
+                   "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2), "first_tokens": tokens[:8]},
+        "roofline": roofline(units, unit_ms, names, "bf16"),
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_c5(cfg, weights, prompt, tokens)
-    print(json.dumps(line))
-    return 0
+    return line
 
 
 def cpu_baseline_c5(cfg, weights, prompt, tokens, budget_s: float = 15.0) -> dict:
@@ -225,18 +447,16 @@ def cpu_baseline_c5(cfg, weights, prompt, tokens, budget_s: float = 15.0) -> dic
         if time.perf_counter() - t0 > budget_s:
             break
     el = time.perf_counter() - t0
-    import os
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
-    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": host_threads(), "kind": "port",
             "sample": f"{n} decode steps of the numpy oracle after the 512-token prefill "
-                      f"({el / n * 1e3:.0f} ms/token, numpy matmul on all host cores)"}
+                      f"({el / n * 1e3:.0f} ms/token, numpy matmul on all host threads)"}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; c3/c4 20; c5 128 tokens)")
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", choices=sorted(WORKLOADS) + ["c5"], default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
@@ -244,65 +464,12 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); "
               "multi-GPU sharding is design-only", file=sys.stderr)
         return 2
-
-    if a.config == "c5":
-        return bench_c5(a)
-
-    from pjrtx_amd.pjrt import Client
-    W = WORKLOADS[a.config]
-    text, inputs, dtypes = make(a.config)
-    client = Client()
-    exe = client.compile(text)
-    bufs = [client.buffer(x, dt) for x, dt in zip(inputs, dtypes)]
-    for b in bufs:
-        b.block_until_ready()
-
-    for _ in range(a.warmup):
-        outs = exe.execute_buffers(bufs)
-    outs[-1].block_until_ready()
-    del outs
-
-    t0 = time.perf_counter()
-    last = None
-    for _ in range(a.steps):
-        last = exe.execute_buffers(bufs)
-    last[-1].block_until_ready()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / a.steps
-    value = W["bytes"] / (ms_per_step / 1e3) / 1e9
-
-    # Dominant kernel: per-launch HIP-event timing on the plugin's stream
-    # (a split reduction's main and combine kernels are timed separately).
-    unit_ms = exe.time_steps(bufs, iters=max(50, a.steps))
-    names = exe.step_names()
-    k = max(range(len(unit_ms)), key=lambda i: unit_ms[i])
-    kernel_ms = unit_ms[k]
-    achieved = W["kernel_bytes"] / (kernel_ms / 1e3) / 1e9
-
-    line = {
-        "metric": "fused-op HBM GB/s (% peak)",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": W["dtype"],
-        "data": "synthetic (seeded numpy inputs, resident in HBM before timing)",
-        "config": {"workload": W["workload"], "desc": W["desc"], "algorithmic_bytes": W["bytes"],
-                   "pct_hbm_peak_end_to_end": round(100 * value / HBM_PEAK_GBPS, 2),
-                   "kernels_per_step": sum(1 for n in names if n != "-"),
-                   "kernel_us": {n: round(t * 1e3, 3) for n, t in zip(names, unit_ms)}},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profiles(a.config),
-                     "kernel": names[k], "kernel_us": round(kernel_ms * 1e3, 3),
-                     "kernel_algorithmic_bytes": W["kernel_bytes"]},
-    }
-    if not a.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(a.config, inputs)
+    heavy = a.config.startswith(("c3", "c4"))
+    if a.steps is None:
+        a.steps = 128 if a.config == "c5" else (20 if heavy else 200)
+    if a.warmup is None:
+        a.warmup = 3 if heavy else 10
+    line = bench_c5(a) if a.config == "c5" else bench_program(a, WORKLOADS[a.config])
     print(json.dumps(line))
     return 0
 

@@ -251,6 +251,23 @@ def scatter_rows_add_int(operand, idx, updates):
     return out.astype(operand.dtype)
 
 
+def scatter_rows_add_f64(operand, idx, updates):
+    """The exact (float64) value of the row scatter-add, for bounding the
+    rounding of any summation order."""
+    out = np.asarray(operand, np.float64).copy()
+    idx = np.asarray(idx)
+    valid = (idx >= 0) & (idx < out.shape[0])
+    np.add.at(out, idx[valid], np.asarray(updates, np.float64)[valid])
+    return out
+
+
+def segment_lengths(idx, rows: int) -> np.ndarray:
+    """Number of in-bounds updates per operand row."""
+    idx = np.asarray(idx)
+    valid = (idx >= 0) & (idx < rows)
+    return np.bincount(idx[valid], minlength=rows)
+
+
 def zipf_indices(n: int, rows: int, seed: int = 0, a: float = 1.1) -> np.ndarray:
     return ((np.random.default_rng(seed).zipf(a, n) - 1) % rows).astype(np.int32)
 

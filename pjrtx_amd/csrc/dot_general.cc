@@ -157,24 +157,25 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
       b_kmajor = true;
     }
     if ((a_fast || a_copy) && (b_kmajor || b_nmajor) && K % 8 == 0) {
-      if (M <= 8 && batch == 1) {
+      if (M <= 8) {
         GemvParams g;
+        g.batch = static_cast<int>(batch);
         g.M = static_cast<int>(M);
         g.N = static_cast<int>(N);
         g.K = static_cast<int>(K);
         g.ldx = a.fs ? a.fs : K;
         g.ldw = b_kmajor ? (b.fs ? b.fs : K) : (b.ks ? b.ks : N);
         g.ldy = N;
-        const int64_t col_blocks = b_kmajor ? (N + 3) / 4 : (N + 2047) / 2048;
-        int64_t ksplit = std::max<int64_t>(1, std::min<int64_t>(512 / std::max<int64_t>(col_blocks, 1), K / 64));
-        if (b_kmajor) ksplit = std::max<int64_t>(1, std::min<int64_t>(ksplit, K / 512));
-        int64_t kchunk = (K + ksplit - 1) / ksplit;
-        kchunk = (kchunk + 7) / 8 * 8;
-        ksplit = (K + kchunk - 1) / kchunk;
-        g.kchunk = static_cast<int>(kchunk);
-        g.ksplit = static_cast<int>(ksplit);
-        MemRef part = dev->allocate(static_cast<size_t>(ksplit * M * N) * 4);
-        launch_gemv(dev->stream(), g, A, B, out, static_cast<float*>(part->ptr), f16, b_kmajor, out_kind);
+        g.x_bs = a.bs;
+        g.w_bs = b.bs;
+        g.y_bs = M * N;
+        g.out_kind = out_kind;
+        MemRef part;
+        if (!b_kmajor) {
+          plan_gemv_split(&g);
+          if (g.ksplit > 1) part = dev->allocate(static_cast<size_t>(batch * g.ksplit * M * N) * 4);
+        }
+        launch_gemv(dev->stream(), g, A, B, out, part ? static_cast<float*>(part->ptr) : nullptr, f16, b_kmajor);
         return;
       }
       GemmParams g;

@@ -20,16 +20,25 @@ struct GemmParams {
 void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const void* B, void* C, bool f16, bool b_kmajor,
                       int out_bytes);
 
-// Y[m][n] = sum_k X[m][k] * W[.]: M in 1..8; W [K][N] (ldw = row stride) or,
-// when K-major, [N][K]. `partials` holds ksplit*M*N floats.
+// Y[b][m][n] = sum_k X[b][m][k] * W[b][.]: M in 1..8 (decode rows). W is
+// [K][N] (N contiguous, row stride ldw) or, when K-major, [N][K] (K
+// contiguous, row stride ldw). Strides in elements; batch strides x_bs,
+// w_bs, y_bs. N-contiguous W is split over K into `ksplit` chunks of
+// `kchunk` rows; `partials` then holds batch*ksplit*M*N floats.
 struct GemvParams {
-  int M = 1, N = 0, K = 0;
+  int batch = 1, M = 1, N = 0, K = 0;
   int64_t ldx = 0, ldw = 0, ldy = 0;
+  int64_t x_bs = 0, w_bs = 0, y_bs = 0;
   int kchunk = 0, ksplit = 1;
+  int out_kind = 0;  // 0 bf16, 1 f16, 2 f32
 };
-// out_kind: 0 bf16, 1 f16, 2 f32
+// Columns per workgroup of the N-contiguous kernel (64 lanes x 8).
+constexpr int kGemvCols = 512;
+// Split plan for an N-contiguous GEMV: fills kchunk / ksplit so the launch
+// reaches about `target_blocks` workgroups.
+void plan_gemv_split(GemvParams* p, int target_blocks = 512);
 void launch_gemv(hipStream_t s, const GemvParams& p, const void* X, const void* W, void* Y, float* partials, bool f16,
-                 bool w_kmajor, int out_kind);
+                 bool w_kmajor);
 
 // Fallback with arbitrary element strides.
 struct FmaGemmParams {

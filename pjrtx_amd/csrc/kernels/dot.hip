@@ -16,6 +16,8 @@
 // MSL dot steps (metal_graph_dot.zig:14-324, scalar FMA only).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels/dot.h"
 
@@ -228,90 +230,161 @@ __global__ void __launch_bounds__(256) mfma_gemm(GemmParams p, const uint16_t* _
 }
 
 // ------------------------------------------------------------------- GEMV
-// y[m][n] = sum_k x[m][k] * W[k][n] for M <= 8, W N-contiguous ([K][N]) or
-// K-contiguous ([N][K]). Pass 1: each workgroup reduces a K-chunk for 2048
-// (N-contiguous) or 256 (K-contiguous) columns into f32 partials; pass 2 sums
-// the chunks in order and rounds.
+// Decode-shaped products (M <= 8) are bound by streaming W once.
+//
+// gemv_n (W [K][N], N contiguous): a workgroup owns 512 columns (one 16-byte
+// vector per lane) and a chunk of K rows; its 4 waves take interleaved rows,
+// each lane issuing 8 row loads before using them so that ~32 KB per
+// workgroup is in flight. The waves' sums are combined through LDS in wave
+// order. With one K chunk the result is rounded and stored directly;
+// otherwise f32 partials go to gemv_reduce, which sums the chunks in a
+// fixed order (deterministic).
+//
+// gemv_k (W [N][K], K contiguous): G lanes share a row (G*8 >= K when K <=
+// 512), so one wave covers 64/G rows; the G partial sums are folded by xor
+// shuffles. One pass, no partials.
+constexpr int kGemvRowsPerLane = 8;
+
+template <bool kF16>
+__device__ __forceinline__ float half_to_f32(uint16_t v) {
+  return kF16 ? f16_bits_to_f32(v) : bf16_bits_to_f32(v);
+}
+
+__device__ __forceinline__ void store_out(void* Y, int64_t i, float v, int out_kind) {
+  if (out_kind == 0) reinterpret_cast<uint16_t*>(Y)[i] = f32_to_bf16_rne(v);
+  else if (out_kind == 1) reinterpret_cast<uint16_t*>(Y)[i] = f32_to_f16_bits(v);
+  else reinterpret_cast<float*>(Y)[i] = v;
+}
+
 template <int kM, bool kF16>
-__global__ void __launch_bounds__(256) gemv_nmajor(GemvParams p, const uint16_t* __restrict__ X,
-                                                   const uint16_t* __restrict__ W, float* __restrict__ part) {
-  const int n = (blockIdx.x * 256 + threadIdx.x) * 8;
-  const int kc = blockIdx.y;
+__global__ void __launch_bounds__(256) gemv_n(GemvParams p, const uint16_t* __restrict__ X,
+                                              const uint16_t* __restrict__ W, float* __restrict__ part,
+                                              void* __restrict__ Y) {
+  __shared__ float red[4][kM][kGemvCols];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int b = blockIdx.z, kc = blockIdx.y;
+  const int n0 = blockIdx.x * kGemvCols;
+  const int n = n0 + lane * 8;
   const int k0 = kc * p.kchunk, k1 = min(p.K, k0 + p.kchunk);
+  const uint16_t* Wb = W + (int64_t)b * p.w_bs;
+  const uint16_t* Xb = X + (int64_t)b * p.x_bs;
   float acc[kM][8];
 #pragma unroll
   for (int m = 0; m < kM; ++m)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
+  const bool full = n + 8 <= p.N;
   if (n < p.N) {
-    const bool full = n + 8 <= p.N;
-    for (int k = k0; k < k1; ++k) {
-      uint16_t w[8];
-      if (full) {
-        *reinterpret_cast<u32x4*>(w) = *reinterpret_cast<const u32x4*>(W + (int64_t)k * p.ldw + n);
-      } else {
-        for (int e = 0; e < 8; ++e) w[e] = (n + e < p.N) ? W[(int64_t)k * p.ldw + n + e] : (uint16_t)0;
+    for (int kb = k0 + wave; kb < k1; kb += 4 * kGemvRowsPerLane) {
+      u32x4 w[kGemvRowsPerLane];
+#pragma unroll
+      for (int r = 0; r < kGemvRowsPerLane; ++r) {
+        const int k = kb + 4 * r;
+        const uint16_t* src = Wb + (int64_t)k * p.ldw + n;
+        if (k < k1 && full) {
+          w[r] = *reinterpret_cast<const u32x4*>(src);
+        } else {
+          uint16_t t[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) t[e] = (k < k1 && n + e < p.N) ? src[e] : (uint16_t)0;
+          w[r] = *reinterpret_cast<const u32x4*>(t);
+        }
       }
 #pragma unroll
-      for (int m = 0; m < kM; ++m) {
-        const float xv = kF16 ? f16_bits_to_f32(X[(int64_t)m * p.ldx + k]) : bf16_bits_to_f32(X[(int64_t)m * p.ldx + k]);
+      for (int r = 0; r < kGemvRowsPerLane; ++r) {
+        const int k = kb + 4 * r;
+        if (k < k1) {
+          const uint16_t* we = reinterpret_cast<const uint16_t*>(&w[r]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[m][e] += xv * (kF16 ? f16_bits_to_f32(w[e]) : bf16_bits_to_f32(w[e]));
+          for (int m = 0; m < kM; ++m) {
+            const float xv = m < p.M ? half_to_f32<kF16>(Xb[(int64_t)m * p.ldx + k]) : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[m][e] += xv * half_to_f32<kF16>(we[e]);
+          }
+        }
       }
     }
+  }
 #pragma unroll
-    for (int m = 0; m < kM; ++m)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (n + e < p.N) part[((int64_t)kc * kM + m) * p.N + n + e] = acc[m][e];
+  for (int m = 0; m < kM; ++m) {
+    float4* dst = reinterpret_cast<float4*>(&red[wave][m][lane * 8]);
+    dst[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+    dst[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kM * kGemvCols; i += 256) {
+    const int m = i / kGemvCols, c = i - m * kGemvCols;
+    const int nn = n0 + c;
+    if (m >= p.M || nn >= p.N) continue;
+    const float v = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
+    if (p.ksplit == 1) {
+      store_out(Y, (int64_t)b * p.y_bs + (int64_t)m * p.ldy + nn, v, p.out_kind);
+    } else {
+      part[(((int64_t)b * p.ksplit + kc) * p.M + m) * p.N + nn] = v;
+    }
   }
 }
 
-template <int kM, bool kF16>
-__global__ void __launch_bounds__(256) gemv_kmajor(GemvParams p, const uint16_t* __restrict__ X,
-                                                   const uint16_t* __restrict__ W, float* __restrict__ part) {
-  // One wave per column n; lanes stride over K in 8-element chunks.
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int kc = blockIdx.y;
-  const int k0 = kc * p.kchunk, k1 = min(p.K, k0 + p.kchunk);
-  if (n >= p.N) return;
+// Sums the K-chunk partials of gemv_n: 32 columns x 8 chunk groups per
+// workgroup; group g adds chunks g, g+8, ... in order, then the 8 group sums
+// are added in group order.
+__global__ void __launch_bounds__(256) gemv_reduce(GemvParams p, const float* __restrict__ part,
+                                                   void* __restrict__ Y) {
+  __shared__ float s[8][33];
+  const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
+  const int n = blockIdx.x * 32 + c, m = blockIdx.y, b = blockIdx.z;
+  float v = 0.f;
+  if (n < p.N) {
+    const float* src = part + ((int64_t)b * p.ksplit * p.M + m) * p.N + n;
+    const int64_t step = (int64_t)p.M * p.N;
+#pragma unroll 4
+    for (int kc = g; kc < p.ksplit; kc += 8) v += src[kc * step];
+  }
+  s[g][c] = v;
+  __syncthreads();
+  if (g == 0 && n < p.N) {
+    float t = s[0][c];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t += s[j][c];
+    store_out(Y, (int64_t)b * p.y_bs + (int64_t)m * p.ldy + n, t, p.out_kind);
+  }
+}
+
+template <int kM, bool kF16, int G>
+__global__ void __launch_bounds__(256) gemv_k(GemvParams p, const uint16_t* __restrict__ X,
+                                              const uint16_t* __restrict__ W, void* __restrict__ Y) {
+  constexpr int kRowsPerWave = 64 / G;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane / G, gl = lane - sub * G;
+  const int n = (blockIdx.x * 4 + wave) * kRowsPerWave + sub;
+  const int b = blockIdx.z;
   float acc[kM];
 #pragma unroll
   for (int m = 0; m < kM; ++m) acc[m] = 0.f;
-  for (int k = k0 + lane * 8; k < k1; k += 512) {
-    uint16_t w[8];
-    if (k + 8 <= k1) *reinterpret_cast<u32x4*>(w) = *reinterpret_cast<const u32x4*>(W + (int64_t)n * p.ldw + k);
-    else
-      for (int e = 0; e < 8; ++e) w[e] = (k + e < k1) ? W[(int64_t)n * p.ldw + k + e] : (uint16_t)0;
+  if (n < p.N) {
+    const uint16_t* wr = W + (int64_t)b * p.w_bs + (int64_t)n * p.ldw;
+    const uint16_t* Xb = X + (int64_t)b * p.x_bs;
+#pragma unroll 4
+    for (int k = gl * 8; k < p.K; k += G * 8) {  // K % 8 == 0 (checked by the caller)
+      const u32x4 w = *reinterpret_cast<const u32x4*>(wr + k);
+      const uint16_t* we = reinterpret_cast<const uint16_t*>(&w);
 #pragma unroll
-    for (int m = 0; m < kM; ++m)
+      for (int m = 0; m < kM; ++m) {
+        if (m >= p.M) break;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(Xb + (int64_t)m * p.ldx + k);
+        const uint16_t* xe = reinterpret_cast<const uint16_t*>(&x);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t xb = (k + e < k1) ? X[(int64_t)m * p.ldx + k + e] : (uint16_t)0;
-        acc[m] += (kF16 ? f16_bits_to_f32(xb) : bf16_bits_to_f32(xb)) * (kF16 ? f16_bits_to_f32(w[e]) : bf16_bits_to_f32(w[e]));
+        for (int e = 0; e < 8; ++e) acc[m] += half_to_f32<kF16>(xe[e]) * half_to_f32<kF16>(we[e]);
       }
+    }
   }
 #pragma unroll
   for (int m = 0; m < kM; ++m) {
     float v = acc[m];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) part[((int64_t)kc * kM + m) * p.N + n] = v;
+    for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (gl == 0 && n < p.N && m < p.M) store_out(Y, (int64_t)b * p.y_bs + (int64_t)m * p.ldy + n, v, p.out_kind);
   }
-}
-
-template <int kM>
-__global__ void __launch_bounds__(256) gemv_finish(GemvParams p, const float* __restrict__ part, void* __restrict__ Y,
-                                                   int out_kind) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over kM * N
-  if (i >= (int64_t)kM * p.N) return;
-  const int m = (int)(i / p.N), n = (int)(i - (int64_t)m * p.N);
-  float s = 0.f;
-  for (int kc = 0; kc < p.ksplit; ++kc) s += part[((int64_t)kc * kM + m) * p.N + n];
-  if (out_kind == 0) reinterpret_cast<uint16_t*>(Y)[(int64_t)m * p.ldy + n] = f32_to_bf16_rne(s);
-  else if (out_kind == 1) reinterpret_cast<uint16_t*>(Y)[(int64_t)m * p.ldy + n] = f32_to_f16_bits(s);
-  else reinterpret_cast<float*>(Y)[(int64_t)m * p.ldy + n] = s;
 }
 
 // --------------------------------------------------------------- fallback
@@ -381,36 +454,59 @@ void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const v
   check("mfma_gemm");
 }
 
+void plan_gemv_split(GemvParams* p, int target_blocks) {
+  const int64_t col_tiles = ((int64_t)p->N + kGemvCols - 1) / kGemvCols * p->batch;
+  const int64_t min_rows = 4 * kGemvRowsPerLane;  // one full load round per wave
+  int64_t ksplit = std::max<int64_t>(1, (target_blocks + col_tiles - 1) / col_tiles);
+  ksplit = std::min<int64_t>(ksplit, std::max<int64_t>(1, p->K / min_rows));
+  int64_t kchunk = (p->K + ksplit - 1) / ksplit;
+  kchunk = (kchunk + 3) / 4 * 4;
+  p->kchunk = static_cast<int>(std::max<int64_t>(kchunk, 4));
+  p->ksplit = static_cast<int>((p->K + p->kchunk - 1) / p->kchunk);
+}
+
 void launch_gemv(hipStream_t s, const GemvParams& p, const void* X, const void* W, void* Y, float* partials, bool f16,
-                 bool w_kmajor, int out_kind) {
+                 bool w_kmajor) {
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const uint16_t* w = static_cast<const uint16_t*>(W);
-#define PJRTX_GEMV(M)                                                                                              \
-  case M:                                                                                                          \
-    if (w_kmajor) {                                                                                                \
-      const dim3 g((p.N + 3) / 4, p.ksplit);                                                                       \
-      if (f16) hipLaunchKernelGGL((gemv_kmajor<M, true>), g, dim3(256), 0, s, p, x, w, partials);                  \
-      else hipLaunchKernelGGL((gemv_kmajor<M, false>), g, dim3(256), 0, s, p, x, w, partials);                     \
-    } else {                                                                                                       \
-      const dim3 g((p.N + 2047) / 2048, p.ksplit);                                                                 \
-      if (f16) hipLaunchKernelGGL((gemv_nmajor<M, true>), g, dim3(256), 0, s, p, x, w, partials);                  \
-      else hipLaunchKernelGGL((gemv_nmajor<M, false>), g, dim3(256), 0, s, p, x, w, partials);                     \
-    }                                                                                                              \
-    hipLaunchKernelGGL((gemv_finish<M>), dim3((unsigned)(((int64_t)M * p.N + 255) / 256)), dim3(256), 0, s, p,     \
-                       partials, Y, out_kind);                                                                     \
-    break;
-  switch (p.M) {
-    PJRTX_GEMV(1)
-    PJRTX_GEMV(2)
-    PJRTX_GEMV(3)
-    PJRTX_GEMV(4)
-    PJRTX_GEMV(5)
-    PJRTX_GEMV(6)
-    PJRTX_GEMV(7)
-    PJRTX_GEMV(8)
-    default: fail(Code::kInternal, "gemv: M must be 1..8");
+  if (p.M < 1 || p.M > 8) fail(Code::kInternal, "gemv: M must be 1..8");
+  if (w_kmajor) {
+    int G = 8;
+    while (G < 64 && G * 8 < p.K) G *= 2;
+    const int rows_per_block = 4 * (64 / G);
+    const dim3 g((unsigned)((p.N + rows_per_block - 1) / rows_per_block), 1, (unsigned)p.batch);
+#define PJRTX_GEMV_K(KM, GG)                                                                                  \
+  if (f16) hipLaunchKernelGGL((gemv_k<KM, true, GG>), g, dim3(256), 0, s, p, x, w, Y);                        \
+  else hipLaunchKernelGGL((gemv_k<KM, false, GG>), g, dim3(256), 0, s, p, x, w, Y);
+#define PJRTX_GEMV_KM(KM)            \
+  switch (G) {                       \
+    case 8: PJRTX_GEMV_K(KM, 8) break;   \
+    case 16: PJRTX_GEMV_K(KM, 16) break; \
+    case 32: PJRTX_GEMV_K(KM, 32) break; \
+    default: PJRTX_GEMV_K(KM, 64) break; \
   }
-#undef PJRTX_GEMV
+    if (p.M == 1) { PJRTX_GEMV_KM(1) }
+    else if (p.M <= 2) { PJRTX_GEMV_KM(2) }
+    else if (p.M <= 4) { PJRTX_GEMV_KM(4) }
+    else { PJRTX_GEMV_KM(8) }
+#undef PJRTX_GEMV_KM
+#undef PJRTX_GEMV_K
+    check("gemv_k");
+    return;
+  }
+  const dim3 g((unsigned)((p.N + kGemvCols - 1) / kGemvCols), (unsigned)p.ksplit, (unsigned)p.batch);
+#define PJRTX_GEMV_N(KM)                                                                          \
+  if (f16) hipLaunchKernelGGL((gemv_n<KM, true>), g, dim3(256), 0, s, p, x, w, partials, Y);      \
+  else hipLaunchKernelGGL((gemv_n<KM, false>), g, dim3(256), 0, s, p, x, w, partials, Y);
+  if (p.M == 1) { PJRTX_GEMV_N(1) }
+  else if (p.M <= 2) { PJRTX_GEMV_N(2) }
+  else if (p.M <= 4) { PJRTX_GEMV_N(4) }
+  else { PJRTX_GEMV_N(8) }
+#undef PJRTX_GEMV_N
+  if (p.ksplit > 1) {
+    const dim3 gr((unsigned)((p.N + 31) / 32), (unsigned)p.M, (unsigned)p.batch);
+    hipLaunchKernelGGL(gemv_reduce, gr, dim3(256), 0, s, p, partials, Y);
+  }
   check("gemv");
 }
 

@@ -52,6 +52,17 @@ void launch_radix_sort(hipStream_t s, uint32_t* keys, uint32_t* vals, uint32_t* 
 // Combiner of the scatter region.
 enum class ScatterOp { kAdd, kSet, kMax, kMin, kMul };
 
+// Row mode, long segments: a segment (the updates of one operand row, in
+// update order) is cut into chunks of kScatterChunk updates. Chunk 0 folds
+// from the operand row, later chunks from their own first update; a row
+// with one chunk writes its result directly (the exact sequential fold),
+// otherwise the chunk partials are folded in chunk order.
+constexpr int kScatterChunk = 256;
+size_t scatter_chunk_scratch_bytes(int64_t rows, int64_t n, int64_t row_elems, DType t);
+void launch_scatter_chunked(hipStream_t s, int64_t rows, int64_t row_elems, int64_t n, int op, DType t,
+                            const void* operand, const void* updates, const uint32_t* perm,
+                            const uint32_t* seg_start, const uint32_t* seg_end, void* scratch, void* out);
+
 struct ScatterFoldParams {
   int64_t rows = 0;       // operand rows (element mode: operand elements)
   int64_t row_elems = 1;  // elements per row (element mode: 1)

@@ -332,6 +332,130 @@ __global__ void __launch_bounds__(64) scatter_fold(ScatterFoldParams p, const ty
   out[t] = K::st(acc);
 }
 
+// ------------------------------------------------------- chunked row fold
+constexpr int kFoldDepth = 16;  // update rows in flight per lane
+
+template <typename T, int VEC>
+struct alignas(sizeof(T) * VEC) VecOf {
+  T v[VEC];
+};
+
+__global__ void __launch_bounds__(256) chunk_count(const uint32_t* __restrict__ seg_start,
+                                                   const uint32_t* __restrict__ seg_end, int64_t rows,
+                                                   uint32_t* __restrict__ cnt) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const uint32_t len = seg_end[r] - seg_start[r];
+  cnt[r] = len <= (uint32_t)kScatterChunk ? 1u : (len + kScatterChunk - 1) / kScatterChunk;
+}
+
+__global__ void __launch_bounds__(256) chunk_rows(const uint32_t* __restrict__ cnt, const uint32_t* __restrict__ off,
+                                                  int64_t rows, uint32_t* __restrict__ chunk_row,
+                                                  uint32_t* __restrict__ total) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const uint32_t o = off[r], c = cnt[r];
+  for (uint32_t q = 0; q < c; ++q) chunk_row[o + q] = (uint32_t)r;
+  if (r == rows - 1) total[0] = o + c;
+}
+
+// One wave per chunk; 4 chunks per workgroup.
+template <typename Tag, int VEC>
+__global__ void __launch_bounds__(256) scatter_chunk_fold(
+    int64_t row_elems, ScatterOp op, const typename StorageOf<Tag>::T* __restrict__ operand,
+    const typename StorageOf<Tag>::T* __restrict__ updates, const uint32_t* __restrict__ perm,
+    const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ seg_end, const uint32_t* __restrict__ cnt,
+    const uint32_t* __restrict__ off, const uint32_t* __restrict__ chunk_row, const uint32_t* __restrict__ total,
+    typename StorageOf<Tag>::T* __restrict__ partial, typename StorageOf<Tag>::T* __restrict__ out) {
+  typedef Codec<Tag> K;
+  typedef typename K::C C;
+  typedef typename StorageOf<Tag>::T T;
+  typedef VecOf<T, VEC> V;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t j = blockIdx.x * 4 + wave;
+  if (j >= total[0]) return;
+  const uint32_t r = chunk_row[j];
+  const uint32_t q = j - off[r];
+  const uint32_t lo = seg_start[r] + q * kScatterChunk;
+  const uint32_t hi = min(lo + (uint32_t)kScatterChunk, seg_end[r]);
+  T* dst = cnt[r] == 1 ? out + (int64_t)r * row_elems : partial + (int64_t)j * row_elems;
+  for (int64_t c0 = (int64_t)lane * VEC; c0 < row_elems; c0 += 64 * VEC) {
+    C acc[VEC];
+    uint32_t i = lo;
+    {
+      const V first = q == 0 ? *reinterpret_cast<const V*>(operand + (int64_t)r * row_elems + c0)
+                             : *reinterpret_cast<const V*>(updates + (int64_t)perm[lo] * row_elems + c0);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = K::ld(first.v[e]);
+      if (q != 0) ++i;
+    }
+    for (; i + kFoldDepth <= hi; i += kFoldDepth) {
+      V u[kFoldDepth];
+#pragma unroll
+      for (int d = 0; d < kFoldDepth; ++d)
+        u[d] = *reinterpret_cast<const V*>(updates + (int64_t)perm[i + d] * row_elems + c0);
+#pragma unroll
+      for (int d = 0; d < kFoldDepth; ++d)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u[d].v[e])));
+    }
+    for (; i < hi; ++i) {
+      const V u = *reinterpret_cast<const V*>(updates + (int64_t)perm[i] * row_elems + c0);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u.v[e])));
+    }
+    V o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o.v[e] = K::st(acc[e]);
+    *reinterpret_cast<V*>(dst + c0) = o;
+  }
+}
+
+// Rows with more than one chunk: fold the chunk partials in chunk order. One
+// wave per row, 4 rows per workgroup.
+template <typename Tag, int VEC>
+__global__ void __launch_bounds__(256) scatter_chunk_combine(int64_t rows, int64_t row_elems, ScatterOp op,
+                                                             const uint32_t* __restrict__ cnt,
+                                                             const uint32_t* __restrict__ off,
+                                                             const typename StorageOf<Tag>::T* __restrict__ partial,
+                                                             typename StorageOf<Tag>::T* __restrict__ out) {
+  typedef Codec<Tag> K;
+  typedef typename K::C C;
+  typedef typename StorageOf<Tag>::T T;
+  typedef VecOf<T, VEC> V;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  if (r >= rows) return;
+  const uint32_t n = cnt[r];
+  if (n <= 1) return;
+  const T* src = partial + (int64_t)off[r] * row_elems;
+  for (int64_t c0 = (int64_t)lane * VEC; c0 < row_elems; c0 += 64 * VEC) {
+    C acc[VEC];
+    const V first = *reinterpret_cast<const V*>(src + c0);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = K::ld(first.v[e]);
+    uint32_t qi = 1;
+    for (; qi + kFoldDepth <= n; qi += kFoldDepth) {
+      V u[kFoldDepth];
+#pragma unroll
+      for (int d = 0; d < kFoldDepth; ++d) u[d] = *reinterpret_cast<const V*>(src + (int64_t)(qi + d) * row_elems + c0);
+#pragma unroll
+      for (int d = 0; d < kFoldDepth; ++d)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u[d].v[e])));
+    }
+    for (; qi < n; ++qi) {
+      const V u = *reinterpret_cast<const V*>(src + (int64_t)qi * row_elems + c0);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u.v[e])));
+    }
+    V o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o.v[e] = K::st(acc[e]);
+    *reinterpret_cast<V*>(out + r * row_elems + c0) = o;
+  }
+}
+
 __global__ void __launch_bounds__(256) zero_u32(uint32_t* __restrict__ a, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) a[i] = 0u;
@@ -406,6 +530,71 @@ void launch_scatter_segments(hipStream_t s, const uint32_t* sorted_keys, int64_t
   hipLaunchKernelGGL(scatter_segments, dim3(blocks(n, 256)), dim3(256), 0, s, sorted_keys, n, invalid, seg_start,
                      seg_end);
   check("scatter_segments");
+}
+
+namespace {
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+int64_t max_chunks(int64_t rows, int64_t n) { return rows + (n + kScatterChunk - 1) / kScatterChunk; }
+}  // namespace
+
+size_t scatter_chunk_scratch_bytes(int64_t rows, int64_t n, int64_t row_elems, DType t) {
+  const int64_t mc = max_chunks(rows, n);
+  return 3 * align256(rows * 4) + align256(mc * 4) + align256(256) + align256(kScanTile * 4) +
+         align256(mc * row_elems * dtype_size(t));
+}
+
+void launch_scatter_chunked(hipStream_t s, int64_t rows, int64_t row_elems, int64_t n, int op_i, DType t,
+                            const void* operand, const void* updates, const uint32_t* perm,
+                            const uint32_t* seg_start, const uint32_t* seg_end, void* scratch, void* out) {
+  if (rows == 0 || row_elems == 0) return;
+  const ScatterOp op = static_cast<ScatterOp>(op_i);
+  const int64_t mc = max_chunks(rows, n);
+  char* b = static_cast<char*>(scratch);
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(b);
+  b += align256(rows * 4);
+  uint32_t* off = reinterpret_cast<uint32_t*>(b);
+  b += align256(rows * 4);
+  b += align256(rows * 4);  // reserved
+  uint32_t* chunk_row = reinterpret_cast<uint32_t*>(b);
+  b += align256(mc * 4);
+  uint32_t* total = reinterpret_cast<uint32_t*>(b);
+  b += align256(256);
+  uint32_t* scan_tmp = reinterpret_cast<uint32_t*>(b);
+  b += align256(kScanTile * 4);
+  void* partial = b;
+  hipLaunchKernelGGL(chunk_count, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, seg_end, rows, cnt);
+  exclusive_scan(s, cnt, off, rows, scan_tmp);
+  hipLaunchKernelGGL(chunk_rows, dim3(blocks(rows, 256)), dim3(256), 0, s, cnt, off, rows, chunk_row, total);
+  check("scatter chunk plan");
+  const size_t es = dtype_size(t);
+  const bool vec = (row_elems * es) % 16 == 0 && (reinterpret_cast<uintptr_t>(operand) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(updates) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  const dim3 g1(blocks(mc, 4)), g2(blocks(rows, 4)), blk(256);
+#define PJRTX_CHUNKED(TAG, VEC)                                                                                      \
+  do {                                                                                                               \
+    typedef StorageOf<TAG>::T T_;                                                                                    \
+    hipLaunchKernelGGL((scatter_chunk_fold<TAG, VEC>), g1, blk, 0, s, row_elems, op, (const T_*)operand,            \
+                       (const T_*)updates, perm, seg_start, seg_end, cnt, off, chunk_row, total, (T_*)partial,       \
+                       (T_*)out);                                                                                    \
+    hipLaunchKernelGGL((scatter_chunk_combine<TAG, VEC>), g2, blk, 0, s, rows, row_elems, op, cnt, off,             \
+                       (const T_*)partial, (T_*)out);                                                                \
+  } while (0)
+#define PJRTX_CHUNKED_T(TAG, V16)            \
+  if (vec) PJRTX_CHUNKED(TAG, V16);          \
+  else PJRTX_CHUNKED(TAG, 1);
+  switch (t) {
+    case DType::kF32: PJRTX_CHUNKED_T(float, 4) break;
+    case DType::kF64: PJRTX_CHUNKED_T(double, 2) break;
+    case DType::kBF16: PJRTX_CHUNKED_T(Bf16Tag, 8) break;
+    case DType::kF16: PJRTX_CHUNKED_T(F16Tag, 8) break;
+    case DType::kS32: PJRTX_CHUNKED_T(int32_t, 4) break;
+    case DType::kU32: PJRTX_CHUNKED_T(uint32_t, 4) break;
+    case DType::kS64: PJRTX_CHUNKED_T(int64_t, 2) break;
+    default: fail(Code::kUnimplemented, std::string("scatter: element type not supported: ") + dtype_name(t));
+  }
+#undef PJRTX_CHUNKED_T
+#undef PJRTX_CHUNKED
+  check("scatter_chunk_fold");
 }
 
 void launch_scatter_fold(hipStream_t s, const ScatterFoldParams& p, DType t, const void* operand, const void* updates,

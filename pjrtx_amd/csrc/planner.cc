@@ -103,6 +103,21 @@ bool fusible_concat(const Op& op) {
   return op.kind == OpKind::kConcatenate && op.operands.size() <= kMaxFusedConcatOperands;
 }
 
+// Relative cost of recomputing an op per element, for the recompute-vs-
+// materialize decision: trigonometric ops (argument reduction) and pow are
+// much dearer than an add; exp/log-type ops somewhat.
+int op_cost(OpKind k) {
+  switch (k) {
+    case OpKind::kSine: case OpKind::kCosine: case OpKind::kTan: case OpKind::kAtan2: case OpKind::kPower:
+      return 12;
+    case OpKind::kExp: case OpKind::kExpm1: case OpKind::kLog: case OpKind::kLog1p: case OpKind::kLogistic:
+    case OpKind::kTanh: case OpKind::kCbrt: case OpKind::kDivide: case OpKind::kRemainder:
+      return 4;
+    default:
+      return 1;
+  }
+}
+
 bool is_library(const Op& op) {
   const OpKind k = op.kind;
   return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
@@ -149,6 +164,7 @@ class Planner {
   void closure(const std::vector<int>& roots, std::vector<int>* ops, std::vector<int>* inputs,
                bool roots_are_outputs = true) const;
   void build_steps(std::vector<Step>* steps);
+  int order_preserving_source(int v) const;
   void merge_siblings(std::vector<Step>* steps);
   void merge_epilogues(std::vector<Step>* steps);
   void schedule(std::vector<Step>* steps);
@@ -200,7 +216,7 @@ void Planner::decide_materialization() {
     PJRTX_CHECK(fusible_op(op), Code::kUnimplemented,
                 std::string("op not supported by the HIP backend: ") + op.name);
     // Elementwise / view op.
-    int c = (op_is_view(op.kind) || op.kind == OpKind::kConcatenate) ? 0 : 1;
+    int c = (op_is_view(op.kind) || op.kind == OpKind::kConcatenate) ? 0 : op_cost(op.kind);
     for (int v : op.operands) {
       if (!mat_.count(v)) c += cost[v];
     }
@@ -254,6 +270,41 @@ void Planner::closure(const std::vector<int>& roots, std::vector<int>* ops, std:
   ops->assign(seen_ops.begin(), seen_ops.end());  // std::set is sorted: program order
 }
 
+// True if `op` is a view whose result has its operand's elements in the same
+// row-major order.
+static bool keeps_row_major_order(const Program& prog, const Op& op) {
+  if (op.operands.empty()) return false;
+  const TensorType& in = prog.type(op.operands[0]);
+  const TensorType& out = prog.type(op.results[0]);
+  if (in.elements() != out.elements()) return false;
+  if (op.kind == OpKind::kReshape) return true;
+  if (op.kind == OpKind::kBroadcastInDim) return std::is_sorted(op.dims.begin(), op.dims.end());
+  if (op.kind == OpKind::kTranspose) {
+    int64_t last = -1;
+    for (int64_t d : op.dims) {  // result dim i reads operand dim op.dims[i]
+      if (in.dims[d] == 1) continue;
+      if (d < last) return false;
+      last = d;
+    }
+    return true;
+  }
+  return false;
+}
+
+int Planner::order_preserving_source(int v) const {
+  int cur = v;
+  for (int hops = 0; hops < 64; ++hops) {
+    auto pi = producer_.find(cur);
+    if (pi == producer_.end()) return -1;
+    const Op& op = prog_.ops[pi->second];
+    if (!keeps_row_major_order(prog_, op)) return -1;
+    const int u = op.operands[0];
+    if (mat_.count(u)) return u;
+    cur = u;
+  }
+  return -1;
+}
+
 void Planner::build_steps(std::vector<Step>* steps) {
   for (size_t i = 0; i < prog_.ops.size(); ++i) {
     const Op& op = prog_.ops[i];
@@ -294,15 +345,13 @@ void Planner::build_steps(std::vector<Step>* steps) {
     if (op.results.empty() || !mat_.count(op.results[0])) continue;
     const int v = op.results[0];
     Step s;
-    // A broadcast that only inserts unit dims (dims increasing) keeps the
-    // row-major order: it is a reshape.
-    bool unit_broadcast = false;
-    if (op.kind == OpKind::kBroadcastInDim && prog_.type(v).elements() == prog_.type(op.operands[0]).elements()) {
-      unit_broadcast = std::is_sorted(op.dims.begin(), op.dims.end());
-    }
-    if ((op.kind == OpKind::kReshape || unit_broadcast) && mat_.count(op.operands[0])) {
+    // A chain of views that keeps the row-major order (reshapes, unit-dim
+    // broadcasts, transposes that only move size-1 dims) over a materialized
+    // value is that value's buffer under another type: no kernel.
+    const int src = order_preserving_source(v);
+    if (src >= 0) {
       s.kind = StepKind::kAlias;
-      s.inputs = op.operands;
+      s.inputs = {src};
       s.outputs = {v};
       s.lib_op = static_cast<int>(i);
       steps->push_back(std::move(s));
@@ -641,8 +690,15 @@ std::string Plan::describe(const Program& prog) const {
       o << "],\"row_schedule\":" << (s.row_schedule ? "true" : "false") << ",\"rows\":" << s.rows
         << ",\"row_len\":" << s.row_len << ",\"splits\":" << s.splits << ",\"chunk\":" << s.chunk;
     }
-    if (s.kind == StepKind::kLibrary)
+    if (s.kind == StepKind::kLibrary) {
       o << ",\"library\":\"" << lib_kind_name(s.lib) << "\",\"in_place\":" << (s.in_place ? "true" : "false");
+      if (s.lib == LibKind::kDot) {  // 2 * output elements * contracted size
+        const Op& d = prog.ops[s.lib_op];
+        int64_t kc = 1;
+        for (int64_t c : d.lhs_contract) kc *= prog.type(d.operands[0]).dims[c];
+        o << ",\"flops\":" << 2 * prog.type(d.results[0]).elements() * kc;
+      }
+    }
     o << ",\"vec\":" << s.vec << ",\"grid\":" << s.grid << ",\"block\":" << s.block;
     o << ",\"release_after\":" << list(s.release_after) << "}";
   }

@@ -163,6 +163,12 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   uint32_t* seg_start = static_cast<uint32_t*>(seg->ptr);
   uint32_t* seg_end = seg_start + rows;
   launch_scatter_segments(s, K, n, p.invalid, seg_start, seg_end, rows);
+  if (p.row_mode) {
+    MemRef cs = dev->allocate(scatter_chunk_scratch_bytes(rows, n, p.row_elems, xt.dtype));
+    launch_scatter_chunked(s, rows, p.row_elems, n, static_cast<int>(sop), xt.dtype, X, U, V, seg_start, seg_end,
+                           cs->ptr, out);
+    return;
+  }
   ScatterFoldParams f;
   f.rows = rows;
   f.row_elems = p.row_elems;

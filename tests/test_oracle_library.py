@@ -133,3 +133,18 @@ def test_attention_oracle_closed_forms():
     k2[0, 2] = 100.0
     ctx2 = ops.bf16_bits_to_f32(ops.attention_bf16(q, ops.f32_to_bf16_bits(k2), v, causal=False))
     np.testing.assert_allclose(ctx2[0], np.broadcast_to(vv[0, 2], (L, D)), rtol=1e-2)
+
+
+def test_scatter_f64_and_segment_lengths():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((5, 3)).astype(np.float32)
+    idx = np.array([0, 4, 4, 9, -2, 4, 1], np.int32)
+    u = rng.standard_normal((7, 3)).astype(np.float32)
+    np.testing.assert_array_equal(ops.segment_lengths(idx, 5), [1, 1, 0, 0, 3])
+    exact = ops.scatter_rows_add_f64(x, idx, u)
+    want = x.astype(np.float64)
+    for j, r in enumerate(idx):
+        if 0 <= r < 5:
+            want[r] += u[j]
+    np.testing.assert_array_equal(exact, want)
+    np.testing.assert_allclose(ops.scatter_rows_add(x, idx, u), exact, rtol=1e-6)
