@@ -293,6 +293,18 @@ def roofline(units, unit_ms, names, dtype: str) -> dict:
     return {**{kk: out[kk] for kk in keys}, "traffic": None, **{kk: v for kk, v in out.items() if kk not in keys}}
 
 
+def unit_table(names, unit_ms) -> dict:
+    """Per-launch-unit microseconds; repeated names get a #k suffix."""
+    out, seen = {}, {}
+    for n, t in zip(names, unit_ms):
+        if n == "-":
+            continue
+        k = seen.get(n, 0)
+        seen[n] = k + 1
+        out[n if k == 0 else f"{n}#{k}"] = round(t * 1e3, 3)
+    return out
+
+
 def traffic_from_profiles(workload: str, kernel: str):
     """HBM bytes per launch of `kernel`, from the counter summary committed
     under profiles/ (null when that kernel was not profiled)."""
@@ -353,7 +365,7 @@ def bench_program(a, W: Workload) -> dict:
                    "pct_peak_end_to_end": round(pct, 2),
                    "hbm_gbps_end_to_end": round(W.bytes / sec / 1e9, 2),
                    "kernels_per_step": sum(1 for n in names if n != "-"),
-                   "kernel_us": {n: round(t * 1e3, 3) for n, t in zip(names, unit_ms) if n != "-"}},
+                   "kernel_us": unit_table(names, unit_ms)},
         "roofline": rf,
     }
     if not a.no_cpu_baseline and W.cpu:

@@ -188,6 +188,21 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
       g.ldc = N;
       g.a_batch_stride = a.bs;
       g.b_batch_stride = b.bs;
+      MemRef bt;
+      if (!b_kmajor) {
+        // The large-tile kernel takes B K-contiguous: transpose an N-contiguous
+        // B ([K][N] per batch) once, at HBM speed, when that kernel applies.
+        GemmParams t = g;
+        t.ldb = K;
+        t.b_batch_stride = N * K;
+        if (use_big_gemm(t) && g.ldb == N && (batch == 1 || b.bs == K * N)) {
+          bt = dev->allocate(static_cast<size_t>(batch * N * K) * 2);
+          launch_transpose16(dev->stream(), B, bt->ptr, batch, K, N, K * N, N * K);
+          B = bt->ptr;
+          g = t;
+          b_kmajor = true;
+        }
+      }
       launch_mfma_gemm(dev->stream(), g, A, B, out, f16, b_kmajor, out_kind == 2 ? 4 : 2);
       return;
     }

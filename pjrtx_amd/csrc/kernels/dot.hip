@@ -229,6 +229,195 @@ __global__ void __launch_bounds__(256) mfma_gemm(GemmParams p, const uint16_t* _
   }
 }
 
+// ------------------------------------------------------------- large GEMM
+// gemm_nt_big: C[b] = A[b] (M x K, K contiguous) * B[b]^T (N x K, K
+// contiguous) for M, N >= 256. 256 x 256 block tile, BK = 64, 512 threads in
+// 2 x 4 waves of 128 x 64 (8 x 4 MFMA 16x16x32 subtiles each, 128 f32
+// accumulators per lane). Operands go global -> registers -> LDS (double
+// buffered, one barrier per K step; the next tile's global loads are in
+// flight while the current one is multiplied). LDS rows are 64 elements
+// (eight 16-byte chunks) with chunk c of row r stored at c ^ ((r >> 1) & 7),
+// so the 16-byte fragment reads of 16 consecutive rows hit distinct banks
+// without padding. The C tile is staged per wave through LDS (same swizzle)
+// and written with 16-byte stores.
+constexpr int GBM = 256, GBN = 256, GBK = 64, GTHREADS = 512;
+
+__device__ __forceinline__ int gswz(int row, int chunk) { return row * GBK + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
+template <bool kF16, int kOutBytes>
+__global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_big(GemmParams p, const uint16_t* __restrict__ A,
+                                                            const uint16_t* __restrict__ B, void* __restrict__ C) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GBM + GBN) * GBK];
+  uint16_t* As = smem;                    // [2][GBM * GBK]
+  uint16_t* Bs = smem + 2 * GBM * GBK;    // [2][GBN * GBK]
+
+  const int tiles_m = (p.M + GBM - 1) / GBM, tiles_n = (p.N + GBN - 1) / GBN;
+  const int per_batch = tiles_m * tiles_n;
+  const int total = per_batch * p.batch;
+  int bid = blockIdx.x;
+  if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;  // contiguous tile runs per XCD
+  const int b = bid / per_batch;
+  const int t = bid - b * per_batch;
+  const int group = 4;  // walk 4 tile-rows at a time so B tiles are reused from L2
+  const int gsize = group * tiles_n;
+  const int g = t / gsize;
+  const int first_m = g * group;
+  const int gm = min(tiles_m - first_m, group);
+  const int tm = first_m + (t - g * gsize) % gm;
+  const int tn = (t - g * gsize) / gm;
+  const int m0 = tm * GBM, n0 = tn * GBN;
+  const uint16_t* Ab = A + (int64_t)b * p.a_batch_stride;
+  const uint16_t* Bb = B + (int64_t)b * p.b_batch_stride;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  u32x4 ra[4], rb[4];
+
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = tid + GTHREADS * j;
+      const int row = c >> 3, k = k0 + (c & 7) * 8;
+      const int m = m0 + row, n = n0 + row;
+      ra[j] = (m < p.M && k < p.K) ? *reinterpret_cast<const u32x4*>(Ab + (int64_t)m * p.lda + k) : zero;
+      rb[j] = (n < p.N && k < p.K) ? *reinterpret_cast<const u32x4*>(Bb + (int64_t)n * p.ldb + k) : zero;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = tid + GTHREADS * j;
+      const int row = c >> 3, ch = c & 7;
+      *reinterpret_cast<u32x4*>(&As[buf * GBM * GBK + gswz(row, ch)]) = ra[j];
+      *reinterpret_cast<u32x4*>(&Bs[buf * GBN * GBK + gswz(row, ch)]) = rb[j];
+    }
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int kt_count = (p.K + GBK - 1) / GBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < kt_count) gload((kt + 1) * GBK);
+    const uint16_t* as = As + buf * GBM * GBK;
+    const uint16_t* bs = Bs + buf * GBN * GBK;
+#pragma unroll
+    for (int kk = 0; kk < GBK; kk += 32) {
+      const int ch = (kk >> 3) + (lane >> 4);
+      u32x4 af[8], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        af[i] = *reinterpret_cast<const u32x4*>(&as[gswz(wm * 128 + i * 16 + (lane & 15), ch)]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bfr[j] = *reinterpret_cast<const u32x4*>(&bs[gswz(wn * 64 + j * 16 + (lane & 15), ch)]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<kF16>(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < kt_count) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds rows (lane/16)*4 + r, column lane%16 of each 16x16
+  // subtile of the wave's 128 x 64 tile.
+  const int wrow0 = m0 + wm * 128, wcol0 = n0 + wn * 64;
+  if constexpr (kOutBytes == 2) {
+    uint16_t* cs = smem + wave * 128 * GBK;  // this wave's 128 x 64 staging tile
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = i * 16 + (lane >> 4) * 4 + r;
+          const int col = j * 16 + (lane & 15);
+          const float v = acc[i][j][r];
+          cs[gswz(row, col >> 3) + (col & 7)] = kF16 ? f32_to_f16_bits(v) : f32_to_bf16_rne(v);
+        }
+    __syncthreads();
+    uint16_t* Cb = reinterpret_cast<uint16_t*>(C) + (int64_t)b * p.M * p.ldc;
+#pragma unroll
+    for (int tt = 0; tt < 16; ++tt) {
+      const int c = lane + 64 * tt;  // 1024 chunks of 8
+      const int row = c >> 3, ch = c & 7;
+      const int m = wrow0 + row, n = wcol0 + ch * 8;
+      if (m >= p.M || n >= p.N) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&cs[gswz(row, ch)]);
+      if (n + 8 <= p.N && p.ldc % 8 == 0) {
+        *reinterpret_cast<u32x4*>(Cb + (int64_t)m * p.ldc + n) = v;
+      } else {
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+        for (int q = 0; q < 8 && n + q < p.N; ++q) Cb[(int64_t)m * p.ldc + n + q] = e[q];
+      }
+    }
+  } else {
+    float* Cb = reinterpret_cast<float*>(C) + (int64_t)b * p.M * p.ldc;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = wrow0 + i * 16 + (lane >> 4) * 4 + r;
+          const int n = wcol0 + j * 16 + (lane & 15);
+          if (m < p.M && n < p.N) Cb[(int64_t)m * p.ldc + n] = acc[i][j][r];
+        }
+  }
+}
+
+// out[b][c][r] = in[b][r][c] for 16-bit elements; 64 x 64 tiles through LDS.
+__global__ void __launch_bounds__(256) transpose16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
+                                                   int64_t rows, int64_t cols, int64_t in_bs, int64_t out_bs) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const uint16_t* src = in + b * in_bs;
+  uint16_t* dst = out + b * out_bs;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = tid + 256 * j;  // 512 chunks of 8
+    const int rr = c >> 3, cc = (c & 7) * 8;
+    const int64_t r = r0 + rr, col = c0 + cc;
+    uint16_t v[8];
+    if (r < rows && col + 8 <= cols && cols % 8 == 0) {
+      *reinterpret_cast<u32x4*>(v) = *reinterpret_cast<const u32x4*>(src + r * cols + col);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (r < rows && col + e < cols) ? src[r * cols + col + e] : (uint16_t)0;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[rr][cc + e] = v[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = tid + 256 * j;
+    const int oc = c >> 3, orr = (c & 7) * 8;  // output row = input column
+    const int64_t orow = c0 + oc, ocol = r0 + orr;
+    if (orow >= cols) continue;
+    uint16_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = tile[orr + e][oc];
+    if (ocol + 8 <= rows && rows % 8 == 0) {
+      *reinterpret_cast<u32x4*>(dst + orow * rows + ocol) = *reinterpret_cast<const u32x4*>(v);
+    } else {
+      for (int e = 0; e < 8 && ocol + e < rows; ++e) dst[orow * rows + ocol + e] = v[e];
+    }
+  }
+}
+
 // ------------------------------------------------------------------- GEMV
 // Decode-shaped products (M <= 8) are bound by streaming W once.
 //
@@ -434,8 +623,42 @@ void check(const char* what) {
 
 }  // namespace
 
+bool use_big_gemm(const GemmParams& p) {
+  // Below one tile per CU the 128 x 128 kernel's 4x more tiles fill the GPU
+  // better (environment: PJRTX_BIG_GEMM_MIN_TILES).
+  const int64_t min_tiles = env_int("PJRTX_BIG_GEMM_MIN_TILES", 256);
+  const int64_t tiles = (int64_t)((p.M + GBM - 1) / GBM) * ((p.N + GBN - 1) / GBN) * p.batch;
+  return p.M >= GBM && p.N >= GBN && p.K % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
+         p.a_batch_stride % 8 == 0 && p.b_batch_stride % 8 == 0 && tiles >= min_tiles && tiles < (int64_t(1) << 31);
+}
+
+void launch_transpose16(hipStream_t s, const void* in, void* out, int64_t batch, int64_t rows, int64_t cols,
+                        int64_t in_bs, int64_t out_bs) {
+  if (batch == 0 || rows == 0 || cols == 0) return;
+  const dim3 grid(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64),
+                  static_cast<unsigned>(batch));
+  hipLaunchKernelGGL(transpose16, grid, dim3(256), 0, s, static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out),
+                     rows, cols, in_bs, out_bs);
+  check("transpose16");
+}
+
 void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const void* B, void* C, bool f16, bool b_kmajor,
                       int out_bytes) {
+  if (b_kmajor && use_big_gemm(p)) {
+    const int64_t tiles = (int64_t)((p.M + GBM - 1) / GBM) * ((p.N + GBN - 1) / GBN) * p.batch;
+    const dim3 grid(static_cast<unsigned>(tiles)), block(GTHREADS);
+    const uint16_t* a = static_cast<const uint16_t*>(A);
+    const uint16_t* b = static_cast<const uint16_t*>(B);
+    if (out_bytes == 2) {
+      if (f16) hipLaunchKernelGGL((gemm_nt_big<true, 2>), grid, block, 0, s, p, a, b, C);
+      else hipLaunchKernelGGL((gemm_nt_big<false, 2>), grid, block, 0, s, p, a, b, C);
+    } else {
+      if (f16) hipLaunchKernelGGL((gemm_nt_big<true, 4>), grid, block, 0, s, p, a, b, C);
+      else hipLaunchKernelGGL((gemm_nt_big<false, 4>), grid, block, 0, s, p, a, b, C);
+    }
+    check("gemm_nt_big");
+    return;
+  }
   const int64_t tiles = (int64_t)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * p.batch;
   if (tiles == 0 || p.K == 0) fail(Code::kInternal, "mfma_gemm: empty problem must be handled by the caller");
   PJRTX_CHECK(tiles < (int64_t(1) << 31), Code::kUnimplemented, "mfma_gemm: too many tiles");

@@ -355,3 +355,45 @@ def test_concatenate_and_pad(client):
     want = np.full((4, 7), -1.0, np.float32)
     want[1::2, 0:5:2] = a
     np.testing.assert_array_equal(got_pad, want)
+
+
+_BIG_GEMM_SHAPES = [
+    ("bmk,bkn", (2, 300, 200), (2, 200, 520), "bf16", None),   # NN: transposed B, ragged M / N / K tail
+    ("bmk,bnk", (3, 512, 136), (3, 264, 136), "bf16", None),   # NT, ragged N, K not a multiple of 64
+    ("mk,kn", (256, 64), (64, 256), "f16", None),              # exactly one tile
+    ("bmk,bnk", (2, 260, 72), (2, 300, 72), "bf16", "f32"),    # f32 output
+]
+
+
+@pytest.mark.parametrize("shape", _BIG_GEMM_SHAPES)
+def test_dot_large_tile_kernel(client, shape, monkeypatch):
+    """The 256 x 256 tile kernel on shapes with ragged edges; the environment
+    lowers its tile-count threshold so that these small problems take it."""
+    monkeypatch.setenv("PJRTX_BIG_GEMM_MIN_TILES", "1")
+    spec, sa, sb, dt, out_dt = shape
+    rng = np.random.default_rng(sum(sa) + sum(sb))
+    if dt == "bf16":
+        to, fr = bf, fb
+    else:
+        to = lambda x: x.astype(np.float16).view(np.uint16)  # noqa: E731
+        fr = lambda b: b.view(np.float16).astype(np.float32)  # noqa: E731
+    a = to(rng.standard_normal(sa).astype(np.float32))
+    b_ = to(rng.standard_normal(sb).astype(np.float32))
+    ls, rs = spec.split(",")
+    lb = tuple(i for i, c in enumerate(ls) if c == "b")
+    rb = tuple(i for i, c in enumerate(rs) if c == "b")
+    lc, rc = (ls.index("k"),), (rs.index("k"),)
+    bld = Builder()
+    x, y = bld.param(sa, dt), bld.param(sb, dt)
+    t = bld.build([bld.dot_general(x, y, batch=(lb, rb), contract=(lc, rc), out_dtype=out_dt)])
+    (out,) = run(client, t, a, b_, dtypes=[dt, dt])
+    want = ops.dot_general_f64(fr(a), fr(b_), lb, rb, lc, rc)
+    assert out.shape == want.shape
+    if out_dt == "f32":
+        np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+    elif dt == "bf16":
+        assert_bf16_close(out, want)
+    else:
+        got = fr(out).astype(np.float64)
+        scale = np.sqrt(np.mean(want ** 2, axis=-1, keepdims=True))
+        assert (np.abs(got - want) / np.maximum(np.abs(want), scale)).max() <= 2e-2
