@@ -410,6 +410,19 @@ def bench_c5(a) -> dict:
     ms_per_step = decode_s * 1e3 / steps
     tokens = [int(x.to_numpy()[0]) for x in toks]
 
+    graph_stats = runner.decode.graph_stats()
+    # The same decode loop with graph replay off, for comparison.
+    os.environ["PJRTX_GRAPHS"] = "0"
+    tok_e, _, caches_e = runner.start(prompt)
+    tok_e.block_until_ready()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok_e, _, caches_e = runner.step_with(tok_e, pos_bufs[i], caches_e)
+    tok_e.block_until_ready()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    os.environ.pop("PJRTX_GRAPHS")
+    del caches_e
+
     plan = json.loads(runner.decode.optimized_program())
     units = launch_units(plan)
     args = runner.weights + [tok, pos_bufs[-1]] + caches
@@ -436,7 +449,8 @@ def bench_c5(a) -> dict:
                    "decode_step_gbps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
                    "launch_units_per_step": sum(1 for n in names if n != "-"),
                    "gpu_us_per_step_by_kind": {kk: round(v, 2) for kk, v in sorted(by_kind.items())},
-                   "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2), "first_tokens": tokens[:8]},
+                   "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2), "first_tokens": tokens[:8],
+                   "graph": graph_stats, "eager_ms_per_step": round(eager_ms, 4)},
         "roofline": roofline(units, unit_ms, names, "bf16"),
     }
     if not a.no_cpu_baseline:

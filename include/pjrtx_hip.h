@@ -90,6 +90,13 @@ PJRTX_HIP_API int pjrtx_executable_step_names(struct PJRT_LoadedExecutable* exe,
  * released intermediate values. */
 PJRTX_HIP_API int pjrtx_executable_stats(struct PJRT_LoadedExecutable* exe, int64_t out[4]);
 
+/* Graph counters of the executable: hipGraph captures and replays.
+ * Repeated executions with the same large argument buffers are captured
+ * once into a hipGraph and replayed (PJRTX_GRAPHS=0 turns this off). The
+ * reference replays an MLX compiled trace instead
+ * (execution_compiled_program.zig:18-67, api.cc:5425-5674). */
+PJRTX_HIP_API int pjrtx_executable_graph_stats(struct PJRT_LoadedExecutable* exe, int64_t out[2]);
+
 #ifdef __cplusplus
 }
 #endif

@@ -172,4 +172,12 @@ int pjrtx_executable_stats(PJRT_LoadedExecutable* exe, int64_t out[4]) {
   });
 }
 
+int pjrtx_executable_graph_stats(PJRT_LoadedExecutable* exe, int64_t out[2]) {
+  return guarded([&] {
+    ExecStats s = exe->exe->stats();
+    out[0] = s.graph_captures;
+    out[1] = s.graph_replays;
+  });
+}
+
 }  // extern "C"

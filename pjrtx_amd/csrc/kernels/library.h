@@ -59,4 +59,15 @@ struct GatherParams {
 void launch_gather(hipStream_t s, const GatherParams& p, const void* operand, const void* indices, void* out,
                    int elem_bytes);
 
+// Copies up to kMaxCopySegments independent byte ranges in one launch (used
+// to stage small arguments into, and results out of, a replayed graph).
+constexpr int kMaxCopySegments = 16;
+struct CopySegments {
+  int n = 0;
+  const void* src[kMaxCopySegments] = {};
+  void* dst[kMaxCopySegments] = {};
+  int64_t bytes[kMaxCopySegments] = {};
+};
+void launch_copy_segments(hipStream_t s, const CopySegments& c);
+
 }  // namespace pjrtx

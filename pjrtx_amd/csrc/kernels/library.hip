@@ -236,4 +236,37 @@ void launch_gather(hipStream_t s, const GatherParams& g, const void* operand, co
   check_launch("gather");
 }
 
+namespace {
+__global__ void __launch_bounds__(256) copy_segments_kernel(CopySegments c) {
+  const int seg = blockIdx.y;
+  if (seg >= c.n) return;
+  const int64_t nb = c.bytes[seg];
+  const char* src = static_cast<const char*>(c.src[seg]);
+  char* dst = static_cast<char*>(c.dst[seg]);
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
+    typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+    const int64_t n16 = nb / 16;
+    for (int64_t i = t; i < n16; i += stride)
+      reinterpret_cast<u32x4_t*>(dst)[i] = reinterpret_cast<const u32x4_t*>(src)[i];
+    for (int64_t i = n16 * 16 + t; i < nb; i += stride) dst[i] = src[i];
+  } else {
+    for (int64_t i = t; i < nb; i += stride) dst[i] = src[i];
+  }
+}
+}  // namespace
+
+void launch_copy_segments(hipStream_t s, const CopySegments& c) {
+  if (c.n <= 0) return;
+  int64_t mx = 0;
+  for (int i = 0; i < c.n; ++i) mx = c.bytes[i] > mx ? c.bytes[i] : mx;
+  if (mx == 0) return;
+  const int64_t blocks = (mx / 16 + 255) / 256;
+  const dim3 grid(static_cast<unsigned>(blocks < 1 ? 1 : (blocks > 1024 ? 1024 : blocks)), static_cast<unsigned>(c.n));
+  hipLaunchKernelGGL(copy_segments_kernel, grid, dim3(256), 0, s, c);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(Code::kInternal, strformat("copy_segments launch failed: %s", hipGetErrorString(e)));
+}
+
 }  // namespace pjrtx

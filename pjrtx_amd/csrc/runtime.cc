@@ -1,5 +1,6 @@
 // Device runtime implementation. See runtime.h.
 #include "runtime.h"
+#include "kernels/library.h"
 
 #include <hip/hiprtc.h>
 #include <sys/stat.h>
@@ -115,6 +116,7 @@ MemRef Device::allocate(size_t bytes) {
   if (bytes == 0) return m;
   make_current();
   m->ptr = alloc_.alloc(bytes, &m->capacity);
+  if (capture_pins_) capture_pins_->push_back(m);
   return m;
 }
 
@@ -474,6 +476,23 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
   Loaded* L = loaded_for(dev);
   std::lock_guard<std::mutex> lk(dev->exec_mutex());
   dev->make_current();
+  // Repeated executions with the same large arguments replay a captured
+  // graph (second call captures, later calls replay).
+  if (graph_candidate(args, donate)) {
+    GraphState& gs = graph_state(dev->ordinal());
+    std::vector<const void*> key = graph_key(args);
+    for (auto& e : gs.entries)
+      if (e->key == key) return replay_graph(dev, e.get(), args, done);
+    bool seen_before = false;
+    for (auto& k : gs.seen) seen_before = seen_before || k == key;
+    if (seen_before) {
+      GraphEntry* g = capture_graph(dev, L, args, key);
+      if (g) return replay_graph(dev, g, args, done);
+    } else {
+      gs.seen.push_back(key);
+      if (gs.seen.size() > 8) gs.seen.erase(gs.seen.begin());
+    }
+  }
   std::vector<MemRef> vals(prog_.values.size());
   for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i]->mem;
   auto donated = [&](size_t i) { return donate && i < donate->size() && (*donate)[i]; };
@@ -523,6 +542,168 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
   for (auto& b : outs) b->ready = ev;
   if (done) *done = ev;
   stats_.executions++;
+  return outs;
+}
+
+// ------------------------------------------------------------ graph replay
+
+namespace {
+constexpr size_t kGraphStagedMaxBytes = 64 * 1024;   // arguments up to this size are copied in
+constexpr size_t kGraphMaxPinnedBytes = 256u << 20;  // graphs holding more memory are not kept
+constexpr size_t kGraphEntriesPerDevice = 4;
+constexpr int kGraphMinLaunches = 8;
+}  // namespace
+
+Executable::GraphState& Executable::graph_state(int ordinal) {
+  std::lock_guard<std::mutex> lk(mu_);
+  return graphs_[ordinal];  // std::map: references stay valid
+}
+
+Executable::GraphEntry::~GraphEntry() {
+  if (exec) (void)hipGraphExecDestroy(exec);
+}
+
+bool Executable::graph_candidate(const std::vector<BufferRef>& args, const std::vector<bool>* donate) const {
+  if (env_int("PJRTX_GRAPHS", 1) == 0) return false;
+  if (args.empty() || const_cast<Executable*>(this)->graph_state(args[0]->dev->ordinal()).disabled) return false;
+  int launches = 0;
+  for (const Step& st : plan_.steps) launches += st.kind != StepKind::kAlias;
+  if (launches < kGraphMinLaunches) return false;
+  for (int k : plan_.written_params)  // in-place writes need the caller's donation
+    if (!donate || static_cast<size_t>(k) >= donate->size() || !(*donate)[k]) return false;
+  return true;
+}
+
+std::vector<const void*> Executable::graph_key(const std::vector<BufferRef>& args) const {
+  std::set<int> written(plan_.written_params.begin(), plan_.written_params.end());
+  std::vector<const void*> key(args.size(), nullptr);
+  for (size_t i = 0; i < args.size(); ++i) {
+    const bool staged = args[i]->mem->bytes <= kGraphStagedMaxBytes && !written.count(static_cast<int>(i));
+    if (!staged) key[i] = args[i]->mem->ptr;
+  }
+  return key;
+}
+
+Executable::GraphEntry* Executable::capture_graph(Device* dev, Loaded* L, const std::vector<BufferRef>& args,
+                                                  std::vector<const void*> key) {
+  GraphState& gs = graph_state(dev->ordinal());
+  auto g = std::make_unique<GraphEntry>();
+  g->key = std::move(key);
+  dev->set_capture_pins(&g->pins);
+  g->staging.resize(args.size());
+  std::vector<MemRef> vals(prog_.values.size());
+  for (size_t i = 0; i < args.size(); ++i) {
+    if (g->key[i] == nullptr) {
+      g->staging[i] = dev->allocate(args[i]->mem->bytes);
+      vals[prog_.params[i]] = g->staging[i];
+    } else {
+      vals[prog_.params[i]] = args[i]->mem;
+    }
+  }
+  for (auto& [v, m] : L->constants) vals[v] = m;
+  hipGraph_t graph = nullptr;
+  bool ok = hipStreamBeginCapture(dev->stream(), hipStreamCaptureModeRelaxed) == hipSuccess;
+  if (ok) {
+    try {
+      for (size_t si = 0; si < plan_.steps.size(); ++si) run_step(L, si, vals);
+    } catch (const std::exception&) {
+      ok = false;
+    }
+    hipError_t e = hipStreamEndCapture(dev->stream(), &graph);
+    ok = ok && e == hipSuccess && graph != nullptr;
+  }
+  (void)hipGetLastError();
+  dev->set_capture_pins(nullptr);
+  // Results must be graph-produced or donated argument memory, each distinct.
+  std::set<const DeviceMemory*> pinned, seen;
+  for (auto& m : g->pins) pinned.insert(m.get());
+  for (int r : prog_.results) {
+    if (!ok) break;
+    const MemRef& m = vals[r];
+    int param = -1;
+    for (size_t i = 0; i < args.size() && param < 0; ++i)
+      if (g->key[i] != nullptr && m.get() == args[i]->mem.get()) param = static_cast<int>(i);
+    const bool internal = m && pinned.count(m.get());
+    if (!m || seen.count(m.get()) || (param < 0 && !internal)) ok = false;
+    if (param >= 0) {  // only donated (written-in-place) arguments may come back as results
+      bool written = false;
+      for (int k : plan_.written_params) written = written || k == param;
+      if (!written) ok = false;
+    }
+    seen.insert(m.get());
+    g->result_param.push_back(param);
+    g->result_mem.push_back(param < 0 ? m : MemRef());
+  }
+  size_t pinned_bytes = 0;
+  for (auto& m : g->pins) pinned_bytes += m->capacity;
+  if (ok) ok = pinned_bytes <= kGraphMaxPinnedBytes;
+  if (ok) ok = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0) == hipSuccess;
+  if (graph) (void)hipGraphDestroy(graph);
+  (void)hipGetLastError();
+  if (!ok) {
+    gs.disabled = true;  // run this executable eagerly from now on
+    return nullptr;
+  }
+  stats_.graph_captures++;
+  if (gs.entries.size() >= kGraphEntriesPerDevice) {
+    auto lru = std::min_element(gs.entries.begin(), gs.entries.end(),
+                                [](const auto& a, const auto& b) { return a->last_use < b->last_use; });
+    // Work already queued on the stream that uses its blocks runs before any
+    // later user of them (single in-order stream).
+    gs.entries.erase(lru);
+  }
+  gs.entries.push_back(std::move(g));
+  return gs.entries.back().get();
+}
+
+std::vector<BufferRef> Executable::replay_graph(Device* dev, GraphEntry* g, const std::vector<BufferRef>& args,
+                                                std::shared_ptr<Event>* done) {
+  GraphState& gs = graph_state(dev->ordinal());
+  g->last_use = ++gs.clock;
+  CopySegments in;
+  for (size_t i = 0; i < args.size(); ++i) {
+    if (g->key[i] != nullptr || !args[i]->mem->bytes) continue;
+    if (in.n == kMaxCopySegments) {
+      launch_copy_segments(dev->stream(), in);
+      in = CopySegments();
+    }
+    in.src[in.n] = args[i]->mem->ptr;
+    in.dst[in.n] = g->staging[i]->ptr;
+    in.bytes[in.n] = static_cast<int64_t>(args[i]->mem->bytes);
+    in.n++;
+  }
+  launch_copy_segments(dev->stream(), in);
+  hip_check(hipGraphLaunch(g->exec, dev->stream()), "hipGraphLaunch");
+  std::vector<BufferRef> outs;
+  CopySegments out;
+  for (size_t r = 0; r < prog_.results.size(); ++r) {
+    auto b = std::make_shared<Buffer>();
+    b->dev = dev;
+    b->type = prog_.type(prog_.results[r]);
+    if (g->result_param[r] >= 0) {
+      b->mem = args[g->result_param[r]]->mem;
+    } else {
+      const MemRef& src = g->result_mem[r];
+      b->mem = dev->allocate(src->bytes);
+      if (src->bytes) {
+        if (out.n == kMaxCopySegments) {
+          launch_copy_segments(dev->stream(), out);
+          out = CopySegments();
+        }
+        out.src[out.n] = src->ptr;
+        out.dst[out.n] = b->mem->ptr;
+        out.bytes[out.n] = static_cast<int64_t>(src->bytes);
+        out.n++;
+      }
+    }
+    outs.push_back(b);
+  }
+  launch_copy_segments(dev->stream(), out);
+  std::shared_ptr<Event> ev = Event::record(dev);
+  for (auto& b : outs) b->ready = ev;
+  if (done) *done = ev;
+  stats_.executions++;
+  stats_.graph_replays++;
   return outs;
 }
 

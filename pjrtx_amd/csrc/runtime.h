@@ -78,8 +78,12 @@ class Device {
   const std::string& name() const { return name_; }
   int64_t total_memory() const { return total_mem_; }
   int compute_units() const { return cus_; }
+  // While set (graph capture), every block allocate() hands out is also
+  // appended here, so the graph that uses it keeps it for its lifetime.
+  void set_capture_pins(std::vector<MemRef>* pins) { capture_pins_ = pins; }
 
  private:
+  std::vector<MemRef>* capture_pins_ = nullptr;
   int ordinal_;
   hipStream_t stream_ = nullptr;
   Allocator alloc_;
@@ -136,6 +140,8 @@ struct ExecStats {
   int64_t kernel_launches = 0;
   int64_t library_calls = 0;
   int64_t released_values = 0;
+  int64_t graph_captures = 0;
+  int64_t graph_replays = 0;
 };
 
 class Executable {
@@ -183,7 +189,35 @@ class Executable {
   std::map<int, std::unique_ptr<Loaded>> loaded_;
   ExecStats stats_;
 
+  // A captured hipGraph of the whole plan for one set of argument
+  // addresses. Small arguments are staged into pinned blocks before each
+  // replay; results the graph produces are copied out to fresh buffers.
+  struct GraphEntry {
+    std::vector<const void*> key;  // per parameter: device address, or null when staged
+    hipGraphExec_t exec = nullptr;
+    std::vector<MemRef> pins;      // every block the graph reads or writes
+    std::vector<MemRef> staging;   // per parameter: staging block (staged parameters)
+    std::vector<int> result_param; // per result: parameter whose memory it is, or -1
+    std::vector<MemRef> result_mem;
+    uint64_t last_use = 0;
+    ~GraphEntry();
+  };
+  struct GraphState {
+    std::vector<std::unique_ptr<GraphEntry>> entries;
+    std::vector<std::vector<const void*>> seen;  // keys run once eagerly
+    bool disabled = false;
+    uint64_t clock = 0;
+  };
+  std::map<int, GraphState> graphs_;  // by device ordinal
+
   Loaded* loaded_for(Device* dev);
+  GraphState& graph_state(int ordinal);
+  bool graph_candidate(const std::vector<BufferRef>& args, const std::vector<bool>* donate) const;
+  std::vector<const void*> graph_key(const std::vector<BufferRef>& args) const;
+  GraphEntry* capture_graph(Device* dev, Loaded* L, const std::vector<BufferRef>& args,
+                            std::vector<const void*> key);
+  std::vector<BufferRef> replay_graph(Device* dev, GraphEntry* g, const std::vector<BufferRef>& args,
+                                      std::shared_ptr<Event>* done);
   // phase: -1 runs the whole step; 0 only the main kernel of a split
   // reduction, 1 only its combine kernel (outputs must already exist).
   void run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int phase = -1);

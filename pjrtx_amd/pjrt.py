@@ -212,6 +212,7 @@ class Plugin:
             "pjrtx_executable_time_steps": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double), c_size_t,
                                             POINTER(c_size_t)],
             "pjrtx_executable_step_names": [c_void_p, c_char_p, c_size_t, POINTER(c_size_t)],
+            "pjrtx_executable_graph_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
         }.items():
             f = getattr(L, name)
@@ -459,6 +460,11 @@ class Executable:
         buf = ctypes.create_string_buffer(need.value)
         self.client.p.hip_check(L.pjrtx_executable_step_names(self.handle, buf, need.value, ctypes.byref(need)))
         return [s for s in buf.value.decode().split("\n") if s]
+
+    def graph_stats(self) -> dict:
+        out = (c_int64 * 2)()
+        self.client.p.hip_check(self.client.p.lib.pjrtx_executable_graph_stats(self.handle, out))
+        return dict(captures=out[0], replays=out[1])
 
     def stats(self) -> dict:
         out = (c_int64 * 4)()
