@@ -126,6 +126,10 @@ class Writer {
 
   std::ostringstream body;              // per-element statements
   std::map<int, std::string> preload;   // value -> preload array name (root identity)
+  // Values that are per-row scalars of a row-fused kernel: any index into
+  // them is the current row (the planner checks this), so they read as the
+  // named variable.
+  std::map<int, std::string> row_scalar;
 
   int add_index(Idx idx) {
     idxs_.push_back(std::move(idx));
@@ -206,6 +210,8 @@ class Writer {
 };
 
 std::string Writer::value(int v, int id) {
+  auto rsv = row_scalar.find(v);
+  if (rsv != row_scalar.end()) return rsv->second;
   const std::string key = memo_key(v, id);
   auto m = memo_.find(key);
   if (m != memo_.end()) return m->second;
@@ -550,6 +556,7 @@ class KernelGen {
   KernelGen(const Program& prog, std::ostringstream& out) : prog_(prog), out_(out) {}
   void loop(Step& s);
   void reduce(Step& s);
+  void row_fused(Step& s);
 
  private:
   const Program& prog_;
@@ -559,7 +566,8 @@ class KernelGen {
     int64_t m = 0;
     for (int v : s.inputs) m = std::max(m, prog_.type(v).elements());
     for (int v : s.outputs) m = std::max(m, prog_.type(v).elements());
-    if (s.kind == StepKind::kReduce) m = std::max(m, num_elements(s.reduce_operand_shape));
+    if (s.kind == StepKind::kReduce || s.kind == StepKind::kRowFused)
+      m = std::max(m, num_elements(s.reduce_operand_shape));
     if (s.kind == StepKind::kLoop) m = std::max(m, num_elements(s.loop_shape));
     return m < (int64_t(1) << 31) ? "uint32_t" : "uint64_t";
   }
@@ -995,6 +1003,199 @@ void KernelGen::reduce(Step& s) {
   out_ << "}\n}\n\n";
 }
 
+// Row-fused kernel: one workgroup per row. Each reduce phase walks the row
+// (16-byte loads; after the first phase the row is served from cache),
+// reduces across the workgroup, and every thread keeps the phase results as
+// per-row scalars; the final elementwise phase writes the row outputs.
+void KernelGen::row_fused(Step& s) {
+  std::map<int, std::string> ptr_of;
+  signature(s, &ptr_of, false);
+  const std::string it = idx_type(s);
+  out_ << "typedef " << it << " idx_t;\n";
+  const Dims& shape = s.reduce_operand_shape;
+  const int rank = static_cast<int>(shape.size());
+  const int nred = static_cast<int>(s.reduce_dims.size());
+  const int nkept = rank - nred;
+  const int vec = s.vec;
+  const int64_t row_len = s.row_len;
+  const int64_t n_all = num_elements(shape);
+  const bool wpr = s.wave_per_row;
+  const int span = (wpr ? 64 : 256) * vec;     // elements per sweep of the row
+  const std::string tix = wpr ? "(threadIdx.x & 63u)" : "threadIdx.x";
+  if (wpr) {
+    out_ << "const idx_t row = (idx_t)blockIdx.x * 4u + (threadIdx.x >> 6);\n";
+    out_ << "if (row >= " << s.rows << "u) return;\n";  // whole wave: no barriers follow
+  } else {
+    out_ << "const idx_t row = (idx_t)blockIdx.x;\n";
+  }
+  std::vector<std::string> multi(rank);
+  {
+    std::string rest = "row";
+    for (int d = nkept - 1; d >= 0; --d) {
+      if (d == 0) {
+        multi[d] = rest;
+      } else {
+        out_ << "const idx_t kd" << d << " = " << rest << " % " << shape[d] << "u;\n";
+        out_ << "const idx_t kq" << d << " = " << rest << " / " << shape[d] << "u;\n";
+        multi[d] = "kd" + std::to_string(d);
+        rest = "kq" + std::to_string(d);
+      }
+    }
+  }
+  std::ostringstream col_digits;
+  {
+    std::string rest = "col";
+    for (int d = rank - 1; d >= nkept; --d) {
+      if (d == nkept) {
+        multi[d] = rest;
+      } else {
+        col_digits << "const idx_t rd" << d << " = " << rest << " % " << shape[d] << "u;\n";
+        col_digits << "const idx_t rq" << d << " = " << rest << " / " << shape[d] << "u;\n";
+        multi[d] = "rd" + std::to_string(d);
+        rest = "rq" + std::to_string(d);
+      }
+    }
+  }
+  const Dims kept(shape.begin(), shape.begin() + nkept);
+  std::map<int, std::string> scalars;
+  auto preloads = [&](Writer& w, std::ostream& decl, std::ostream& load) {
+    for (int v : s.inputs) {
+      if (prog_.type(v).elements() != n_all) continue;
+      const std::string st = dtype_storage_ctype(prog_.type(v).dtype);
+      const std::string name = "pre_" + ptr_of[v];
+      decl << st << " " << name << "[" << vec << "];\n";
+      load << "ldv<" << st << ", " << vec << ">(" << name << ", " << ptr_of[v] << ", row * " << row_len
+           << "u + c, 0u, true);\n";
+      w.preload[v] = name;
+    }
+  };
+  int phase = 0;
+  for (Step& ph : s.phases) {
+    const std::string P = "p" + std::to_string(phase++);
+    Writer w(prog_, ptr_of, it);
+    w.row_scalar = scalars;
+    Idx root;
+    root.key = "R";
+    root.shape = shape;
+    root.lin = "lin";
+    root.identity = true;
+    root.multi = multi;
+    const int rid = w.add_index(root);
+    std::ostringstream pre_decl, pre_load;
+    preloads(w, pre_decl, pre_load);
+    if (ph.kind == StepKind::kReduce) {
+      std::vector<Accum> accs;
+      std::vector<std::string> xs;
+      for (size_t r = 0; r < ph.reduces.size(); ++r) {
+        const ReduceSpec& rs = ph.reduces[r];
+        Accum a;
+        a.kind = rs.kind;
+        a.vt = prog_.type(rs.results[0]).dtype;
+        a.acc_t = acc_ctype(rs.kind, a.vt);
+        a.v = P + "_acc" + std::to_string(r);
+        accs.push_back(a);
+        xs.push_back(w.value(rs.inputs[0], rid));
+      }
+      const std::string body = w.body.str();
+      for (auto& a : accs) {
+        out_ << a.acc_t << " " << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
+        out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[4];\n";
+      }
+      out_ << "for (idx_t c = " << tix << " * " << vec << "u; c < " << row_len << "u; c += " << span << "u) {\n";
+      out_ << pre_decl.str() << pre_load.str();
+      out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
+      out_ << "const idx_t col = c + j;\nconst idx_t lin = row * " << row_len << "u + col;\n";
+      out_ << col_digits.str() << body;
+      for (size_t r = 0; r < accs.size(); ++r)
+        out_ << combine_stmt(accs[r].kind, accs[r].vt, accs[r].v, "(" + accs[r].acc_t + ")(" + xs[r] + ")") << "\n";
+      out_ << "}\n}\n";
+      // Wave butterfly, then every thread folds the 4 wave partials in wave
+      // order (same value in all threads, deterministic).
+      // (xor partners add the same two values, so every lane ends with the
+      // same bits).
+      for (auto& a : accs) {
+        out_ << "#pragma unroll\nfor (int m = 32; m >= 1; m >>= 1) {\n";
+        out_ << "const " << a.acc_t << " o = wave_shfl_xor(" << a.v << ", m);\n";
+        out_ << combine_stmt(a.kind, a.vt, a.v, "o") << "\n}\n";
+        if (!wpr) out_ << "if ((threadIdx.x & 63) == 0) sm_" << a.v << "[threadIdx.x >> 6] = " << a.v << ";\n";
+      }
+      if (!wpr) {
+        out_ << "__syncthreads();\n";
+        for (auto& a : accs) {
+          out_ << a.v << " = sm_" << a.v << "[0];\n";
+          out_ << "for (int k = 1; k < 4; ++k) { " << combine_stmt(a.kind, a.vt, a.v, "sm_" + a.v + "[k]") << " }\n";
+        }
+      }
+      // Fold the init values, round, and evaluate this phase's outputs.
+      Writer e(prog_, ptr_of, it);
+      e.row_scalar = scalars;
+      Idx oroot;
+      oroot.key = "O";
+      oroot.shape = kept;
+      oroot.lin = "row";
+      oroot.multi.assign(multi.begin(), multi.begin() + nkept);
+      const int oid = e.add_index(oroot);
+      Idx sidx;
+      sidx.key = "S";
+      sidx.lin = "0";
+      const int scal = e.add_index(sidx);
+      std::ostringstream fin;
+      for (size_t r = 0; r < accs.size(); ++r) {
+        const Accum& a = accs[r];
+        const ReduceSpec& rs = ph.reduces[r];
+        fin << combine_stmt(a.kind, a.vt, a.v, "(" + a.acc_t + ")(" + e.value(rs.inits[0], scal) + ")") << "\n";
+        const std::string rv = P + "_res" + std::to_string(r);
+        const DType vt = a.vt;
+        if (a.kind == ReducerKind::kAnd || a.kind == ReducerKind::kOr || !dtype_is_float(vt))
+          fin << "const " << dtype_compute_ctype(vt) << " " << rv << " = (" << dtype_compute_ctype(vt) << ")" << a.v
+              << ";\n";
+        else
+          fin << "const " << dtype_compute_ctype(vt) << " " << rv << " = " << round_to(vt, a.v) << ";\n";
+        e.row_scalar[rs.results[0]] = rv;
+      }
+      std::vector<std::pair<int, std::string>> outs;
+      for (int v : ph.outputs) outs.push_back({v, e.value(v, oid)});
+      std::ostringstream decl, assign;
+      for (auto& [v, expr] : outs) {
+        const std::string name = P + "_v" + std::to_string(v);
+        decl << dtype_compute_ctype(prog_.type(v).dtype) << " " << name << ";\n";
+        assign << name << " = " << expr << ";\n";
+        scalars[v] = name;
+      }
+      out_ << decl.str() << "{\n" << fin.str() << e.body.str() << assign.str() << "}\n";
+      for (size_t o = 0; o < s.outputs.size(); ++o)
+        if (scalars.count(s.outputs[o]) && prog_.type(s.outputs[o]).dims == kept &&
+            std::find(ph.outputs.begin(), ph.outputs.end(), s.outputs[o]) != ph.outputs.end())
+          out_ << "if (" << tix << " == 0) out" << o << "[row] = "
+               << to_storage(prog_.type(s.outputs[o]).dtype, scalars[s.outputs[o]]) << ";\n";
+    } else {
+      // Elementwise phase over the row.
+      std::vector<std::pair<size_t, std::string>> outs;
+      for (size_t o = 0; o < s.outputs.size(); ++o)
+        if (std::find(ph.outputs.begin(), ph.outputs.end(), s.outputs[o]) != ph.outputs.end())
+          outs.push_back({o, w.value(s.outputs[o], rid)});
+      const std::string body = w.body.str();
+      out_ << "for (idx_t c = " << tix << " * " << vec << "u; c < " << row_len << "u; c += " << span << "u) {\n";
+      out_ << pre_decl.str() << pre_load.str();
+      for (auto& [o, expr] : outs)
+        out_ << dtype_storage_ctype(prog_.type(s.outputs[o]).dtype) << " res" << o << "[" << vec << "];\n";
+      out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
+      out_ << "const idx_t col = c + j;\nconst idx_t lin = row * " << row_len << "u + col;\n";
+      out_ << col_digits.str() << body;
+      for (auto& [o, expr] : outs)
+        out_ << "res" << o << "[j] = " << to_storage(prog_.type(s.outputs[o]).dtype, expr) << ";\n";
+      out_ << "}\n";
+      for (auto& [o, expr] : outs) {
+        const DType t = prog_.type(s.outputs[o]).dtype;
+        out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", row * " << row_len
+             << "u + c, res" << o << ", 0u, true);\n";
+      }
+      out_ << "}\n";
+    }
+  }
+  out_ << "}\n\n";
+}
+
 }  // namespace
 
 std::string generate_kernels(const Program& prog, Plan& plan) {
@@ -1003,6 +1204,7 @@ std::string generate_kernels(const Program& prog, Plan& plan) {
   for (Step& s : plan.steps) {
     if (s.kind == StepKind::kLoop) gen.loop(s);
     else if (s.kind == StepKind::kReduce) gen.reduce(s);
+    else if (s.kind == StepKind::kRowFused) gen.row_fused(s);
   }
   return out.str();
 }

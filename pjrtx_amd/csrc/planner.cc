@@ -167,6 +167,9 @@ class Planner {
   int order_preserving_source(int v) const;
   void merge_siblings(std::vector<Step>* steps);
   void merge_epilogues(std::vector<Step>* steps);
+  void fuse_row_chains(std::vector<Step>* steps);
+  bool row_uses_ok(const Step& x, const std::set<int>& produced, const Dims& shape, size_t nkept) const;
+  void shape_row_fused(Step* s);
   void schedule(std::vector<Step>* steps);
   void liveness();
   void shape_reduce(Step* s);
@@ -496,6 +499,148 @@ void Planner::merge_epilogues(std::vector<Step>* steps) {
   }
 }
 
+// Every use of a value derived from an earlier phase must be at the current
+// row: elementwise ops over the kept shape, and broadcasts of the kept shape
+// onto the leading dims of the row operand.
+bool Planner::row_uses_ok(const Step& x, const std::set<int>& produced, const Dims& shape, size_t nkept) const {
+  const Dims kept(shape.begin(), shape.begin() + nkept);
+  std::set<int> derived(produced.begin(), produced.end());
+  std::vector<int> ops = x.ops;
+  ops.insert(ops.end(), x.epilogue_ops.begin(), x.epilogue_ops.end());
+  std::sort(ops.begin(), ops.end());
+  for (int oi : ops) {
+    const Op& op = prog_.ops[oi];
+    bool uses = false;
+    for (int u : op.operands) uses = uses || derived.count(u);
+    if (!uses) continue;
+    if (op.kind == OpKind::kBroadcastInDim) {
+      if (prog_.type(op.operands[0]).dims != kept || prog_.type(op.results[0]).dims != shape) return false;
+      for (size_t k = 0; k < op.dims.size(); ++k)
+        if (op.dims[k] != static_cast<int64_t>(k)) return false;
+      continue;
+    }
+    if (!op_is_elementwise(op.kind) || op.results.empty() || prog_.type(op.results[0]).dims != kept) return false;
+    for (int u : op.operands)  // other operands: kept-shaped derived values or scalars
+      if (!derived.count(u) && prog_.type(u).rank() != 0 && prog_.type(u).dims != kept) return false;
+    derived.insert(op.results[0]);
+  }
+  return true;
+}
+
+void Planner::fuse_row_chains(std::vector<Step>* steps) {
+  auto reduce_shape_ok = [&](const Step& r, Dims* shape, size_t* nkept, int64_t* row_len) {
+    if (r.kind != StepKind::kReduce) return false;
+    const Dims& sh = r.reduce_operand_shape;
+    const size_t rank = sh.size(), nred = r.reduce_dims.size();
+    if (nred == 0 || nred > rank) return false;
+    for (size_t k = 0; k < nred; ++k)
+      if (r.reduce_dims[k] != static_cast<int64_t>(rank - nred + k)) return false;
+    int64_t len = 1;
+    for (size_t d = rank - nred; d < rank; ++d) len *= sh[d];
+    if (len < 32 || len > opts_.row_fuse_max || num_elements(sh) >= (int64_t(1) << 32)) return false;
+    for (const ReduceSpec& rs : r.reduces)
+      if (rs.kind == ReducerKind::kArgMax || rs.kind == ReducerKind::kArgMin) return false;
+    *shape = sh;
+    *nkept = rank - nred;
+    *row_len = len;
+    return true;
+  };
+  for (size_t a = 0; a < steps->size(); ++a) {
+    Dims shape;
+    size_t nkept = 0;
+    int64_t row_len = 0;
+    if (!reduce_shape_ok((*steps)[a], &shape, &nkept, &row_len)) continue;
+    std::vector<size_t> group = {a};
+    std::set<int> produced((*steps)[a].outputs.begin(), (*steps)[a].outputs.end());
+    for (size_t b = a + 1; b < steps->size(); ++b) {
+      const Step& x = (*steps)[b];
+      bool dep = false;
+      for (int v : x.inputs) dep = dep || produced.count(v);
+      if (!dep) continue;
+      Dims xs;
+      size_t xk = 0;
+      int64_t xl = 0;
+      const bool red = reduce_shape_ok(x, &xs, &xk, &xl) && xs == shape && xk == nkept;
+      const bool loop = x.kind == StepKind::kLoop && x.loop_shape == shape;
+      if ((!red && !loop) || !row_uses_ok(x, produced, shape, nkept)) break;
+      group.push_back(b);
+      produced.insert(x.outputs.begin(), x.outputs.end());
+      if (loop) break;  // the elementwise pass ends a chain
+    }
+    if (group.size() < 2) continue;
+    // A later member may read a value that an unfused step in between
+    // produces from an earlier member: then the chain cannot be one kernel.
+    std::set<int> member_outs;
+    for (size_t g : group) member_outs.insert((*steps)[g].outputs.begin(), (*steps)[g].outputs.end());
+    bool blocked = false;
+    for (size_t b = a + 1; b <= group.back() && !blocked; ++b) {
+      if (std::find(group.begin(), group.end(), b) != group.end()) continue;
+      const Step& x = (*steps)[b];
+      bool reads_group = false;
+      for (int v : x.inputs) reads_group = reads_group || member_outs.count(v);
+      if (!reads_group) continue;
+      for (size_t g : group)
+        for (int v : (*steps)[g].inputs)
+          if (std::find(x.outputs.begin(), x.outputs.end(), v) != x.outputs.end()) blocked = true;
+    }
+    if (blocked) continue;
+    Step f;
+    f.kind = StepKind::kRowFused;
+    f.reduce_operand_shape = shape;
+    f.reduce_dims = (*steps)[a].reduce_dims;
+    std::set<int> group_ops;
+    for (size_t g : group) {
+      const Step& x = (*steps)[g];
+      group_ops.insert(x.ops.begin(), x.ops.end());
+      group_ops.insert(x.epilogue_ops.begin(), x.epilogue_ops.end());
+      for (const ReduceSpec& rs : x.reduces) group_ops.insert(rs.op_index);
+    }
+    for (size_t g : group) {
+      const Step& x = (*steps)[g];
+      for (int v : x.inputs)
+        if (!member_outs.count(v) && std::find(f.inputs.begin(), f.inputs.end(), v) == f.inputs.end())
+          f.inputs.push_back(v);
+      for (int v : x.outputs) {  // stored only when read outside the kernel
+        bool outside = outputs_.count(v) > 0;
+        auto it = users_.find(v);
+        if (it != users_.end())
+          for (int u : it->second) outside = outside || !group_ops.count(u);
+        if (outside) f.outputs.push_back(v);
+      }
+      f.phases.push_back(x);
+    }
+    if (f.outputs.empty()) continue;
+    for (size_t k = group.size(); k-- > 0;) steps->erase(steps->begin() + group[k]);
+    steps->insert(steps->begin() + a, std::move(f));
+  }
+}
+
+void Planner::shape_row_fused(Step* s) {
+  const Dims& shape = s->reduce_operand_shape;
+  int64_t rows = 1, row_len = 1;
+  const size_t nred = s->reduce_dims.size();
+  for (size_t d = 0; d < shape.size(); ++d) (d + nred < shape.size() ? rows : row_len) *= shape[d];
+  s->rows = rows;
+  s->row_len = row_len;
+  s->row_schedule = true;
+  size_t min_size = 8;
+  for (int v : s->inputs)
+    if (prog_.type(v).elements() == num_elements(shape)) min_size = std::min(min_size, dtype_size(prog_.type(v).dtype));
+  for (int v : s->outputs)
+    if (prog_.type(v).elements() == num_elements(shape)) min_size = std::min(min_size, dtype_size(prog_.type(v).dtype));
+  int vec = static_cast<int>(16 / std::max<size_t>(min_size, 1));
+  vec = std::max(1, std::min(vec, 8));
+  while (vec > 1 && row_len % vec != 0) vec /= 2;
+  s->vec = vec;
+  s->splits = 1;
+  s->chunk = row_len;
+  // Many short rows: a wave per row needs no workgroup barrier and packs
+  // four rows per workgroup.
+  s->wave_per_row = rows >= 1024 && row_len <= 4096;
+  s->grid = static_cast<uint32_t>(s->wave_per_row ? (rows + 3) / 4 : rows);
+  s->block = 256;
+}
+
 void Planner::schedule(std::vector<Step>* steps) {
   auto v2s = value_to_step(*steps);
   const size_t n = steps->size();
@@ -638,6 +783,7 @@ Plan Planner::run() {
   build_steps(&steps);
   if (opts_.fuse_siblings) merge_siblings(&steps);
   if (opts_.fuse_epilogues) merge_epilogues(&steps);
+  if (opts_.row_fuse_max > 0) fuse_row_chains(&steps);
   schedule(&steps);
   int kernel_id = 0;
   for (Step& s : steps) {
@@ -647,6 +793,9 @@ Plan Planner::run() {
     } else if (s.kind == StepKind::kReduce) {
       shape_reduce(&s);
       s.name = strformat("pjrtx_fusion_reduce_%d", kernel_id++);
+    } else if (s.kind == StepKind::kRowFused) {
+      shape_row_fused(&s);
+      s.name = strformat("pjrtx_fusion_row_%d", kernel_id++);
     }
   }
   plan_.steps = std::move(steps);
@@ -669,7 +818,7 @@ std::string Plan::describe(const Program& prog) const {
     const Step& s = steps[i];
     if (i) o << ",";
     const char* kind = s.kind == StepKind::kLoop ? "loop" : s.kind == StepKind::kReduce ? "reduce"
-                     : s.kind == StepKind::kAlias ? "alias" : "library";
+                     : s.kind == StepKind::kAlias ? "alias" : s.kind == StepKind::kRowFused ? "rowfused" : "library";
     o << "{\"kind\":\"" << kind << "\",\"name\":\"" << s.name << "\"";
     o << ",\"inputs\":" << list(s.inputs) << ",\"outputs\":" << list(s.outputs);
     auto bytes_of = [&](const std::vector<int>& vs) {
@@ -684,6 +833,9 @@ std::string Plan::describe(const Program& prog) const {
     o << "],\"epilogue\":[";
     for (size_t k = 0; k < s.epilogue_ops.size(); ++k) o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.epilogue_ops[k]].kind) << "\"";
     o << "]";
+    if (s.kind == StepKind::kRowFused)
+      o << ",\"phases\":" << s.phases.size() << ",\"rows\":" << s.rows << ",\"row_len\":" << s.row_len
+        << ",\"wave_per_row\":" << (s.wave_per_row ? "true" : "false");
     if (s.kind == StepKind::kReduce) {
       o << ",\"reducers\":[";
       for (size_t k = 0; k < s.reduces.size(); ++k) o << (k ? "," : "") << "\"" << reducer_name(s.reduces[k].kind) << "\"";

@@ -41,7 +41,11 @@ struct ReduceSpec {
   std::vector<int> results;  // result values
 };
 
-enum class StepKind { kLoop, kReduce, kAlias, kLibrary };
+// kRowFused: a chain of row reductions over the same trailing dims plus the
+// elementwise pass that consumes them, as one kernel with one workgroup per
+// row (softmax, RMSNorm, layer norm). `phases` holds the fused steps in
+// order; earlier phases' results are per-row scalars in later phases.
+enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused };
 
 enum class LibKind { kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad };
 const char* lib_kind_name(LibKind k);
@@ -83,6 +87,10 @@ struct Step {
   uint32_t block = 256;
 
   std::vector<int> release_after;  // intermediate values dead after this step
+
+  // kRowFused
+  std::vector<Step> phases;
+  bool wave_per_row = false;  // one wave per row (4 rows per workgroup), else one workgroup per row
 };
 
 struct Plan {
@@ -108,6 +116,10 @@ struct PlanOptions {
   int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 1024);
   bool fuse_siblings = true;
   bool fuse_epilogues = true;
+  // Row chains (reduce -> reduce/loop over the same rows) become one kernel
+  // when a row has at most this many elements (environment:
+  // PJRTX_ROW_FUSE_MAX, 0 disables).
+  int64_t row_fuse_max = env_int("PJRTX_ROW_FUSE_MAX", 16384);
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());

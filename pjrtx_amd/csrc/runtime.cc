@@ -377,7 +377,7 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
   L->scratch.resize(plan_.steps.size());
   for (size_t i = 0; i < plan_.steps.size(); ++i) {
     const Step& s = plan_.steps[i];
-    if (s.kind == StepKind::kLoop || s.kind == StepKind::kReduce) {
+    if (s.kind == StepKind::kLoop || s.kind == StepKind::kReduce || s.kind == StepKind::kRowFused) {
       hip_check(hipModuleGetFunction(&L->funcs[i], L->module, s.name.c_str()), "hipModuleGetFunction");
     }
     if (s.combine_grid) {
@@ -431,11 +431,12 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       stats_.library_calls++;
       return;
     case StepKind::kLoop:
-    case StepKind::kReduce: {
+    case StepKind::kReduce:
+    case StepKind::kRowFused: {
       if (phase != 1)
         for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
       if (s.kind == StepKind::kLoop && num_elements(s.loop_shape) == 0) return;
-      if (s.kind == StepKind::kReduce && s.rows == 0) return;
+      if ((s.kind == StepKind::kReduce || s.kind == StepKind::kRowFused) && s.rows == 0) return;
       std::vector<void*> ptrs;
       ptrs.reserve(s.inputs.size() + s.outputs.size() + 2);
       for (int v : s.inputs) ptrs.push_back(vals[v] ? vals[v]->ptr : nullptr);

@@ -50,8 +50,10 @@ def test_full_reduce_and_middle_axis(plugin):
     assert all(not st["row_schedule"] for st in p["steps"])
 
 
-def test_multi_use_cheap_value_is_recomputed(plugin):
-    # softmax-like: exp(x - max) feeds both the sum and the divide.
+def test_multi_use_cheap_value_is_recomputed(plugin, monkeypatch):
+    # softmax-like: exp(x - max) feeds both the sum and the divide (row
+    # fusion off, so that the three passes stay separate steps).
+    monkeypatch.setenv("PJRTX_ROW_FUSE_MAX", "0")
     b = Builder()
     x = b.param((8, 128), "f32")
     mx = b.max(x, [1])
@@ -66,7 +68,39 @@ def test_multi_use_cheap_value_is_recomputed(plugin):
     assert "exponential" in p["steps"][1]["ops"] and "exponential" in p["steps"][2]["ops"]
 
 
-def test_liveness_releases_intermediates(plugin):
+def _softmax(b, x, via=None):
+    mx = b.max(x, [1])
+    if via is not None:
+        mx = via(mx)
+    e = b.exp(b.subtract(x, b.broadcast_in_dim(mx, x.shape, [0])))
+    s = b.sum(e, [1])
+    return b.divide(e, b.broadcast_in_dim(s, x.shape, [0]))
+
+
+def test_softmax_is_one_row_kernel(plugin):
+    b = Builder()
+    x = b.param((8, 128), "f32")
+    p = plan(plugin, b.build([_softmax(b, x)]))
+    assert [st["kind"] for st in p["steps"]] == ["rowfused"]
+    assert p["steps"][0]["phases"] == 3 and p["steps"][0]["rows"] == 8 and p["steps"][0]["row_len"] == 128
+    # the row max and sum stay in registers: only the softmax output is stored
+    assert len(p["steps"][0]["outputs"]) == 1
+
+
+def test_row_fusion_refuses_reindexed_row_values(plugin):
+    # the max is reversed before it is broadcast: row r would need row 7-r's
+    # value, so the phases cannot share one workgroup per row.
+    b = Builder()
+    x = b.param((8, 128), "f32")
+    p = plan(plugin, b.build([_softmax(b, x, via=lambda m: b.reverse(m, [0]))]))
+    # max stays its own reduction; sum -> divide still fuse (the reversed max
+    # is read from memory there, like any input).
+    assert [st["kind"] for st in p["steps"]] == ["reduce", "rowfused"]
+    assert p["steps"][0]["reducers"] == ["max"] and p["steps"][1]["phases"] == 2
+
+
+def test_liveness_releases_intermediates(plugin, monkeypatch):
+    monkeypatch.setenv("PJRTX_ROW_FUSE_MAX", "0")  # keep the max as a buffer between two steps
     b = Builder()
     x = b.param((4, 256), "f32")
     mx = b.max(x, [1])
