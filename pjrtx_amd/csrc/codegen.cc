@@ -1003,10 +1003,17 @@ void KernelGen::reduce(Step& s) {
   out_ << "}\n}\n\n";
 }
 
-// Row-fused kernel: one workgroup per row. Each reduce phase walks the row
-// (16-byte loads; after the first phase the row is served from cache),
-// reduces across the workgroup, and every thread keeps the phase results as
-// per-row scalars; the final elementwise phase writes the row outputs.
+// Row-fused kernel: one workgroup (or one wave) per row. Each reduce phase
+// walks the row, reduces across the workgroup, and every thread keeps the
+// phase results as per-row scalars; the final elementwise phase writes the
+// row outputs. When a thread's share of the row fits in registers
+// (kRowCacheRegs 32-bit registers over all full-shape inputs) the whole share
+// is loaded once, with every 16-byte load in flight together, and all phases
+// read the registers; otherwise each phase streams the row again (the
+// re-reads hit the cache).
+constexpr int64_t kRowCacheRegs = 64;
+constexpr int64_t kRowCacheSweeps = 16;
+
 void KernelGen::row_fused(Step& s) {
   std::map<int, std::string> ptr_of;
   signature(s, &ptr_of, false);
@@ -1058,11 +1065,50 @@ void KernelGen::row_fused(Step& s) {
   }
   const Dims kept(shape.begin(), shape.begin() + nkept);
   std::map<int, std::string> scalars;
-  auto preloads = [&](Writer& w, std::ostream& decl, std::ostream& load) {
+  // Register-resident share of the row: sweep k covers columns
+  // tix*vec + k*span .. +vec (vec divides row_len, so a sweep that starts
+  // inside the row is whole).
+  const int64_t sweeps = (row_len + span - 1) / span;
+  int64_t cache_regs = 0;
+  for (int v : s.inputs)
+    if (prog_.type(v).elements() == n_all)
+      cache_regs += sweeps * vec * static_cast<int64_t>(std::max<size_t>(dtype_size(prog_.type(v).dtype), 4)) / 4;
+  const bool cached = sweeps <= kRowCacheSweeps && cache_regs <= kRowCacheRegs;
+  const bool ragged = row_len % span != 0;
+  auto sweep_open = [&](std::ostream& o) {
+    if (cached) {
+      o << "#pragma unroll\nfor (int k = 0; k < " << sweeps << "; ++k) {\n";
+      o << "const idx_t c = " << tix << " * " << vec << "u + (idx_t)k * " << span << "u;\n";
+      if (ragged) o << "if (c < " << row_len << "u) {\n";
+    } else {
+      o << "for (idx_t c = " << tix << " * " << vec << "u; c < " << row_len << "u; c += " << span << "u) {\n";
+    }
+  };
+  auto sweep_close = [&](std::ostream& o) { o << ((cached && ragged) ? "}\n}\n" : "}\n"); };
+  if (cached) {
     for (int v : s.inputs) {
       if (prog_.type(v).elements() != n_all) continue;
       const std::string st = dtype_storage_ctype(prog_.type(v).dtype);
+      out_ << st << " pre_" << ptr_of[v] << "[" << sweeps << "][" << vec << "];\n";
+    }
+    sweep_open(out_);
+    for (int v : s.inputs) {
+      if (prog_.type(v).elements() != n_all) continue;
+      const std::string st = dtype_storage_ctype(prog_.type(v).dtype);
+      out_ << "ldv<" << st << ", " << vec << ">(pre_" << ptr_of[v] << "[k], " << ptr_of[v] << ", row * " << row_len
+           << "u + c, 0u, true);\n";
+    }
+    sweep_close(out_);
+  }
+  auto preloads = [&](Writer& w, std::ostream& decl, std::ostream& load) {
+    for (int v : s.inputs) {
+      if (prog_.type(v).elements() != n_all) continue;
       const std::string name = "pre_" + ptr_of[v];
+      if (cached) {
+        w.preload[v] = name + "[k]";
+        continue;
+      }
+      const std::string st = dtype_storage_ctype(prog_.type(v).dtype);
       decl << st << " " << name << "[" << vec << "];\n";
       load << "ldv<" << st << ", " << vec << ">(" << name << ", " << ptr_of[v] << ", row * " << row_len
            << "u + c, 0u, true);\n";
@@ -1101,14 +1147,15 @@ void KernelGen::row_fused(Step& s) {
         out_ << a.acc_t << " " << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
         out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[4];\n";
       }
-      out_ << "for (idx_t c = " << tix << " * " << vec << "u; c < " << row_len << "u; c += " << span << "u) {\n";
+      sweep_open(out_);
       out_ << pre_decl.str() << pre_load.str();
       out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
       out_ << "const idx_t col = c + j;\nconst idx_t lin = row * " << row_len << "u + col;\n";
       out_ << col_digits.str() << body;
       for (size_t r = 0; r < accs.size(); ++r)
         out_ << combine_stmt(accs[r].kind, accs[r].vt, accs[r].v, "(" + accs[r].acc_t + ")(" + xs[r] + ")") << "\n";
-      out_ << "}\n}\n";
+      out_ << "}\n";
+      sweep_close(out_);
       // Wave butterfly, then every thread folds the 4 wave partials in wave
       // order (same value in all threads, deterministic).
       // (xor partners add the same two values, so every lane ends with the
@@ -1175,7 +1222,7 @@ void KernelGen::row_fused(Step& s) {
         if (std::find(ph.outputs.begin(), ph.outputs.end(), s.outputs[o]) != ph.outputs.end())
           outs.push_back({o, w.value(s.outputs[o], rid)});
       const std::string body = w.body.str();
-      out_ << "for (idx_t c = " << tix << " * " << vec << "u; c < " << row_len << "u; c += " << span << "u) {\n";
+      sweep_open(out_);
       out_ << pre_decl.str() << pre_load.str();
       for (auto& [o, expr] : outs)
         out_ << dtype_storage_ctype(prog_.type(s.outputs[o]).dtype) << " res" << o << "[" << vec << "];\n";
@@ -1190,7 +1237,7 @@ void KernelGen::row_fused(Step& s) {
         out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", row * " << row_len
              << "u + c, res" << o << ", 0u, true);\n";
       }
-      out_ << "}\n";
+      sweep_close(out_);
     }
   }
   out_ << "}\n\n";
