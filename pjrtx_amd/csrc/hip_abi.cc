@@ -118,6 +118,7 @@ int pjrtx_hip_synchronize(int device) {
 int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
   return guarded([&] {
     Program prog = parse_stablehlo(std::string(text, len));
+    rewrite_program(&prog);
     Plan plan = make_plan(prog);
     copy_out(plan.describe(prog), out, cap, needed);
   });
@@ -126,6 +127,7 @@ int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t*
 int pjrtx_compile_check(const char* text, size_t len, const char* arch, size_t* code_size) {
   return guarded([&] {
     Program prog = parse_stablehlo(std::string(text, len));
+    rewrite_program(&prog);
     Plan plan = make_plan(prog);
     size_t n = 0;
     if (plan.num_fusion_kernels > 0) n = compile_kernels(plan.kernel_source, arch ? arch : "gfx950").size();
@@ -136,6 +138,7 @@ int pjrtx_compile_check(const char* text, size_t len, const char* arch, size_t* 
 int pjrtx_kernel_source(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
   return guarded([&] {
     Program prog = parse_stablehlo(std::string(text, len));
+    rewrite_program(&prog);
     Plan plan = make_plan(prog);
     copy_out(kernel_translation_unit(plan.kernel_source), out, cap, needed);
   });

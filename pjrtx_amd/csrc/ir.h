@@ -38,6 +38,10 @@ enum class OpKind {
   kConcatenate, kPad, kDynamicSlice, kDynamicUpdateSlice,
   // reductions and library ops
   kReduce, kDotGeneral, kGather, kScatter,
+  // stablehlo.custom_call (only known targets pass validation), and the
+  // fused attention op that the program rewrite produces from a
+  // scaled-dot-product-attention custom call or the unfused pattern.
+  kCustomCall, kAttention,
   kReturn,
 };
 
@@ -50,6 +54,22 @@ enum class CmpType { kNotSet, kFloat, kTotalOrder, kSigned, kUnsigned };
 
 // Nested computation of reduce / scatter (its own parameters, ops, return).
 struct Region;
+
+// kAttention: out = softmax_k(scale * round?(q.k) over allowed keys) . v per
+// (batch, head, query). Operands (q, k, v[, offset scalar]). Allowed keys:
+// k < kv_len and, when causal, k <= q_coef * q + offset (+ the offset
+// operand when present).
+struct AttentionAttrs {
+  // Operand layouts: 0 = [B, H, S, D] (the unfused dot_general form),
+  // 1 = [B, S, H, D], 2 = [S, H, D] (the custom call's rank 4 / rank 3).
+  int layout = 0;
+  double scale = 1.0;
+  bool causal = false;
+  int q_coef = 1;
+  int64_t offset = 0;
+  bool has_offset_operand = false;
+  bool round_scores = false;
+};
 
 struct Op {
   OpKind kind = OpKind::kReturn;
@@ -91,6 +111,10 @@ struct Op {
 
   // reduce / scatter body
   std::vector<Region> regions;
+
+  // custom_call target name; kAttention attributes
+  std::string target;
+  AttentionAttrs attn;
 };
 
 struct Region {

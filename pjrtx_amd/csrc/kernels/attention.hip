@@ -1,0 +1,493 @@
+// Fused attention for gfx950: softmax(scale * Q.K^T, masked) . V in one
+// kernel, the score matrix never leaving the chip.
+//
+//  * attn_tiles (bf16 / f16, head dim 64 or 128): a workgroup owns 128
+//    queries of one (batch, head), 32 per wave, and walks the allowed keys in
+//    blocks of 64 staged through LDS (K row-major, V transposed). Each wave
+//    computes S^T = K.Q^T on v_mfma_f32_16x16x32 so that a lane holds 16
+//    scores of ONE query: the row max and sum are a 16-value in-lane fold
+//    plus two xor shuffles. The exponentials, rounded to the input type, are
+//    the B operand of O^T += V^T.P^T directly from registers (the V^T tile
+//    stores keys in the order a lane holds them), and the running output is
+//    rescaled per lane by its own query's factor. Q stays in registers for
+//    the whole walk. Workgroups take the heaviest (latest) query tiles first;
+//    when B*H is a multiple of 8, one head's query tiles run on one XCD so
+//    its K and V are served from that XCD's L2.
+//  * attn_rows (any element type, head dim <= 512): one workgroup per query
+//    row, its 4 waves splitting the keys in blocks of 64 (one key per lane
+//    for the scores, then lanes across the head dim for P.V), combined at the
+//    end in wave order. Decode (one query) and f32 take this kernel.
+//
+// Both use the online-softmax recurrence (running max m, sum l, output
+// rescaled by exp(m_old - m_new)); a row with no allowed key yields 0/0 =
+// NaN as the unfused softmax does.
+//
+// Replaces the reference's scaled-dot-product-attention custom call
+// (reference: src/backend/mlx_metal/api.cc:4928-5062, which calls
+// mlx::core::fast::scaled_dot_product_attention with the boolean mask of
+// api.cc:937-950) and, through the planner's rewrite, its unfused
+// dot_general / softmax / dot_general path (api.cc:3349-3498, 3982-4044).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "common.h"
+#include "kernels/attention.h"
+
+namespace pjrtx {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+template <bool kF16>
+__device__ __forceinline__ uint16_t from_f32(float x) {
+  if constexpr (kF16) return f32_to_f16(x);
+  else return f32_to_bf16_rne(x);
+}
+template <bool kF16>
+__device__ __forceinline__ float to_f32(uint16_t x) {
+  if constexpr (kF16) return f16_to_f32(x);
+  else return bf16_to_f32(x);
+}
+
+template <bool kF16>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                   0);
+}
+
+__device__ __forceinline__ int64_t read_offset(const AttnParams& p) {
+  int64_t off = 0;
+  if (p.offset_ptr) {
+    switch (p.offset_bytes) {
+      case 8: off += *static_cast<const int64_t*>(p.offset_ptr); break;
+      case 4:
+        off += p.offset_signed ? (int64_t)*static_cast<const int32_t*>(p.offset_ptr)
+                               : (int64_t)*static_cast<const uint32_t*>(p.offset_ptr);
+        break;
+      case 2:
+        off += p.offset_signed ? (int64_t)*static_cast<const int16_t*>(p.offset_ptr)
+                               : (int64_t)*static_cast<const uint16_t*>(p.offset_ptr);
+        break;
+      default:
+        off += p.offset_signed ? (int64_t)*static_cast<const int8_t*>(p.offset_ptr)
+                               : (int64_t)*static_cast<const uint8_t*>(p.offset_ptr);
+        break;
+    }
+    if (p.offset_as_s32) off = (int64_t)(int32_t)(uint32_t)(uint64_t)off;
+  }
+  return off + p.offset;
+}
+
+// Last allowed key of query q, clamped to [-1, Skv - 1].
+__device__ __forceinline__ int key_limit(const AttnParams& p, int64_t off, int64_t q) {
+  const int64_t lim = p.causal ? (int64_t)p.q_coef * q + off : (int64_t)p.Skv - 1;
+  return (int)std::max<int64_t>(-1, std::min<int64_t>(lim, (int64_t)p.Skv - 1));
+}
+
+// ---------------------------------------------------------------- tiles
+
+constexpr int FQ = 128;  // queries per workgroup (32 per wave)
+constexpr int FK = 64;   // keys per block
+
+// K tile [FK][D]: 16-byte chunk `ch` of key row `row`, XOR-swizzled so the
+// 16 rows a fragment read touches fall in distinct banks.
+template <int D>
+__device__ __forceinline__ int kswz(int row, int ch) {
+  if constexpr (D == 128) return row * 128 + ((ch ^ (row & 15)) << 3);
+  else return row * 64 + ((ch ^ ((row >> 1) & 7)) << 3);
+}
+// V^T tile [D][FK] (64 key positions per head-dim row), same swizzle idea.
+__device__ __forceinline__ int vswz(int row, int ch) { return row * 64 + ((ch ^ ((row >> 1) & 7)) << 3); }
+// Position of block key j in a V^T row. Lane group g of a wave holds, for a
+// 32-key step, keys 4g..4g+3 and 16+4g..16+4g+3 of its S^T tiles; placing
+// them at positions 8g..8g+7 makes the lane's P values a contiguous B
+// fragment.
+__device__ __forceinline__ int vpos(int key) {
+  return (key & 32) | (((key & 15) >> 2) << 3) | (((key >> 4) & 1) << 2) | (key & 3);
+}
+
+template <bool kF16, int D>
+__global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_t* __restrict__ Q,
+                                                     const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+                                                     uint16_t* __restrict__ O) {
+  constexpr int NCH = D / 8;   // 16-byte chunks per row
+  constexpr int NDS = D / 32;  // MFMA k-steps over the head dim
+  constexpr int NDT = D / 16;  // 16-wide output tiles over the head dim
+  constexpr int KPT = D / 32;  // K chunks per thread; V keys per thread
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[FK * D];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * FK];
+
+  const int nq = (p.Sq + FQ - 1) / FQ;
+  const int BH = p.B * p.Hq;
+  const int bid = blockIdx.x;
+  int bh, qtile;
+  if (BH % 8 == 0) {
+    const int x = bid & 7, n = bid >> 3;
+    bh = (n / nq) * 8 + x;
+    qtile = nq - 1 - n % nq;
+  } else {
+    bh = bid % BH;
+    qtile = nq - 1 - bid / BH;
+  }
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int q0 = qtile * FQ;
+  const uint16_t* Qp = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h;
+  const uint16_t* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
+  const uint16_t* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
+  uint16_t* Op = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  // Q fragments: the B operand of S^T = K.Q^T (lane: query c16 of the
+  // 16-query tile, head dims 32*ds + 8*g .. +8).
+  u32x4 qf[2][NDS];
+  int lim[2];
+  const int64_t off = read_offset(p);
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = q0 + wave * 32 + qt * 16 + c16;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+      qf[qt][ds] = q < p.Sq ? *reinterpret_cast<const u32x4*>(Qp + (int64_t)q * p.q_s + ds * 32 + g * 8) : zero;
+    lim[qt] = key_limit(p, off, q);
+  }
+  // Keys the workgroup needs, and the prefix that needs no mask.
+  const int kend = key_limit(p, off, std::min(q0 + FQ, p.Sq) - 1) + 1;
+  const int free_end = key_limit(p, off, q0) + 1;  // q_coef >= 0: the first query has the lowest limit
+  const int nblocks = (kend + FK - 1) / FK;
+
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  f32x4 oacc[NDT][2];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) oacc[dt][0] = oacc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 kreg[KPT], vreg[KPT];
+  const int vdc = tid % NCH, vkg = tid / NCH;  // V: head-dim chunk, key group of KPT keys
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int c = tid + 256 * j;
+      const int key = kb * FK + c / NCH;
+      kreg[j] = key < p.Skv ? *reinterpret_cast<const u32x4*>(Kp + (int64_t)key * p.k_s + (c % NCH) * 8) : zero;
+    }
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+      const int key = kb * FK + vkg * KPT + r;
+      vreg[r] = key < p.Skv ? *reinterpret_cast<const u32x4*>(Vp + (int64_t)key * p.v_s + vdc * 8) : zero;
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int c = tid + 256 * j;
+      *reinterpret_cast<u32x4*>(&Ks[kswz<D>(c / NCH, c % NCH)]) = kreg[j];
+    }
+    const int pos = vpos(vkg * KPT);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t e[KPT];
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) e[r] = (vreg[r][i >> 1] >> (16 * (i & 1))) & 0xffffu;
+      const int at = vswz(vdc * 8 + i, pos >> 3) + (pos & 7);
+      if constexpr (KPT == 4) {
+        *reinterpret_cast<u32x2*>(&Vt[at]) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+      } else {
+        *reinterpret_cast<uint32_t*>(&Vt[at]) = e[0] | (e[1] << 16);
+      }
+    }
+  };
+
+  if (nblocks > 0) {
+    gload(0);
+    lstore();
+  }
+  __syncthreads();
+  for (int kb = 0; kb < nblocks; ++kb) {
+    if (kb + 1 < nblocks) gload(kb + 1);
+    // S^T[key][query] for the wave's 32 queries and the block's 64 keys.
+    f32x4 sacc[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) sacc[kt][0] = sacc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&Ks[kswz<D>(kt * 16 + c16, ds * 4 + g)]);
+        sacc[kt][0] = mfma16<kF16>(a, qf[0][ds], sacc[kt][0]);
+        sacc[kt][1] = mfma16<kF16>(a, qf[1][ds], sacc[kt][1]);
+      }
+    }
+    const bool need_mask = kb * FK + FK > free_end;
+    u32x4 pf[2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float s[4][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = sacc[kt][qt][r];
+          if (p.round_scores) x = to_f32<kF16>(from_f32<kF16>(x));
+          x *= p.scale;
+          if (need_mask && kb * FK + kt * 16 + g * 4 + r > lim[qt]) x = -INFINITY;
+          s[kt][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m[qt], mx);
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = expf(m[qt] - mref);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[kt][r] = expf(s[kt][r] - mref);
+          ps += s[kt][r];
+        }
+      ps += __shfl_xor(ps, 16);
+      ps += __shfl_xor(ps, 32);
+      l[qt] = l[qt] * alpha + ps;
+      m[qt] = mnew;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt][qt] *= alpha;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          w[j] = (uint32_t)from_f32<kF16>(s[2 * st][2 * j]) | ((uint32_t)from_f32<kF16>(s[2 * st][2 * j + 1]) << 16);
+          w[2 + j] = (uint32_t)from_f32<kF16>(s[2 * st + 1][2 * j]) |
+                     ((uint32_t)from_f32<kF16>(s[2 * st + 1][2 * j + 1]) << 16);
+        }
+        pf[qt][st] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+    // O^T[d][query] += V^T[d][key] . P^T[key][query]
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&Vt[vswz(dt * 16 + c16, st * 4 + g)]);
+        oacc[dt][0] = mfma16<kF16>(a, pf[0][st], oacc[dt][0]);
+        oacc[dt][1] = mfma16<kF16>(a, pf[1][st], oacc[dt][1]);
+      }
+    }
+    __syncthreads();
+    if (kb + 1 < nblocks) lstore();
+    __syncthreads();
+  }
+
+  // Lane: query c16 of tile qt, head dims 16*dt + 4*g .. +4.
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = q0 + wave * 32 + qt * 16 + c16;
+    if (q >= p.Sq) continue;
+    uint16_t* orow = Op + (int64_t)q * p.o_s;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      uint32_t w[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        w[j] = (uint32_t)from_f32<kF16>(oacc[dt][qt][2 * j] / l[qt]) |
+               ((uint32_t)from_f32<kF16>(oacc[dt][qt][2 * j + 1] / l[qt]) << 16);
+      *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{w[0], w[1]};
+    }
+  }
+}
+
+// ----------------------------------------------------------------- rows
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  __device__ static float get(float x) { return x; }
+  __device__ static float put(float x) { return x; }
+};
+template <>
+struct Elem<uint16_t> {  // bf16
+  __device__ static float get(uint16_t x) { return bf16_to_f32(x); }
+  __device__ static uint16_t put(float x) { return f32_to_bf16_rne(x); }
+};
+template <>
+struct Elem<_Float16> {
+  __device__ static float get(_Float16 x) { return (float)x; }
+  __device__ static _Float16 put(float x) { return (_Float16)x; }
+};
+
+// Head dims [lane*DPL, lane*DPL + DPL) belong to the lane in the P.V pass.
+template <typename T, int DPL>
+__global__ void __launch_bounds__(256) attn_rows(AttnParams p, const T* __restrict__ Q, const T* __restrict__ K,
+                                                 const T* __restrict__ V, T* __restrict__ O) {
+  constexpr int DMAX = 64 * DPL;
+  __shared__ float qs[DMAX];
+  __shared__ float wm[4], wl[4];
+  __shared__ float wo[4][DMAX];
+  const int row = blockIdx.x;
+  const int q = row % p.Sq;
+  const int bh = row / p.Sq;
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const T* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
+  const T* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
+  const T* qrow = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h + (int64_t)q * p.q_s;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int D = p.D;
+  for (int d = tid; d < D; d += 256) qs[d] = Elem<T>::get(qrow[d]);
+  __syncthreads();
+  const int nkeys = key_limit(p, read_offset(p), q) + 1;
+  const int nb = (nkeys + 63) / 64;
+  float m = -INFINITY, l = 0.f, o[DPL];
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) o[c] = 0.f;
+  for (int kb = wave; kb < nb; kb += 4) {
+    const int key = kb * 64 + lane;
+    float s = -INFINITY;
+    if (key < nkeys) {
+      const T* kr = Kp + (int64_t)key * p.k_s;
+      float acc = 0.f;
+      for (int d = 0; d < D; ++d) acc += qs[d] * Elem<T>::get(kr[d]);
+      if (p.round_scores) acc = Elem<T>::get(Elem<T>::put(acc));
+      s = acc * p.scale;
+    }
+    float mx = s;
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
+    const float mnew = fmaxf(m, mx);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = expf(m - mref);
+    const float pe = expf(s - mref);
+    float ps = pe;
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) ps += __shfl_xor(ps, k);
+    l = l * alpha + ps;
+    m = mnew;
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) o[c] *= alpha;
+    const int last = nkeys - 1;
+#pragma unroll 8
+    for (int j = 0; j < 64; ++j) {
+      const float pj = __shfl(pe, j);
+      const T* vr = Vp + (int64_t)std::min(kb * 64 + j, last) * p.v_s + lane * DPL;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c)
+        if (lane * DPL + c < D) o[c] += pj * Elem<T>::get(vr[c]);
+    }
+  }
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) wo[wave][lane * DPL + c] = o[c];
+  __syncthreads();
+  if (wave != 0) return;
+  const float mall = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  const float mref = mall == -INFINITY ? 0.f : mall;
+  float f[4], lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    f[w] = expf(wm[w] - mref);
+    lsum += wl[w] * f[w];
+  }
+  T* orow = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s;
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) {
+    const int d = lane * DPL + c;
+    if (d >= D) continue;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) acc += wo[w][d] * f[w];
+    orow[d] = Elem<T>::put(acc / lsum);
+  }
+}
+
+template <typename T>
+void launch_rows(hipStream_t s, const AttnParams& p, const void* Q, const void* K, const void* V, void* out) {
+  const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(p.B) * p.Hq * p.Sq)), block(256);
+  const T* q = static_cast<const T*>(Q);
+  const T* k = static_cast<const T*>(K);
+  const T* v = static_cast<const T*>(V);
+  T* o = static_cast<T*>(out);
+  if (p.D <= 64) hipLaunchKernelGGL((attn_rows<T, 1>), grid, block, 0, s, p, q, k, v, o);
+  else if (p.D <= 128) hipLaunchKernelGGL((attn_rows<T, 2>), grid, block, 0, s, p, q, k, v, o);
+  else if (p.D <= 256) hipLaunchKernelGGL((attn_rows<T, 4>), grid, block, 0, s, p, q, k, v, o);
+  else hipLaunchKernelGGL((attn_rows<T, 8>), grid, block, 0, s, p, q, k, v, o);
+}
+
+}  // namespace
+
+bool attention_uses_tiles(const AttnParams& p, DType t) {
+  if (t != DType::kBF16 && t != DType::kF16) return false;
+  if (p.D != 64 && p.D != 128) return false;
+  if (p.Sq < 16) return false;
+  for (int64_t st : {p.q_b, p.q_h, p.q_s, p.k_b, p.k_h, p.k_s, p.v_b, p.v_h, p.v_s})
+    if (st % 8 != 0) return false;
+  for (int64_t st : {p.o_b, p.o_h, p.o_s})
+    if (st % 4 != 0) return false;
+  return true;
+}
+
+void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
+                      void* out) {
+  PJRTX_CHECK(p.B >= 1 && p.Hq >= 1 && p.Hkv >= 1 && p.Hq % p.Hkv == 0 && p.D >= 1 && p.Sq >= 0 && p.Skv >= 0,
+              Code::kInvalidArgument, "attention: bad shape");
+  PJRTX_CHECK(p.D <= 512, Code::kUnimplemented, "attention: head dim above 512");
+  PJRTX_CHECK(p.causal == 0 || p.q_coef == 0 || p.q_coef == 1, Code::kInternal, "attention: mask slope must be 0 or 1");
+  if (p.Sq == 0) return;
+  if (attention_uses_tiles(p, t)) {
+    const int64_t grid = static_cast<int64_t>(p.B) * p.Hq * ((p.Sq + FQ - 1) / FQ);
+    PJRTX_CHECK(grid < (int64_t(1) << 31), Code::kUnimplemented, "attention: too many query tiles");
+    const bool f16 = t == DType::kF16;
+    const uint16_t* q = static_cast<const uint16_t*>(Q);
+    const uint16_t* k = static_cast<const uint16_t*>(K);
+    const uint16_t* v = static_cast<const uint16_t*>(V);
+    uint16_t* o = static_cast<uint16_t*>(out);
+    const dim3 g(static_cast<uint32_t>(grid)), block(256);
+    if (p.D == 128) {
+      if (f16) hipLaunchKernelGGL((attn_tiles<true, 128>), g, block, 0, s, p, q, k, v, o);
+      else hipLaunchKernelGGL((attn_tiles<false, 128>), g, block, 0, s, p, q, k, v, o);
+    } else {
+      if (f16) hipLaunchKernelGGL((attn_tiles<true, 64>), g, block, 0, s, p, q, k, v, o);
+      else hipLaunchKernelGGL((attn_tiles<false, 64>), g, block, 0, s, p, q, k, v, o);
+    }
+  } else {
+    PJRTX_CHECK(static_cast<int64_t>(p.B) * p.Hq * p.Sq < (int64_t(1) << 31), Code::kUnimplemented,
+                "attention: too many query rows");
+    switch (t) {
+      case DType::kF32: launch_rows<float>(s, p, Q, K, V, out); break;
+      case DType::kBF16: launch_rows<uint16_t>(s, p, Q, K, V, out); break;
+      case DType::kF16: launch_rows<_Float16>(s, p, Q, K, V, out); break;
+      default: fail(Code::kUnimplemented, "attention: element type must be f32, bf16 or f16");
+    }
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(Code::kInternal, strformat("attention launch failed: %s", hipGetErrorString(e)));
+}
+
+}  // namespace pjrtx

@@ -183,6 +183,7 @@ GatherParams make_gather_params(const Program& prog, const Op& op) {
 
 void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
+void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 
 void run_library_step(Device* dev, const Program& prog, const Step& step, std::vector<MemRef>& vals) {
   const Op& op = prog.ops.at(step.lib_op);
@@ -210,6 +211,9 @@ void run_library_step(Device* dev, const Program& prog, const Step& step, std::v
       return;
     case LibKind::kScatter:
       run_scatter(dev, prog, op, vals);
+      return;
+    case LibKind::kAttention:
+      run_attention(dev, prog, op, vals);
       return;
     default:
       fail(Code::kUnimplemented, std::string("library op not available: ") + lib_kind_name(step.lib));

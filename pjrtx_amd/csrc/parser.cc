@@ -157,6 +157,8 @@ const OpInfo kOpTable[] = {
     {"dot", OpKind::kDotGeneral},
     {"gather", OpKind::kGather},
     {"scatter", OpKind::kScatter},
+    {"custom_call", OpKind::kCustomCall},
+    {"pjrtx.attention", OpKind::kAttention},
     {"return", OpKind::kReturn},
 };
 
@@ -789,6 +791,9 @@ void Parser::parse_generic_attrs(const std::string& dict, Op* op) {
           {"LE", CmpDir::kLE}, {"GT", CmpDir::kGT}, {"GE", CmpDir::kGE}};
       for (auto& dd : dirs)
         if (d == dd.first) op->cmp_dir = dd.second;
+    } else if (key == "call_target_name") {
+      const size_t q0 = val.find('"'), q1 = val.rfind('"');
+      if (q0 != std::string::npos && q1 > q0) op->target = val.substr(q0 + 1, q1 - q0 - 1);
     } else if (key == "dot_dimension_numbers") {
       size_t lt = val.find('<');
       size_t gt = val.rfind('>');
@@ -1011,6 +1016,16 @@ Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint
     expect("->");
     sig_outputs = type_list_maybe_parens();
   } else {
+    if (op.kind == OpKind::kCustomCall) {  // custom_call @target(%a, ...) {attrs} : (...) -> ...
+      op.target = symbol();
+      expect("(");
+      if (!try_lit(")")) {
+        do {
+          op.operands.push_back(lookup(ssa_name()));
+        } while (try_lit(","));
+        expect(")");
+      }
+    }
     // Pretty form: items until the top-level ':'.
     while (true) {
       ws();

@@ -478,6 +478,7 @@ static PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
                           static_cast<long long>(replicas), static_cast<long long>(partitions)));
     std::string text(args->program->code, args->program->code_size);
     Program prog = parse_stablehlo(text);
+    rewrite_program(&prog);
     PJRTX_CHECK(prog.num_partitions == 1 && prog.num_replicas == 1, Code::kUnimplemented,
                 "pjrtx runs on one device: module asks for more than one partition or replica");
     Plan plan = make_plan(prog);

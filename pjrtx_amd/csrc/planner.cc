@@ -33,6 +33,7 @@ const char* lib_kind_name(LibKind k) {
     case LibKind::kDynamicUpdateSlice: return "dynamic_update_slice";
     case LibKind::kConcatenate: return "concatenate";
     case LibKind::kPad: return "pad";
+    case LibKind::kAttention: return "attention";
   }
   return "?";
 }
@@ -122,7 +123,7 @@ bool is_library(const Op& op) {
   const OpKind k = op.kind;
   return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
          k == OpKind::kDynamicSlice || k == OpKind::kDynamicUpdateSlice ||
-         (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad;
+         (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad || k == OpKind::kAttention;
 }
 
 LibKind lib_kind_of(OpKind k) {
@@ -130,6 +131,7 @@ LibKind lib_kind_of(OpKind k) {
     case OpKind::kDotGeneral: return LibKind::kDot;
     case OpKind::kGather: return LibKind::kGather;
     case OpKind::kScatter: return LibKind::kScatter;
+    case OpKind::kAttention: return LibKind::kAttention;
     case OpKind::kDynamicSlice: return LibKind::kDynamicSlice;
     case OpKind::kDynamicUpdateSlice: return LibKind::kDynamicUpdateSlice;
     case OpKind::kConcatenate: return LibKind::kConcatenate;
@@ -849,6 +851,16 @@ std::string Plan::describe(const Program& prog) const {
         int64_t kc = 1;
         for (int64_t c : d.lhs_contract) kc *= prog.type(d.operands[0]).dims[c];
         o << ",\"flops\":" << 2 * prog.type(d.results[0]).elements() * kc;
+      }
+      if (s.lib == LibKind::kAttention) {  // q.k and p.v over every (query, key) pair
+        const Op& d = prog.ops[s.lib_op];
+        const TensorType& q = prog.type(d.operands[0]);
+        const TensorType& k = prog.type(d.operands[1]);
+        const int sa = d.attn.layout == 0 ? 2 : d.attn.layout == 1 ? 1 : 0;
+        o << ",\"flops\":" << 4 * q.elements() * k.dims[sa] << ",\"causal\":" << (d.attn.causal ? "true" : "false")
+          << ",\"q_coef\":" << d.attn.q_coef << ",\"offset\":" << d.attn.offset
+          << ",\"offset_operand\":" << (d.attn.has_offset_operand ? "true" : "false") << ",\"scale\":" << strformat("%.17g", d.attn.scale)
+          << ",\"layout\":" << d.attn.layout;
       }
     }
     o << ",\"vec\":" << s.vec << ",\"grid\":" << s.grid << ",\"block\":" << s.block;

@@ -47,7 +47,9 @@ struct ReduceSpec {
 // order; earlier phases' results are per-row scalars in later phases.
 enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused };
 
-enum class LibKind { kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad };
+enum class LibKind {
+  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention
+};
 const char* lib_kind_name(LibKind k);
 
 struct Step {
@@ -123,6 +125,12 @@ struct PlanOptions {
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
+
+// Program rewrites before planning (attention.cc): lowers supported
+// custom calls, fuses the softmax-attention pattern into one kAttention op
+// (unless PJRTX_FUSED_ATTENTION=0) and drops ops left without users.
+// Unsupported custom-call targets fail with kUnimplemented.
+void rewrite_program(Program* prog);
 
 // Emits the HIP source of every generated step (codegen.cc).
 std::string generate_kernels(const Program& prog, Plan& plan);

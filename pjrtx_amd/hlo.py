@@ -254,6 +254,18 @@ class Builder:
         types = ", ".join([x.type, update.type] + [s.type for s in starts])
         return self._emit(f"stablehlo.dynamic_update_slice {names} : ({types}) -> {x.type}", x.shape, x.dtype)
 
+    def custom_call(self, target: str, operands: list[T], shape, dtype: str, generic: bool = False) -> T:
+        """stablehlo.custom_call as JAX prints it (pretty form), or the generic
+        "stablehlo.custom_call"(...) {call_target_name = ...} form."""
+        names = ", ".join(o.name for o in operands)
+        types = ", ".join(o.type for o in operands)
+        out = tensor_type(shape, dtype)
+        if generic:
+            return self._emit(f'"stablehlo.custom_call"({names}) {{api_version = 2 : i32, backend_config = "", '
+                              f'call_target_name = "{target}"}} : ({types}) -> {out}', shape, dtype)
+        return self._emit(f'stablehlo.custom_call @{target}({names}) {{api_version = 2 : i32, backend_config = ""}} : '
+                          f"({types}) -> {out}", shape, dtype)
+
     def pad(self, x: T, value: T, low, high, interior) -> T:
         shape = tuple(lo + hi + d + max(d - 1, 0) * it for d, lo, hi, it in zip(x.shape, low, high, interior))
         f = lambda v: ", ".join(str(a) for a in v)  # noqa: E731

@@ -52,12 +52,13 @@ def c2_argmax_only(rows: int, vocab: int, dtype: str = "bf16") -> str:
     return b.build([vals, idx])
 
 
-def c3_attention(batch: int = 8, heads: int = 32, seq: int = 2048, head_dim: int = 128, causal: bool = True) -> str:
+def c3_attention(batch: int = 8, heads: int = 32, seq: int = 2048, head_dim: int = 128, causal: bool = True,
+                 dtype: str = "bf16") -> str:
     """scores = einsum('bhqd,bhkd->bhqk', q, k); causal mask via select;
     softmax in f32; context = einsum('bhqk,bhkd->bhqd', p, v) -> bf16."""
     b = Builder("jit_c3_attention")
     shp = (batch, heads, seq, head_dim)
-    q, k, v = b.param(shp, "bf16"), b.param(shp, "bf16"), b.param(shp, "bf16")
+    q, k, v = b.param(shp, dtype), b.param(shp, dtype), b.param(shp, dtype)
     s = b.dot_general(q, k, batch=((0, 1), (0, 1)), contract=((3,), (3,)))          # [B,H,S,S] bf16
     if causal:
         row = b.iota((seq, seq), 0)
@@ -68,7 +69,7 @@ def c3_attention(batch: int = 8, heads: int = 32, seq: int = 2048, head_dim: int
     m = b.max(sf, [3])
     e = b.exp(b.subtract(sf, b.broadcast_in_dim(m, sf.shape, [0, 1, 2])))
     z = b.sum(e, [3])
-    p = b.convert(b.divide(e, b.broadcast_in_dim(z, sf.shape, [0, 1, 2])), "bf16")
+    p = b.convert(b.divide(e, b.broadcast_in_dim(z, sf.shape, [0, 1, 2])), dtype)
     ctx = b.dot_general(p, v, batch=((0, 1), (0, 1)), contract=((3,), (2,)))        # [B,H,S,D]
     return b.build([ctx])
 

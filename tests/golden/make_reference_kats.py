@@ -43,6 +43,14 @@ KATS = {
                         "set": [104, 105, 106, 107, 4, 5, 6, 7, 100, 101, 102, 103, 12, 13, 14, 15,
                                 108, 109, 110, 111, 112, 113, 114, 115],
                         "source": "api_test.cc:2226-2308"},
+    # api_test.cc:271-309 — scaled-dot-product-attention custom call, f32,
+    # q [1,1,2] ([q,h,hd]), k/v [2,1,2], token_index 0 (u32)
+    "sdpa_one_head": {"q_shape": [1, 1, 2], "kv_shape": [2, 1, 2], "q": [1, 0], "k": [1, 0, 0, 1], "v": [10, 0, 0, 20],
+                      "token_index": 0, "expected": [10, 0], "source": "api_test.cc:271-309"},
+    # api_test.cc:311-352 — four query heads over two key/value heads
+    "sdpa_grouped_heads": {"q_shape": [1, 4, 2], "kv_shape": [2, 2, 2], "q": [1, 0, 1, 0, 1, 0, 1, 0],
+                           "k": [1, 0, 0, 1, 1, 0, 0, 1], "v": [10, 0, 20, 0, 0, 30, 0, 40], "token_index": 0,
+                           "expected": [10, 0, 10, 0, 20, 0, 20, 0], "source": "api_test.cc:311-352"},
 }
 
 if __name__ == "__main__":
