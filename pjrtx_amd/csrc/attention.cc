@@ -194,9 +194,8 @@ class Matcher {
     return true;
   }
 
-  // Fewest queries per (batch, head) worth fusing: below it (decode) the
-  // unfused GEMV / row-softmax / GEMV path is faster than the row kernel.
-  static constexpr int64_t kMinQueries = 16;
+  // Fewest queries per (batch, head) worth fusing.
+  static constexpr int64_t kMinQueries = 1;
 
  private:
   Program& prog_;
@@ -490,8 +489,11 @@ void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<M
   AttnParams p = attention_params(prog, op);
   auto ptr = [&](int v) -> void* { return vals[v] ? vals[v]->ptr : nullptr; };
   if (op.attn.has_offset_operand) p.offset_ptr = ptr(op.operands[3]);
-  launch_attention(dev->stream(), p, prog.type(op.operands[0]).dtype, ptr(op.operands[0]), ptr(op.operands[1]),
-                   ptr(op.operands[2]), ptr(op.results[0]));
+  const DType t = prog.type(op.operands[0]).dtype;
+  const size_t scratch_bytes = attention_scratch_bytes(p, t);
+  MemRef scratch = scratch_bytes ? dev->allocate(scratch_bytes) : nullptr;
+  launch_attention(dev->stream(), p, t, ptr(op.operands[0]), ptr(op.operands[1]), ptr(op.operands[2]),
+                   ptr(op.results[0]), scratch ? static_cast<float*>(scratch->ptr) : nullptr);
 }
 
 }  // namespace pjrtx

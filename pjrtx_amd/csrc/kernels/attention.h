@@ -35,11 +35,19 @@ struct AttnParams {
 };
 
 // True when the MFMA tile kernel takes the problem (16-bit types, head dim
-// 64 or 128, 16-byte aligned rows, Sq >= 16); otherwise the row kernel runs.
+// 64 or 128, 16-byte aligned rows, Sq >= 16, scale > 0).
 bool attention_uses_tiles(const AttnParams& p, DType t);
-// Launches the kernel for element type t (bf16, f16 or f32; Q, K, V and out
-// share it).
+
+// Kernel choice: MFMA tiles; the split-key decode kernel (head dim a
+// power-of-two count of 16-byte chunks from 4 to 32, aligned rows); or the
+// generic row kernel.
+enum class AttnPath { kTiles, kDecode, kRows };
+AttnPath attention_path(const AttnParams& p, DType t, int* nsplit, int* keys_per_split);
+// Device scratch the launch needs (split-key partials), 0 if none.
+size_t attention_scratch_bytes(const AttnParams& p, DType t);
+// Launches the kernels for element type t (bf16, f16 or f32; Q, K, V and out
+// share it). `scratch` holds attention_scratch_bytes(p, t) bytes.
 void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
-                      void* out);
+                      void* out, float* scratch);
 
 }  // namespace pjrtx

@@ -65,6 +65,23 @@ __device__ __forceinline__ float to_f32(uint16_t x) {
   else return bf16_to_f32(x);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded (to nearest even) and packed as 16-bit values, low
+// half first: one v_cvt_pk_* on gfx950.
+template <bool kF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (kF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <bool kF16>
+__device__ __forceinline__ float round16(float x) {
+  if constexpr (kF16) return (float)(_Float16)x;
+  else return (float)(__bf16)x;
+}
+
 template <bool kF16>
 __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
   if constexpr (kF16)
@@ -125,7 +142,7 @@ __device__ __forceinline__ int vpos(int key) {
   return (key & 32) | (((key & 15) >> 2) << 3) | (((key >> 4) & 1) << 2) | (key & 3);
 }
 
-template <bool kF16, int D>
+template <bool kF16, int D, bool kRound>
 __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_t* __restrict__ Q,
                                                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                                                      uint16_t* __restrict__ O) {
@@ -178,6 +195,7 @@ __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_
   const int free_end = key_limit(p, off, q0) + 1;  // q_coef >= 0: the first query has the lowest limit
   const int nblocks = (kend + FK - 1) / FK;
 
+  const float c2 = p.scale * 1.44269504088896340736f;  // scale * log2(e)
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
   f32x4 oacc[NDT][2];
 #pragma unroll
@@ -243,6 +261,9 @@ __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_
     u32x4 pf[2][2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
+      // Max on the unscaled scores (scale > 0), exponentials as
+      // exp2(s * scale * log2(e) - m * scale * log2(e)): one FMA and one
+      // v_exp_f32 per score.
       float s[4][4];
       float mx = -INFINITY;
 #pragma unroll
@@ -250,8 +271,7 @@ __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float x = sacc[kt][qt][r];
-          if (p.round_scores) x = to_f32<kF16>(from_f32<kF16>(x));
-          x *= p.scale;
+          if constexpr (kRound) x = round16<kF16>(x);
           if (need_mask && kb * FK + kt * 16 + g * 4 + r > lim[qt]) x = -INFINITY;
           s[kt][r] = x;
           mx = fmaxf(mx, x);
@@ -259,33 +279,29 @@ __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float mnew = fmaxf(m[qt], mx);
-      const float mref = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = expf(m[qt] - mref);
+      const float mc = (mnew == -INFINITY ? 0.f : mnew) * c2;
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] * c2 - mc);  // 0 while m is -inf, 1 when m is unchanged
       float ps = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          s[kt][r] = expf(s[kt][r] - mref);
+          s[kt][r] = __builtin_amdgcn_exp2f(fmaf(s[kt][r], c2, -mc));
           ps += s[kt][r];
         }
       ps += __shfl_xor(ps, 16);
       ps += __shfl_xor(ps, 32);
       l[qt] = l[qt] * alpha + ps;
       m[qt] = mnew;
+      if (!__all(alpha == 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) oacc[dt][qt] *= alpha;
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          w[j] = (uint32_t)from_f32<kF16>(s[2 * st][2 * j]) | ((uint32_t)from_f32<kF16>(s[2 * st][2 * j + 1]) << 16);
-          w[2 + j] = (uint32_t)from_f32<kF16>(s[2 * st + 1][2 * j]) |
-                     ((uint32_t)from_f32<kF16>(s[2 * st + 1][2 * j + 1]) << 16);
-        }
-        pf[qt][st] = u32x4{w[0], w[1], w[2], w[3]};
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt][qt] *= alpha;
       }
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        pf[qt][st] = u32x4{pack2<kF16>(s[2 * st][0], s[2 * st][1]), pack2<kF16>(s[2 * st][2], s[2 * st][3]),
+                           pack2<kF16>(s[2 * st + 1][0], s[2 * st + 1][1]),
+                           pack2<kF16>(s[2 * st + 1][2], s[2 * st + 1][3])};
     }
     // O^T[d][query] += V^T[d][key] . P^T[key][query]
 #pragma unroll
@@ -310,12 +326,9 @@ __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_
     uint16_t* orow = Op + (int64_t)q * p.o_s;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      uint32_t w[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        w[j] = (uint32_t)from_f32<kF16>(oacc[dt][qt][2 * j] / l[qt]) |
-               ((uint32_t)from_f32<kF16>(oacc[dt][qt][2 * j + 1] / l[qt]) << 16);
-      *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{w[0], w[1]};
+      const f32x4 o = oacc[dt][qt];
+      *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) =
+          u32x2{pack2<kF16>(o[0] / l[qt], o[1] / l[qt]), pack2<kF16>(o[2] / l[qt], o[3] / l[qt])};
     }
   }
 }
@@ -427,6 +440,177 @@ __global__ void __launch_bounds__(256) attn_rows(AttnParams p, const T* __restri
   }
 }
 
+// --------------------------------------------------------------- decode
+
+// Few queries per (batch, head): grid (query rows, key splits). Each of the
+// 4 waves takes 64 keys per step: lane j scores key j (its K row read as
+// 16-byte chunks, all in flight together; q from LDS), the wave folds the
+// online softmax, then the lanes regroup as (16-byte head-dim chunk c, key
+// group g) for P.V so that each V row is read as one coalesced span. The
+// workgroup merges its waves (and key groups) through LDS in a fixed order;
+// with one split that is the output, otherwise (m, l, O) partials go to
+// `part` and attn_combine merges the splits in split order.
+constexpr int DK = 64;
+
+template <typename T, int NCH>
+__global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __restrict__ Q, const T* __restrict__ K,
+                                                   const T* __restrict__ V, T* __restrict__ O,
+                                                   float* __restrict__ part, int keys_per_split) {
+  constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk
+  constexpr int D = NCH * EPC;
+  constexpr int G = 64 / NCH;          // key groups in the P.V pass
+  constexpr int KG = DK / G;           // keys per group
+  __shared__ float qs[D];
+  __shared__ float ow[4][64][EPC];
+  __shared__ float mw[4], lw[4];
+  const int row = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
+  const int q = row % p.Sq;
+  const int bh = row / p.Sq;
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const T* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
+  const T* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (tid < D) qs[tid] = Elem<T>::get(Q[(int64_t)b * p.q_b + (int64_t)h * p.q_h + (int64_t)q * p.q_s + tid]);
+  __syncthreads();
+  const int nkeys = key_limit(p, read_offset(p), q) + 1;
+  const int k0 = split * keys_per_split;
+  const int k1 = std::min(nkeys, k0 + keys_per_split);
+  const int c = lane % NCH, grp = lane / NCH;
+  float m = -INFINITY, l = 0.f, o[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) o[e] = 0.f;
+  for (int kb = k0 + wave * DK; kb < k1; kb += 4 * DK) {
+    const int key = kb + lane;
+    float sc = -INFINITY;
+    if (key < k1) {
+      const T* kr = Kp + (int64_t)key * p.k_s;
+      u32x4 kv[NCH];
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) kv[i] = *reinterpret_cast<const u32x4*>(kr + i * EPC);
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const T* e8 = reinterpret_cast<const T*>(&kv[i]);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc += qs[i * EPC + e] * Elem<T>::get(e8[e]);
+      }
+      if (p.round_scores) acc = Elem<T>::get(Elem<T>::put(acc));
+      sc = acc * p.scale;
+    }
+    float mx = sc;
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
+    const float mnew = fmaxf(m, mx);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = expf(m - mref);
+    const float pe = expf(sc - mref);
+    float ps = pe;
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) ps += __shfl_xor(ps, k);
+    l = l * alpha + ps;
+    m = mnew;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) o[e] *= alpha;
+    // P.V: lane (c, grp) reads chunk c of keys kb + grp*KG + i; keys past k1
+    // weigh 0 and read the last allowed row instead.
+    u32x4 vv[KG];
+#pragma unroll
+    for (int i = 0; i < KG; ++i) {
+      const int kk = std::min(kb + grp * KG + i, k1 - 1);
+      vv[i] = *reinterpret_cast<const u32x4*>(Vp + (int64_t)kk * p.v_s + c * EPC);
+    }
+#pragma unroll
+    for (int i = 0; i < KG; ++i) {
+      const float pj = __shfl(pe, grp * KG + i);
+      const T* e8 = reinterpret_cast<const T*>(&vv[i]);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) o[e] += pj * Elem<T>::get(e8[e]);
+    }
+  }
+  if (lane == 0) {
+    mw[wave] = m;
+    lw[wave] = l;
+  }
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) ow[wave][lane][e] = o[e];
+  __syncthreads();
+  if (tid >= D) return;
+  const int cc = tid / EPC, ee = tid % EPC;
+  const float mall = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+  const float mref = mall == -INFINITY ? 0.f : mall;
+  float lsum = 0.f, acc = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = expf(mw[w] - mref);
+    lsum += lw[w] * f;
+    float ow_sum = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) ow_sum += ow[w][g * NCH + cc][ee];
+    acc += ow_sum * f;
+  }
+  if (nsplit == 1) {
+    O[(int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s + tid] = Elem<T>::put(acc / lsum);
+    return;
+  }
+  float* pr = part + ((int64_t)row * nsplit + split) * (D + 2);
+  pr[2 + tid] = acc;
+  if (tid == 0) {
+    pr[0] = mall;
+    pr[1] = lsum;
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_combine(AttnParams p, const float* __restrict__ part, int nsplit,
+                                                    T* __restrict__ O) {
+  const int row = blockIdx.x;
+  const int q = row % p.Sq;
+  const int bh = row / p.Sq;
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int D = p.D;
+  const float* pr = part + (int64_t)row * nsplit * (D + 2);
+  float mall = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mall = fmaxf(mall, pr[(int64_t)s * (D + 2)]);
+  const float mref = mall == -INFINITY ? 0.f : mall;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float lsum = 0.f, acc = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* ps = pr + (int64_t)s * (D + 2);
+      const float f = expf(ps[0] - mref);
+      lsum += ps[1] * f;
+      acc += ps[2 + d] * f;
+    }
+    O[(int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s + d] = Elem<T>::put(acc / lsum);
+  }
+}
+
+template <typename T>
+bool decode_fits(const AttnParams& p) {
+  constexpr int EPC = 16 / sizeof(T);
+  if (p.D % EPC != 0) return false;
+  const int nch = p.D / EPC;
+  if (nch != 4 && nch != 8 && nch != 16 && nch != 32) return false;
+  for (int64_t st : {p.k_b, p.k_h, p.k_s, p.v_b, p.v_h, p.v_s})
+    if (st % EPC != 0) return false;
+  return true;
+}
+
+template <typename T>
+void launch_decode(hipStream_t s, const AttnParams& p, const T* q, const T* k, const T* v, T* o, float* part,
+                   int nsplit, int keys_per_split) {
+  constexpr int EPC = 16 / sizeof(T);
+  const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(p.B) * p.Hq * p.Sq), static_cast<uint32_t>(nsplit));
+  const dim3 block(256);
+  switch (p.D / EPC) {
+    case 4: hipLaunchKernelGGL((attn_decode<T, 4>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
+    case 8: hipLaunchKernelGGL((attn_decode<T, 8>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
+    case 16: hipLaunchKernelGGL((attn_decode<T, 16>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
+    default: hipLaunchKernelGGL((attn_decode<T, 32>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
+  }
+  if (nsplit > 1) hipLaunchKernelGGL((attn_combine<T>), dim3(grid.x), dim3(128), 0, s, p, part, nsplit, o);
+}
+
 template <typename T>
 void launch_rows(hipStream_t s, const AttnParams& p, const void* Q, const void* K, const void* V, void* out) {
   const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(p.B) * p.Hq * p.Sq)), block(256);
@@ -444,6 +628,7 @@ void launch_rows(hipStream_t s, const AttnParams& p, const void* Q, const void* 
 
 bool attention_uses_tiles(const AttnParams& p, DType t) {
   if (t != DType::kBF16 && t != DType::kF16) return false;
+  if (!(p.scale > 0.f)) return false;  // the tile kernel takes the row max before scaling
   if (p.D != 64 && p.D != 128) return false;
   if (p.Sq < 16) return false;
   for (int64_t st : {p.q_b, p.q_h, p.q_s, p.k_b, p.k_h, p.k_s, p.v_b, p.v_h, p.v_s})
@@ -453,14 +638,52 @@ bool attention_uses_tiles(const AttnParams& p, DType t) {
   return true;
 }
 
+AttnPath attention_path(const AttnParams& p, DType t, int* nsplit, int* keys_per_split) {
+  *nsplit = 1;
+  *keys_per_split = 0;
+  if (attention_uses_tiles(p, t)) return AttnPath::kTiles;
+  const bool fits = t == DType::kF32 ? decode_fits<float>(p) : t == DType::kBF16 ? decode_fits<uint16_t>(p)
+                    : t == DType::kF16 ? decode_fits<_Float16>(p) : false;
+  if (!fits) return AttnPath::kRows;
+  // Splits of whole 256-key steps (4 waves x 64 keys), at most 64 of them.
+  const int steps = std::max(1, (p.Skv + 4 * DK - 1) / (4 * DK));
+  const int n = std::min(steps, 64);
+  const int per = (steps + n - 1) / n;
+  *keys_per_split = per * 4 * DK;
+  *nsplit = (p.Skv + *keys_per_split - 1) / *keys_per_split;
+  if (*nsplit < 1) *nsplit = 1;
+  return AttnPath::kDecode;
+}
+
+size_t attention_scratch_bytes(const AttnParams& p, DType t) {
+  int nsplit = 1, per = 0;
+  if (attention_path(p, t, &nsplit, &per) != AttnPath::kDecode || nsplit == 1) return 0;
+  return static_cast<size_t>(p.B) * p.Hq * p.Sq * nsplit * (p.D + 2) * sizeof(float);
+}
+
 void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
-                      void* out) {
+                      void* out, float* scratch) {
   PJRTX_CHECK(p.B >= 1 && p.Hq >= 1 && p.Hkv >= 1 && p.Hq % p.Hkv == 0 && p.D >= 1 && p.Sq >= 0 && p.Skv >= 0,
               Code::kInvalidArgument, "attention: bad shape");
   PJRTX_CHECK(p.D <= 512, Code::kUnimplemented, "attention: head dim above 512");
   PJRTX_CHECK(p.causal == 0 || p.q_coef == 0 || p.q_coef == 1, Code::kInternal, "attention: mask slope must be 0 or 1");
   if (p.Sq == 0) return;
-  if (attention_uses_tiles(p, t)) {
+  int nsplit = 1, per = 0;
+  const AttnPath path = attention_path(p, t, &nsplit, &per);
+  if (path == AttnPath::kDecode) {
+    PJRTX_CHECK(static_cast<int64_t>(p.B) * p.Hq * p.Sq < (int64_t(1) << 31), Code::kUnimplemented,
+                "attention: too many query rows");
+    PJRTX_CHECK(nsplit == 1 || scratch != nullptr, Code::kInternal, "attention: split decode needs scratch");
+    if (t == DType::kF32)
+      launch_decode<float>(s, p, static_cast<const float*>(Q), static_cast<const float*>(K),
+                           static_cast<const float*>(V), static_cast<float*>(out), scratch, nsplit, per);
+    else if (t == DType::kBF16)
+      launch_decode<uint16_t>(s, p, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
+                              static_cast<const uint16_t*>(V), static_cast<uint16_t*>(out), scratch, nsplit, per);
+    else
+      launch_decode<_Float16>(s, p, static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
+                              static_cast<const _Float16*>(V), static_cast<_Float16*>(out), scratch, nsplit, per);
+  } else if (path == AttnPath::kTiles) {
     const int64_t grid = static_cast<int64_t>(p.B) * p.Hq * ((p.Sq + FQ - 1) / FQ);
     PJRTX_CHECK(grid < (int64_t(1) << 31), Code::kUnimplemented, "attention: too many query tiles");
     const bool f16 = t == DType::kF16;
@@ -469,13 +692,17 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     const uint16_t* v = static_cast<const uint16_t*>(V);
     uint16_t* o = static_cast<uint16_t*>(out);
     const dim3 g(static_cast<uint32_t>(grid)), block(256);
-    if (p.D == 128) {
-      if (f16) hipLaunchKernelGGL((attn_tiles<true, 128>), g, block, 0, s, p, q, k, v, o);
-      else hipLaunchKernelGGL((attn_tiles<false, 128>), g, block, 0, s, p, q, k, v, o);
-    } else {
-      if (f16) hipLaunchKernelGGL((attn_tiles<true, 64>), g, block, 0, s, p, q, k, v, o);
-      else hipLaunchKernelGGL((attn_tiles<false, 64>), g, block, 0, s, p, q, k, v, o);
-    }
+#define PJRTX_ATTN(F16, DIM, RND) hipLaunchKernelGGL((attn_tiles<F16, DIM, RND>), g, block, 0, s, p, q, k, v, o)
+    const bool rnd = p.round_scores != 0;
+    if (p.D == 128 && f16 && rnd) PJRTX_ATTN(true, 128, true);
+    else if (p.D == 128 && f16) PJRTX_ATTN(true, 128, false);
+    else if (p.D == 128 && rnd) PJRTX_ATTN(false, 128, true);
+    else if (p.D == 128) PJRTX_ATTN(false, 128, false);
+    else if (f16 && rnd) PJRTX_ATTN(true, 64, true);
+    else if (f16) PJRTX_ATTN(true, 64, false);
+    else if (rnd) PJRTX_ATTN(false, 64, true);
+    else PJRTX_ATTN(false, 64, false);
+#undef PJRTX_ATTN
   } else {
     PJRTX_CHECK(static_cast<int64_t>(p.B) * p.Hq * p.Sq < (int64_t(1) << 31), Code::kUnimplemented,
                 "attention: too many query rows");

@@ -45,6 +45,14 @@ def test_llama_prefill_fuses_every_layer(plugin):
     assert "rowfused" not in [s["kind"] for s in pre["steps"] if s.get("row_len") == L.TINY.max_len]
 
 
+def test_llama_decode_fuses_every_layer(plugin):
+    dec = plan(plugin, L.decode_program(L.TINY))
+    att = [s for s in dec["steps"] if s.get("library") == "attention"]
+    assert len(att) == L.TINY.layers
+    for s in att:  # key <= pos, pos read on the device
+        assert s["causal"] and s["q_coef"] == 0 and s["offset"] == 0 and s["offset_operand"] and len(s["inputs"]) == 4
+
+
 def test_decode_mask_reads_position_on_device(plugin):
     """The decode step's mask (key <= pos, pos a program argument) as a
     pattern with 16 queries: q_coef 0 and the position as a 4th operand."""

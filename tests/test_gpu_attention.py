@@ -84,6 +84,8 @@ def test_sdpa_f32_rows(client, qs, kvs, tok):
     ((5, 8, 64), (40, 2, 64), 30),               # grouped heads, row kernel
     ((1, 200, 8, 128), (1, 333, 2, 128), 100),   # tile kernel, ragged lengths, grouped heads
     ((2, 130, 4, 64), (2, 130, 4, 64), 0),       # tile kernel, head dim 64, causal from 0
+    ((1, 2, 4, 64), (1, 2000, 2, 64), 100),      # decode, 8 key splits of which 7 are empty
+    ((1, 1, 8, 128), (1, 5000, 8, 128), 4321),   # decode, 20 key splits
 ])
 def test_sdpa_16bit(client, dt, qs, kvs, tok):
     rng = np.random.default_rng(qs[-2] * 7 + kvs[-3] + tok)
