@@ -256,16 +256,20 @@ def cpu_baseline(W: Workload, inputs, budget_s: float = 10.0) -> dict:
 def launch_units(plan: dict) -> list[dict]:
     """The plan's launch units in the order pjrtx_executable_time_steps
     reports them (a split reduction is a main and a combine unit), each with
-    its algorithmic bytes (inputs read once + outputs written; 0 for a
-    combine pass, which only reads the partial slots) and dot flops."""
+    its algorithmic bytes (the planner's figure: inputs read once + outputs
+    written, gathered rows only for a gather, the window only for an in-place
+    dynamic_update_slice; 0 for a combine pass, which only reads the partial
+    slots) and dot flops."""
     units = []
     for st in plan["steps"]:
         if st["kind"] == "alias":
             units.append({"name": "-", "bytes": 0, "flops": 0})
             continue
         name = st["name"] or ("lib:" + st.get("library", "?"))
-        units.append({"name": name, "bytes": sum(st["in_bytes"]) + sum(st["out_bytes"]),
-                      "flops": st.get("flops", 0)})
+        # A causal attention step does (and is credited with) only the
+        # unmasked (query, key) pairs.
+        units.append({"name": name, "bytes": st["algorithmic_bytes"],
+                      "flops": st.get("effective_flops", st.get("flops", 0))})
         if st["kind"] == "reduce" and st.get("splits", 1) > 1:
             units.append({"name": name + "_combine", "bytes": 0, "flops": 0})
     return units

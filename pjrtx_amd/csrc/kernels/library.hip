@@ -132,6 +132,30 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherUnits p, const T* __r
   out[i] = operand[src / p.unit_elems];
 }
 
+// Row gather (take along axis 0 of whole rows, JAX's embedding lookup): a
+// workgroup copies up to 1024 16-byte units of one output row; the row index
+// is read once per thread and clamped as StableHLO clamps gather starts.
+constexpr int64_t kGatherRowChunk = 1024;
+
+__global__ void __launch_bounds__(256) gather_rows_kernel(const u32x4* __restrict__ operand,
+                                                          const void* __restrict__ indices, int idx_bytes,
+                                                          int idx_signed, int64_t op_rows, int64_t units_per_row,
+                                                          int64_t nchunks, u32x4* __restrict__ out) {
+  const int64_t bid = blockIdx.x;
+  const int64_t r = bid / nchunks, chunk = bid - r * nchunks;
+  const int64_t src = clamp64(load_index(indices, r, idx_bytes, idx_signed), 0, op_rows - 1);
+  const u32x4* srow = operand + src * units_per_row;
+  u32x4* drow = out + r * units_per_row;
+  const int64_t u0 = chunk * kGatherRowChunk + threadIdx.x;
+  u32x4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (u0 + 256 * j < units_per_row) v[j] = srow[u0 + 256 * j];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (u0 + 256 * j < units_per_row) drow[u0 + 256 * j] = v[j];
+}
+
 int64_t blocks_for(int64_t n) { return (n + 255) / 256; }
 
 void check_launch(const char* what) {
@@ -205,6 +229,30 @@ void launch_gather(hipStream_t s, const GatherParams& g, const void* operand, co
   int64_t total = 1;
   for (int d = 0; d < g.out_rank; ++d) total *= g.out_dims[d];
   if (total == 0) return;
+  // Whole rows of a row-major operand selected by one index per output row.
+  {
+    const int nwin = g.op_rank - 1;
+    const int nbatch = g.out_rank - nwin;
+    bool rows = g.op_rank >= 1 && g.n_index == 1 && g.start_map[0] == 0 && g.n_batching == 0 && g.slice[0] == 1 &&
+                nbatch >= 0 && (g.ivd == g.idx_rank || g.ivd == g.idx_rank - 1);
+    for (int d = 1; d < g.op_rank && rows; ++d) rows = g.slice[d] == g.op_dims[d] && g.out_map[nbatch + d - 1] == -d - 1;
+    for (int d = 0; d < nbatch && rows; ++d) rows = g.out_map[d] == d && d != g.ivd;
+    int64_t row_elems = 1;
+    for (int d = 1; d < g.op_rank; ++d) row_elems *= g.op_dims[d];
+    rows = rows && (row_elems * elem_bytes) % 16 == 0 && reinterpret_cast<uintptr_t>(operand) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if (rows) {
+      const int64_t upr = row_elems * elem_bytes / 16;
+      const int64_t out_rows = total / row_elems;
+      const int64_t nchunks = (upr + kGatherRowChunk - 1) / kGatherRowChunk;
+      PJRTX_CHECK(out_rows * nchunks < (int64_t(1) << 31), Code::kUnimplemented, "gather: too many rows");
+      hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(out_rows * nchunks)), dim3(256), 0, s,
+                         static_cast<const u32x4*>(operand), indices, g.idx_bytes, g.idx_signed, g.op_dims[0], upr,
+                         nchunks, static_cast<u32x4*>(out));
+      check_launch("gather_rows");
+      return;
+    }
+  }
   p.unit_elems = 1;
   p.vector_inner = 0;
   // Rows of the operand's innermost dim copied whole: 16-byte units.

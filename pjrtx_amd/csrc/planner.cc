@@ -187,6 +187,8 @@ void Planner::decide_materialization() {
     for (int v : op.operands) users_[v].push_back(static_cast<int>(i));
   }
   std::map<int, int> cost;  // inlined op count of a non-materialized value
+  // Materialized buffers that recomputing a non-materialized value reads.
+  std::map<int, std::set<int>> reads;
   for (size_t i = 0; i < prog_.ops.size(); ++i) {
     const Op& op = prog_.ops[i];
     if (op.kind == OpKind::kReturn) {
@@ -234,16 +236,30 @@ void Planner::decide_materialization() {
         c -= cost[u];
       }
     }
-    cost[op.results[0]] = c;
-  }
-  // Multi-use values whose recompute would be expensive are materialized.
-  for (size_t i = 0; i < prog_.ops.size(); ++i) {
-    const Op& op = prog_.ops[i];
-    if (!fusible_op(op) || op.results.empty()) continue;
+    std::set<int> rd;
+    for (int u : op.operands) {
+      if (mat_.count(u)) {
+        rd.insert(u);
+      } else {
+        auto it = reads.find(u);
+        if (it != reads.end()) rd.insert(it->second.begin(), it->second.end());
+      }
+    }
+    // A value read by several kernels is recomputed in each unless that
+    // costs too many ops, or reads half again as many bytes as the value
+    // (a residual stream x + f(x) + g(...) would otherwise re-read every
+    // earlier layer's output in every later kernel).
     const int v = op.results[0];
-    if (mat_.count(v) || is_splat_constant(prog_, op)) continue;
-    const size_t nusers = users_[v].size();
-    if (nusers > 1 && cost[v] > opts_.recompute_limit) mat_.insert(v);
+    int64_t rbytes = 0;
+    for (int w : rd) rbytes += prog_.type(w).bytes();
+    if (users_[v].size() > 1 && !is_splat_constant(prog_, op) &&
+        (c > opts_.recompute_limit || (rd.size() > 1 && 2 * rbytes > 3 * prog_.type(v).bytes()))) {
+      mat_.insert(v);
+      c = 0;
+      rd.clear();
+    }
+    cost[v] = c;
+    reads[v] = std::move(rd);
   }
   // A splat constant that needs a buffer (library operand, program output,
   // non-literal reduce init) is uploaded once at load, like any constant.
@@ -829,6 +845,27 @@ std::string Plan::describe(const Program& prog) const {
       return b + "]";
     };
     o << ",\"in_bytes\":" << bytes_of(s.inputs) << ",\"out_bytes\":" << bytes_of(s.outputs);
+    // Bytes the step must move at minimum: every input read once and every
+    // output written once, except where a library op touches only part of an
+    // input (gather and dynamic_slice read the selected rows; an in-place
+    // dynamic_update_slice reads and writes only the update's window).
+    int64_t alg = 0;
+    for (int v : s.inputs) alg += prog.type(v).bytes();
+    for (int v : s.outputs) alg += prog.type(v).bytes();
+    if (s.kind == StepKind::kLibrary) {
+      const Op& d = prog.ops[s.lib_op];
+      const int64_t out = prog.type(d.results[0]).bytes();
+      if (s.lib == LibKind::kGather) {
+        alg = 2 * out + prog.type(d.operands[1]).bytes();
+      } else if (s.lib == LibKind::kDynamicSlice) {
+        alg = 2 * out;
+        for (size_t k = 1; k < d.operands.size(); ++k) alg += prog.type(d.operands[k]).bytes();
+      } else if (s.lib == LibKind::kDynamicUpdateSlice && s.in_place) {
+        alg = 2 * prog.type(d.operands[1]).bytes();
+        for (size_t k = 2; k < d.operands.size(); ++k) alg += prog.type(d.operands[k]).bytes();
+      }
+    }
+    o << ",\"algorithmic_bytes\":" << alg;
     std::vector<std::string> names;
     o << ",\"ops\":[";
     for (size_t k = 0; k < s.ops.size(); ++k) o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.ops[k]].kind) << "\"";
@@ -857,7 +894,17 @@ std::string Plan::describe(const Program& prog) const {
         const TensorType& q = prog.type(d.operands[0]);
         const TensorType& k = prog.type(d.operands[1]);
         const int sa = d.attn.layout == 0 ? 2 : d.attn.layout == 1 ? 1 : 0;
-        o << ",\"flops\":" << 4 * q.elements() * k.dims[sa] << ",\"causal\":" << (d.attn.causal ? "true" : "false")
+        // Pairs the mask allows (static masks only; a runtime offset leaves
+        // the count at every pair).
+        const int64_t sq = q.dims[sa], skv = k.dims[sa];
+        int64_t pairs = sq * skv;
+        if (d.attn.causal && !d.attn.has_offset_operand) {
+          pairs = 0;
+          for (int64_t i = 0; i < sq; ++i)
+            pairs += std::max<int64_t>(0, std::min<int64_t>(skv, d.attn.q_coef * i + d.attn.offset + 1));
+        }
+        o << ",\"flops\":" << 4 * q.elements() * skv << ",\"effective_flops\":" << 4 * (q.elements() / sq) * pairs
+          << ",\"causal\":" << (d.attn.causal ? "true" : "false")
           << ",\"q_coef\":" << d.attn.q_coef << ",\"offset\":" << d.attn.offset
           << ",\"offset_operand\":" << (d.attn.has_offset_operand ? "true" : "false") << ",\"scale\":" << strformat("%.17g", d.attn.scale)
           << ",\"layout\":" << d.attn.layout;

@@ -30,6 +30,7 @@ def test_c3_attention_is_one_step(plugin, monkeypatch):
     s = p["steps"][0]
     assert s["causal"] and s["q_coef"] == 1 and s["offset"] == 0 and not s["offset_operand"]
     assert s["scale"] == 1.0 and s["inputs"] == [0, 1, 2] and s["flops"] == 4 * 2 * 4 * 256 * 256 * 128
+    assert s["effective_flops"] == 4 * 2 * 4 * 128 * (256 * 257 // 2)  # causal: query i reads i + 1 keys
     monkeypatch.setenv("PJRTX_FUSED_ATTENTION", "0")
     assert kinds(plan(plugin, programs.c3_attention(2, 4, 256, 128))) == ["dot_general", "rowfused", "dot_general"]
 
