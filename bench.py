@@ -337,12 +337,17 @@ def bench_program(a, W: Workload) -> dict:
     if outs:
         outs[-1].block_until_ready()
     del outs
+    # The timed region is the plugin's own execute loop (pjrtx_executable_run:
+    # the PJRT execute path, synchronized before and after), so the ctypes
+    # client's per-call cost is left out; the Python-loop figure is reported
+    # beside it.
+    ms_per_step = exe.run_loop(bufs, a.steps) / a.steps
     t0 = time.perf_counter()
     last = None
     for _ in range(a.steps):
         last = exe.execute_buffers(bufs)
     last[-1].block_until_ready()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / a.steps
+    py_ms_per_step = (time.perf_counter() - t0) * 1e3 / a.steps
     del last
 
     plan = json.loads(exe.optimized_program())
@@ -369,6 +374,7 @@ def bench_program(a, W: Workload) -> dict:
                    "pct_peak_end_to_end": round(pct, 2),
                    "hbm_gbps_end_to_end": round(W.bytes / sec / 1e9, 2),
                    "kernels_per_step": sum(1 for n in names if n != "-"),
+                   "python_client_ms_per_step": round(py_ms_per_step, 5),
                    "kernel_us": unit_table(names, unit_ms)},
         "roofline": rf,
     }

@@ -81,6 +81,18 @@ struct PJRT_Buffer;
 PJRTX_HIP_API int pjrtx_executable_time_steps(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
                                 size_t num_args, int iters, double* ms, size_t cap, size_t* steps);
 
+/* Executes the executable `iters` times back to back on its device stream,
+ * through the same path as PJRT_LoadedExecutable_Execute (argument checks,
+ * graph capture and replay, output allocation; nothing donated), dropping
+ * each call's outputs, and writes the wall milliseconds from a synchronized
+ * start to the synchronized end of the last call to *ms_total. This is the
+ * steady-state execute loop without a host language's per-call binding cost.
+ * Replaces the reference's steady-execute measurement
+ * (src/plugin/jax/jax_llama_like_inference.py:291-296, timing
+ * execute_executable_program, metalcpp_api.cc:961-1161). */
+PJRTX_HIP_API int pjrtx_executable_run(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
+                                       size_t num_args, int iters, double* ms_total);
+
 /* Names of the executable's launch units, in the order of
  * pjrtx_executable_time_steps, '\n'-separated: the kernel name, or
  * "lib:<kind>" for a library step, "-" for a view that launches nothing. */

@@ -542,9 +542,9 @@ std::string combine_stmt(ReducerKind k, DType t, const std::string& a, const std
     case ReducerKind::kAnd: return a + " = " + a + " & (uint32_t)(" + b + ");";
     case ReducerKind::kOr: return a + " = " + a + " | (uint32_t)(" + b + ");";
     case ReducerKind::kMax:
-      return a + " = " + (f ? (d ? "max_d(" : "max_f(") : "max_i(") + a + ", " + b + ");";
+      return a + " = " + (f ? (d ? "max_d(" : "max_r(") : "max_i(") + a + ", " + b + ");";
     case ReducerKind::kMin:
-      return a + " = " + (f ? (d ? "min_d(" : "min_f(") : "min_i(") + a + ", " + b + ");";
+      return a + " = " + (f ? (d ? "min_d(" : "min_r(") : "min_i(") + a + ", " + b + ");";
     default: return "";
   }
 }

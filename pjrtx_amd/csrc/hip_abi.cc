@@ -1,4 +1,5 @@
 // pjrtx_hip_* C ABI (declared in include/pjrtx_hip.h).
+#include <chrono>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -154,6 +155,29 @@ int pjrtx_executable_time_steps(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* 
     std::vector<double> t = exe->exe->time_steps(dev, in, iters);
     if (steps) *steps = t.size();
     for (size_t i = 0; i < t.size() && i < cap; ++i) ms[i] = t[i];
+  });
+}
+
+int pjrtx_executable_run(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* args, size_t num_args, int iters,
+                         double* ms_total) {
+  return guarded([&] {
+    PJRTX_CHECK(exe && iters > 0 && ms_total, Code::kInvalidArgument, "run: bad arguments");
+    PJRTX_CHECK(!exe->deleted, Code::kFailedPrecondition, "run: executable was deleted");
+    std::vector<BufferRef> in;
+    for (size_t i = 0; i < num_args; ++i) {
+      PJRTX_CHECK(args[i] && !args[i]->buf->deleted, Code::kInvalidArgument, "run: argument is null or deleted");
+      in.push_back(args[i]->buf);
+    }
+    Device* dev = in.empty() ? exe->devices.at(0)->dev : in[0]->dev;
+    dev->make_current();
+    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < iters; ++i) {
+      std::shared_ptr<Event> done;
+      std::vector<BufferRef> outs = exe->exe->execute(dev, in, &done, nullptr);
+    }
+    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    *ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   });
 }
 

@@ -229,8 +229,13 @@ PJRTX_DEV bool argmin_better(float va, I ia, float vb, I ib) {
 PJRTX_DEV bool argmax_take(float x, float acc) { return x > acc || (isnan_f(x) && !isnan_f(acc)); }
 PJRTX_DEV bool argmin_take(float x, float acc) { return x < acc || (isnan_f(x) && !isnan_f(acc)); }
 // NaN-propagating running max/min (an accumulator that saw NaN stays NaN).
-PJRTX_DEV float max_seq(float acc, float x) { return (x > acc || isnan_f(x)) ? x : acc; }
-PJRTX_DEV float min_seq(float acc, float x) { return (x < acc || isnan_f(x)) ? x : acc; }
+// Reduction max/min: IEEE 754-2019 maximum/minimum (NaN propagates, -0 <
+// +0), so the result does not depend on the order partials are combined in.
+// gfx950 folds two new values per v_maximum3_f32 / v_minimum3_f32.
+PJRTX_DEV float max_r(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+PJRTX_DEV float min_r(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+PJRTX_DEV float max_seq(float acc, float x) { return max_r(acc, x); }
+PJRTX_DEV float min_seq(float acc, float x) { return min_r(acc, x); }
 
 // ------------------------------------------------------ wavefront reductions
 // 64-lane wavefronts: xor-butterfly over lane offsets 32..1. Every lane ends

@@ -213,6 +213,7 @@ class Plugin:
                                             POINTER(c_size_t)],
             "pjrtx_executable_step_names": [c_void_p, c_char_p, c_size_t, POINTER(c_size_t)],
             "pjrtx_executable_graph_stats": [c_void_p, POINTER(c_int64)],
+            "pjrtx_executable_run": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double)],
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
         }.items():
             f = getattr(L, name)
@@ -452,6 +453,15 @@ class Executable:
         self.client.p.hip_check(L.pjrtx_executable_time_steps(self.handle, arr, len(args), iters, ms, cap,
                                                               ctypes.byref(n)))
         return [ms[i] for i in range(n.value)]
+
+    def run_loop(self, args: list[Buffer], iters: int) -> float:
+        """Wall ms of `iters` back-to-back executions run by the plugin's own
+        loop (pjrtx_executable_run), synchronized on both sides."""
+        L = self.client.p.lib
+        arr = (c_void_p * max(1, len(args)))(*[b.handle for b in args])
+        ms = c_double(0.0)
+        self.client.p.hip_check(L.pjrtx_executable_run(self.handle, arr, len(args), iters, ctypes.byref(ms)))
+        return ms.value
 
     def step_names(self) -> list[str]:
         L = self.client.p.lib
