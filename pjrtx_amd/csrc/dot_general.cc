@@ -157,6 +157,24 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
       b_kmajor = true;
     }
     if ((a_fast || a_copy) && (b_kmajor || b_nmajor) && K % 8 == 0) {
+      if (M <= 8 && batch == 1 && !b_kmajor && !a_copy && gemv_wide_fits(static_cast<int>(M), static_cast<int>(K),
+                                                                           static_cast<int>((N + 63) / 64)) &&
+          N % 8 == 0 && (K == 1 || b.ks % 8 == 0)) {
+        GemvGroup g;
+        g.count = 1;
+        g.M = static_cast<int>(M);
+        g.K = static_cast<int>(K);
+        g.ldx = a.fs ? a.fs : K;
+        g.out_kind = out_kind;
+        g.m[0].W = B;
+        g.m[0].Y = out;
+        g.m[0].N = static_cast<int>(N);
+        g.m[0].ldw = b.ks ? b.ks : N;
+        g.m[0].ldy = N;
+        g.m[0].tile0 = 0;
+        launch_gemv_wide(dev->stream(), g, A, f16);
+        return;
+      }
       if (M <= 8) {
         GemvParams g;
         g.batch = static_cast<int>(batch);
@@ -232,6 +250,58 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
   f.b_ns = b.fs;
   f.b_ks = b.ks;
   launch_fma_gemm(dev->stream(), f, A, B, out, lt.dtype, ot.dtype);
+}
+
+// A dot group (planner: dots sharing one LHS): one gemv_wide launch when
+// every member is a decode-shaped product over the same X with an
+// N-contiguous weight; otherwise the members run one by one.
+void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops, std::vector<MemRef>& vals) {
+  GemvGroup g;
+  bool ok = ops.size() >= 1 && ops.size() <= static_cast<size_t>(kMaxGemvMembers);
+  const void* X = nullptr;
+  DType in_t = DType::kInvalid;
+  int tiles = 0;
+  for (size_t i = 0; i < ops.size() && ok; ++i) {
+    const Op& op = prog.ops.at(ops[i]);
+    const TensorType& lt = prog.type(op.operands[0]);
+    const TensorType& rt = prog.type(op.operands[1]);
+    const TensorType& ot = prog.type(op.results[0]);
+    ok = op.kind == OpKind::kDotGeneral && lt.rank() == 2 && rt.rank() == 2 && op.lhs_batch.empty() &&
+         op.lhs_contract == Dims{1} && op.rhs_contract == Dims{0} && (lt.dtype == DType::kBF16 || lt.dtype == DType::kF16) &&
+         rt.dtype == lt.dtype && (ot.dtype == lt.dtype || ot.dtype == DType::kF32);
+    if (!ok) break;
+    const int64_t M = lt.dims[0], K = lt.dims[1], N = rt.dims[1];
+    const int out_kind = ot.dtype == DType::kBF16 ? 0 : (ot.dtype == DType::kF16 ? 1 : 2);
+    const void* A = vals[op.operands[0]]->ptr;
+    const void* W = vals[op.operands[1]]->ptr;
+    ok = M >= 1 && M <= 4 && K % 8 == 0 && N % 8 == 0 && aligned16(A) && aligned16(W) && N < (int64_t(1) << 30) &&
+         M * K <= kGemvWideMaxX;
+    if (i == 0) {
+      X = A;
+      in_t = lt.dtype;
+      g.M = static_cast<int>(M);
+      g.K = static_cast<int>(K);
+      g.ldx = K;
+      g.out_kind = out_kind;
+    } else {
+      ok = ok && A == X && lt.dtype == in_t && g.M == M && g.K == K && g.out_kind == out_kind;
+    }
+    if (!ok) break;
+    GemvMember& m = g.m[i];
+    m.W = W;
+    m.Y = vals[op.results[0]]->ptr;
+    m.N = static_cast<int>(N);
+    m.ldw = N;
+    m.ldy = N;
+    m.tile0 = tiles;
+    tiles += static_cast<int>((N + 63) / 64);
+  }
+  if (ok && gemv_wide_fits(g.M, g.K, tiles)) {
+    g.count = static_cast<int>(ops.size());
+    launch_gemv_wide(dev->stream(), g, X, in_t == DType::kF16);
+    return;
+  }
+  for (int oi : ops) run_dot_general(dev, prog, prog.ops.at(oi), vals);
 }
 
 }  // namespace pjrtx

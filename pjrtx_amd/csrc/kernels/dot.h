@@ -47,6 +47,32 @@ void plan_gemv_split(GemvParams* p, int target_blocks = 512);
 void launch_gemv(hipStream_t s, const GemvParams& p, const void* X, const void* W, void* Y, float* partials, bool f16,
                  bool w_kmajor);
 
+// Decode GEMVs sharing one X (the reference's dot group: Q/K/V projections
+// of one normalized row, executable_metal_graph_lowering_fusion.zig:394-424):
+// up to 4 weights W_i [K][N_i] (N contiguous, row stride ldw), outputs Y_i
+// [M][N_i] (row stride ldy), optionally Y_i = add_i + round(X.W_i) with add_i
+// shaped like Y_i. One launch, one pass over each W, no split-K partials.
+constexpr int kMaxGemvMembers = 4;
+constexpr int64_t kGemvWideMaxX = 16384;  // M * K floats staged in LDS
+struct GemvMember {
+  const void* W = nullptr;
+  void* Y = nullptr;
+  const void* add = nullptr;
+  int N = 0;
+  int64_t ldw = 0, ldy = 0;
+  int tile0 = 0;  // first workgroup of this member (64 columns each)
+};
+struct GemvGroup {
+  int count = 0, M = 1, K = 0;
+  int64_t ldx = 0;
+  int out_kind = 0;  // 0 bf16, 1 f16, 2 f32
+  GemvMember m[kMaxGemvMembers];
+};
+// True when the one-pass kernel applies: M <= 4, M*K <= kGemvWideMaxX and at
+// least 32 workgroups (64 columns each) over the members.
+bool gemv_wide_fits(int M, int K, int total_tiles);
+void launch_gemv_wide(hipStream_t s, const GemvGroup& g, const void* X, bool f16);
+
 // Fallback with arbitrary element strides.
 struct FmaGemmParams {
   int64_t batch = 1, M = 0, N = 0, K = 0;

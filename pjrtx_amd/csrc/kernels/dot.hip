@@ -539,6 +539,100 @@ __global__ void __launch_bounds__(256) gemv_reduce(GemvParams p, const float* __
   }
 }
 
+// gemv_wide (W [K][N], N contiguous, one X for up to 4 weights): a
+// 1024-thread workgroup owns 64 columns of one member over the whole K, so
+// no partials and no second launch. Lane (rg, cc) reads 16 bytes of row
+// w*8 + rg + 128*r for r < 8 (eight rows in flight), X comes from LDS; the
+// 8 row groups fold by xor shuffles and the 16 waves through LDS in wave
+// order (deterministic). An optional addend (a residual) is added to the
+// rounded product and rounded again, as the unfused add would.
+constexpr int kWideCols = 64, kWideDepth = 8;
+
+template <int kM, bool kF16>
+__global__ void __launch_bounds__(1024) gemv_wide(GemvGroup g, const uint16_t* __restrict__ X) {
+  extern __shared__ float xs[];  // kM * K
+  __shared__ float red[16][kM][kWideCols];
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGemvMembers; ++i)
+    if (i < g.count && (int)blockIdx.x >= g.m[i].tile0) mi = i;
+  const GemvMember mb = g.m[mi];
+  const int n0 = ((int)blockIdx.x - mb.tile0) * kWideCols;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rg = lane >> 3, cc = lane & 7;
+  const int n = n0 + cc * 8;
+  const int K = g.K;
+  for (int i = threadIdx.x; i < g.M * K; i += 1024) {
+    const int m = i / K, k = i - m * K;
+    xs[i] = half_to_f32<kF16>(X[(int64_t)m * g.ldx + k]);
+  }
+  __syncthreads();
+  float acc[kM][8];
+#pragma unroll
+  for (int m = 0; m < kM; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
+  const uint16_t* W = static_cast<const uint16_t*>(mb.W);
+  if (n < mb.N) {
+    for (int kb = wave * 8 + rg; kb < K; kb += 128 * kWideDepth) {
+      u32x4 w[kWideDepth];
+#pragma unroll
+      for (int r = 0; r < kWideDepth; ++r) {
+        const int k = kb + 128 * r;
+        w[r] = k < K ? *reinterpret_cast<const u32x4*>(W + (int64_t)k * mb.ldw + n) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int r = 0; r < kWideDepth; ++r) {
+        const int k = kb + 128 * r;
+        if (k < K) {
+          const uint16_t* we = reinterpret_cast<const uint16_t*>(&w[r]);
+#pragma unroll
+          for (int m = 0; m < kM; ++m) {
+            const float xv = m < g.M ? xs[m * K + k] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[m][e] += xv * half_to_f32<kF16>(we[e]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kM; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[m][e];
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[m][e] = v;
+    }
+  if (rg == 0) {
+#pragma unroll
+    for (int m = 0; m < kM; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wave][m][cc * 8 + e] = acc[m][e];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kM * kWideCols; i += 1024) {
+    const int m = i / kWideCols, c = i - m * kWideCols;
+    const int nn = n0 + c;
+    if (m >= g.M || nn >= mb.N) continue;
+    float v = red[0][m][c];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) v += red[w][m][c];
+    const int64_t at = (int64_t)m * mb.ldy + nn;
+    if (mb.add) {
+      const float y = g.out_kind == 2 ? v : (g.out_kind == 1 ? f16_bits_to_f32(f32_to_f16_bits(v))
+                                                           : bf16_bits_to_f32(f32_to_bf16_rne(v)));
+      const float a = g.out_kind == 2 ? static_cast<const float*>(mb.add)[at]
+                      : (g.out_kind == 1 ? f16_bits_to_f32(static_cast<const uint16_t*>(mb.add)[at])
+                                         : bf16_bits_to_f32(static_cast<const uint16_t*>(mb.add)[at]));
+      v = a + y;
+    }
+    store_out(mb.Y, at, v, g.out_kind);
+  }
+}
+
 template <int kM, bool kF16, int G>
 __global__ void __launch_bounds__(256) gemv_k(GemvParams p, const uint16_t* __restrict__ X,
                                               const uint16_t* __restrict__ W, void* __restrict__ Y) {
@@ -731,6 +825,32 @@ void launch_gemv(hipStream_t s, const GemvParams& p, const void* X, const void* 
     hipLaunchKernelGGL(gemv_reduce, gr, dim3(256), 0, s, p, partials, Y);
   }
   check("gemv");
+}
+
+bool gemv_wide_fits(int M, int K, int total_tiles) {
+  return M >= 1 && M <= 4 && K >= 1 && (int64_t)M * K <= kGemvWideMaxX && total_tiles >= 32;
+}
+
+void launch_gemv_wide(hipStream_t s, const GemvGroup& g, const void* X, bool f16) {
+  PJRTX_CHECK(g.count >= 1 && g.count <= kMaxGemvMembers && g.M >= 1 && g.M <= 4 && (int64_t)g.M * g.K <= kGemvWideMaxX,
+              Code::kInternal, "gemv_wide: bad group");
+  int tiles = 0;
+  for (int i = 0; i < g.count; ++i) {
+    PJRTX_CHECK(g.m[i].tile0 == tiles && g.m[i].N % 8 == 0 && g.m[i].ldw % 8 == 0, Code::kInternal,
+                "gemv_wide: bad member layout");
+    tiles += (g.m[i].N + kWideCols - 1) / kWideCols;
+  }
+  const size_t lds = static_cast<size_t>(g.M) * g.K * sizeof(float);
+  const uint16_t* x = static_cast<const uint16_t*>(X);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(1024);
+#define PJRTX_WIDE(KM)                                                                   \
+  if (f16) hipLaunchKernelGGL((gemv_wide<KM, true>), grid, block, lds, s, g, x);        \
+  else hipLaunchKernelGGL((gemv_wide<KM, false>), grid, block, lds, s, g, x);
+  if (g.M == 1) { PJRTX_WIDE(1) }
+  else if (g.M == 2) { PJRTX_WIDE(2) }
+  else { PJRTX_WIDE(4) }
+#undef PJRTX_WIDE
+  check("gemv_wide");
 }
 
 void launch_fma_gemm(hipStream_t s, const FmaGemmParams& p, const void* A, const void* B, void* C, DType in,

@@ -184,6 +184,7 @@ GatherParams make_gather_params(const Program& prog, const Op& op) {
 void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
+void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops, std::vector<MemRef>& vals);
 
 void run_library_step(Device* dev, const Program& prog, const Step& step, std::vector<MemRef>& vals) {
   const Op& op = prog.ops.at(step.lib_op);
@@ -214,6 +215,9 @@ void run_library_step(Device* dev, const Program& prog, const Step& step, std::v
       return;
     case LibKind::kAttention:
       run_attention(dev, prog, op, vals);
+      return;
+    case LibKind::kDotGroup:
+      run_dot_group(dev, prog, step.group_ops, vals);
       return;
     default:
       fail(Code::kUnimplemented, std::string("library op not available: ") + lib_kind_name(step.lib));

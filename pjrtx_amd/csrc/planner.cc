@@ -34,6 +34,7 @@ const char* lib_kind_name(LibKind k) {
     case LibKind::kConcatenate: return "concatenate";
     case LibKind::kPad: return "pad";
     case LibKind::kAttention: return "attention";
+    case LibKind::kDotGroup: return "dot_group";
   }
   return "?";
 }
@@ -326,10 +327,60 @@ int Planner::order_preserving_source(int v) const {
   return -1;
 }
 
+// Decode-shaped dot (the reference's dot group candidates,
+// executable_metal_graph_lowering_fusion.zig:394-424): [M, K] x [K, N] with
+// M <= 4, 16-bit operands.
+static bool group_candidate(const Program& prog, const Op& op) {
+  if (op.kind != OpKind::kDotGeneral || op.operands.size() != 2) return false;
+  const TensorType& l = prog.type(op.operands[0]);
+  const TensorType& r = prog.type(op.operands[1]);
+  return l.rank() == 2 && r.rank() == 2 && op.lhs_batch.empty() && op.rhs_batch.empty() &&
+         op.lhs_contract == Dims{1} && op.rhs_contract == Dims{0} && l.dims[0] <= 4 && l.dtype == r.dtype &&
+         (l.dtype == DType::kBF16 || l.dtype == DType::kF16);
+}
+
 void Planner::build_steps(std::vector<Step>* steps) {
+  // Dots sharing one LHS, each RHS defined before the first of them (so no
+  // member can depend on another), up to 4 per group.
+  std::map<int, std::vector<int>> groups;
+  std::set<int> grouped;
+  if (opts_.group_dots) {
+    for (size_t i = 0; i < prog_.ops.size(); ++i) {
+      const Op& a = prog_.ops[i];
+      if (grouped.count(static_cast<int>(i)) || !group_candidate(prog_, a)) continue;
+      std::vector<int> members = {static_cast<int>(i)};
+      for (size_t j = i + 1; j < prog_.ops.size() && members.size() < 4; ++j) {
+        const Op& b = prog_.ops[j];
+        if (grouped.count(static_cast<int>(j)) || !group_candidate(prog_, b) || b.operands[0] != a.operands[0]) continue;
+        if (prog_.type(b.results[0]).dtype != prog_.type(a.results[0]).dtype) continue;
+        auto pr = producer_.find(b.operands[1]);
+        if (pr != producer_.end() && pr->second >= static_cast<int>(i)) continue;
+        members.push_back(static_cast<int>(j));
+      }
+      if (members.size() < 2) continue;
+      groups[static_cast<int>(i)] = members;
+      grouped.insert(members.begin(), members.end());
+    }
+  }
   for (size_t i = 0; i < prog_.ops.size(); ++i) {
     const Op& op = prog_.ops[i];
     if (op.kind == OpKind::kReturn || op.kind == OpKind::kConstant) continue;  // constants: literals or resident
+    if (grouped.count(static_cast<int>(i))) {
+      auto g = groups.find(static_cast<int>(i));
+      if (g == groups.end()) continue;  // a later member: emitted with its group
+      Step s;
+      s.kind = StepKind::kLibrary;
+      s.lib = LibKind::kDotGroup;
+      s.lib_op = static_cast<int>(i);
+      s.group_ops = g->second;
+      s.inputs.push_back(op.operands[0]);
+      for (int m : g->second) {
+        s.inputs.push_back(prog_.ops[m].operands[1]);
+        s.outputs.push_back(prog_.ops[m].results[0]);
+      }
+      steps->push_back(std::move(s));
+      continue;
+    }
     if (op.kind == OpKind::kReduce) {
       Step s;
       s.kind = StepKind::kReduce;
@@ -883,11 +934,17 @@ std::string Plan::describe(const Program& prog) const {
     }
     if (s.kind == StepKind::kLibrary) {
       o << ",\"library\":\"" << lib_kind_name(s.lib) << "\",\"in_place\":" << (s.in_place ? "true" : "false");
-      if (s.lib == LibKind::kDot) {  // 2 * output elements * contracted size
-        const Op& d = prog.ops[s.lib_op];
-        int64_t kc = 1;
-        for (int64_t c : d.lhs_contract) kc *= prog.type(d.operands[0]).dims[c];
-        o << ",\"flops\":" << 2 * prog.type(d.results[0]).elements() * kc;
+      if (s.lib == LibKind::kDot || s.lib == LibKind::kDotGroup) {  // 2 * output elements * contracted size
+        int64_t flops = 0;
+        const std::vector<int> ops = s.lib == LibKind::kDot ? std::vector<int>{s.lib_op} : s.group_ops;
+        for (int oi : ops) {
+          const Op& d = prog.ops[oi];
+          int64_t kc = 1;
+          for (int64_t c : d.lhs_contract) kc *= prog.type(d.operands[0]).dims[c];
+          flops += 2 * prog.type(d.results[0]).elements() * kc;
+        }
+        o << ",\"flops\":" << flops;
+        if (s.lib == LibKind::kDotGroup) o << ",\"group_size\":" << s.group_ops.size();
       }
       if (s.lib == LibKind::kAttention) {  // q.k and p.v over every (query, key) pair
         const Op& d = prog.ops[s.lib_op];

@@ -48,7 +48,7 @@ struct ReduceSpec {
 enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused };
 
 enum class LibKind {
-  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention
+  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup
 };
 const char* lib_kind_name(LibKind k);
 
@@ -93,6 +93,9 @@ struct Step {
   // kRowFused
   std::vector<Step> phases;
   bool wave_per_row = false;  // one wave per row (4 rows per workgroup), else one workgroup per row
+
+  // kDotGroup: the dot_general ops (program order) sharing one LHS
+  std::vector<int> group_ops;
 };
 
 struct Plan {
@@ -122,6 +125,9 @@ struct PlanOptions {
   // when a row has at most this many elements (environment:
   // PJRTX_ROW_FUSE_MAX, 0 disables).
   int64_t row_fuse_max = env_int("PJRTX_ROW_FUSE_MAX", 16384);
+  // Decode-shaped dots that share their LHS (Q/K/V, gate/up projections)
+  // become one step (environment: PJRTX_DOT_GROUPS, 0 disables).
+  bool group_dots = env_int("PJRTX_DOT_GROUPS", 1) != 0;
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());

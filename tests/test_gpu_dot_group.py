@@ -1,0 +1,61 @@
+"""Dot groups (planner: decode-shaped dots sharing one LHS, the reference's
+dot group of executable_metal_graph_lowering_fusion.zig:394-424) run as one
+gemv_wide launch. Each member must equal float64 within the bf16/f16 bar and
+be bit-identical to the same dot planned alone (same kernel, same summation
+order)."""
+import json
+
+import numpy as np
+import pytest
+
+from oracle import ops
+from pjrtx_amd.hlo import Builder
+
+pytestmark = pytest.mark.gpu
+
+
+def _program(M, K, Ns, dt):
+    b = Builder()
+    x = b.param((M, K), dt)
+    ws = [b.param((K, n), dt) for n in Ns]
+    return b.build([b.dot_general(x, w, contract=((1,), (0,))) for w in ws])
+
+
+def _bits(rng, shape, dt, scale=1.0):
+    v = (scale * rng.standard_normal(shape)).astype(np.float32)
+    return ops.f32_to_bf16_bits(v) if dt == "bf16" else v.astype(np.float16)
+
+
+def _f64(a, dt):
+    return (ops.bf16_bits_to_f32(a) if dt == "bf16" else np.asarray(a, np.float32)).astype(np.float64)
+
+
+@pytest.mark.parametrize("M,K,Ns,dt", [
+    (1, 2048, (2048, 512, 512), "bf16"),     # q/k/v with grouped-query k/v widths
+    (1, 2048, (5632, 5632), "bf16"),         # gate / up
+    (2, 1024, (1024, 2048, 64, 4096), "f16"),
+    (4, 4096, (2048, 2048), "bf16"),
+    (4, 8192, (2048, 2048), "bf16"),         # M*K past the LDS stage: members run one by one
+])
+def test_dot_group_matches_oracle_and_single_dots(client, monkeypatch, M, K, Ns, dt):
+    rng = np.random.default_rng(K + sum(Ns) + M)
+    x = _bits(rng, (M, K), dt)
+    ws = [_bits(rng, (K, n), dt, 1 / np.sqrt(K)) for n in Ns]
+    text = _program(M, K, Ns, dt)
+    exe = client.compile(text)
+    steps = json.loads(exe.optimized_program())["steps"]
+    assert [s.get("library") for s in steps] == ["dot_group"]
+    assert steps[0]["group_size"] == len(Ns)
+    outs = exe(x, *ws, dtypes=[dt] * (1 + len(Ns)))
+    monkeypatch.setenv("PJRTX_DOT_GROUPS", "0")
+    single = client.compile(text)
+    assert [s.get("library") for s in json.loads(single.optimized_program())["steps"]] == ["dot_general"] * len(Ns)
+    alone = single(x, *ws, dtypes=[dt] * (1 + len(Ns)))
+    for got, ref, w, n in zip(outs, alone, ws, Ns):
+        want = _f64(x, dt) @ _f64(w, dt)
+        g = _f64(got, dt)
+        assert np.abs(g - want).max() <= 2e-2 * np.abs(want).max()
+        # Bit-identical where the dot alone takes the same one-pass kernel
+        # (at least 32 column tiles) or the group falls back to single dots.
+        if (n // 64 >= 32 and M * K <= 16384) or M * K > 16384:
+            np.testing.assert_array_equal(got, ref)

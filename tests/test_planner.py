@@ -177,3 +177,23 @@ def test_generated_code_has_no_packed_f32(plugin):
     src = plugin.kernel_source(programs.c1_elementwise_rowsum(64, 256))
     assert "v_pk_" not in src
     assert "pjrtx_fusion_reduce_0" in src
+
+
+def test_decode_dots_sharing_an_lhs_form_groups(plugin, monkeypatch):
+    from pjrtx_amd import llama_like as L
+    steps = plan(plugin, L.decode_program(L.TINY))["steps"]
+    groups = [s["group_size"] for s in steps if s.get("library") == "dot_group"]
+    assert groups == [3, 2] * L.TINY.layers  # q/k/v and gate/up of every layer
+    monkeypatch.setenv("PJRTX_DOT_GROUPS", "0")
+    assert not [s for s in plan(plugin, L.decode_program(L.TINY))["steps"] if s.get("library") == "dot_group"]
+
+
+def test_dot_group_refuses_a_member_that_depends_on_another(plugin):
+    b = Builder()
+    x = b.param((1, 64), "bf16")
+    w = b.param((64, 64), "bf16")
+    y = b.dot_general(x, w, contract=((1,), (0,)))
+    w2 = b.multiply(w, b.broadcast_in_dim(b.reshape(y, (64,)), (64, 64), [1]))  # depends on the first dot
+    z = b.dot_general(x, w2, contract=((1,), (0,)))
+    steps = plan(plugin, b.build([y, z]))["steps"]
+    assert "dot_group" not in [s.get("library") for s in steps]
