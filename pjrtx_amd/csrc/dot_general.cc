@@ -252,6 +252,42 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
   launch_fma_gemm(dev->stream(), f, A, B, out, lt.dtype, ot.dtype);
 }
 
+// A dot whose result only feeds `add(dot, x)`: out = x + round(dot) as the
+// one-pass GEMV's epilogue, or, when that kernel does not apply to these
+// buffers, the dot into a temporary followed by the elementwise add.
+void run_dot_residual(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, int add, int out) {
+  const TensorType& lt = prog.type(op.operands[0]);
+  const TensorType& rt = prog.type(op.operands[1]);
+  const TensorType& ot = prog.type(op.results[0]);
+  const void* A = vals[op.operands[0]]->ptr;
+  const void* W = vals[op.operands[1]]->ptr;
+  const bool ok = lt.rank() == 2 && rt.rank() == 2 && op.lhs_batch.empty() && op.lhs_contract == Dims{1} &&
+                  op.rhs_contract == Dims{0} && (lt.dtype == DType::kBF16 || lt.dtype == DType::kF16) &&
+                  rt.dtype == lt.dtype && ot.dtype == lt.dtype && lt.dims[1] % 8 == 0 && rt.dims[1] % 8 == 0 &&
+                  aligned16(W) && gemv_wide_fits(static_cast<int>(lt.dims[0]), static_cast<int>(lt.dims[1]),
+                                                 static_cast<int>((rt.dims[1] + 63) / 64));
+  if (ok) {
+    GemvGroup g;
+    g.count = 1;
+    g.M = static_cast<int>(lt.dims[0]);
+    g.K = static_cast<int>(lt.dims[1]);
+    g.ldx = lt.dims[1];
+    g.out_kind = lt.dtype == DType::kF16 ? 1 : 0;
+    g.m[0].W = W;
+    g.m[0].Y = vals[out]->ptr;
+    g.m[0].add = vals[add]->ptr;
+    g.m[0].N = static_cast<int>(rt.dims[1]);
+    g.m[0].ldw = rt.dims[1];
+    g.m[0].ldy = rt.dims[1];
+    launch_gemv_wide(dev->stream(), g, A, lt.dtype == DType::kF16);
+    return;
+  }
+  vals[op.results[0]] = dev->allocate(ot.bytes());
+  run_dot_general(dev, prog, op, vals);
+  launch_add(dev->stream(), vals[add]->ptr, vals[op.results[0]]->ptr, vals[out]->ptr, ot.elements(), ot.dtype);
+  vals[op.results[0]].reset();
+}
+
 // A dot group (planner: dots sharing one LHS): one gemv_wide launch when
 // every member is a decode-shaped product over the same X with an
 // N-contiguous weight; otherwise the members run one by one.

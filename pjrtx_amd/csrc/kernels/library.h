@@ -7,6 +7,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "common.h"
+
 namespace pjrtx {
 
 constexpr int kMaxRank = 8;
@@ -58,6 +60,10 @@ struct GatherParams {
 };
 void launch_gather(hipStream_t s, const GatherParams& p, const void* operand, const void* indices, void* out,
                    int elem_bytes);
+
+// out[i] = a[i] + y[i] computed in f32 and rounded to the element type
+// (bf16, f16 or f32): the unfused elementwise add.
+void launch_add(hipStream_t s, const void* a, const void* y, void* out, int64_t n, DType t);
 
 // Copies up to kMaxCopySegments independent byte ranges in one launch (used
 // to stage small arguments into, and results out of, a replayed graph).

@@ -158,6 +158,23 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const u32x4* __restric
 
 int64_t blocks_for(int64_t n) { return (n + 255) / 256; }
 
+__device__ __forceinline__ float bf16f(uint16_t v) { return __builtin_bit_cast(float, (uint32_t)v << 16); }
+
+__global__ void __launch_bounds__(256) add_kernel(const void* __restrict__ a, const void* __restrict__ y,
+                                                  void* __restrict__ out, int64_t n, int kind) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  if (kind == 2) {
+    static_cast<float*>(out)[i] = static_cast<const float*>(a)[i] + static_cast<const float*>(y)[i];
+  } else if (kind == 1) {
+    const float v = (float)static_cast<const _Float16*>(a)[i] + (float)static_cast<const _Float16*>(y)[i];
+    static_cast<_Float16*>(out)[i] = (_Float16)v;
+  } else {
+    const float v = bf16f(static_cast<const uint16_t*>(a)[i]) + bf16f(static_cast<const uint16_t*>(y)[i]);
+    static_cast<uint16_t*>(out)[i] = __builtin_bit_cast(uint16_t, (__bf16)v);
+  }
+}
+
 void check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(Code::kInternal, strformat("%s launch failed: %s", what, hipGetErrorString(e)));
@@ -220,6 +237,14 @@ void launch_fill(hipStream_t s, void* dst, const void* value, int64_t n, int ele
     default: fail(Code::kInternal, "fill: bad element size");
   }
   check_launch("fill");
+}
+
+void launch_add(hipStream_t s, const void* a, const void* y, void* out, int64_t n, DType t) {
+  if (n == 0) return;
+  const int kind = t == DType::kF32 ? 2 : (t == DType::kF16 ? 1 : 0);
+  PJRTX_CHECK(t == DType::kF32 || t == DType::kF16 || t == DType::kBF16, Code::kInternal, "add: element type");
+  hipLaunchKernelGGL(add_kernel, dim3(static_cast<unsigned>(blocks_for(n))), dim3(256), 0, s, a, y, out, n, kind);
+  check_launch("add");
 }
 
 void launch_gather(hipStream_t s, const GatherParams& g, const void* operand, const void* indices, void* out,

@@ -185,6 +185,7 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
 void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops, std::vector<MemRef>& vals);
+void run_dot_residual(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, int add, int out);
 
 void run_library_step(Device* dev, const Program& prog, const Step& step, std::vector<MemRef>& vals) {
   const Op& op = prog.ops.at(step.lib_op);
@@ -208,7 +209,8 @@ void run_library_step(Device* dev, const Program& prog, const Step& step, std::v
       return;
     }
     case LibKind::kDot:
-      run_dot_general(dev, prog, op, vals);
+      if (step.dot_add >= 0) run_dot_residual(dev, prog, op, vals, step.dot_add, step.outputs[0]);
+      else run_dot_general(dev, prog, op, vals);
       return;
     case LibKind::kScatter:
       run_scatter(dev, prog, op, vals);

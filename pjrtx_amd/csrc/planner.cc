@@ -170,6 +170,7 @@ class Planner {
   int order_preserving_source(int v) const;
   void merge_siblings(std::vector<Step>* steps);
   void merge_epilogues(std::vector<Step>* steps);
+  void merge_dot_residuals(std::vector<Step>* steps);
   void fuse_row_chains(std::vector<Step>* steps);
   bool row_uses_ok(const Step& x, const std::set<int>& produced, const Dims& shape, size_t nkept) const;
   void shape_row_fused(Step* s);
@@ -490,6 +491,53 @@ void Planner::merge_siblings(std::vector<Step>* steps) {
         changed = true;
       }
     }
+  }
+}
+
+// True when run_dot_general takes the one-pass GEMV for this dot (shape
+// conditions; buffer alignment is checked again at run time).
+static bool one_pass_gemv(const Program& prog, const Op& op) {
+  if (op.kind != OpKind::kDotGeneral || op.operands.size() != 2) return false;
+  const TensorType& l = prog.type(op.operands[0]);
+  const TensorType& r = prog.type(op.operands[1]);
+  if (l.rank() != 2 || r.rank() != 2 || !op.lhs_batch.empty() || op.lhs_contract != Dims{1} ||
+      op.rhs_contract != Dims{0} || l.dtype != r.dtype || (l.dtype != DType::kBF16 && l.dtype != DType::kF16))
+    return false;
+  const int64_t M = l.dims[0], K = l.dims[1], N = r.dims[1];
+  return M >= 1 && M <= 4 && K % 8 == 0 && N % 8 == 0 && M * K <= 16384 && (N + 63) / 64 >= 32;
+}
+
+// add(dot, x) where the dot's only reader is that add: the dot step writes
+// x + round(dot) directly (the GEMV's epilogue), one launch and one buffer
+// fewer (a residual connection after an output or down projection).
+void Planner::merge_dot_residuals(std::vector<Step>* steps) {
+  std::map<int, int> readers;
+  for (const Step& s : *steps)
+    for (int v : s.inputs) readers[v]++;
+  auto v2s = value_to_step(*steps);
+  for (size_t g = 0; g < steps->size(); ++g) {
+    Step& G = (*steps)[g];
+    if (G.kind != StepKind::kLoop || G.outputs.size() != 1 || G.ops.size() != 1 || G.inputs.size() != 2) continue;
+    const Op& add = prog_.ops[G.ops[0]];
+    if (add.kind != OpKind::kAdd || add.results[0] != G.outputs[0]) continue;
+    for (int side = 0; side < 2; ++side) {
+      const int d = add.operands[side], x = add.operands[1 - side];
+      if (d == x || !v2s.count(d) || readers[d] != 1 || outputs_.count(d)) continue;
+      Step& D = (*steps)[v2s[d]];
+      if (D.kind != StepKind::kLibrary || D.lib != LibKind::kDot || D.dot_add >= 0 || D.outputs.size() != 1) continue;
+      const Op& dot = prog_.ops[D.lib_op];
+      if (!one_pass_gemv(prog_, dot) || prog_.type(x).dims != prog_.type(d).dims ||
+          prog_.type(x).dtype != prog_.type(d).dtype || prog_.type(G.outputs[0]).dtype != prog_.type(d).dtype)
+        continue;
+      D.dot_add = x;
+      D.inputs.push_back(x);
+      D.outputs = G.outputs;
+      mat_.erase(d);
+      steps->erase(steps->begin() + g);
+      --g;
+      break;
+    }
+    v2s = value_to_step(*steps);
   }
 }
 
@@ -852,6 +900,7 @@ Plan Planner::run() {
   build_steps(&steps);
   if (opts_.fuse_siblings) merge_siblings(&steps);
   if (opts_.fuse_epilogues) merge_epilogues(&steps);
+  if (opts_.dot_residual) merge_dot_residuals(&steps);
   if (opts_.row_fuse_max > 0) fuse_row_chains(&steps);
   schedule(&steps);
   int kernel_id = 0;
@@ -945,6 +994,7 @@ std::string Plan::describe(const Program& prog) const {
         }
         o << ",\"flops\":" << flops;
         if (s.lib == LibKind::kDotGroup) o << ",\"group_size\":" << s.group_ops.size();
+        if (s.dot_add >= 0) o << ",\"residual_add\":" << s.dot_add;
       }
       if (s.lib == LibKind::kAttention) {  // q.k and p.v over every (query, key) pair
         const Op& d = prog.ops[s.lib_op];

@@ -96,6 +96,9 @@ struct Step {
 
   // kDotGroup: the dot_general ops (program order) sharing one LHS
   std::vector<int> group_ops;
+  // kDot: value added to the rounded product (a residual add merged into the
+  // dot); the step's output is then the sum, not the dot's own result.
+  int dot_add = -1;
 };
 
 struct Plan {
@@ -128,6 +131,9 @@ struct PlanOptions {
   // Decode-shaped dots that share their LHS (Q/K/V, gate/up projections)
   // become one step (environment: PJRTX_DOT_GROUPS, 0 disables).
   bool group_dots = env_int("PJRTX_DOT_GROUPS", 1) != 0;
+  // A decode-shaped dot whose only reader is `add(dot, x)` writes the sum
+  // itself (environment: PJRTX_DOT_RESIDUAL, 0 disables).
+  bool dot_residual = env_int("PJRTX_DOT_RESIDUAL", 1) != 0;
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());

@@ -59,3 +59,25 @@ def test_dot_group_matches_oracle_and_single_dots(client, monkeypatch, M, K, Ns,
         # (at least 32 column tiles) or the group falls back to single dots.
         if (n // 64 >= 32 and M * K <= 16384) or M * K > 16384:
             np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,K,N,dt", [(1, 2048, 2048, "bf16"), (2, 5632, 2048, "f16"), (1, 2048, 32000, "bf16")])
+def test_residual_add_merged_into_dot(client, monkeypatch, M, K, N, dt):
+    """x + dot(h, w) with the dot read only by the add: one launch writing
+    the sum, bit-identical to the dot followed by the elementwise add."""
+    rng = np.random.default_rng(K + N)
+    b = Builder()
+    h, w, x = b.param((M, K), dt), b.param((K, N), dt), b.param((M, N), dt)
+    text = b.build([b.add(x, b.dot_general(h, w, contract=((1,), (0,))))])
+    args = [_bits(rng, (M, K), dt), _bits(rng, (K, N), dt, 1 / np.sqrt(K)), _bits(rng, (M, N), dt)]
+    exe = client.compile(text)
+    steps = json.loads(exe.optimized_program())["steps"]
+    assert len(steps) == 1 and "residual_add" in steps[0]
+    (got,) = exe(*args, dtypes=[dt] * 3)
+    monkeypatch.setenv("PJRTX_DOT_RESIDUAL", "0")
+    plain = client.compile(text)
+    assert len(json.loads(plain.optimized_program())["steps"]) == 2
+    (want,) = plain(*args, dtypes=[dt] * 3)
+    np.testing.assert_array_equal(got, want)
+    ref = _f64(args[2], dt) + _f64(args[0], dt) @ _f64(args[1], dt)
+    assert np.abs(_f64(got, dt) - ref).max() <= 2e-2 * np.abs(ref).max()

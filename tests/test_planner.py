@@ -197,3 +197,13 @@ def test_dot_group_refuses_a_member_that_depends_on_another(plugin):
     z = b.dot_general(x, w2, contract=((1,), (0,)))
     steps = plan(plugin, b.build([y, z]))["steps"]
     assert "dot_group" not in [s.get("library") for s in steps]
+
+
+def test_residual_add_merges_into_decode_dot(plugin, monkeypatch):
+    from pjrtx_amd import llama_like as L
+    steps = plan(plugin, L.decode_program(L.FULL))["steps"]
+    merged = [s for s in steps if "residual_add" in s]
+    assert len(merged) >= 2 * L.FULL.layers - 1  # o-proj and down-proj residuals
+    assert all(s.get("library") == "dot_general" for s in merged)
+    monkeypatch.setenv("PJRTX_DOT_RESIDUAL", "0")
+    assert not [s for s in plan(plugin, L.decode_program(L.FULL))["steps"] if "residual_add" in s]
