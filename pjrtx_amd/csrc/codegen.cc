@@ -790,10 +790,45 @@ void KernelGen::reduce(Step& s) {
   // In-thread update. A thread visits its elements by increasing index, so
   // the in-order forms (argmax_take, max_seq, min_seq) give the same result
   // as the full pair comparator with fewer instructions.
-  auto combine_elem = [&](std::ostream& o) {
+  // Whole vec-element sub-chunks of the row schedule fold an argmax in two
+  // phases: the sub-chunk's max (IEEE maximum, NaN propagating; two new
+  // values per instruction), then the first element equal to it (or the
+  // first NaN) found by a backward scan, merged into the running pair with
+  // the in-order rule. Same winner and value bits as the element-wise fold.
+  auto is_arg = [](const Accum& a) { return a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin; };
+  auto two_phase_decl = [&](std::ostream& o) {
+    for (size_t r = 0; r < accs.size(); ++r)
+      if (is_arg(accs[r]))
+        o << "float xa" << r << "[" << vec << "]; " << ait << " ia" << r << "[" << vec << "]; float mc" << r << " = "
+          << (accs[r].kind == ReducerKind::kArgMax ? "-__builtin_inff()" : "__builtin_inff()") << ";\n";
+  };
+  auto two_phase_finish = [&](std::ostream& o) {
     for (size_t r = 0; r < accs.size(); ++r) {
       const Accum& a = accs[r];
-      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
+      if (!is_arg(a)) continue;
+      const char* take = a.kind == ReducerKind::kArgMax ? "argmax_take" : "argmin_take";
+      const std::string R = std::to_string(r);
+      o << "{ float sv = mc" << R << "; " << ait << " si = 0;\n";
+      o << "if (__any(mc" << R << " != mc" << R << ")) {\n";
+      o << "const bool mn = mc" << R << " != mc" << R << ";\n";
+      o << "#pragma unroll\nfor (int j = " << vec - 1 << "; j >= 0; --j) { const bool hit = mn ? (xa" << R << "[j] != xa"
+        << R << "[j]) : (xa" << R << "[j] == mc" << R << "); sv = hit ? xa" << R << "[j] : sv; si = hit ? ia" << R
+        << "[j] : si; }\n";
+      o << "} else {\n";
+      o << "#pragma unroll\nfor (int j = " << vec - 1 << "; j >= 0; --j) { const bool hit = xa" << R << "[j] == mc" << R
+        << "; sv = hit ? xa" << R << "[j] : sv; si = hit ? ia" << R << "[j] : si; }\n";
+      o << "}\n";
+      o << "const bool bt = " << take << "(sv, " << a.v << "); " << a.v << " = bt ? sv : " << a.v << "; " << a.i
+        << " = bt ? si : " << a.i << "; }\n";
+    }
+  };
+  auto combine_elem = [&](std::ostream& o, bool two_phase) {
+    for (size_t r = 0; r < accs.size(); ++r) {
+      const Accum& a = accs[r];
+      if (two_phase && is_arg(a)) {
+        o << "xa" << r << "[j] = (float)" << xs[r][0] << "; ia" << r << "[j] = (" << ait << ")" << xs[r][1] << "; mc" << r
+          << " = " << (a.kind == ReducerKind::kArgMax ? "max_r(" : "min_r(") << "mc" << r << ", xa" << r << "[j]);\n";
+      } else if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
         const char* take = a.kind == ReducerKind::kArgMax ? "argmax_take" : "argmin_take";
         o << "{ const float xv = (float)" << xs[r][0] << "; const bool bt = " << take << "(xv, " << a.v << "); " << a.v
           << " = bt ? xv : " << a.v << "; " << a.i << " = bt ? (" << ait << ")" << xs[r][1] << " : " << a.i << "; }\n";
@@ -817,18 +852,23 @@ void KernelGen::reduce(Step& s) {
     out_ << "const idx_t cu = c + (idx_t)u * " << span << "u;\n";
     for (auto& [v, pname] : w.preload) out_ << "const auto& " << pname << " = pre_" << ptr_of[v] << "[u];\n";
     // Whole sub-chunk in range: no per-element guard.
+    const bool two_phase = vec > 1 && std::any_of(accs.begin(), accs.end(), [&](const Accum& a) {
+      return is_arg(a) && a.acc_t == "float";
+    });
     out_ << "if (cu + " << vec << "u <= c1) {\n";
+    if (two_phase) two_phase_decl(out_);
     out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
     out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
     out_ << col_digits.str() << elem_body;
-    combine_elem(out_);
+    combine_elem(out_, two_phase);
     out_ << "}\n";
+    if (two_phase) two_phase_finish(out_);
     out_ << "} else if (cu < c1) {\n";
     out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
     out_ << "if (cu + j < c1) {\n";
     out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
     out_ << col_digits.str() << elem_body;
-    combine_elem(out_);
+    combine_elem(out_, false);
     out_ << "}\n}\n}\n";
     out_ << "}\n}\n";
     // Shared slots for the cross-wave step of the block reductions.
@@ -950,7 +990,7 @@ void KernelGen::reduce(Step& s) {
     }
     out_ << "const idx_t lin = " << lin << ";\n";
     out_ << elem_body;
-    combine_elem(out_);
+    combine_elem(out_, false);
     out_ << "}\n";
   }
   // Final: fold in the init values, evaluate the epilogue, store.
