@@ -626,7 +626,33 @@ void KernelGen::loop(Step& s) {
   const int rid = w.add_index(root);
   w.multi_of(rid);  // unused digits are dropped by the compiler
   std::vector<std::string> vals;
-  for (int v : s.outputs) vals.push_back(w.value(v, rid));
+  for (size_t o = 0; o < s.outputs.size(); ++o) {
+    auto ww = s.window_out.find(static_cast<int>(o));
+    vals.push_back(w.value(ww == s.window_out.end() ? s.outputs[o] : ww->second.update, rid));
+  }
+  // Window outputs (fused in-place dynamic_update_slice): clamped starts,
+  // read once per thread.
+  for (auto& [o, ww] : s.window_out) {
+    const Dims& od = prog_.type(ww.operand).dims;
+    for (size_t d = 0; d < ww.starts.size(); ++d) {
+      const int sv = ww.starts[d];
+      std::string e;
+      auto pi = ptr_of.find(sv);
+      if (pi != ptr_of.end()) {
+        e = "(int64_t)" + pi->second + "[0]";
+      } else {
+        const Op* c = nullptr;
+        for (const Op& op : prog_.ops)
+          if (!op.results.empty() && op.results[0] == sv) c = &op;
+        PJRTX_CHECK(c && c->kind == OpKind::kConstant, Code::kInternal, "window start is neither an input nor a constant");
+        e = "(int64_t)(" + literal_expr(prog_, *c, 0) + ")";
+      }
+      const int64_t hi = od[d] - s.loop_shape[d];
+      out_ << "int64_t ws" << o << "_" << d << " = " << e << ";\n";
+      out_ << "ws" << o << "_" << d << " = ws" << o << "_" << d << " < 0 ? 0 : (ws" << o << "_" << d << " > " << hi
+           << " ? " << hi << " : ws" << o << "_" << d << ");\n";
+    }
+  }
   out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
   out_ << "const idx_t lin = full ? base + j : ((base + j < n) ? base + j : n - 1u);\n";
   out_ << w.body.str();
@@ -635,7 +661,23 @@ void KernelGen::loop(Step& s) {
   out_ << "}\n";
   for (size_t o = 0; o < s.outputs.size(); ++o) {
     const DType t = prog_.type(s.outputs[o]).dtype;
-    out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", base, res" << o << ", n, full);\n";
+    auto ww = s.window_out.find(static_cast<int>(o));
+    if (ww == s.window_out.end()) {
+      out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", base, res" << o << ", n, full);\n";
+      continue;
+    }
+    // The thread's vec elements lie in one innermost row of the window
+    // (the window spans that dim, a multiple of vec): one store at the
+    // window position of `base`.
+    const Dims& od = prog_.type(ww->second.operand).dims;
+    out_ << "{ uint32_t rem = base, dst = 0;\n";
+    int64_t stride = 1;
+    for (int d = static_cast<int>(od.size()) - 1; d >= 0; --d) {
+      out_ << "{ const uint32_t c = rem % " << s.loop_shape[d] << "u; rem /= " << s.loop_shape[d] << "u; dst += (c + (uint32_t)ws"
+           << o << "_" << d << ") * " << stride << "u; }\n";
+      stride *= od[d];
+    }
+    out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", dst, res" << o << ", dst + (n - base), full); }\n";
   }
   out_ << "}\n\n";
 }

@@ -171,6 +171,8 @@ class Planner {
   void merge_siblings(std::vector<Step>* steps);
   void merge_epilogues(std::vector<Step>* steps);
   void merge_dot_residuals(std::vector<Step>* steps);
+  void merge_sibling_loops(std::vector<Step>* steps);
+  void absorb_window_updates();
   void fuse_row_chains(std::vector<Step>* steps);
   bool row_uses_ok(const Step& x, const std::set<int>& produced, const Dims& shape, size_t nkept) const;
   void shape_row_fused(Step* s);
@@ -507,6 +509,41 @@ static bool one_pass_gemv(const Program& prog, const Op& op) {
   return M >= 1 && M <= 4 && K % 8 == 0 && N % 8 == 0 && M * K <= 16384 && (N + 63) / 64 >= 32;
 }
 
+// Elementwise steps over the same shape that do not depend on each other
+// become one multi-output kernel (RoPE of q and of k; the cos and sin
+// tables): one launch, and inputs they share are read once per element.
+// A later step joins an earlier one only when all its inputs are produced
+// before that step, so it can run there.
+void Planner::merge_sibling_loops(std::vector<Step>* steps) {
+  constexpr size_t kMaxMergedOutputs = 8;
+  auto v2s = value_to_step(*steps);
+  for (size_t a = 0; a < steps->size(); ++a) {
+    if ((*steps)[a].kind != StepKind::kLoop) continue;
+    for (size_t b = a + 1; b < steps->size(); ++b) {
+      Step& A = (*steps)[a];
+      const Step& B = (*steps)[b];
+      if (B.kind != StepKind::kLoop || B.loop_shape != A.loop_shape ||
+          A.outputs.size() + B.outputs.size() > kMaxMergedOutputs)
+        continue;
+      bool early = true;
+      for (int v : B.inputs) {
+        auto it = v2s.find(v);
+        if (it != v2s.end() && it->second >= static_cast<int>(a)) early = false;
+      }
+      if (!early) continue;
+      std::set<int> ops(A.ops.begin(), A.ops.end());
+      ops.insert(B.ops.begin(), B.ops.end());
+      A.ops.assign(ops.begin(), ops.end());
+      for (int v : B.inputs)
+        if (std::find(A.inputs.begin(), A.inputs.end(), v) == A.inputs.end()) A.inputs.push_back(v);
+      A.outputs.insert(A.outputs.end(), B.outputs.begin(), B.outputs.end());
+      steps->erase(steps->begin() + b);
+      v2s = value_to_step(*steps);
+      --b;
+    }
+  }
+}
+
 // add(dot, x) where the dot's only reader is that add: the dot step writes
 // x + round(dot) directly (the GEMV's epilogue), one launch and one buffer
 // fewer (a residual connection after an output or down projection).
@@ -826,6 +863,99 @@ void Planner::liveness() {
   }
 }
 
+// An in-place dynamic_update_slice whose update has the shape of an earlier
+// elementwise kernel's root is written by that kernel, at the window's
+// clamped offset, instead of by its own launch (a KV-cache row written where
+// RoPE computes it; the value row copied by the same kernel). Requires the
+// window to span the operand's innermost dim (the kernel's vector stores stay
+// in one row) and nothing between the kernel and the update to touch the
+// operand. Release lists are rebuilt afterwards.
+void Planner::absorb_window_updates() {
+  std::vector<Step>& steps = plan_.steps;
+  std::map<int, int> v2s = value_to_step(steps);
+  auto before = [&](int v, size_t j) {  // value available before step j
+    auto it = v2s.find(v);
+    if (it == v2s.end()) return true;  // parameter or resident constant
+    return it->second < static_cast<int>(j);
+  };
+  bool changed = false;
+  for (size_t i = 0; i < steps.size(); ++i) {
+    Step& D = steps[i];
+    if (D.kind != StepKind::kLibrary || D.lib != LibKind::kDynamicUpdateSlice || !D.in_place) continue;
+    const Op& op = prog_.ops[D.lib_op];
+    const int v0 = op.operands[0], u = op.operands[1], r = op.results[0];
+    const TensorType& ut = prog_.type(u);
+    const TensorType& ot = prog_.type(v0);
+    if (ut.rank() == 0 || ut.dims.back() != ot.dims.back() || ut.elements() == 0) continue;
+    std::vector<int> starts(op.operands.begin() + 2, op.operands.end());
+    // The update's buffer, seen through order-preserving view aliases.
+    int src = u;
+    while (v2s.count(src) && steps[v2s[src]].kind == StepKind::kAlias) src = steps[v2s[src]].inputs[0];
+    int target = -1;
+    for (int j = static_cast<int>(i) - 1; j >= 0 && target < 0; --j) {
+      const Step& L = steps[j];
+      // Nothing from j to i may read or write the operand or the result.
+      bool clear = true;
+      for (size_t k = j + 1; k < i && clear; ++k) {
+        for (int v : steps[k].inputs) clear &= v != v0 && v != r;
+        for (int v : steps[k].outputs) clear &= v != v0;
+      }
+      if (!clear) break;
+      if (L.kind != StepKind::kLoop || L.loop_shape != ut.dims || L.window_out.size() >= 2) continue;
+      if (ut.dims.back() % L.vec != 0) continue;
+      const bool own = std::find(L.outputs.begin(), L.outputs.end(), u) != L.outputs.end();
+      bool ok = own || before(src, j);
+      for (int sv : starts) ok &= before(sv, j) || is_splat_constant(prog_, prog_.ops[producer_.at(sv)]);
+      if (ok) target = j;
+    }
+    if (target < 0) continue;
+    Step& L = steps[target];
+    const bool own = std::find(L.outputs.begin(), L.outputs.end(), u) != L.outputs.end();
+    Step::WindowWrite ww;
+    ww.operand = v0;
+    ww.update = own ? u : src;
+    ww.starts = starts;
+    if (!own && std::find(L.inputs.begin(), L.inputs.end(), src) == L.inputs.end()) L.inputs.push_back(src);
+    for (int sv : starts) {
+      auto pi = producer_.find(sv);
+      const bool lit = pi != producer_.end() && is_splat_constant(prog_, prog_.ops[pi->second]);
+      if (!lit && std::find(L.inputs.begin(), L.inputs.end(), sv) == L.inputs.end()) L.inputs.push_back(sv);
+    }
+    L.window_out[static_cast<int>(L.outputs.size())] = ww;
+    L.outputs.push_back(r);
+    // The update no longer needs its own buffer when the DUS was its only reader.
+    if (own && !outputs_.count(u)) {
+      bool read = false;
+      for (size_t k = 0; k < steps.size(); ++k)
+        if (k != i)
+          for (int v : steps[k].inputs) read |= v == u;
+      if (!read) {
+        const int pos = static_cast<int>(std::find(L.outputs.begin(), L.outputs.end(), u) - L.outputs.begin());
+        L.outputs.erase(L.outputs.begin() + pos);
+        std::map<int, Step::WindowWrite> moved;
+        for (auto& [k, w] : L.window_out) moved[k > pos ? k - 1 : k] = w;
+        L.window_out = std::move(moved);
+        mat_.erase(u);
+      }
+    }
+    steps.erase(steps.begin() + i);
+    --i;
+    v2s = value_to_step(steps);
+    changed = true;
+  }
+  if (!changed) return;
+  for (Step& s : steps) s.release_after.clear();
+  std::set<int> persistent(prog_.params.begin(), prog_.params.end());
+  for (int c : plan_.constants) persistent.insert(c);
+  std::map<int, int> last_use;
+  for (size_t i = 0; i < steps.size(); ++i)
+    for (int v : steps[i].inputs) last_use[v] = static_cast<int>(i);
+  for (auto& [v, i] : last_use) {
+    if (persistent.count(v) || outputs_.count(v)) continue;
+    steps[i].release_after.push_back(v);
+  }
+}
+
 void Planner::shape_loop(Step* s) {
   const int64_t n = num_elements(s->loop_shape);
   // 16-byte accesses for the narrowest element touched at the root index.
@@ -902,6 +1032,7 @@ Plan Planner::run() {
   if (opts_.fuse_epilogues) merge_epilogues(&steps);
   if (opts_.dot_residual) merge_dot_residuals(&steps);
   if (opts_.row_fuse_max > 0) fuse_row_chains(&steps);
+  if (opts_.fuse_siblings) merge_sibling_loops(&steps);
   schedule(&steps);
   int kernel_id = 0;
   for (Step& s : steps) {
@@ -919,6 +1050,7 @@ Plan Planner::run() {
   plan_.steps = std::move(steps);
   plan_.num_fusion_kernels = kernel_id;
   liveness();
+  if (opts_.fuse_siblings) absorb_window_updates();
   return std::move(plan_);
 }
 
@@ -972,6 +1104,15 @@ std::string Plan::describe(const Program& prog) const {
     o << "],\"epilogue\":[";
     for (size_t k = 0; k < s.epilogue_ops.size(); ++k) o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.epilogue_ops[k]].kind) << "\"";
     o << "]";
+    if (!s.window_out.empty()) {
+      o << ",\"window_outputs\":[";
+      bool first = true;
+      for (auto& [k, w] : s.window_out) {
+        o << (first ? "" : ",") << "{\"output\":" << s.outputs[k] << ",\"operand\":" << w.operand << "}";
+        first = false;
+      }
+      o << "]";
+    }
     if (s.kind == StepKind::kRowFused)
       o << ",\"phases\":" << s.phases.size() << ",\"rows\":" << s.rows << ",\"row_len\":" << s.row_len
         << ",\"wave_per_row\":" << (s.wave_per_row ? "true" : "false");

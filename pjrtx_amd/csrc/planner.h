@@ -99,6 +99,18 @@ struct Step {
   // kDot: value added to the rounded product (a residual add merged into the
   // dot); the step's output is then the sum, not the dot's own result.
   int dot_add = -1;
+
+  // kLoop: outputs that are dynamic_update_slice results written in place.
+  // Output `outputs[k]` shares the buffer of `operand`; the kernel stores
+  // the update (the value `update`, computed in the kernel or read from
+  // `update` when it is one of the step's inputs) into the window at the
+  // clamped `starts` (scalar values; steps' inputs unless splat constants).
+  struct WindowWrite {
+    int operand = -1;
+    int update = -1;
+    std::vector<int> starts;
+  };
+  std::map<int, WindowWrite> window_out;  // output position -> window write
 };
 
 struct Plan {

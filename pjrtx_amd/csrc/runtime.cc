@@ -433,8 +433,14 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
     case StepKind::kLoop:
     case StepKind::kReduce:
     case StepKind::kRowFused: {
-      if (phase != 1)
-        for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
+      if (phase != 1) {
+        for (size_t k = 0; k < s.outputs.size(); ++k) {
+          auto ww = s.window_out.find(static_cast<int>(k));
+          // A fused in-place dynamic_update_slice result is its operand's buffer.
+          vals[s.outputs[k]] = ww != s.window_out.end() ? vals[ww->second.operand]
+                                                        : dev->allocate(prog_.type(s.outputs[k]).bytes());
+        }
+      }
       if (s.kind == StepKind::kLoop && num_elements(s.loop_shape) == 0) return;
       if ((s.kind == StepKind::kReduce || s.kind == StepKind::kRowFused) && s.rows == 0) return;
       std::vector<void*> ptrs;
