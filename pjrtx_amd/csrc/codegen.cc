@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <set>
 #include <sstream>
@@ -551,6 +552,42 @@ std::string combine_stmt(ReducerKind k, DType t, const std::string& a, const std
 
 std::string arg_better(ReducerKind k) { return k == ReducerKind::kArgMax ? "argmax_better" : "argmin_better"; }
 
+// Wavefront all-reduce of `v` (type `ty`) with the fold `comb(a, b)` (a
+// statement updating a): four DPP exchange steps within rows of 16 lanes,
+// then the four row values read from lanes 0, 16, 32, 48 and folded in a
+// fixed tree. Every lane ends with the same value; the order is fixed, so
+// the result is deterministic.
+std::string wave_allreduce(const std::string& ty, const std::string& v,
+                           const std::function<std::string(const std::string&, const std::string&)>& comb) {
+  std::ostringstream o;
+  o << "{ " << ty << " o_;\n";
+  for (const char* c : {"kDppXor1", "kDppXor2", "kDppHalfMirror", "kDppMirror"})
+    o << "o_ = dpp_move<" << c << ">(" << v << "); " << comb(v, "o_") << "\n";
+  o << ty << " w1_ = lane_value(" << v << ", 16), w2_ = lane_value(" << v << ", 32), w3_ = lane_value(" << v << ", 48);\n";
+  o << v << " = lane_value(" << v << ", 0);\n";
+  o << comb(v, "w1_") << " " << comb("w2_", "w3_") << " " << comb(v, "w2_") << "\n}\n";
+  return o.str();
+}
+
+// The same for an argmax/argmin (value, index) pair under its comparator.
+std::string wave_allreduce_arg(ReducerKind k, const std::string& ity, const std::string& v, const std::string& i) {
+  const std::string better = arg_better(k);
+  std::ostringstream o;
+  auto take = [&](const std::string& av, const std::string& ai, const std::string& bv, const std::string& bi) {
+    return "if (" + better + "(" + bv + ", " + bi + ", " + av + ", " + ai + ")) { " + av + " = " + bv + "; " + ai + " = " + bi +
+           "; }";
+  };
+  o << "{ float ov_; " << ity << " oi_;\n";
+  for (const char* c : {"kDppXor1", "kDppXor2", "kDppHalfMirror", "kDppMirror"})
+    o << "ov_ = dpp_move<" << c << ">(" << v << "); oi_ = dpp_move<" << c << ">(" << i << "); " << take(v, i, "ov_", "oi_")
+      << "\n";
+  o << "float w1v_ = lane_value(" << v << ", 16), w2v_ = lane_value(" << v << ", 32), w3v_ = lane_value(" << v << ", 48);\n";
+  o << ity << " w1i_ = lane_value(" << i << ", 16), w2i_ = lane_value(" << i << ", 32), w3i_ = lane_value(" << i << ", 48);\n";
+  o << v << " = lane_value(" << v << ", 0); " << i << " = lane_value(" << i << ", 0);\n";
+  o << take(v, i, "w1v_", "w1i_") << " " << take("w2v_", "w2i_", "w3v_", "w3i_") << " " << take(v, i, "w2v_", "w2i_") << "\n}\n";
+  return o.str();
+}
+
 class KernelGen {
  public:
   KernelGen(const Program& prog, std::ostringstream& out) : prog_(prog), out_(out) {}
@@ -799,11 +836,18 @@ void KernelGen::reduce(Step& s) {
       const std::string st = dtype_storage_ctype(t);
       const std::string name = "pre_" + ptr_of[v];
       pre_decl << st << " " << name << "[" << unroll << "][" << vec << "];\n";
+      // row_len and chunk are multiples of vec, so a sub-chunk lies wholly
+      // inside or wholly outside [c0, c1): whole 16-byte loads only.
       pre_load << "ldv<" << st << ", " << vec << ">(" << name << "[u], " << ptr_of[v] << ", row * " << s.row_len
-               << "u + cu, row * " << s.row_len << "u + c1, cu + " << vec << "u <= c1);\n";
+               << "u + cu, 0u, true);\n";
       w.preload[v] = "P_" + ptr_of[v];
     }
+    if (s.row_len % vec != 0 || s.chunk % vec != 0)
+      fail(Code::kInternal, "reduce kernel: row length and chunk must be multiples of the vector width");
   }
+  // f32 sums of f16 values (JAX's f16 sum: convert f16->f32, add) fold each
+  // element with one mixed-precision FMA on the f16 value (add_f16v).
+  std::vector<bool> f16_sum(s.reduces.size(), false);
   for (size_t r = 0; r < s.reduces.size(); ++r) {
     const ReduceSpec& rs = s.reduces[r];
     for (int v : rs.inputs) {
@@ -811,12 +855,17 @@ void KernelGen::reduce(Step& s) {
       // running max/min is kept on the unconverted value and rounded once in
       // the final step (which rounds to the result type anyway).
       const bool mm = rs.kind == ReducerKind::kMax || rs.kind == ReducerKind::kMin;
+      const bool sum32 = rs.kind == ReducerKind::kSum && rs.inputs.size() == 1 && prog_.type(v).dtype == DType::kF32;
       int src = v;
       for (const Op& op : prog_.ops) {
-        if (!mm || op.results.empty() || op.results[0] != v || op.kind != OpKind::kConvert) continue;
+        if (op.results.empty() || op.results[0] != v || op.kind != OpKind::kConvert) continue;
         const DType from = prog_.type(op.operands[0]).dtype, to = prog_.type(v).dtype;
         const bool f32ish = [](DType t) { return t == DType::kF32 || t == DType::kF16 || t == DType::kBF16; }(from);
-        if (f32ish && (to == DType::kF32 || to == DType::kF16 || to == DType::kBF16)) src = op.operands[0];
+        if (mm && f32ish && (to == DType::kF32 || to == DType::kF16 || to == DType::kBF16)) src = op.operands[0];
+        if (sum32 && from == DType::kF16) {
+          src = op.operands[0];
+          f16_sum[r] = true;
+        }
       }
       xs[r].push_back(w.value(src, rid));
     }
@@ -829,25 +878,40 @@ void KernelGen::reduce(Step& s) {
     if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
       out_ << ait << " " << a.i << " = " << aimax << ";\n";
   }
-  // In-thread update. A thread visits its elements by increasing index, so
-  // the in-order forms (argmax_take, max_seq, min_seq) give the same result
-  // as the full pair comparator with fewer instructions.
+  // In-thread update. A thread visits its elements by increasing column, so
+  // when the index operand is the column the in-order forms (argmax_take,
+  // max_seq, min_seq) give the same result as the full pair comparator with
+  // fewer instructions; any other index operand folds with the comparator.
+  // An index operand that is an iota along the one reduced dimension is the
+  // column itself (the deferred scan below recomputes it instead of keeping
+  // it).
+  std::vector<bool> idx_is_col(s.reduces.size(), false);
+  for (size_t r = 0; r < s.reduces.size(); ++r) {
+    const ReduceSpec& rs = s.reduces[r];
+    if (rs.inputs.size() != 2 || red_dims.size() != 1) continue;
+    for (const Op& op : prog_.ops)
+      if (!op.results.empty() && op.results[0] == rs.inputs[1] && op.kind == OpKind::kIota && is_red(static_cast<int>(op.dim)) &&
+          prog_.type(rs.inputs[1]).dims == shape && !dtype_is_float(prog_.type(rs.inputs[1]).dtype))
+        idx_is_col[r] = true;
+  }
+  auto is_arg = [](const Accum& a) { return a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin; };
+  // Float-valued argmax/argmin: the two-phase and deferred folds apply.
+  auto fast_arg = [&](size_t r) { return is_arg(accs[r]) && accs[r].acc_t == "float"; };
   // Whole vec-element sub-chunks of the row schedule fold an argmax in two
   // phases: the sub-chunk's max (IEEE maximum, NaN propagating; two new
   // values per instruction), then the first element equal to it (or the
   // first NaN) found by a backward scan, merged into the running pair with
   // the in-order rule. Same winner and value bits as the element-wise fold.
-  auto is_arg = [](const Accum& a) { return a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin; };
   auto two_phase_decl = [&](std::ostream& o) {
     for (size_t r = 0; r < accs.size(); ++r)
-      if (is_arg(accs[r]))
+      if (fast_arg(r) && idx_is_col[r])
         o << "float xa" << r << "[" << vec << "]; " << ait << " ia" << r << "[" << vec << "]; float mc" << r << " = "
           << (accs[r].kind == ReducerKind::kArgMax ? "-__builtin_inff()" : "__builtin_inff()") << ";\n";
   };
   auto two_phase_finish = [&](std::ostream& o) {
     for (size_t r = 0; r < accs.size(); ++r) {
       const Accum& a = accs[r];
-      if (!is_arg(a)) continue;
+      if (!fast_arg(r) || !idx_is_col[r]) continue;
       const char* take = a.kind == ReducerKind::kArgMax ? "argmax_take" : "argmin_take";
       const std::string R = std::to_string(r);
       o << "{ float sv = mc" << R << "; " << ait << " si = 0;\n";
@@ -864,19 +928,123 @@ void KernelGen::reduce(Step& s) {
         << " = bt ? si : " << a.i << "; }\n";
     }
   };
-  auto combine_elem = [&](std::ostream& o, bool two_phase) {
+  // Single-pass row schedule (each thread's share fits one unrolled pass)
+  // defers the argmax index entirely: the pass keeps the values in registers
+  // and folds only the IEEE maximum of each vec-element sub-chunk (shared
+  // with a max over the same values). Each wavefront then finds its own
+  // winner with no barrier: its maximum m (NaN if any lane saw one); with
+  // the column as index, the first sub-chunk u (in column order: u, then
+  // lane) whose maximum is m, found by one ballot per u, then that lane's
+  // first element equal to m (or first NaN). Any other index operand scans
+  // every element for the lowest index among those equal to m, then takes
+  // the wavefront's lowest (all of them tie on value). The winner is the
+  // comparator's (NaN first, then the larger value, ties to the lower index)
+  // with that element's value bits; the wavefront winners meet in the block
+  // step.
+  auto ident = [&](size_t r) {
+    return accs[r].kind == ReducerKind::kArgMax || accs[r].kind == ReducerKind::kMax ? std::string("-__builtin_inff()")
+                                                                                      : std::string("__builtin_inff()");
+  };
+  // A float max/min over the same values as a deferred argmax/argmin folds
+  // that argmax's sub-chunk maxima instead of every element.
+  std::vector<int> shares(accs.size(), -1);
+  for (size_t r = 0; r < accs.size(); ++r) {
+    const Accum& a = accs[r];
+    if (a.acc_t != "float" || (a.kind != ReducerKind::kMax && a.kind != ReducerKind::kMin)) continue;
+    for (size_t r2 = 0; r2 < accs.size(); ++r2)
+      if (fast_arg(r2) && xs[r2][0] == xs[r][0] &&
+          (accs[r2].kind == ReducerKind::kArgMax) == (a.kind == ReducerKind::kMax)) {
+        shares[r] = static_cast<int>(r2);
+        break;
+      }
+  }
+  auto deferred_decl = [&](std::ostream& o) {
+    for (size_t r = 0; r < accs.size(); ++r) {
+      if (!fast_arg(r)) continue;
+      o << "float xa" << r << "[" << unroll << "][" << vec << "]; float mu" << r << "[" << unroll << "]; ";
+      if (!idx_is_col[r]) o << ait << " ia" << r << "[" << unroll << "][" << vec << "]; ";
+      o << "\n";
+    }
+  };
+  std::vector<bool> wave_done(accs.size(), false);
+  auto deferred_finish = [&](std::ostream& o, int full_u) {
     for (size_t r = 0; r < accs.size(); ++r) {
       const Accum& a = accs[r];
-      if (two_phase && is_arg(a)) {
+      if (!fast_arg(r)) continue;
+      wave_done[r] = true;
+      const std::string R = std::to_string(r);
+      const char* mx = a.kind == ReducerKind::kArgMax ? "max_r" : "min_r";
+      const std::string span = std::to_string(256 * vec) + "u";
+      o << "{ float bm = mu" << R << "[0];\n";
+      o << "#pragma unroll\nfor (int u = 1; u < " << unroll << "; ++u) bm = " << mx << "(bm, mu" << R << "[u]);\n";
+      o << wave_allreduce("float", "bm", [&](const std::string& x, const std::string& y) {
+        return x + " = " + mx + "(" + x + ", " + y + ");";
+      });
+      o << "const bool bn = bm != bm;\n";
+      o << "const idx_t c = c0 + threadIdx.x * " << vec << "u;\n";
+      if (idx_is_col[r]) {
+        o << "int fu = -1; unsigned long long fm = 0ull;\n";
+        o << "#pragma unroll\nfor (int u = " << unroll - 1 << "; u >= 0; --u) {\n";
+        o << "const bool ok = u < " << full_u << " || c + (idx_t)u * " << span << " < c1;\n";
+        o << "const unsigned long long m = __ballot(ok && (bn ? mu" << R << "[u] != mu" << R << "[u] : mu" << R
+          << "[u] == bm));\n";
+        o << "if (m) { fu = u; fm = m; }\n}\n";
+        o << a.v << " = bm; " << a.i << " = " << aimax << ";\n";
+        o << "if (fm) {\n";
+        o << "const int L = __ffsll(fm) - 1;\n";
+        o << "float sv = bm; int sj = 0;\n";
+        o << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
+        o << "if (u == fu) {\n";
+        o << "#pragma unroll\nfor (int j = " << vec - 1 << "; j >= 0; --j) {\n";
+        o << "const float x = xa" << R << "[u][j]; const bool hit = bn ? x != x : x == bm;\n";
+        o << "sv = hit ? x : sv; sj = hit ? j : sj;\n}\n}\n}\n";
+        o << a.v << " = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), L));\n";
+        o << a.i << " = (" << ait << ")(c0 + ((threadIdx.x & ~63u) + (idx_t)L) * " << vec << "u + (idx_t)fu * " << span
+          << " + (idx_t)__builtin_amdgcn_readlane(sj, L));\n";
+        o << "}\n}\n";
+      } else {
+        o << "float sv = bm; " << ait << " si = " << aimax << ";\n";
+        o << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
+        o << "const bool ok = u < " << full_u << " || c + (idx_t)u * " << span << " < c1;\n";
+        o << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
+        o << "const float x = xa" << R << "[u][j]; const " << ait << " ix = ia" << R << "[u][j];\n";
+        o << "const bool hit = ok && (bn ? x != x : x == bm) && ix < si;\n";
+        o << "sv = hit ? x : sv; si = hit ? ix : si;\n}\n}\n";
+        o << ait << " wi = si;\n";
+        o << wave_allreduce(ait, "wi", [](const std::string& x, const std::string& y) {
+          return x + " = " + y + " < " + x + " ? " + y + " : " + x + ";";
+        });
+        o << a.v << " = wave_value_at(sv, si == wi); " << a.i << " = wi; }\n";
+      }
+    }
+  };
+  // mode 0: element-wise fold; 1: per-sub-chunk two-phase argmax; 2: deferred argmax.
+  auto combine_elem = [&](std::ostream& o, int mode) {
+    for (size_t r = 0; r < accs.size(); ++r) {
+      const Accum& a = accs[r];
+      const char* mx = a.kind == ReducerKind::kArgMax ? "max_r(" : "min_r(";
+      if (mode == 1 && fast_arg(r) && idx_is_col[r]) {
         o << "xa" << r << "[j] = (float)" << xs[r][0] << "; ia" << r << "[j] = (" << ait << ")" << xs[r][1] << "; mc" << r
-          << " = " << (a.kind == ReducerKind::kArgMax ? "max_r(" : "min_r(") << "mc" << r << ", xa" << r << "[j]);\n";
-      } else if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
+          << " = " << mx << "mc" << r << ", xa" << r << "[j]);\n";
+      } else if (mode == 2 && fast_arg(r)) {
+        o << "xa" << r << "[u][j] = (float)" << xs[r][0] << "; ";
+        if (!idx_is_col[r]) o << "ia" << r << "[u][j] = (" << ait << ")" << xs[r][1] << "; ";
+        o << "mu" << r << "[u] = " << mx << "mu" << r << "[u], xa" << r << "[u][j]);\n";
+      } else if (mode == 2 && shares[r] >= 0) {
+        // folded from the sub-chunk maximum after the element loop
+      } else if ((a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) && idx_is_col[r]) {
         const char* take = a.kind == ReducerKind::kArgMax ? "argmax_take" : "argmin_take";
         o << "{ const float xv = (float)" << xs[r][0] << "; const bool bt = " << take << "(xv, " << a.v << "); " << a.v
           << " = bt ? xv : " << a.v << "; " << a.i << " = bt ? (" << ait << ")" << xs[r][1] << " : " << a.i << "; }\n";
+      } else if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) {
+        o << "{ const float xv = (float)" << xs[r][0] << "; const " << ait << " xi = (" << ait << ")" << xs[r][1]
+          << "; if (" << arg_better(a.kind) << "(xv, xi, " << a.v << ", " << a.i << ")) { " << a.v << " = xv; " << a.i
+          << " = xi; } }\n";
       } else if ((a.kind == ReducerKind::kMax || a.kind == ReducerKind::kMin) && a.acc_t == "float") {
         o << a.v << " = " << (a.kind == ReducerKind::kMax ? "max_seq(" : "min_seq(") << a.v << ", (float)(" << xs[r][0]
           << "));\n";
+      } else if (f16_sum[r] && a.acc_t == "float") {
+        o << a.v << " = add_f16v(" << a.v << ", " << xs[r][0] << ");\n";
       } else {
         o << combine_stmt(a.kind, a.vt, a.v, "(" + a.acc_t + ")(" + xs[r][0] + ")") << "\n";
       }
@@ -884,60 +1052,95 @@ void KernelGen::reduce(Step& s) {
   };
   if (s.row_schedule) {
     const int64_t span = 256 * vec;
+    bool any_fast = false, any_two_phase = false;
+    for (size_t r = 0; r < accs.size(); ++r) {
+      any_fast = any_fast || fast_arg(r);
+      any_two_phase = any_two_phase || (fast_arg(r) && idx_is_col[r]);
+    }
+    // chunk <= span * unroll: the loop below would run at most once.
+    const bool single = s.chunk <= span * unroll;
+    const bool deferred = single && vec > 1 && any_fast;
+    const bool two_phase = !deferred && vec > 1 && any_two_phase;
+    // Single pass: the first full_u sub-chunks are in range for every thread
+    // of every split (the shortest split is the last), so they need no guard.
+    int full_u = 0;
+    if (single) {
+      const int64_t min_len = s.row_len - (s.splits - 1) * s.chunk;
+      while (full_u < unroll && full_u * span + span <= min_len) ++full_u;
+    }
     out_ << pre_decl.str();
-    out_ << "for (idx_t c = c0 + threadIdx.x * " << vec << "u; c < c1; c += " << span * unroll << "u) {\n";
+    if (deferred) deferred_decl(out_);
+    if (single)
+      out_ << "{\nconst idx_t c = c0 + threadIdx.x * " << vec << "u;\n";
+    else
+      out_ << "for (idx_t c = c0 + threadIdx.x * " << vec << "u; c < c1; c += " << span * unroll << "u) {\n";
+    // Loads are unconditional (an out-of-range sub-chunk reads the split's
+    // first one and is not folded), so they retire in issue order and each
+    // sub-chunk waits only for its own.
     out_ << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
-    out_ << "const idx_t cu = c + (idx_t)u * " << span << "u;\n";
+    out_ << "const idx_t cu = (u < " << full_u << " || c + (idx_t)u * " << span << "u < c1) ? c + (idx_t)u * " << span
+         << "u : c0;\n";
     out_ << pre_load.str();
     out_ << "}\n";
     out_ << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
     out_ << "const idx_t cu = c + (idx_t)u * " << span << "u;\n";
     for (auto& [v, pname] : w.preload) out_ << "const auto& " << pname << " = pre_" << ptr_of[v] << "[u];\n";
-    // Whole sub-chunk in range: no per-element guard.
-    const bool two_phase = vec > 1 && std::any_of(accs.begin(), accs.end(), [&](const Accum& a) {
-      return is_arg(a) && a.acc_t == "float";
-    });
-    out_ << "if (cu + " << vec << "u <= c1) {\n";
+    out_ << "if (u < " << full_u << " || cu < c1) {\n";
     if (two_phase) two_phase_decl(out_);
+    if (deferred)
+      for (size_t r = 0; r < accs.size(); ++r)
+        if (fast_arg(r)) out_ << "mu" << r << "[u] = " << ident(r) << ";\n";
     out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
     out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
     out_ << col_digits.str() << elem_body;
-    combine_elem(out_, two_phase);
+    combine_elem(out_, deferred ? 2 : two_phase ? 1 : 0);
     out_ << "}\n";
     if (two_phase) two_phase_finish(out_);
-    out_ << "} else if (cu < c1) {\n";
-    out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
-    out_ << "if (cu + j < c1) {\n";
-    out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
-    out_ << col_digits.str() << elem_body;
-    combine_elem(out_, false);
-    out_ << "}\n}\n}\n";
-    out_ << "}\n}\n";
+    if (deferred)
+      for (size_t r = 0; r < accs.size(); ++r)
+        if (shares[r] >= 0)
+          out_ << accs[r].v << " = " << (accs[r].kind == ReducerKind::kMax ? "max_r(" : "min_r(") << accs[r].v << ", mu"
+               << shares[r] << "[u]);\n";
+    out_ << "}\n";
+    if (deferred && full_u < unroll) {
+      out_ << "else {\n";
+      for (size_t r = 0; r < accs.size(); ++r)
+        if (fast_arg(r))
+          out_ << "mu" << r << "[u] = " << ident(r) << ";\n#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) xa" << r
+               << "[u][j] = 0.f;\n";
+      out_ << "}\n";
+    }
+    out_ << "}\n";
+    if (full_u < unroll && w.preload.size() > 0) {
+      out_ << "#pragma unroll\nfor (int u = " << full_u << "; u < " << unroll << "; ++u) {\n";
+      for (auto& [v, pname] : w.preload) out_ << "keep_live(pre_" << ptr_of[v] << "[u]);\n";
+      out_ << "}\n";
+    }
+    out_ << "}\n";
+    if (deferred) deferred_finish(out_, full_u);
     // Shared slots for the cross-wave step of the block reductions.
     for (auto& a : accs) {
       out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[4];\n";
       if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << "__shared__ " << ait << " sm_" << a.i << "[4];\n";
     }
-    // Block reduction: 64-lane xor butterfly, then the 4 wave results are
+    // Block reduction: wavefront all-reduce, then the 4 wave results are
     // combined in wave order by thread 0 (fixed order: deterministic).
-    auto wave_reduce = [&]() {
-      for (auto& a : accs) {
+    auto wave_reduce = [&](bool skip_done) {
+      for (size_t r = 0; r < accs.size(); ++r) {
+        const Accum& a = accs[r];
+        if (skip_done && wave_done[r]) continue;
         const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
-        out_ << "#pragma unroll\nfor (int m = 32; m >= 1; m >>= 1) {\n";
         if (am) {
-          out_ << "const float ov = wave_shfl_xor(" << a.v << ", m);\n";
-          out_ << "const " << ait << " oi = wave_shfl_xor(" << a.i << ", m);\n";
-          out_ << "if (" << arg_better(a.kind) << "(ov, oi, " << a.v << ", " << a.i << ")) { " << a.v << " = ov; " << a.i
-               << " = oi; }\n";
+          out_ << wave_allreduce_arg(a.kind, ait, a.v, a.i);
         } else {
-          out_ << "const " << a.acc_t << " o = wave_shfl_xor(" << a.v << ", m);\n";
-          out_ << combine_stmt(a.kind, a.vt, a.v, "o") << "\n";
+          const ReducerKind k = a.kind;
+          const DType vt = a.vt;
+          out_ << wave_allreduce(a.acc_t, a.v, [&](const std::string& x, const std::string& y) { return combine_stmt(k, vt, x, y); });
         }
-        out_ << "}\n";
       }
     };
     auto block_reduce = [&]() {
-      wave_reduce();
+      wave_reduce(true);
       out_ << "if ((threadIdx.x & 63) == 0) {\n";
       for (auto& a : accs) {
         out_ << "sm_" << a.v << "[threadIdx.x >> 6] = " << a.v << ";\n";
@@ -1008,7 +1211,7 @@ void KernelGen::reduce(Step& s) {
         if (am) out_ << a.i << " = (" << ait << ")slot[" << slots << "u + row * " << s.splits << "u + lane];\n";
         out_ << "}\n";
       }
-      wave_reduce();
+      wave_reduce(false);
       out_ << "if (lane != 0) return;\n";
     } else {
       out_ << "if (threadIdx.x != 0) return;\n";
@@ -1032,7 +1235,7 @@ void KernelGen::reduce(Step& s) {
     }
     out_ << "const idx_t lin = " << lin << ";\n";
     out_ << elem_body;
-    combine_elem(out_, false);
+    combine_elem(out_, 0);
     out_ << "}\n";
   }
   // Final: fold in the init values, evaluate the epilogue, store.
@@ -1238,14 +1441,12 @@ void KernelGen::row_fused(Step& s) {
         out_ << combine_stmt(accs[r].kind, accs[r].vt, accs[r].v, "(" + accs[r].acc_t + ")(" + xs[r] + ")") << "\n";
       out_ << "}\n";
       sweep_close(out_);
-      // Wave butterfly, then every thread folds the 4 wave partials in wave
-      // order (same value in all threads, deterministic).
-      // (xor partners add the same two values, so every lane ends with the
-      // same bits).
+      // Wavefront all-reduce (every lane ends with the same bits), then every
+      // thread folds the 4 wave partials in wave order (deterministic).
       for (auto& a : accs) {
-        out_ << "#pragma unroll\nfor (int m = 32; m >= 1; m >>= 1) {\n";
-        out_ << "const " << a.acc_t << " o = wave_shfl_xor(" << a.v << ", m);\n";
-        out_ << combine_stmt(a.kind, a.vt, a.v, "o") << "\n}\n";
+        const ReducerKind k = a.kind;
+        const DType vt = a.vt;
+        out_ << wave_allreduce(a.acc_t, a.v, [&](const std::string& x, const std::string& y) { return combine_stmt(k, vt, x, y); });
         if (!wpr) out_ << "if ((threadIdx.x & 63) == 0) sm_" << a.v << "[threadIdx.x >> 6] = " << a.v << ";\n";
       }
       if (!wpr) {

@@ -41,6 +41,15 @@ PJRTX_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 PJRTX_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 PJRTX_DEV uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 PJRTX_DEV float round_f16(float f) { return (float)(_Float16)f; }
+// acc + x for an x holding an f16 value: one mixed-precision FMA, x * 1.0 +
+// acc with the f16 operand widened exactly and one f32 rounding, which is
+// the f32 add's result bit for bit in one instruction instead of two.
+PJRTX_DEV float add_f16v(float acc, float x) {
+  const _Float16 h = (_Float16)x;
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(acc));
+  return r;
+}
 
 // Storage <-> compute for each element kind.
 PJRTX_DEV float ld_f32(const float* p, uint32_t i) { return p[i]; }
@@ -80,6 +89,28 @@ PJRTX_DEV void ldv(S (&dst)[N], const S* __restrict__ src, uint32_t base, uint32
   } else {
 #pragma unroll
     for (int j = 0; j < N; ++j) dst[j] = (base + j < n) ? src[base + j] : src[n - 1];
+  }
+}
+
+// Keeps the registers of a load live to this point (an empty asm reading
+// them), so that a load whose other uses sit inside a branch is still issued
+// with the loads before it instead of being moved into that branch.
+template <typename S, int N>
+PJRTX_DEV void keep_live(const S (&a)[N]) {
+  if constexpr (sizeof(a) % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(a) / 4); ++i) {
+      uint32_t w;
+      __builtin_memcpy(&w, reinterpret_cast<const char*>(a) + 4 * i, 4);
+      asm volatile("" ::"v"(w));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      uint32_t w = 0;
+      __builtin_memcpy(&w, &a[i], sizeof(S) < 4 ? sizeof(S) : 4);
+      asm volatile("" ::"v"(w));
+    }
   }
 }
 
@@ -254,4 +285,47 @@ PJRTX_DEV T wave_shfl_xor(T v, int mask) {
   } else {
     return (T)__shfl_xor((int)v, mask, 64);
   }
+}
+
+// DPP lane exchanges within rows of 16 lanes (no LDS round trip): xor 1
+// and xor 2 as quad permutations, then the half-row and row mirrors, which
+// pair each lane with the other half of its 8- (16-) lane group; once the
+// earlier steps made those halves uniform that is the xor 4 (xor 8) partner.
+// After the four steps every row of 16 lanes holds one value; lane_value
+// reads a row's value from a lane (0, 16, 32, 48) into a uniform register.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int kCtrl, typename T>
+PJRTX_DEV T dpp_move(T v) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, kCtrl, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), kCtrl, 0xf, 0xf, false);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+  } else {
+    return (T)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xf, 0xf, false);
+  }
+}
+
+template <typename T>
+PJRTX_DEV T lane_value(T v, int lane) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+  } else {
+    return (T)__builtin_amdgcn_readlane((int)v, lane);
+  }
+}
+
+// `v` of the lowest lane whose `mine` is true, in every lane (some lane's
+// `mine` must be true).
+PJRTX_DEV float wave_value_at(float v, bool mine) {
+  const unsigned long long own = __ballot(mine);
+  return __shfl(v, __ffsll(own) - 1, 64);
 }

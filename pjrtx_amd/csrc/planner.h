@@ -133,7 +133,7 @@ struct PlanOptions {
   int recompute_limit = 24;
   // Target number of workgroups a reduction launch should reach.
   // (environment: PJRTX_REDUCE_TARGET_BLOCKS)
-  int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 1024);
+  int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 512);
   bool fuse_siblings = true;
   bool fuse_epilogues = true;
   // Row chains (reduce -> reduce/loop over the same rows) become one kernel

@@ -109,6 +109,25 @@ Device::~Device() {
 
 void Device::make_current() const { hip_check(hipSetDevice(ordinal_), "hipSetDevice"); }
 
+hipEvent_t Device::take_event() {
+  {
+    std::lock_guard<std::mutex> lk(ev_mu_);
+    if (!ev_free_.empty()) {
+      hipEvent_t e = ev_free_.back();
+      ev_free_.pop_back();
+      return e;
+    }
+  }
+  hipEvent_t e = nullptr;
+  hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+  return e;
+}
+
+void Device::give_event(hipEvent_t e) {
+  std::lock_guard<std::mutex> lk(ev_mu_);
+  ev_free_.push_back(e);
+}
+
 MemRef Device::allocate(size_t bytes) {
   auto m = std::make_shared<DeviceMemory>();
   m->dev = this;
@@ -172,22 +191,52 @@ std::shared_ptr<Event> Event::failed(Code code, const std::string& msg) {
   return e;
 }
 
+// The event is lazy: a hipEventRecord after every execution costs the host
+// more than a kernel launch and stops HIP from batching the launches that
+// follow, and most results are never asked whether they are ready. The
+// hipEvent is recorded when readiness is first asked for; it then marks a
+// stream position at or after this work, and the stream runs in order, so
+// readiness is never reported before the work is done (at worst after some
+// later work too).
 std::shared_ptr<Event> Event::record(Device* dev) {
   auto e = std::shared_ptr<Event>(new Event());
-  dev->make_current();
-  hip_check(hipEventCreateWithFlags(&e->ev_, hipEventDisableTiming), "hipEventCreate");
-  hip_check(hipEventRecord(e->ev_, dev->stream()), "hipEventRecord");
   e->dev_ = dev;
+  e->lazy_ = true;
   return e;
 }
 
+bool Event::materialize_locked() {
+  if (ev_ || !lazy_) return true;
+  dev_->make_current();
+  ev_ = dev_->take_event();
+  const hipError_t r = hipEventRecord(ev_, dev_->stream());
+  if (r != hipSuccess) {
+    done_ = true;
+    code_ = Code::kInternal;
+    msg_ = std::string("hipEventRecord failed: ") + hipGetErrorString(r);
+    return false;
+  }
+  return true;
+}
+
 Event::~Event() {
-  if (ev_) (void)hipEventDestroy(ev_);
+  if (!ev_) return;
+  if (dev_) dev_->give_event(ev_);
+  else (void)hipEventDestroy(ev_);
 }
 
 bool Event::is_ready() {
   std::lock_guard<std::mutex> lk(mu_);
   if (done_) return true;
+  if (lazy_ && !ev_) {
+    // An idle stream has finished this work; otherwise record now.
+    dev_->make_current();
+    if (hipStreamQuery(dev_->stream()) == hipSuccess) {
+      done_ = true;
+      return true;
+    }
+    if (!materialize_locked()) return true;
+  }
   hipError_t q = hipEventQuery(ev_);
   if (q == hipSuccess) {
     done_ = true;
@@ -200,11 +249,14 @@ bool Event::is_ready() {
 }
 
 void Event::await() {
+  hipEvent_t ev = nullptr;
   {
     std::lock_guard<std::mutex> lk(mu_);
     if (done_) return;
+    if (!materialize_locked()) return;
+    ev = ev_;
   }
-  hipError_t e = hipEventSynchronize(ev_);
+  hipError_t e = hipEventSynchronize(ev);
   std::lock_guard<std::mutex> lk(mu_);
   done_ = true;
   if (e != hipSuccess) {

@@ -81,9 +81,15 @@ class Device {
   // While set (graph capture), every block allocate() hands out is also
   // appended here, so the graph that uses it keeps it for its lifetime.
   void set_capture_pins(std::vector<MemRef>* pins) { capture_pins_ = pins; }
+  // Completion events (timing disabled) are reused: an execution records
+  // one, and it returns here when the last Event holding it is destroyed.
+  hipEvent_t take_event();
+  void give_event(hipEvent_t e);
 
  private:
   std::vector<MemRef>* capture_pins_ = nullptr;
+  std::mutex ev_mu_;
+  std::vector<hipEvent_t> ev_free_;
   int ordinal_;
   hipStream_t stream_ = nullptr;
   Allocator alloc_;
@@ -98,7 +104,9 @@ class Event : public std::enable_shared_from_this<Event> {
  public:
   static std::shared_ptr<Event> ready();
   static std::shared_ptr<Event> failed(Code code, const std::string& msg);
-  static std::shared_ptr<Event> record(Device* dev);  // marks the stream's current tail
+  // Marks the stream's current tail. The hipEvent itself is recorded only
+  // when readiness is first asked for (see Event::record).
+  static std::shared_ptr<Event> record(Device* dev);
   ~Event();
   bool is_ready();
   void await();  // blocks until done
@@ -109,9 +117,13 @@ class Event : public std::enable_shared_from_this<Event> {
 
  private:
   Event() = default;
+  // Records the hipEvent of a lazy event (caller holds mu_); false, with the
+  // error stored, if recording failed.
+  bool materialize_locked();
   std::mutex mu_;
   hipEvent_t ev_ = nullptr;
   Device* dev_ = nullptr;
+  bool lazy_ = false;
   bool done_ = false;
   Code code_ = Code::kOk;
   std::string msg_;

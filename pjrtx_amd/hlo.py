@@ -344,10 +344,13 @@ class Builder:
         return self._emit(f"stablehlo.reduce({x.name} init: {init.name}) applies stablehlo.{op} across dimensions = "
                           f"[{d}] : ({x.type}, {init.type}) -> {tensor_type(shape, x.dtype)}", shape, x.dtype)
 
-    def argmax(self, x: T, axis: int, index_dtype: str = "s32", both: bool = True, kind: str = "max"):
+    def argmax(self, x: T, axis: int, index_dtype: str = "s32", both: bool = True, kind: str = "max",
+               idx: T | None = None):
         """Two-operand reduce over (x, iota) with JAX's argmax/argmin
-        comparator (NaN wins, ties -> lowest index). Returns (values, indices)."""
-        idx = self.iota(x.shape, axis, index_dtype)
+        comparator (NaN wins, ties -> lowest index). Returns (values, indices).
+        `idx` replaces the iota as the index operand."""
+        if idx is None:
+            idx = self.iota(x.shape, axis, index_dtype)
         init_v = self.constant(float("-inf") if kind == "max" else float("inf"), x.dtype)
         init_i = self.constant(0, index_dtype)
         shape = tuple(s for i, s in enumerate(x.shape) if i != axis)
