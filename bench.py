@@ -504,7 +504,7 @@ def main() -> int:
     if a.steps is None:
         a.steps = 128 if a.config == "c5" else (20 if heavy else 200)
     if a.warmup is None:
-        a.warmup = 3 if heavy else 10
+        a.warmup = 10
     line = bench_c5(a) if a.config == "c5" else bench_program(a, WORKLOADS[a.config])
     print(json.dumps(line))
     return 0

@@ -84,7 +84,7 @@ def build(jobs: int | None = None, debug: bool = False, verbose: bool = True) ->
         objs = list(ex.map(lambda s: compile_one(s, debug), srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp),
-           "-lhiprtc", "-Wl,--no-undefined", "-Wl,-rpath,/opt/rocm/lib"]
+           "-lhiprtc", "-lhipblaslt", "-Wl,--no-undefined", "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -7,6 +7,7 @@
 // merged; otherwise it is first copied into that canonical layout.
 #include <algorithm>
 
+#include "blaslt.h"
 #include "kernels/dot.h"
 #include "kernels/library.h"
 #include "runtime.h"
@@ -206,6 +207,9 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
       g.ldc = N;
       g.a_batch_stride = a.bs;
       g.b_batch_stride = b.bs;
+      if (batch * M * N * K > 0 && blaslt_wanted(g) &&
+          blaslt_gemm(dev, g, A, B, out, f16, b_kmajor, out_kind == 2 ? 4 : 2))
+        return;
       MemRef bt;
       if (!b_kmajor) {
         // The large-tile kernel takes B K-contiguous: transpose an N-contiguous

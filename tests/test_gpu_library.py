@@ -397,3 +397,41 @@ def test_dot_large_tile_kernel(client, shape, monkeypatch):
         got = fr(out).astype(np.float64)
         scale = np.sqrt(np.mean(want ** 2, axis=-1, keepdims=True))
         assert (np.abs(got - want) / np.maximum(np.abs(want), scale)).max() <= 2e-2
+
+
+_LIBRARY_GEMM_SHAPES = [
+    ("mk,kn", (4096, 512), (512, 4096), None),          # N-contiguous B
+    ("mk,nk", (4096, 384), (4096, 384), None),          # K-contiguous B
+    ("bmk,bkn", (4, 2048, 256), (4, 256, 2048), None),  # strided batches
+    ("mk,kn", (4096, 256), (256, 4096), "f32"),         # f32 output
+]
+
+
+@pytest.mark.parametrize("shape", _LIBRARY_GEMM_SHAPES)
+def test_dot_library_gemm_matches_own_kernels(client, shape, monkeypatch):
+    """Plain products that fill the GPU go to hipBLASLt: same tolerance to the
+    float64 product as the own MFMA kernels (PJRTX_BLASLT=0), and the same
+    bits on every call."""
+    spec, sa, sb, out_dt = shape
+    rng = np.random.default_rng(sum(sa) + sum(sb))
+    a = bf(rng.standard_normal(sa).astype(np.float32))
+    b_ = bf(rng.standard_normal(sb).astype(np.float32))
+    ls, rs = spec.split(",")
+    lb = tuple(i for i, c in enumerate(ls) if c == "b")
+    rb = tuple(i for i, c in enumerate(rs) if c == "b")
+    lc, rc = (ls.index("k"),), (rs.index("k"),)
+    bld = Builder()
+    x, y = bld.param(sa, "bf16"), bld.param(sb, "bf16")
+    t = bld.build([bld.dot_general(x, y, batch=(lb, rb), contract=(lc, rc), out_dtype=out_dt)])
+    want = ops.dot_general_f64(fb(a), fb(b_), lb, rb, lc, rc)
+    exe = client.compile(t)
+    (lib1,) = exe(a, b_, dtypes=["bf16", "bf16"])
+    (lib2,) = exe(a, b_, dtypes=["bf16", "bf16"])
+    np.testing.assert_array_equal(lib1, lib2)
+    monkeypatch.setenv("PJRTX_BLASLT", "0")
+    (own,) = client.compile(t)(a, b_, dtypes=["bf16", "bf16"])
+    for out in (lib1, own):
+        if out_dt == "f32":
+            np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+        else:
+            assert_bf16_close(out, want)
