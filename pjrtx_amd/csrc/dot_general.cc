@@ -102,6 +102,14 @@ MemRef canonicalize(Device* dev, const TensorType& t, const Dims& batch, const D
 
 }  // namespace
 
+// Workgroups of the one-pass GEMV for a single product with N columns.
+int single_wide_tiles(int64_t N) {
+  GemvGroup one;
+  one.count = 1;
+  one.m[0].N = static_cast<int>(N);
+  return gemv_wide_tiles(one);
+}
+
 void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
   const TensorType& lt = prog.type(op.operands[0]);
   const TensorType& rt = prog.type(op.operands[1]);
@@ -158,9 +166,9 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
       b_kmajor = true;
     }
     if ((a_fast || a_copy) && (b_kmajor || b_nmajor) && K % 8 == 0) {
-      if (M <= 8 && batch == 1 && !b_kmajor && !a_copy && gemv_wide_fits(static_cast<int>(M), static_cast<int>(K),
-                                                                           static_cast<int>((N + 63) / 64)) &&
-          N % 8 == 0 && (K == 1 || b.ks % 8 == 0)) {
+      if (M <= 8 && batch == 1 && !b_kmajor && !a_copy && N < (int64_t(1) << 30) &&
+          gemv_wide_fits(static_cast<int>(M), static_cast<int>(K), single_wide_tiles(N)) && N % 8 == 0 &&
+          (K == 1 || b.ks % 8 == 0)) {
         GemvGroup g;
         g.count = 1;
         g.M = static_cast<int>(M);
@@ -172,7 +180,6 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
         g.m[0].N = static_cast<int>(N);
         g.m[0].ldw = b.ks ? b.ks : N;
         g.m[0].ldy = N;
-        g.m[0].tile0 = 0;
         launch_gemv_wide(dev->stream(), g, A, f16);
         return;
       }
@@ -268,8 +275,8 @@ void run_dot_residual(Device* dev, const Program& prog, const Op& op, std::vecto
   const bool ok = lt.rank() == 2 && rt.rank() == 2 && op.lhs_batch.empty() && op.lhs_contract == Dims{1} &&
                   op.rhs_contract == Dims{0} && (lt.dtype == DType::kBF16 || lt.dtype == DType::kF16) &&
                   rt.dtype == lt.dtype && ot.dtype == lt.dtype && lt.dims[1] % 8 == 0 && rt.dims[1] % 8 == 0 &&
-                  aligned16(W) && gemv_wide_fits(static_cast<int>(lt.dims[0]), static_cast<int>(lt.dims[1]),
-                                                 static_cast<int>((rt.dims[1] + 63) / 64));
+                  aligned16(W) && rt.dims[1] < (int64_t(1) << 30) &&
+                  gemv_wide_fits(static_cast<int>(lt.dims[0]), static_cast<int>(lt.dims[1]), single_wide_tiles(rt.dims[1]));
   if (ok) {
     GemvGroup g;
     g.count = 1;
@@ -333,11 +340,12 @@ void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops
     m.N = static_cast<int>(N);
     m.ldw = N;
     m.ldy = N;
-    m.tile0 = tiles;
-    tiles += static_cast<int>((N + 63) / 64);
+  }
+  if (ok) {
+    g.count = static_cast<int>(ops.size());
+    tiles = gemv_wide_tiles(g);
   }
   if (ok && gemv_wide_fits(g.M, g.K, tiles)) {
-    g.count = static_cast<int>(ops.size());
     launch_gemv_wide(dev->stream(), g, X, in_t == DType::kF16);
     return;
   }

@@ -60,7 +60,7 @@ struct GemvMember {
   const void* add = nullptr;
   int N = 0;
   int64_t ldw = 0, ldy = 0;
-  int tile0 = 0;  // first workgroup of this member (64 columns each)
+  int tile0 = 0;  // first workgroup of this member (set by launch_gemv_wide)
 };
 struct GemvGroup {
   int count = 0, M = 1, K = 0;
@@ -68,10 +68,14 @@ struct GemvGroup {
   int out_kind = 0;  // 0 bf16, 1 f16, 2 f32
   GemvMember m[kMaxGemvMembers];
 };
+// Columns per workgroup for a group (32 or 64; environment PJRTX_GEMV_COLS
+// forces one) and the group's workgroup count at that width.
+int gemv_wide_cols(const GemvGroup& g);
+int gemv_wide_tiles(const GemvGroup& g);
 // True when the one-pass kernel applies: M <= 4, M*K <= kGemvWideMaxX and at
-// least 32 workgroups (64 columns each) over the members.
+// least 32 workgroups over the members (gemv_wide_tiles).
 bool gemv_wide_fits(int M, int K, int total_tiles);
-void launch_gemv_wide(hipStream_t s, const GemvGroup& g, const void* X, bool f16);
+void launch_gemv_wide(hipStream_t s, GemvGroup g, const void* X, bool f16);
 
 // Fallback with arbitrary element strides.
 struct FmaGemmParams {

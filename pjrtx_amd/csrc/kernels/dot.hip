@@ -540,26 +540,35 @@ __global__ void __launch_bounds__(256) gemv_reduce(GemvParams p, const float* __
 }
 
 // gemv_wide (W [K][N], N contiguous, one X for up to 4 weights): a
-// 1024-thread workgroup owns 64 columns of one member over the whole K, so
-// no partials and no second launch. Lane (rg, cc) reads 16 bytes of row
-// w*8 + rg + 128*r for r < 8 (eight rows in flight), X comes from LDS; the
-// 8 row groups fold by xor shuffles and the 16 waves through LDS in wave
-// order (deterministic). An optional addend (a residual) is added to the
-// rounded product and rounded again, as the unfused add would.
-constexpr int kWideCols = 64, kWideDepth = 8;
+// 1024-thread workgroup owns kCols (32 or 64) columns of one member over
+// the whole K, so no partials and no second launch. kCols / 8 lanes share a
+// row (16 bytes each); lane (rg, cc) reads row w*RG + rg + 16*RG*r for
+// r < 8 (eight rows in flight, RG = 64 / (kCols / 8) rows per wave), X comes
+// from LDS; the row groups fold by xor shuffles and the 16 waves through LDS
+// in wave order (deterministic). Narrower tiles give a narrow product more
+// workgroups; consecutive narrow tiles (which share cache lines) run on one
+// XCD. An optional addend (a residual) is added to the rounded product and
+// rounded again, as the unfused add would.
+constexpr int kWideDepth = 8;
 
-template <int kM, bool kF16>
+template <int kM, bool kF16, int kCols>
 __global__ void __launch_bounds__(1024) gemv_wide(GemvGroup g, const uint16_t* __restrict__ X) {
+  constexpr int kLanesPerRow = kCols / 8, kRowGroups = 64 / kLanesPerRow, kRowStep = 16 * kRowGroups;
   extern __shared__ float xs[];  // kM * K
-  __shared__ float red[16][kM][kWideCols];
+  __shared__ float red[16][kM][kCols];
+  int t = blockIdx.x;
+  const int tiles = gridDim.x;
+  // Narrow tiles share cache lines with their neighbours: keep neighbours on
+  // one XCD (consecutive workgroup ids go to different XCDs).
+  if (kCols < 64 && tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
   int mi = 0;
 #pragma unroll
   for (int i = 1; i < kMaxGemvMembers; ++i)
-    if (i < g.count && (int)blockIdx.x >= g.m[i].tile0) mi = i;
+    if (i < g.count && t >= g.m[i].tile0) mi = i;
   const GemvMember mb = g.m[mi];
-  const int n0 = ((int)blockIdx.x - mb.tile0) * kWideCols;
+  const int n0 = (t - mb.tile0) * kCols;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int rg = lane >> 3, cc = lane & 7;
+  const int rg = lane / kLanesPerRow, cc = lane % kLanesPerRow;
   const int n = n0 + cc * 8;
   const int K = g.K;
   for (int i = threadIdx.x; i < g.M * K; i += 1024) {
@@ -574,16 +583,16 @@ __global__ void __launch_bounds__(1024) gemv_wide(GemvGroup g, const uint16_t* _
     for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
   const uint16_t* W = static_cast<const uint16_t*>(mb.W);
   if (n < mb.N) {
-    for (int kb = wave * 8 + rg; kb < K; kb += 128 * kWideDepth) {
+    for (int kb = wave * kRowGroups + rg; kb < K; kb += kRowStep * kWideDepth) {
       u32x4 w[kWideDepth];
 #pragma unroll
       for (int r = 0; r < kWideDepth; ++r) {
-        const int k = kb + 128 * r;
+        const int k = kb + kRowStep * r;
         w[r] = k < K ? *reinterpret_cast<const u32x4*>(W + (int64_t)k * mb.ldw + n) : u32x4{0u, 0u, 0u, 0u};
       }
 #pragma unroll
       for (int r = 0; r < kWideDepth; ++r) {
-        const int k = kb + 128 * r;
+        const int k = kb + kRowStep * r;
         if (k < K) {
           const uint16_t* we = reinterpret_cast<const uint16_t*>(&w[r]);
 #pragma unroll
@@ -601,9 +610,8 @@ __global__ void __launch_bounds__(1024) gemv_wide(GemvGroup g, const uint16_t* _
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = acc[m][e];
-      v += __shfl_xor(v, 8);
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+#pragma unroll
+      for (int sh = kLanesPerRow; sh < 64; sh <<= 1) v += __shfl_xor(v, sh);
       acc[m][e] = v;
     }
   if (rg == 0) {
@@ -613,8 +621,8 @@ __global__ void __launch_bounds__(1024) gemv_wide(GemvGroup g, const uint16_t* _
       for (int e = 0; e < 8; ++e) red[wave][m][cc * 8 + e] = acc[m][e];
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < kM * kWideCols; i += 1024) {
-    const int m = i / kWideCols, c = i - m * kWideCols;
+  for (int i = threadIdx.x; i < kM * kCols; i += 1024) {
+    const int m = i / kCols, c = i - m * kCols;
     const int nn = n0 + c;
     if (m >= g.M || nn >= mb.N) continue;
     float v = red[0][m][c];
@@ -827,28 +835,52 @@ void launch_gemv(hipStream_t s, const GemvParams& p, const void* X, const void* 
   check("gemv");
 }
 
+int gemv_wide_cols(const GemvGroup& g) {
+  const int64_t forced = env_int("PJRTX_GEMV_COLS", 0);
+  if (forced == 32 || forced == 64) return static_cast<int>(forced);
+  // Measured per launch (M = 1): 64-column tiles for groups and wide
+  // products (q/k/v 6.5 us, gate/up 11.6 us, lm_head 26 us; 32 columns cost
+  // 3-30% more there); 32-column tiles when 64-column ones would leave fewer
+  // than 64 workgroups (a 5632 x 2048 product: 9.7 us instead of 11.8).
+  int64_t tiles64 = 0;
+  for (int i = 0; i < g.count; ++i) tiles64 += (g.m[i].N + 63) / 64;
+  return tiles64 >= 64 ? 64 : 32;
+}
+
+int gemv_wide_tiles(const GemvGroup& g) {
+  const int cols = gemv_wide_cols(g);
+  int64_t tiles = 0;
+  for (int i = 0; i < g.count; ++i) tiles += (g.m[i].N + cols - 1) / cols;
+  return static_cast<int>(std::min<int64_t>(tiles, int64_t(1) << 30));
+}
+
 bool gemv_wide_fits(int M, int K, int total_tiles) {
   return M >= 1 && M <= 4 && K >= 1 && (int64_t)M * K <= kGemvWideMaxX && total_tiles >= 32;
 }
 
-void launch_gemv_wide(hipStream_t s, const GemvGroup& g, const void* X, bool f16) {
+void launch_gemv_wide(hipStream_t s, GemvGroup g, const void* X, bool f16) {
   PJRTX_CHECK(g.count >= 1 && g.count <= kMaxGemvMembers && g.M >= 1 && g.M <= 4 && (int64_t)g.M * g.K <= kGemvWideMaxX,
               Code::kInternal, "gemv_wide: bad group");
+  const int cols = gemv_wide_cols(g);
   int tiles = 0;
   for (int i = 0; i < g.count; ++i) {
-    PJRTX_CHECK(g.m[i].tile0 == tiles && g.m[i].N % 8 == 0 && g.m[i].ldw % 8 == 0, Code::kInternal,
-                "gemv_wide: bad member layout");
-    tiles += (g.m[i].N + kWideCols - 1) / kWideCols;
+    PJRTX_CHECK(g.m[i].N % 8 == 0 && g.m[i].ldw % 8 == 0, Code::kInternal, "gemv_wide: bad member layout");
+    g.m[i].tile0 = tiles;
+    tiles += (g.m[i].N + cols - 1) / cols;
   }
   const size_t lds = static_cast<size_t>(g.M) * g.K * sizeof(float);
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const dim3 grid(static_cast<unsigned>(tiles)), block(1024);
-#define PJRTX_WIDE(KM)                                                                   \
-  if (f16) hipLaunchKernelGGL((gemv_wide<KM, true>), grid, block, lds, s, g, x);        \
-  else hipLaunchKernelGGL((gemv_wide<KM, false>), grid, block, lds, s, g, x);
-  if (g.M == 1) { PJRTX_WIDE(1) }
-  else if (g.M == 2) { PJRTX_WIDE(2) }
-  else { PJRTX_WIDE(4) }
+#define PJRTX_WIDE(KM, C)                                                                  \
+  if (f16) hipLaunchKernelGGL((gemv_wide<KM, true, C>), grid, block, lds, s, g, x);        \
+  else hipLaunchKernelGGL((gemv_wide<KM, false, C>), grid, block, lds, s, g, x);
+#define PJRTX_WIDE_M(C)             \
+  if (g.M == 1) { PJRTX_WIDE(1, C) } \
+  else if (g.M == 2) { PJRTX_WIDE(2, C) } \
+  else { PJRTX_WIDE(4, C) }
+  if (cols == 32) { PJRTX_WIDE_M(32) }
+  else { PJRTX_WIDE_M(64) }
+#undef PJRTX_WIDE_M
 #undef PJRTX_WIDE
   check("gemv_wide");
 }

@@ -1,4 +1,5 @@
 // Fusion planner implementation. See planner.h for the contract.
+#include "kernels/dot.h"
 #include "planner.h"
 
 #include <algorithm>
@@ -506,7 +507,11 @@ static bool one_pass_gemv(const Program& prog, const Op& op) {
       op.rhs_contract != Dims{0} || l.dtype != r.dtype || (l.dtype != DType::kBF16 && l.dtype != DType::kF16))
     return false;
   const int64_t M = l.dims[0], K = l.dims[1], N = r.dims[1];
-  return M >= 1 && M <= 4 && K % 8 == 0 && N % 8 == 0 && M * K <= 16384 && (N + 63) / 64 >= 32;
+  if (M < 1 || M > 4 || K % 8 != 0 || N % 8 != 0 || N >= (int64_t(1) << 30)) return false;
+  GemvGroup one;
+  one.count = 1;
+  one.m[0].N = static_cast<int>(N);
+  return gemv_wide_fits(static_cast<int>(M), static_cast<int>(K), gemv_wide_tiles(one));
 }
 
 // Elementwise steps over the same shape that do not depend on each other

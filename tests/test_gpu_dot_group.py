@@ -46,6 +46,12 @@ def test_dot_group_matches_oracle_and_single_dots(client, monkeypatch, M, K, Ns,
     steps = json.loads(exe.optimized_program())["steps"]
     assert [s.get("library") for s in steps] == ["dot_group"]
     assert steps[0]["group_size"] == len(Ns)
+    auto = exe(x, *ws, dtypes=[dt] * (1 + len(Ns)))   # the column width the launcher picks
+    for got, w in zip(auto, ws):
+        want = _f64(x, dt) @ _f64(w, dt)
+        assert np.abs(_f64(got, dt) - want).max() <= 2e-2 * np.abs(want).max()
+    # At one forced width the group and each dot alone share the summation order.
+    monkeypatch.setenv("PJRTX_GEMV_COLS", "64")
     outs = exe(x, *ws, dtypes=[dt] * (1 + len(Ns)))
     monkeypatch.setenv("PJRTX_DOT_GROUPS", "0")
     single = client.compile(text)
@@ -56,7 +62,8 @@ def test_dot_group_matches_oracle_and_single_dots(client, monkeypatch, M, K, Ns,
         g = _f64(got, dt)
         assert np.abs(g - want).max() <= 2e-2 * np.abs(want).max()
         # Bit-identical where the dot alone takes the same one-pass kernel
-        # (at least 32 column tiles) or the group falls back to single dots.
+        # (at least 32 tiles of 64 columns) or the group falls back to single
+        # dots.
         if (n // 64 >= 32 and M * K <= 16384) or M * K > 16384:
             np.testing.assert_array_equal(got, ref)
 
