@@ -38,6 +38,9 @@ enum class OpKind {
   kConcatenate, kPad, kDynamicSlice, kDynamicUpdateSlice,
   // reductions and library ops
   kReduce, kDotGeneral, kGather, kScatter,
+  // control flow: regions[0] = cond (state -> pred), regions[1] = body
+  // (state -> state); operands = initial state, results = final state
+  kWhile,
   // stablehlo.custom_call (only known targets pass validation), and the
   // fused attention op that the program rewrite produces from a
   // scaled-dot-product-attention custom call or the unfused pattern.

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstring>
 #include <functional>
+#include <set>
 #include <unordered_map>
 
 #include "ir.h"
@@ -157,6 +158,7 @@ const OpInfo kOpTable[] = {
     {"dot", OpKind::kDotGeneral},
     {"gather", OpKind::kGather},
     {"scatter", OpKind::kScatter},
+    {"while", OpKind::kWhile},
     {"custom_call", OpKind::kCustomCall},
     {"pjrtx.attention", OpKind::kAttention},
     {"return", OpKind::kReturn},
@@ -460,6 +462,8 @@ class Parser {
   void parse_dense(const TensorType& t, Op* op);
   void parse_generic_attrs(const std::string& dict, Op* op);
   void parse_dnums(const std::string& body, Op* op);
+  void inline_region(Region* region, const std::function<int(int)>& outer, int depth);
+  void close_over_captures(Op* op);
   void inline_into(const std::string& fname, const std::vector<int>& args, std::vector<int>* results,
                    std::vector<Op>* out, int depth);
 };
@@ -495,6 +499,7 @@ Program Parser::run() {
   prog_.param_alias = main.param_alias;
   std::vector<int> results;
   inline_into("main", main.params, &results, &prog_.ops, 0);
+  for (Op& op : prog_.ops) close_over_captures(&op);
   prog_.results = results;
   Op ret;
   ret.kind = OpKind::kReturn;
@@ -535,6 +540,7 @@ void Parser::inline_into(const std::string& fname, const std::vector<int>& args,
     }
     Op op = op0;
     for (int& v : op.operands) v = map_val(v);
+    for (Region& r : op.regions) inline_region(&r, map_val, depth);
     if (!is_main) {
       // Fresh result ids so that a function called twice yields distinct values.
       for (int& v : op.results) {
@@ -545,6 +551,66 @@ void Parser::inline_into(const std::string& fname, const std::vector<int>& args,
     }
     out->push_back(std::move(op));
   }
+}
+
+// Values a region reads that it does not define (its own block arguments
+// and op results, nested regions included), in first-use order.
+static void region_free_values(const Region& r, std::set<int>* defined, std::vector<int>* free_vals,
+                               std::set<int>* seen) {
+  for (int v : r.params) defined->insert(v);
+  for (const Op& op : r.ops) {
+    for (int v : op.operands)
+      if (!defined->count(v) && seen->insert(v).second) free_vals->push_back(v);
+    for (const Region& inner : op.regions) region_free_values(inner, defined, free_vals, seen);
+    for (int v : op.results) defined->insert(v);
+  }
+}
+
+// A while reads its regions' captured values as operands after the loop
+// state (op.sizes = {state count}), so that liveness and scheduling see
+// them like any other input; nested whiles first.
+void Parser::close_over_captures(Op* op) {
+  for (Region& r : op->regions)
+    for (Op& inner : r.ops) close_over_captures(&inner);
+  if (op->kind != OpKind::kWhile) return;
+  if (op->regions.size() != 2) error("while needs a cond and a body region");
+  const size_t n_state = op->operands.size();
+  std::set<int> seen;
+  std::vector<int> free_vals;
+  for (const Region& r : op->regions) {
+    std::set<int> defined;
+    region_free_values(r, &defined, &free_vals, &seen);
+  }
+  op->sizes = {static_cast<int64_t>(n_state)};
+  for (int v : free_vals) op->operands.push_back(v);
+}
+
+// Inside a region (a while's cond or body): values captured from the
+// enclosing function are remapped like the function's own, and calls are
+// inlined in place; the region keeps its own return.
+void Parser::inline_region(Region* region, const std::function<int(int)>& outer, int depth) {
+  std::unordered_map<int, int> remap;
+  std::function<int(int)> map_val = [&](int v) {
+    auto r = remap.find(v);
+    return r == remap.end() ? outer(v) : r->second;
+  };
+  std::vector<Op> ops;
+  for (const Op& op0 : region->ops) {
+    if (op0.name.rfind("call:", 0) == 0) {
+      std::vector<int> call_args;
+      for (int v : op0.operands) call_args.push_back(map_val(v));
+      std::vector<int> call_results;
+      inline_into(op0.name.substr(5), call_args, &call_results, &ops, depth + 1);
+      if (call_results.size() != op0.results.size()) error("call result count mismatch for " + op0.name);
+      for (size_t i = 0; i < call_results.size(); ++i) remap[op0.results[i]] = call_results[i];
+      continue;
+    }
+    Op op = op0;
+    for (int& v : op.operands) v = map_val(v);
+    for (Region& r : op.regions) inline_region(&r, map_val, depth);
+    ops.push_back(std::move(op));
+  }
+  region->ops = std::move(ops);
 }
 
 // Donation attributes of an entry argument, as jax.jit(donate_argnums=...)
@@ -1015,6 +1081,36 @@ Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint
     }
     expect("->");
     sig_outputs = type_list_maybe_parens();
+  } else if (op.kind == OpKind::kWhile) {
+    // while(%iterArg = %init, ...) : t, ... cond { ... } do { ... }: the
+    // iteration names are the block arguments of both regions.
+    std::vector<std::string> iter_names;
+    expect("(");
+    if (!try_lit(")")) {
+      do {
+        iter_names.push_back(ssa_name());
+        expect("=");
+        op.operands.push_back(lookup(ssa_name()));
+      } while (try_lit(","));
+      expect(")");
+    }
+    if (peek() == '{') parse_generic_attrs(balanced(), &op);
+    if (!iter_names.empty()) {
+      expect(":");
+      do {
+        sig_outputs.push_back(type());
+      } while (try_lit(","));
+    }
+    if (sig_outputs.size() != iter_names.size()) error("while: state names and types differ in count");
+    std::vector<std::pair<std::string, TensorType>> args;
+    for (size_t i = 0; i < iter_names.size(); ++i) args.emplace_back(iter_names[i], sig_outputs[i]);
+    for (const char* kw : {"cond", "do"}) {
+      if (!try_word(kw)) error(std::string("while: expected '") + kw + "' region");
+      expect("{");
+      Region region;
+      parse_region_body(&region, args);
+      op.regions.push_back(std::move(region));
+    }
   } else {
     if (op.kind == OpKind::kCustomCall) {  // custom_call @target(%a, ...) {attrs} : (...) -> ...
       op.target = symbol();

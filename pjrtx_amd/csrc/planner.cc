@@ -3,6 +3,7 @@
 #include "planner.h"
 
 #include <algorithm>
+#include <cstring>
 #include <cstdio>
 #include <functional>
 #include <queue>
@@ -36,6 +37,7 @@ const char* lib_kind_name(LibKind k) {
     case LibKind::kPad: return "pad";
     case LibKind::kAttention: return "attention";
     case LibKind::kDotGroup: return "dot_group";
+    case LibKind::kWhile: return "while";
   }
   return "?";
 }
@@ -125,7 +127,8 @@ bool is_library(const Op& op) {
   const OpKind k = op.kind;
   return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
          k == OpKind::kDynamicSlice || k == OpKind::kDynamicUpdateSlice ||
-         (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad || k == OpKind::kAttention;
+         (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad || k == OpKind::kAttention ||
+         k == OpKind::kWhile;
 }
 
 LibKind lib_kind_of(OpKind k) {
@@ -138,9 +141,114 @@ LibKind lib_kind_of(OpKind k) {
     case OpKind::kDynamicUpdateSlice: return LibKind::kDynamicUpdateSlice;
     case OpKind::kConcatenate: return LibKind::kConcatenate;
     case OpKind::kPad: return LibKind::kPad;
+    case OpKind::kWhile: return LibKind::kWhile;
     default: return LibKind::kCopy;
   }
 }
+
+namespace {
+
+// The value of a scalar integer constant op.
+bool scalar_int_literal(const Program& prog, const Op& op, int64_t* out) {
+  if (op.kind != OpKind::kConstant || op.results.size() != 1) return false;
+  const TensorType& t = prog.type(op.results[0]);
+  if (t.rank() != 0 || op.literal.size() < dtype_size(t.dtype)) return false;
+  const uint8_t* b = op.literal.data();
+  switch (t.dtype) {
+    case DType::kS8: *out = static_cast<int8_t>(b[0]); return true;
+    case DType::kU8: *out = b[0]; return true;
+    case DType::kS16: { int16_t v; std::memcpy(&v, b, 2); *out = v; return true; }
+    case DType::kU16: { uint16_t v; std::memcpy(&v, b, 2); *out = v; return true; }
+    case DType::kS32: { int32_t v; std::memcpy(&v, b, 4); *out = v; return true; }
+    case DType::kU32: { uint32_t v; std::memcpy(&v, b, 4); *out = v; return true; }
+    case DType::kS64: { int64_t v; std::memcpy(&v, b, 8); *out = v; return true; }
+    default: return false;
+  }
+}
+
+// The integer constant a value holds, looking through the ops of `ops`.
+bool value_int_constant(const Program& prog, const std::vector<Op>& ops, int v, int64_t* out) {
+  for (const Op& op : ops)
+    if (!op.results.empty() && op.results[0] == v) return scalar_int_literal(prog, op, out);
+  return false;
+}
+
+// Iteration count of `while (i CMP bound) { ...; i += step }` when the
+// counter's start, the bound and the step are integer constants (JAX's
+// fori_loop / scan form), else -1. `outer` holds the ops that define the
+// loop's operands.
+int64_t static_trip_count(const Program& prog, const std::vector<Op>& outer, const Op& op) {
+  if (op.regions.size() != 2 || op.sizes.empty()) return -1;
+  const Region& cond = op.regions[0];
+  const Region& body = op.regions[1];
+  const size_t n_state = static_cast<size_t>(op.sizes[0]);
+  // The cond: constants, one compare, and the return of its result.
+  if (cond.ops.empty() || cond.ops.back().kind != OpKind::kReturn || cond.ops.back().operands.size() != 1) return -1;
+  const Op* cmpp = nullptr;
+  for (size_t i = 0; i + 1 < cond.ops.size(); ++i) {
+    const Op& o = cond.ops[i];
+    if (o.kind == OpKind::kConstant) continue;
+    if (o.kind != OpKind::kCompare || cmpp) return -1;
+    cmpp = &o;
+  }
+  if (!cmpp) return -1;
+  const Op& cmp = *cmpp;
+  if (cmp.results.size() != 1 || cmp.results[0] != cond.ops.back().operands[0]) return -1;
+  if (cmp.cmp_dir != CmpDir::kLT && cmp.cmp_dir != CmpDir::kLE && cmp.cmp_dir != CmpDir::kGT &&
+      cmp.cmp_dir != CmpDir::kGE)
+    return -1;
+  // The counter: a state element compared on the left.
+  size_t ci = n_state;
+  for (size_t i = 0; i < n_state; ++i)
+    if (cond.params[i] == cmp.operands[0]) ci = i;
+  if (ci == n_state) return -1;
+  // The bound: a captured constant, or a state element the body passes
+  // through unchanged whose initial value is constant.
+  int64_t bound = 0, start = 0, step = 0;
+  const int bv = cmp.operands[1];
+  bool have_bound = value_int_constant(prog, cond.ops, bv, &bound) || value_int_constant(prog, outer, bv, &bound);
+  if (!have_bound) {
+    const Op& bret = body.ops.back();
+    for (size_t j = 0; j < n_state && !have_bound; ++j)
+      if (cond.params[j] == bv && bret.kind == OpKind::kReturn && j < bret.operands.size() &&
+          bret.operands[j] == body.params[j])
+        have_bound = value_int_constant(prog, outer, op.operands[j], &bound);
+  }
+  if (!have_bound || !value_int_constant(prog, outer, op.operands[ci], &start)) return -1;
+  // The step: the body returns counter + constant (or constant + counter).
+  const Op& ret = body.ops.back();
+  if (ret.kind != OpKind::kReturn || ci >= ret.operands.size()) return -1;
+  const int next = ret.operands[ci];
+  bool have_step = false;
+  for (const Op& o : body.ops) {
+    if (o.results.empty() || o.results[0] != next) continue;
+    if (o.kind != OpKind::kAdd || o.operands.size() != 2) return -1;
+    const int other = o.operands[0] == body.params[ci] ? o.operands[1]
+                      : o.operands[1] == body.params[ci] ? o.operands[0] : -1;
+    if (other < 0) return -1;
+    have_step = value_int_constant(prog, body.ops, other, &step) || value_int_constant(prog, outer, other, &step);
+  }
+  if (!have_step || step == 0) return -1;
+  // Counts of at most 2^31 iterations; the counter must not wrap on the way.
+  const CmpDir d = cmp.cmp_dir;
+  int64_t trips = 0;
+  if (d == CmpDir::kLT || d == CmpDir::kLE) {
+    const int64_t last = d == CmpDir::kLT ? bound - 1 : bound;
+    if (step < 0) return start > last ? 0 : -1;
+    trips = start > last ? 0 : (last - start) / step + 1;
+  } else {
+    const int64_t last = d == CmpDir::kGT ? bound + 1 : bound;
+    if (step > 0) return start < last ? 0 : -1;
+    trips = start < last ? 0 : (start - last) / (-step) + 1;
+  }
+  if (trips > (int64_t(1) << 31)) return -1;
+  const TensorType& ct = prog.type(op.operands[ci]);
+  if (ct.dtype == DType::kS32 && (start + (trips + 1) * step > INT32_MAX || start + (trips + 1) * step < INT32_MIN))
+    return -1;
+  return trips;
+}
+
+}  // namespace
 
 class Planner {
  public:
@@ -414,6 +522,7 @@ void Planner::build_steps(std::vector<Step>* steps) {
       s.lib_op = static_cast<int>(i);
       s.inputs = op.operands;
       s.outputs = op.results;
+      if (op.kind == OpKind::kWhile) s.while_trips = static_trip_count(prog_, prog_.ops, op);
       steps->push_back(std::move(s));
       continue;
     }
@@ -1142,6 +1251,7 @@ std::string Plan::describe(const Program& prog) const {
         if (s.lib == LibKind::kDotGroup) o << ",\"group_size\":" << s.group_ops.size();
         if (s.dot_add >= 0) o << ",\"residual_add\":" << s.dot_add;
       }
+      if (s.lib == LibKind::kWhile) o << ",\"while_trips\":" << s.while_trips;
       if (s.lib == LibKind::kAttention) {  // q.k and p.v over every (query, key) pair
         const Op& d = prog.ops[s.lib_op];
         const TensorType& q = prog.type(d.operands[0]);

@@ -48,7 +48,7 @@ struct ReduceSpec {
 enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused };
 
 enum class LibKind {
-  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup
+  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup, kWhile
 };
 const char* lib_kind_name(LibKind k);
 
@@ -99,6 +99,10 @@ struct Step {
   // kDot: value added to the rounded product (a residual add merged into the
   // dot); the step's output is then the sum, not the dot's own result.
   int dot_add = -1;
+  // kWhile: the iteration count when constants fix it (a counter from a
+  // constant start, compared with a constant bound, advanced by a constant
+  // step), else -1 (the predicate is read every iteration).
+  int64_t while_trips = -1;
 
   // kLoop: outputs that are dynamic_update_slice results written in place.
   // Output `outputs[k]` shares the buffer of `operand`; the kernel stores

@@ -402,8 +402,138 @@ std::vector<char> compile_kernels(const std::string& body, const std::string& ar
 
 // ---------------------------------------------------------------- executable
 
+namespace {
+
+// A while's region as a program of its own: parameters are the loop state
+// (the region's block arguments) then the captured values; results are the
+// region's return operands.
+Program region_program(const Program& prog, const Op& op, int which) {
+  const Region& r = op.regions.at(which);
+  Program sub;
+  sub.module_name = prog.module_name + (which == 0 ? ".while_cond" : ".while_body");
+  sub.values = prog.values;
+  const size_t n_state = op.sizes.empty() ? op.operands.size() : static_cast<size_t>(op.sizes[0]);
+  sub.params = r.params;
+  for (size_t i = n_state; i < op.operands.size(); ++i) sub.params.push_back(op.operands[i]);
+  sub.param_alias.assign(sub.params.size(), -1);
+  for (const Op& o : r.ops) {
+    if (o.kind == OpKind::kReturn) sub.results = o.operands;
+    sub.ops.push_back(o);
+  }
+  PJRTX_CHECK(!sub.ops.empty() && sub.ops.back().kind == OpKind::kReturn, Code::kInvalidArgument,
+              "while region does not end with a return");
+  return sub;
+}
+
+MemRef copy_block(Device* dev, const MemRef& m) {
+  MemRef c = dev->allocate(m->bytes);
+  if (m->bytes)
+    hip_check(hipMemcpyAsync(c->ptr, m->ptr, m->bytes, hipMemcpyDeviceToDevice, dev->stream()), "hipMemcpyAsync(D2D)");
+  return c;
+}
+
+}  // namespace
+
 Executable::Executable(Program prog, Plan plan, std::string fingerprint, std::string name)
-    : prog_(std::move(prog)), plan_(std::move(plan)), fingerprint_(std::move(fingerprint)), name_(std::move(name)) {}
+    : prog_(std::move(prog)), plan_(std::move(plan)), fingerprint_(std::move(fingerprint)), name_(std::move(name)) {
+  for (size_t si = 0; si < plan_.steps.size(); ++si) {
+    const Step& s = plan_.steps[si];
+    if (s.kind != StepKind::kLibrary || s.lib != LibKind::kWhile) continue;
+    const Op& op = prog_.ops.at(s.lib_op);
+    auto w = std::make_unique<WhileLoop>();
+    for (int which = 0; which < 2; ++which) {
+      Program sub = region_program(prog_, op, which);
+      rewrite_program(&sub);
+      Plan sp = make_plan(sub);
+      auto e = std::make_unique<Executable>(std::move(sub), std::move(sp), fingerprint_, name_ + (which ? ".body" : ".cond"));
+      (which == 0 ? w->cond : w->body) = std::move(e);
+    }
+    w->trips = s.while_trips;
+    loops_[si] = std::move(w);
+  }
+}
+
+int64_t Executable::while_trips(size_t si) const {
+  auto it = loops_.find(si);
+  return it == loops_.end() ? -1 : it->second->trips;
+}
+
+std::vector<MemRef> Executable::run_values(Device* dev, const std::vector<MemRef>& args) {
+  PJRTX_CHECK(args.size() == prog_.params.size(), Code::kInternal, "run_values: argument count");
+  Loaded* L = loaded_for(dev);
+  std::vector<MemRef> vals(prog_.values.size());
+  for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i];
+  for (auto& [v, m] : L->constants) vals[v] = m;
+  for (size_t si = 0; si < plan_.steps.size(); ++si) {
+    run_step(L, si, vals);
+    for (int v : plan_.steps[si].release_after) vals[v].reset();
+  }
+  std::vector<MemRef> out;
+  for (int r : prog_.results) {
+    PJRTX_CHECK(vals[r] != nullptr, Code::kInternal, "run_values: result value was not produced");
+    out.push_back(vals[r]);
+  }
+  return out;
+}
+
+// Runs a while step: the loop state lives in device blocks the loop owns.
+// With a constant-fixed count the body runs that many times back to back
+// (no host round trip); otherwise each iteration runs the cond, reads its
+// predicate on the host and stops when it is false (the reference's
+// general while: execution_control_flow_while.zig, which only runs a
+// recognised f32 counter pattern on the device).
+void Executable::run_while(Loaded* L, size_t si, std::vector<MemRef>& vals) {
+  Device* dev = L->dev;
+  const Step& s = plan_.steps[si];
+  const Op& op = prog_.ops.at(s.lib_op);
+  WhileLoop& w = *loops_.at(si);
+  const size_t n = static_cast<size_t>(op.sizes.at(0));
+  std::vector<MemRef> state(n), caps;
+  for (size_t i = 0; i < n; ++i) state[i] = vals[op.operands[i]];
+  for (size_t i = n; i < op.operands.size(); ++i) caps.push_back(vals[op.operands[i]]);
+  auto args_for = [&](const Executable& region) {
+    std::vector<MemRef> a = state;
+    a.insert(a.end(), caps.begin(), caps.end());
+    // A captured value the region writes in place is the caller's, and the
+    // cond must not change the state: those get copies.
+    for (int k : region.plan().written_params)
+      if ((static_cast<size_t>(k) >= n || &region == w.cond.get()) && a[k]) a[k] = copy_block(dev, a[k]);
+    return a;
+  };
+  // The body writes these state blocks in place: each must be the loop's
+  // alone (not the caller's value, a constant or another state slot).
+  auto own_written = [&]() {
+    for (int k : w.body->plan().written_params)
+      if (static_cast<size_t>(k) < n && state[k] && state[k].use_count() > 1) state[k] = copy_block(dev, state[k]);
+  };
+  auto run_body = [&]() {
+    own_written();
+    std::vector<MemRef> next = w.body->run_values(dev, args_for(*w.body));
+    PJRTX_CHECK(next.size() == n, Code::kInternal, "while body returned the wrong number of values");
+    state = std::move(next);
+  };
+  if (w.trips >= 0) {
+    for (int64_t t = 0; t < w.trips; ++t) run_body();
+  } else {
+    for (;;) {
+      std::vector<MemRef> pred = w.cond->run_values(dev, args_for(*w.cond));
+      PJRTX_CHECK(pred.size() == 1 && pred[0]->bytes >= 1, Code::kInternal, "while cond must return one predicate");
+      uint8_t go = 0;
+      hip_check(hipMemcpyAsync(&go, pred[0]->ptr, 1, hipMemcpyDeviceToHost, dev->stream()), "hipMemcpyAsync(pred)");
+      hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+      if (!go) break;
+      run_body();
+    }
+  }
+  // A result that is still one of the operands' blocks (a passed-through
+  // state element, or no iteration at all) gets its own copy.
+  for (size_t i = 0; i < n; ++i) {
+    bool shared = false;
+    for (int v : op.operands) shared = shared || (vals[v] && vals[v].get() == state[i].get());
+    vals[op.results[i]] = shared ? copy_block(dev, state[i]) : state[i];
+  }
+  stats_.library_calls++;
+}
 
 Executable::~Executable() {
   for (auto& [ord, L] : loaded_) {
@@ -474,6 +604,10 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       vals[s.outputs[0]] = vals[s.inputs[0]];
       return;
     case StepKind::kLibrary:
+      if (s.lib == LibKind::kWhile) {
+        run_while(L, si, vals);
+        return;
+      }
       if (s.in_place) {
         vals[s.outputs[0]] = vals[prog_.ops[s.lib_op].operands[0]];
       } else {
@@ -624,6 +758,7 @@ Executable::GraphEntry::~GraphEntry() {
 
 bool Executable::graph_candidate(const std::vector<BufferRef>& args, const std::vector<bool>* donate) const {
   if (env_int("PJRTX_GRAPHS", 1) == 0) return false;
+  if (!loops_.empty()) return false;  // a while reads its predicate on the host
   if (args.empty() || const_cast<Executable*>(this)->graph_state(args[0]->dev->ordinal()).disabled) return false;
   int launches = 0;
   for (const Step& st : plan_.steps) launches += st.kind != StepKind::kAlias;

@@ -176,6 +176,12 @@ class Executable {
   std::vector<double> time_steps(Device* dev, const std::vector<BufferRef>& args, int iters);
   // Kernel name of each launch unit ("lib:<kind>" for library steps).
   std::vector<std::string> unit_names() const;
+  // Runs the plan on device memory: `args` bound to the parameters, one
+  // block per result (a result may be an argument's block). Used for the
+  // regions of a while loop; the caller holds the device's execute lock.
+  std::vector<MemRef> run_values(Device* dev, const std::vector<MemRef>& args);
+  // Iteration count of the while step `si` when constants fix it, else -1.
+  int64_t while_trips(size_t si) const;
 
   const Program& program() const { return prog_; }
   const Plan& plan() const { return plan_; }
@@ -193,8 +199,18 @@ class Executable {
     std::map<int, MemRef> constants;           // value id -> resident buffer
     std::vector<MemRef> scratch;               // per step partials
   };
+  // A while loop's cond and body compiled as programs of their own
+  // (parameters: the loop state, then the values the regions capture), and
+  // its iteration count when constants fix it (-1 otherwise).
+  struct WhileLoop {
+    std::unique_ptr<Executable> cond, body;
+    int64_t trips = -1;
+  };
+  void run_while(Loaded* L, size_t si, std::vector<MemRef>& vals);
+
   Program prog_;
   Plan plan_;
+  std::map<size_t, std::unique_ptr<WhileLoop>> loops_;
   std::string fingerprint_, name_;
   std::vector<char> code_;
   std::mutex mu_;

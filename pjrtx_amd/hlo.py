@@ -381,6 +381,37 @@ class Builder:
         self.lines.extend(body)
         return T(f"{name}#0", shape, x.dtype), T(f"{name}#1", shape, index_dtype)
 
+    def while_loop(self, state: list[T], cond_fn, body_fn) -> list[T]:
+        """stablehlo.while in the pretty form jax.jit prints for lax.while_loop
+        / fori_loop: `cond_fn(*args)` returns a pred scalar, `body_fn(*args)`
+        the next state (same types). Values built before the loop may be
+        used inside (captured)."""
+        base = self._fresh()[1:]
+        args = [T(f"%iterArg_{base}_{i}", s.shape, s.dtype) for i, s in enumerate(state)]
+        outer = self.lines
+        regions = []
+        for fn in (cond_fn, body_fn):
+            self.lines = []
+            out = fn(*args)
+            out = out if isinstance(out, (list, tuple)) else [out]
+            names = ", ".join(o.name for o in out)
+            types = ", ".join(o.type for o in out)
+            regions.append(self.lines + [f"    stablehlo.return {names} : {types}"])
+        self.lines = outer
+        res = self._fresh()
+        inits = ", ".join(f"{a.name} = {s.name}" for a, s in zip(args, state))
+        types = ", ".join(s.type for s in state)
+        count = f":{len(state)}" if len(state) > 1 else ""
+        self.lines.append(f"    {res}{count} = stablehlo.while({inits}) : {types}")
+        self.lines.append("     cond {")
+        self.lines.extend("  " + line for line in regions[0])
+        self.lines.append("    } do {")
+        self.lines.extend("  " + line for line in regions[1])
+        self.lines.append("    }")
+        if len(state) == 1:
+            return [T(res, state[0].shape, state[0].dtype)]
+        return [T(f"{res}#{i}", s.shape, s.dtype) for i, s in enumerate(state)]
+
     # JAX-level helpers --------------------------------------------------
     def sum(self, x: T, axes) -> T:
         """jnp.sum: f16/bf16 inputs are summed in f32 and converted back."""
