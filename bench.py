@@ -433,6 +433,20 @@ def bench_c5(a) -> dict:
     os.environ.pop("PJRTX_GRAPHS")
     del caches_e
 
+    # All decode steps in one execute: the step inside an on-device while
+    # loop over a constant count (compiled and warmed before timing).
+    looped = client.compile(L.generate_program(cfg, steps))
+    tok_l, _, caches_l = runner.start(prompt)
+    looped.execute_buffers(runner.weights + [tok_l, pos_bufs[0]] + caches_l)[0].block_until_ready()
+    tok_l, _, caches_l = runner.start(prompt)
+    tok_l.block_until_ready()
+    t0 = time.perf_counter()
+    outs_l = looped.execute_buffers(runner.weights + [tok_l, pos_bufs[0]] + caches_l)
+    outs_l[0].block_until_ready()
+    loop_ms = (time.perf_counter() - t0) * 1e3 / steps
+    loop_match = [int(x) for x in outs_l[0].to_numpy()] == tokens[1:]
+    del outs_l, caches_l
+
     plan = json.loads(runner.decode.optimized_program())
     units = launch_units(plan)
     args = runner.weights + [tok, pos_bufs[-1]] + caches
@@ -460,7 +474,8 @@ def bench_c5(a) -> dict:
                    "launch_units_per_step": sum(1 for n in names if n != "-"),
                    "gpu_us_per_step_by_kind": {kk: round(v, 2) for kk, v in sorted(by_kind.items())},
                    "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2), "first_tokens": tokens[:8],
-                   "graph": graph_stats, "eager_ms_per_step": round(eager_ms, 4)},
+                   "graph": graph_stats, "eager_ms_per_step": round(eager_ms, 4),
+                   "one_execute_ms_per_step": round(loop_ms, 4), "one_execute_tokens_match": loop_match},
         "roofline": roofline(units, unit_ms, names, "bf16"),
     }
     if not a.no_cpu_baseline:

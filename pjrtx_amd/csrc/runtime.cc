@@ -415,7 +415,13 @@ Program region_program(const Program& prog, const Op& op, int which) {
   const size_t n_state = op.sizes.empty() ? op.operands.size() : static_cast<size_t>(op.sizes[0]);
   sub.params = r.params;
   for (size_t i = n_state; i < op.operands.size(); ++i) sub.params.push_back(op.operands[i]);
+  // The body may write its state in place (a KV cache updated by a
+  // dynamic_update_slice): the state blocks are donors, and run_while hands
+  // the body only blocks the loop owns alone. Captured values and the
+  // cond's arguments are never written.
   sub.param_alias.assign(sub.params.size(), -1);
+  if (which == 1)
+    for (size_t i = 0; i < n_state; ++i) sub.param_alias[i] = -2;
   for (const Op& o : r.ops) {
     if (o.kind == OpKind::kReturn) sub.results = o.operands;
     sub.ops.push_back(o);

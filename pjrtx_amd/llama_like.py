@@ -256,6 +256,32 @@ def decode_program(cfg: LlamaConfig) -> str:
     return b.build(m.forward(token, b.reshape(pos, (1,)), pos, caches))
 
 
+def generate_program(cfg: LlamaConfig, steps: int) -> str:
+    """`steps` greedy decode steps in one program (a fori_loop: stablehlo.while
+    over a constant count). Arguments: the weights, the token the prefill
+    produced, its position, the caches (donated). Results: the `steps` tokens
+    that follow, then the caches."""
+    b = Builder("jit_llama_generate")
+    m = _Model(b, cfg)
+    token = b.param((1,), "s32")
+    pos0 = b.param((), "s32")
+    caches = [b.param(cache_shape(cfg), "bf16", donate=True) for _ in range(2 * cfg.layers)]
+    outs0 = b.broadcast_in_dim(b.constant(0, "s32"), (steps,), [])
+    n = b.constant(steps, "s32")
+
+    def body(i, tok, *rest):
+        cs, outs = list(rest[:-1]), rest[-1]
+        pos = b.add(pos0, i)
+        res = m.forward(tok, b.reshape(pos, (1,)), pos, cs)
+        nxt, new_caches = res[0], res[2:]
+        outs = b.dynamic_update_slice(outs, nxt, [i])
+        return [b.add(i, b.constant(1, "s32")), nxt] + list(new_caches) + [outs]
+
+    state = [b.constant(0, "s32"), token] + caches + [outs0]
+    final = b.while_loop(state, lambda i, *rest: b.compare("LT", i, n), body)
+    return b.build([final[-1]] + final[2:-1])
+
+
 # ------------------------------------------------------------------ driver
 
 class LlamaRunner:
@@ -290,6 +316,24 @@ class LlamaRunner:
         scalar). The caches are donated; the new ones are returned."""
         outs = self.decode.execute_buffers(self.weights + [token_buf, pos_buf] + caches)
         return outs[0], outs[1], outs[2:]
+
+    def generate_in_one_execute(self, prompt: np.ndarray, new_tokens: int):
+        """Greedy decode as one prefill execute plus one execute of
+        generate_program (all decode steps in an on-device loop). Returns
+        (tokens int32 [new_tokens], timings dict)."""
+        if not hasattr(self, "looped") or self.looped[0] != new_tokens:
+            self.looped = (new_tokens, self.client.compile(generate_program(self.cfg, new_tokens - 1)))
+        pos = self.client.buffer(np.array(len(prompt), np.int32))
+        t0 = time.perf_counter()
+        tok, _, caches = self.start(prompt)
+        tok.block_until_ready()
+        t1 = time.perf_counter()
+        outs = self.looped[1].execute_buffers(self.weights + [tok, pos] + caches)
+        outs[0].block_until_ready()
+        t2 = time.perf_counter()
+        rest = outs[0].to_numpy()
+        toks = np.concatenate([tok.to_numpy().astype(np.int32), rest.astype(np.int32)])
+        return toks, {"prefill_s": t1 - t0, "decode_s": t2 - t1, "decode_steps": new_tokens - 1}
 
     def generate(self, prompt: np.ndarray, new_tokens: int, keep_logits: bool = False):
         """Greedy decode of `new_tokens` tokens after `prompt`. Returns

@@ -143,3 +143,24 @@ def test_full_decode_step_equals_longer_prefill(full, client):
                                [client.buffer(z, "bf16") for _ in range(2 * cfg.layers)])
     a, b = _gpu_logits(step_logits), _gpu_logits(outs[1])
     assert np.abs(a - b).max() <= TOL * np.abs(b).max()
+
+
+def test_tiny_decode_loop_in_one_execute_matches_per_step(tiny):
+    """All decode steps in one execute (stablehlo.while over a constant
+    count) give the same greedy tokens as one execute per step."""
+    runner, _ = tiny
+    cfg = L.TINY
+    prompt = L.prompt_tokens(cfg, seed=3)
+    per_step, _, _ = runner.generate(prompt, cfg.new_tokens)
+    looped, timing = runner.generate_in_one_execute(prompt, cfg.new_tokens)
+    np.testing.assert_array_equal(looped, per_step)
+    assert timing["decode_steps"] == cfg.new_tokens - 1
+
+
+def test_full_decode_loop_in_one_execute_matches_per_step(full):
+    runner, _ = full
+    cfg = L.FULL
+    prompt = L.prompt_tokens(cfg, seed=1)
+    per_step, _, _ = runner.generate(prompt, 16)
+    looped, _ = runner.generate_in_one_execute(prompt, 16)
+    np.testing.assert_array_equal(looped, per_step)

@@ -100,3 +100,10 @@ module @jit_g {
 def test_generic_form_and_call_inside_body():
     step = _plan(GENERIC)["steps"][0]
     assert step["library"] == "while" and step["while_trips"] == 3
+
+
+def test_llama_generate_program_runs_a_fixed_count():
+    from pjrtx_amd import llama_like as L
+    plan = _plan(L.generate_program(L.TINY, 5))
+    loops = [s for s in plan["steps"] if s.get("library") == "while"]
+    assert len(loops) == 1 and loops[0]["while_trips"] == 5
