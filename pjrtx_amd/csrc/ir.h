@@ -41,6 +41,10 @@ enum class OpKind {
   // control flow: regions[0] = cond (state -> pred), regions[1] = body
   // (state -> state); operands = initial state, results = final state
   kWhile,
+  // stablehlo.sort: operands sorted together along `dim` by the comparator
+  // in regions[0]; chlo.top_k: the k largest along the last dim (k in
+  // `sizes[0]`), results (values, s32 indices)
+  kSort, kTopK,
   // stablehlo.custom_call (only known targets pass validation), and the
   // fused attention op that the program rewrite produces from a
   // scaled-dot-product-attention custom call or the unfused pattern.

@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include "runtime.h"
+#include "sort_op.h"
 
 namespace pjrtx {
 
@@ -220,6 +221,9 @@ void run_library_step(Device* dev, const Program& prog, const Step& step, std::v
       return;
     case LibKind::kDotGroup:
       run_dot_group(dev, prog, step.group_ops, vals);
+      return;
+    case LibKind::kSort:
+      run_sort(dev, prog, op, vals);
       return;
     default:
       fail(Code::kUnimplemented, std::string("library op not available: ") + lib_kind_name(step.lib));

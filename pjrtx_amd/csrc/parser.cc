@@ -159,6 +159,8 @@ const OpInfo kOpTable[] = {
     {"gather", OpKind::kGather},
     {"scatter", OpKind::kScatter},
     {"while", OpKind::kWhile},
+    {"sort", OpKind::kSort},
+    {"top_k", OpKind::kTopK},
     {"custom_call", OpKind::kCustomCall},
     {"pjrtx.attention", OpKind::kAttention},
     {"return", OpKind::kReturn},
@@ -461,6 +463,10 @@ class Parser {
   void parse_region_body(Region* region, const std::vector<std::pair<std::string, TensorType>>& args);
   void parse_dense(const TensorType& t, Op* op);
   void parse_generic_attrs(const std::string& dict, Op* op);
+  Op parse_top_k(const std::vector<std::string>& result_names, std::vector<std::string>* out_names);
+  Op parse_composite(const std::vector<std::string>& result_names, std::vector<std::string>* out_names);
+  void bind_results(Op* op, const std::vector<TensorType>& types, const std::vector<std::string>& result_names,
+                    std::vector<std::string>* out_names);
   void parse_dnums(const std::string& body, Op* op);
   void inline_region(Region* region, const std::function<int(int)>& outer, int depth);
   void close_over_captures(Op* op);
@@ -975,6 +981,94 @@ void Parser::parse_dense(const TensorType& t, Op* op) {
   }
 }
 
+void Parser::bind_results(Op* op, const std::vector<TensorType>& types, const std::vector<std::string>& result_names,
+                          std::vector<std::string>* out_names) {
+  std::vector<std::string> names;
+  if (result_names.size() == 1 && types.size() > 1) {
+    for (size_t i = 0; i < types.size(); ++i) names.push_back(result_names[0] + "#" + std::to_string(i));
+  } else {
+    names = result_names;
+  }
+  if (names.size() != types.size()) error("result name count does not match signature");
+  for (size_t i = 0; i < types.size(); ++i) {
+    int id = new_value(types[i], names[i]);
+    bind(names[i], id);
+    op->results.push_back(id);
+  }
+  if (out_names) *out_names = names;
+}
+
+// chlo.top_k(%x, k = K) : tensor<...xN> -> (tensor<...xK>, tensor<...xKxi32>)
+// (reference: stablehlo_topk_import.zig:71-79).
+Op Parser::parse_top_k(const std::vector<std::string>& result_names, std::vector<std::string>* out_names) {
+  Op op;
+  op.kind = OpKind::kTopK;
+  op.name = "chlo.top_k";
+  expect("(");
+  op.operands.push_back(lookup(ssa_name()));
+  expect(",");
+  if (!try_word("k")) error("chlo.top_k: expected 'k = <int>'");
+  expect("=");
+  op.sizes = {integer()};
+  expect(")");
+  if (peek() == '{') balanced();
+  expect(":");
+  if (peek() == '(') {
+    balanced();
+  } else {
+    type();
+  }
+  expect("->");
+  bind_results(&op, type_list_maybe_parens(), result_names, out_names);
+  if (op.results.size() != 2) error("chlo.top_k must have two results");
+  return op;
+}
+
+// stablehlo.composite "name" %a, ... {composite_attributes = {...},
+// decomposition = @f} : (...) -> ...: a top_k composite (name containing
+// "top_k", as stablehlo_topk_import.zig:81-97 recognises) becomes the top_k
+// op with k from the result type; any other composite is a call of its
+// decomposition.
+Op Parser::parse_composite(const std::vector<std::string>& result_names, std::vector<std::string>* out_names) {
+  Op op;
+  const std::string cname = string_lit();
+  std::vector<int> operands;
+  while (peek() == '%') {
+    operands.push_back(lookup(ssa_name()));
+    if (!try_lit(",")) break;
+  }
+  std::string decomposition;
+  if (peek() == '{') {
+    const std::string dict = balanced();
+    const size_t d = dict.find("decomposition");
+    if (d != std::string::npos) {
+      const size_t at = dict.find('@', d);
+      size_t e = at + 1;
+      while (e < dict.size() && (std::isalnum(static_cast<unsigned char>(dict[e])) || dict[e] == '_' ||
+                                 dict[e] == '.' || dict[e] == '$' || dict[e] == '-'))
+        ++e;
+      if (at != std::string::npos) decomposition = dict.substr(at + 1, e - at - 1);
+    }
+  }
+  expect(":");
+  balanced();  // (operand types)
+  expect("->");
+  std::vector<TensorType> rts = type_list_maybe_parens();
+  op.operands = operands;
+  if (cname.find("top_k") != std::string::npos && operands.size() == 1 && rts.size() == 2 &&
+      rts[0].rank() >= 1) {
+    op.kind = OpKind::kTopK;
+    op.name = "chlo.top_k";
+    op.sizes = {rts[0].dims.back()};
+  } else {
+    if (decomposition.empty()) error("stablehlo.composite without a decomposition", Code::kUnimplemented);
+    op.name = "call:" + decomposition;
+  }
+  bind_results(&op, rts, result_names, out_names);
+  if (rts.size() > 1 && op.name.rfind("call:", 0) == 0) bind(result_names[0], op.results[0]);
+  return op;
+}
+
 Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint,
                     std::vector<std::string>* out_names) {
   Op op;
@@ -1019,6 +1113,8 @@ Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint
     if (rts.size() > 1) bind(result_names[0], op.results[0]);
     return op;
   }
+  if (full == "chlo.top_k") return parse_top_k(result_names, out_names);
+  if (full == "stablehlo.composite") return parse_composite(result_names, out_names);
   std::string mnemonic = full;
   if (mnemonic.rfind("stablehlo.", 0) == 0) mnemonic = mnemonic.substr(10);
   else if (mnemonic.rfind("mhlo.", 0) == 0) mnemonic = mnemonic.substr(5);

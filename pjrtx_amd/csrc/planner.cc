@@ -1,6 +1,7 @@
 // Fusion planner implementation. See planner.h for the contract.
 #include "kernels/dot.h"
 #include "planner.h"
+#include "sort_op.h"
 
 #include <algorithm>
 #include <cstring>
@@ -38,6 +39,7 @@ const char* lib_kind_name(LibKind k) {
     case LibKind::kAttention: return "attention";
     case LibKind::kDotGroup: return "dot_group";
     case LibKind::kWhile: return "while";
+    case LibKind::kSort: return "sort";
   }
   return "?";
 }
@@ -128,7 +130,7 @@ bool is_library(const Op& op) {
   return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
          k == OpKind::kDynamicSlice || k == OpKind::kDynamicUpdateSlice ||
          (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad || k == OpKind::kAttention ||
-         k == OpKind::kWhile;
+         k == OpKind::kWhile || k == OpKind::kSort || k == OpKind::kTopK;
 }
 
 LibKind lib_kind_of(OpKind k) {
@@ -142,6 +144,8 @@ LibKind lib_kind_of(OpKind k) {
     case OpKind::kConcatenate: return LibKind::kConcatenate;
     case OpKind::kPad: return LibKind::kPad;
     case OpKind::kWhile: return LibKind::kWhile;
+    case OpKind::kSort:
+    case OpKind::kTopK: return LibKind::kSort;
     default: return LibKind::kCopy;
   }
 }
@@ -523,6 +527,7 @@ void Planner::build_steps(std::vector<Step>* steps) {
       s.inputs = op.operands;
       s.outputs = op.results;
       if (op.kind == OpKind::kWhile) s.while_trips = static_trip_count(prog_, prog_.ops, op);
+      if (s.lib == LibKind::kSort) check_sort_supported(prog_, op);
       steps->push_back(std::move(s));
       continue;
     }

@@ -48,7 +48,7 @@ struct ReduceSpec {
 enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused };
 
 enum class LibKind {
-  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup, kWhile
+  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup, kWhile, kSort
 };
 const char* lib_kind_name(LibKind k);
 

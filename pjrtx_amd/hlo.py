@@ -381,6 +381,53 @@ class Builder:
         self.lines.extend(body)
         return T(f"{name}#0", shape, x.dtype), T(f"{name}#1", shape, index_dtype)
 
+    def sort(self, operands: list[T], dimension: int = -1, direction: str = "LT",
+             compare_type: str | None = None, swap: bool = False) -> list[T]:
+        """stablehlo.sort in the generic form jax.jit prints (jnp.sort,
+        jnp.argsort): operands sorted together by operand 0 under
+        `compare direction, lhs_0, rhs_0` (`swap` compares rhs_0 with lhs_0).
+        compare_type defaults to TOTALORDER for floats, SIGNED/UNSIGNED for
+        integers."""
+        x = operands[0]
+        dim = dimension % len(x.shape)
+        if compare_type is None:
+            if x.dtype in ("f32", "f16", "bf16", "f64"):
+                compare_type = "TOTALORDER"
+            else:
+                compare_type = "UNSIGNED" if x.dtype.startswith("u") or x.dtype == "pred" else "SIGNED"
+        name = self._fresh()
+        b = name[1:]
+        args = []
+        for i, o in enumerate(operands):
+            st = tensor_type((), o.dtype)
+            args += [f"%s{b}_l{i}: {st}", f"%s{b}_r{i}: {st}"]
+        sx = tensor_type((), x.dtype)
+        lhs, rhs = (f"%s{b}_r0", f"%s{b}_l0") if swap else (f"%s{b}_l0", f"%s{b}_r0")
+        ins = ", ".join(o.name for o in operands)
+        in_t = ", ".join(o.type for o in operands)
+        out_t = in_t if len(operands) == 1 else f"({in_t})"
+        res = f"{name}:{len(operands)}" if len(operands) > 1 else name
+        self.lines += [
+            f'    {res} = "stablehlo.sort"({ins}) <{{dimension = {dim} : i64, is_stable = true}}> ({{',
+            f"    ^bb0({', '.join(args)}):",
+            f"      %s{b}_c = stablehlo.compare  {direction}, {lhs}, {rhs},  {compare_type} : ({sx}, {sx}) -> "
+            f"{tensor_type((), 'pred')}",
+            f"      stablehlo.return %s{b}_c : {tensor_type((), 'pred')}",
+            f"    }}) : ({in_t}) -> {out_t}",
+        ]
+        if len(operands) == 1:
+            return [T(name, x.shape, x.dtype)]
+        return [T(f"{name}#{i}", o.shape, o.dtype) for i, o in enumerate(operands)]
+
+    def top_k(self, x: T, k: int) -> tuple[T, T]:
+        """chlo.top_k (lax.top_k): the k largest along the last dim, largest
+        first, and their s32 positions."""
+        name = self._fresh()
+        shape = tuple(x.shape[:-1]) + (k,)
+        vt, it = tensor_type(shape, x.dtype), tensor_type(shape, "s32")
+        self.lines.append(f"    {name}:2 = chlo.top_k({x.name}, k = {k}) : {x.type} -> ({vt}, {it})")
+        return T(f"{name}#0", shape, x.dtype), T(f"{name}#1", shape, "s32")
+
     def while_loop(self, state: list[T], cond_fn, body_fn) -> list[T]:
         """stablehlo.while in the pretty form jax.jit prints for lax.while_loop
         / fori_loop: `cond_fn(*args)` returns a pred scalar, `body_fn(*args)`

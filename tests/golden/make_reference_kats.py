@@ -51,6 +51,11 @@ KATS = {
     "sdpa_grouped_heads": {"q_shape": [1, 4, 2], "kv_shape": [2, 2, 2], "q": [1, 0, 1, 0, 1, 0, 1, 0],
                            "k": [1, 0, 0, 1, 1, 0, 0, 1], "v": [10, 0, 20, 0, 0, 30, 0, 40], "token_index": 0,
                            "expected": [10, 0, 10, 0, 20, 0, 20, 0], "source": "api_test.cc:311-352"},
+    # api_test.cc:2310-2360 — f32 [2,3] sorted along axis 1, its argsort, and
+    # an s32 payload taken along that order
+    "sort_kv": {"input": [[3, 1, 2], [6, 4, 5]], "sorted": [[1, 2, 3], [4, 5, 6]], "order": [[1, 2, 0], [1, 2, 0]],
+                "values": [[10, 11, 12], [20, 21, 22]], "values_sorted": [[11, 12, 10], [21, 22, 20]],
+                "source": "api_test.cc:2310-2360"},
 }
 
 if __name__ == "__main__":
