@@ -14,6 +14,8 @@ BASELINE.json's configs:
   c4s/c4i  configs[3]: Zipf(1.1) scatter-add of [1048576,256] updates into
            [65536,256], f32 / int32
   c5       configs[4]: llama-like greedy decode, tokens/s (a step is one token)
+  topk     lax.top_k(logits, 50) over [64,128256] bf16 (sort row, not a
+           BASELINE config)
   copy     counter calibration stream (not a bench line)
 
 Prints one JSON line: the whole-job rate, the dominant kernel's roofline
@@ -161,6 +163,12 @@ def _c4s(dtype: str):
     return programs.c4_scatter_add(rows, dim, n, dtype), [x, idx, upd], [None, None, None]
 
 
+def _topk():
+    from oracle import ops
+    from pjrtx_amd import programs
+    return programs.topk_logits(64, 128256, 50), [ops.c2_inputs(64, 128256, seed=0)], ["bf16"]
+
+
 # --------------------------------------------------------------- CPU legs
 
 def _cpu_c1(inputs):
@@ -205,6 +213,11 @@ def _cpu_c4s(inputs):
     return (lambda: fn(x, idx[:n], upd[:n])), 1 / 64, "1/64 of the updates, numpy np.add.at in update order"
 
 
+def _cpu_topk(inputs):
+    from oracle import sort
+    return (lambda: sort.top_k(inputs[0], 50, bf16=True)), 1.0, "full workload, numpy oracle (stable argsort)"
+
+
 WORKLOADS = {
     "c2": Workload("argmax2_f16reduce_64x128256_bf16",
                    "two-output argmax over logits [64,128256] bf16 + f16 sum/max/min of logits.astype(f16)",
@@ -224,6 +237,8 @@ WORKLOADS = {
     "c4i": Workload("scatter_add_zipf1.1_1048576x256_into_65536_s32",
                     "operand.at[idx].add(updates), Zipf(1.1) idx, int32 (bit-exact)",
                     lambda: _c4s("s32"), 1073741824 + 4194304 + 2 * 67108864, "int32", cpu=_cpu_c4s),
+    "topk": Workload("top_k50_64x128256_bf16", "lax.top_k(logits, 50), logits [64,128256] bf16 (chlo.top_k)",
+                     _topk, 64 * 128256 * 2 + 64 * 50 * (2 + 4), "bf16", cpu=_cpu_topk),
     # Calibration only (not a bench line): a plain f32 stream of known size
     # whose FETCH_SIZE / WRITE_SIZE readings scale the other workloads' counters.
     "copy": Workload("stream_negate_8192x4096_f32", "out = -x, x [8192,4096] f32 (counter calibration)",

@@ -46,6 +46,7 @@ struct LocalPass {
   uint64_t* dst = nullptr;
   int64_t keep = 0, dst_stride = 0;
   int write_out = 0;
+  int filter = 0;             // sort only the words that can be among the first `keep` (or out_n)
   SortGather g;
 };
 
@@ -76,6 +77,15 @@ __device__ __forceinline__ uint32_t key_image(uint32_t raw, const SortRows& r) {
   return r.descending ? (~img & mask) : img;
 }
 
+// Minimum over the wave's 64 lanes, in every lane (a butterfly of lane swaps).
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint64_t o = __shfl_xor(v, d, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
 template <typename T>
 __device__ __forceinline__ void copy_elem(const void* src, void* dst, int64_t s, int64_t d) {
   static_cast<T*>(dst)[d] = static_cast<const T*>(src)[s];
@@ -104,34 +114,117 @@ __global__ void __launch_bounds__(kLocalThreads) sort_local_kernel(LocalPass p) 
   const int64_t blk = blockIdx.x - row * p.blocks_per_row;
   const int B = p.block;
   const int64_t base = blk * B;
+  // Loads in batches of kBatch per thread, all issued before any is used
+  // (one outstanding load per thread would leave the kernel latency-bound).
+  constexpr int kBatch = 8;
+  const int bd = static_cast<int>(blockDim.x);
   if (p.list) {
     const uint64_t* src = p.list + row * p.list_stride;
-    for (int i = threadIdx.x; i < B; i += blockDim.x) {
-      const int64_t idx = base + i;
-      s[i] = idx < p.list_len ? src[idx] : kSentinel;
+    for (int i0 = 0; i0 < B; i0 += kBatch * bd) {
+      uint64_t w[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int i = i0 + q * bd + static_cast<int>(threadIdx.x);
+        const int64_t idx = base + i;
+        w[q] = (i < B && idx < p.list_len) ? src[idx] : kSentinel;
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int i = i0 + q * bd + static_cast<int>(threadIdx.x);
+        if (i < B) s[i] = w[q];
+      }
     }
   } else {
     const int64_t outer = row / p.r.inner, j = row - outer * p.r.inner;
     const int64_t row0 = outer * p.r.n * p.r.inner + j;
-    for (int i = threadIdx.x; i < B; i += blockDim.x) {
-      const int64_t idx = base + i;
-      uint64_t w = kSentinel;
-      if (idx < p.r.n) {
-        const uint32_t raw = load_key(p.keys, row0 + idx * p.r.inner, p.r.key_bits);
-        w = (static_cast<uint64_t>(key_image(raw, p.r)) << 32) | static_cast<uint64_t>(idx);
+    for (int i0 = 0; i0 < B; i0 += kBatch * bd) {
+      uint32_t raw[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int i = i0 + q * bd + static_cast<int>(threadIdx.x);
+        const int64_t idx = base + i;
+        raw[q] = (i < B && idx < p.r.n) ? load_key(p.keys, row0 + idx * p.r.inner, p.r.key_bits) : 0u;
       }
-      s[i] = w;
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int i = i0 + q * bd + static_cast<int>(threadIdx.x);
+        const int64_t idx = base + i;
+        if (i < B)
+          s[i] = idx < p.r.n ? ((static_cast<uint64_t>(key_image(raw[q], p.r)) << 32) | static_cast<uint64_t>(idx))
+                             : kSentinel;
+      }
     }
   }
   __syncthreads();
-  for (int64_t k = p.k_first; k <= p.k_last; k <<= 1) {
+  int M = B;  // words the network sorts
+  if (p.filter) {
+    // Only the first `need` words are wanted. Each wave takes the r-th
+    // smallest of its lanes' minima (r = need / waves, rounded up): the wave
+    // then holds r distinct words at or below it, so the largest of the
+    // waves' values, T, has at least `need` words at or below it, and every
+    // word below the need-th is <= T. Only the words <= T are sorted.
+    __shared__ uint64_t wave_t[kLocalThreads / 64];
+    __shared__ uint32_t cnt;
+    const int need = static_cast<int>(p.write_out ? p.g.out_n : p.keep);
+    const int waves = bd / 64, wv = static_cast<int>(threadIdx.x) / 64;
+    const int r = (need + waves - 1) / waves;
+    // B is a multiple of the workgroup size (both powers of two, B >= 256),
+    // so `q < nm` is uniform across the workgroup.
+    constexpr int kMine = kSortBlock / kLocalThreads;
+    const int nm = B / bd;
+    uint64_t mine[kMine];
+    uint64_t lo = kSentinel;
+#pragma unroll
+    for (int q = 0; q < kMine; ++q) {
+      if (q < nm) {
+        mine[q] = s[threadIdx.x + q * bd];
+        lo = mine[q] < lo ? mine[q] : lo;
+      }
+    }
+    if (threadIdx.x == 0) cnt = 0;
+    uint64_t t = kSentinel, v = lo;
+    for (int round = 0; round < r; ++round) {
+      t = wave_min_u64(v);
+      const uint64_t owner = __ballot(v == t);  // words are distinct: one lane, or none once all are sentinels
+      if (static_cast<int>(__lane_id()) == __ffsll(static_cast<unsigned long long>(owner)) - 1) v = kSentinel;
+    }
+    if (__lane_id() == 0) wave_t[wv] = t;
+    __syncthreads();
+    uint64_t T = 0;
+    for (int w = 0; w < waves; ++w) T = wave_t[w] > T ? wave_t[w] : T;
+#pragma unroll
+    for (int q = 0; q < kMine; ++q) {
+      if (q >= nm) break;
+      // One LDS atomic per wave: the wave's slots, then each lane's rank.
+      const bool take = mine[q] <= T;
+      const uint64_t mask = __ballot(take);
+      if (mask) {
+        uint32_t base = 0;
+        if (__lane_id() == 0) base = atomicAdd(&cnt, static_cast<uint32_t>(__popcll(mask)));
+        base = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(base)));
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+        if (take) s[base + rank] = mine[q];
+      }
+    }
+    __syncthreads();
+    const int m = static_cast<int>(cnt);
+    M = 2;
+    while (M < m) M <<= 1;
+    for (int i = m + threadIdx.x; i < M; i += bd) s[i] = kSentinel;
+    __syncthreads();
+  }
+  for (int64_t k = p.k_first; k <= (p.filter ? M : p.k_last); k <<= 1) {
+    // Within a block only bit log2(k) of the row position matters: it is the
+    // block's (base & k) when k >= B, else the position's own bit.
+    const bool block_up = !p.global_dir || k < B || (base & k) == 0;
+    const int kb = k < B ? static_cast<int>(k) : 0;
     for (int64_t jj = (k == p.k_first ? p.j_first : k >> 1); jj > 0; jj >>= 1) {
       const int j = static_cast<int>(jj);
-      for (int t = threadIdx.x; t < B / 2; t += blockDim.x) {
+      for (int t = threadIdx.x; t < M / 2; t += blockDim.x) {
         const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
         const int l = i | j;
-        const int64_t ig = p.global_dir ? base + i : i;
-        const bool up = (ig & k) == 0;
+        const bool up = block_up == ((i & kb) == 0);
         const uint64_t a = s[i], b = s[l];
         if ((a > b) == up) {
           s[i] = b;
@@ -236,6 +329,7 @@ void sort_rows(hipStream_t s, const SortRows& r, const void* keys, const SortGat
     p.block = static_cast<int>(pow2_at_least(std::max<int64_t>(r.n, 2)));
     p.k_first = 2, p.k_last = p.block, p.j_first = 1;
     p.write_out = 1;
+    p.filter = 8 * g.out_n <= p.block && p.block >= 256;
     local(s, p, r.rows);
     return;
   }
@@ -248,6 +342,7 @@ void sort_rows(hipStream_t s, const SortRows& r, const void* keys, const SortGat
     p.blocks_per_row = (r.n + kSortBlock - 1) / kSortBlock;
     p.k_first = 2, p.k_last = kSortBlock, p.j_first = 1;
     p.keep = L.kp;
+    p.filter = 8 * L.kp <= kSortBlock;
     p.dst = a;
     p.dst_stride = L.len1;
     local(s, p, r.rows);
@@ -271,6 +366,7 @@ void sort_rows(hipStream_t s, const SortRows& r, const void* keys, const SortGat
     f.k_first = 2, f.k_last = f.block, f.j_first = 1;
     f.dst = nullptr;
     f.write_out = 1;
+    f.filter = 8 * g.out_n <= f.block && f.block >= 256;
     local(s, f, r.rows);
     return;
   }

@@ -119,3 +119,11 @@ def c4_scatter_add(rows: int = 65536, dim: int = 256, n: int = 1048576, dtype: s
     out = b.scatter(x, iv, upd, update_window_dims=[1], inserted_window_dims=[0], scatter_dims_to_operand_dims=[0],
                     index_vector_dim=1, combiner=combiner)
     return b.build([out])
+
+
+def topk_logits(rows: int = 64, vocab: int = 128256, k: int = 50) -> str:
+    """lax.top_k over bf16 logits (sampling's candidate set): chlo.top_k."""
+    b = Builder("jit_topk")
+    logits = b.param((rows, vocab), "bf16")
+    v, i = b.top_k(logits, k)
+    return b.build([v, i])
