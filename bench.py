@@ -412,6 +412,14 @@ def bench_c5(a) -> dict:
     weights = L.init_weights(cfg, seed=0)
     runner = L.LlamaRunner(client, cfg, weights)
     setup_s = time.perf_counter() - t
+    # Weight upload rate (pageable numpy -> HBM, the staged H2D path).
+    t = time.perf_counter()
+    again = [client.buffer(w, "bf16") for w in weights]
+    for wb in again:
+        wb.block_until_ready()
+    upload_s = time.perf_counter() - t
+    upload_bytes = sum(w.nbytes for w in weights)
+    del again
     prompt = L.prompt_tokens(cfg, seed=1)
     p = len(prompt)
     pos_bufs = [client.buffer(np.array(p + i, np.int32)) for i in range(steps)]
@@ -484,7 +492,8 @@ def bench_c5(a) -> dict:
         "data": "synthetic (random-init bf16 weights 0.02*N(0,1) seed 0, random 512-token prompt seed 1)",
         "config": {"workload": "llama_like_decode_8L_d2048_h16x128_ffn5632_v32000_prompt512",
                    "prefill_ms": round(prefill_s * 1e3, 3), "prefill_tokens_per_s": round(p / prefill_s, 1),
-                   "setup_s": round(setup_s, 1), "decode_step_hbm_bytes": step_bytes,
+                   "setup_s": round(setup_s, 1), "weights_upload_ms": round(upload_s * 1e3, 1),
+                   "weights_upload_gbps": round(upload_bytes / upload_s / 1e9, 1), "decode_step_hbm_bytes": step_bytes,
                    "decode_step_gbps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
                    "launch_units_per_step": sum(1 for n in names if n != "-"),
                    "gpu_us_per_step_by_kind": {kk: round(v, 2) for kk, v in sorted(by_kind.items())},

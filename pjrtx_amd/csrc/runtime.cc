@@ -293,8 +293,12 @@ BufferRef buffer_from_host(Device* dev, const TensorType& t, const void* data, c
       }
     }
     dev->make_current();
-    hip_check(hipMemcpyAsync(b->mem->ptr, data, bytes, hipMemcpyHostToDevice, dev->stream()), "hipMemcpyAsync(H2D)");
-    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    if (staged_upload_wanted(bytes)) {
+      staged_upload(dev, b->mem->ptr, data, bytes);
+    } else {
+      hip_check(hipMemcpyAsync(b->mem->ptr, data, bytes, hipMemcpyHostToDevice, dev->stream()), "hipMemcpyAsync(H2D)");
+      hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    }
   }
   b->ready = Event::ready();
   return b;

@@ -139,6 +139,11 @@ struct Buffer {
 using BufferRef = std::shared_ptr<Buffer>;
 
 BufferRef buffer_from_host(Device* dev, const TensorType& t, const void* data, const int64_t* byte_strides);
+
+// Large host-to-device copies through a pinned staging ring on a copy
+// stream (transfer.cc); returns when the data is on the device.
+bool staged_upload_wanted(size_t bytes);
+void staged_upload(Device* dev, void* dst, const void* src, size_t bytes);
 void buffer_to_host(const Buffer& b, void* dst, size_t dst_size);
 
 // hiprtc compile of generated kernel source for the device arch, cached in

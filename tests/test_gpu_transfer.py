@@ -1,0 +1,42 @@
+"""Host-to-device uploads: the direct path (small arrays) and the pinned
+staging ring on its own copy stream (arrays of 64 MiB and more) return the
+host bytes exactly, and an upload into a block that queued device work has
+just released waits for that work (allocation is ordered on the compute
+stream, the staged copy runs on another)."""
+import numpy as np
+import pytest
+
+from pjrtx_amd.hlo import Builder
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape,dtype", [((1000,), np.float32), ((3, 5, 7), np.int8), ((4096, 4096), np.float32),
+                                         ((40 * 2**20 + 3,), np.int16), ((70 * 2**20 + 1,), np.uint8),
+                                         ((9 * 2**20 + 5,), np.float64)])
+def test_upload_roundtrip(client, shape, dtype):
+    rng = np.random.default_rng(1)
+    a = rng.integers(-100, 100, shape).astype(dtype) if np.dtype(dtype).kind in "iu" else \
+        rng.standard_normal(shape).astype(dtype)
+    b = client.buffer(a)
+    np.testing.assert_array_equal(b.to_numpy(), a)
+
+
+def test_staged_upload_waits_for_queued_work(client):
+    n = 64 * 2**20  # 256 MiB of f32: staged
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(n, dtype=np.float32)
+    bld = Builder("jit_sq")
+    p = bld.param((n,), "f32")
+    r = bld.sum(bld.multiply(p, p), [0])
+    exe = client.compile(bld.build([r]))
+    want = float(np.sum(x.astype(np.float64) ** 2))
+    xb = client.buffer(x)
+    for _ in range(3):
+        out = exe.execute_buffers([xb])[0]   # queued, not awaited
+        xb.delete()                          # its block returns to the allocator
+        y = rng.standard_normal(n, dtype=np.float32)
+        xb = client.buffer(y)                # may reuse that block
+        assert abs(float(out.to_numpy()) - want) <= 1e-4 * want
+        np.testing.assert_array_equal(xb.to_numpy(), y)
+        x, want = y, float(np.sum(y.astype(np.float64) ** 2))
