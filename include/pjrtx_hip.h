@@ -56,6 +56,12 @@ PJRTX_HIP_API int pjrtx_hip_synchronize(int device);
  * compile-time half of pjrtx_metalcpp_executable_program_create
  * (metalcpp_api.cc:1296) together with the Zig planner
  * (program_build.zig:10-207). */
+/* Compile-cache counters of this process: compiles that reused a cached
+ * parsed and planned program, compiles that built one, entries held (any
+ * pointer may be NULL). Replaces the reference's executable-cache stats
+ * (src/runtime/executable_cache.zig:9-25, hits / misses / resident_entries). */
+PJRTX_HIP_API int pjrtx_compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries);
+
 PJRTX_HIP_API int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed);
 
 /* As pjrtx_plan_json, and also compiles the generated fusion kernels with

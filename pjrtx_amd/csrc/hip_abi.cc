@@ -116,6 +116,10 @@ int pjrtx_hip_synchronize(int device) {
   });
 }
 
+int pjrtx_compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries) {
+  return guarded([&] { compile_cache_stats(hits, misses, entries); });
+}
+
 int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
   return guarded([&] {
     Program prog = parse_stablehlo(std::string(text, len));

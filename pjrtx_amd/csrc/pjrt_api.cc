@@ -477,13 +477,11 @@ static PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* args) {
                 strformat("pjrtx runs on one device: compile asked for %lld replicas x %lld partitions",
                           static_cast<long long>(replicas), static_cast<long long>(partitions)));
     std::string text(args->program->code, args->program->code_size);
-    Program prog = parse_stablehlo(text);
-    rewrite_program(&prog);
-    PJRTX_CHECK(prog.num_partitions == 1 && prog.num_replicas == 1, Code::kUnimplemented,
+    std::shared_ptr<const CompiledProgram> cp = compile_program_cached(text);
+    PJRTX_CHECK(cp->prog.num_partitions == 1 && cp->prog.num_replicas == 1, Code::kUnimplemented,
                 "pjrtx runs on one device: module asks for more than one partition or replica");
-    Plan plan = make_plan(prog);
-    std::string name = prog.module_name.empty() ? "main" : prog.module_name;
-    auto exe = std::make_shared<Executable>(std::move(prog), std::move(plan), fingerprint_of(text), name);
+    std::string name = cp->prog.module_name.empty() ? "main" : cp->prog.module_name;
+    auto exe = std::make_shared<Executable>(cp->prog, cp->plan, fingerprint_of(text), name);
     PJRT_Device* d0 = args->client->devices.at(0);
     exe->load(d0->dev);  // compile kernels and upload constants now
     auto* le = new PJRT_LoadedExecutable();

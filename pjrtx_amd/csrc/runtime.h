@@ -140,6 +140,15 @@ using BufferRef = std::shared_ptr<Buffer>;
 
 BufferRef buffer_from_host(Device* dev, const TensorType& t, const void* data, const int64_t* byte_strides);
 
+// A program text parsed, rewritten and planned, shared by the compiles of
+// the same text under the same PJRTX_* environment (compile_cache.cc).
+struct CompiledProgram {
+  Program prog;
+  Plan plan;
+};
+std::shared_ptr<const CompiledProgram> compile_program_cached(const std::string& text);
+void compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries);
+
 // Large host-to-device copies through a pinned staging ring on a copy
 // stream (transfer.cc); returns when the data is on the device.
 bool staged_upload_wanted(size_t bytes);

@@ -215,6 +215,7 @@ class Plugin:
             "pjrtx_executable_graph_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_executable_run": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double)],
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
+            "pjrtx_compile_cache_stats": [POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)],
         }.items():
             f = getattr(L, name)
             f.argtypes = argtypes
@@ -290,6 +291,12 @@ class Plugin:
         n = c_int(0)
         self.hip_check(self.lib.pjrtx_hip_device_count(ctypes.byref(n)))
         return n.value
+
+    def compile_cache_stats(self) -> dict:
+        """{"hits", "misses", "entries"} of the process's compile cache."""
+        h, m, e = c_int64(0), c_int64(0), c_int64(0)
+        self.hip_check(self.lib.pjrtx_compile_cache_stats(ctypes.byref(h), ctypes.byref(m), ctypes.byref(e)))
+        return {"hits": h.value, "misses": m.value, "entries": e.value}
 
 
 def plugin() -> Plugin:
