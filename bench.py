@@ -270,7 +270,8 @@ def cpu_baseline(W: Workload, inputs, budget_s: float = 10.0) -> dict:
 
 def launch_units(plan: dict) -> list[dict]:
     """The plan's launch units in the order pjrtx_executable_time_steps
-    reports them (a split reduction is a main and a combine unit), each with
+    reports them (a split reduction with a separate combine kernel is a main
+    and a combine unit), each with
     its algorithmic bytes (the planner's figure: inputs read once + outputs
     written, gathered rows only for a gather, the window only for an in-place
     dynamic_update_slice; 0 for a combine pass, which only reads the partial
@@ -285,7 +286,7 @@ def launch_units(plan: dict) -> list[dict]:
         # unmasked (query, key) pairs.
         units.append({"name": name, "bytes": st["algorithmic_bytes"],
                       "flops": st.get("effective_flops", st.get("flops", 0))})
-        if st["kind"] == "reduce" and st.get("splits", 1) > 1:
+        if st["kind"] == "reduce" and st.get("splits", 1) > 1 and not st.get("fused_combine", False):
             units.append({"name": name + "_combine", "bytes": 0, "flops": 0})
     return units
 

@@ -1177,7 +1177,53 @@ void KernelGen::reduce(Step& s) {
       }
     }
     block_reduce();
-    if (split) {
+    // Fold of a row's partials by one wavefront, lane k reading split k
+    // (wavefront all-reduce over the lanes: a fixed order, so the result does
+    // not depend on which workgroup folds or on the launch).
+    auto fold_partials = [&]() {
+      for (size_t r = 0; r < accs.size(); ++r) {
+        const Accum& a = accs[r];
+        const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
+        out_ << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
+        if (am) out_ << a.i << " = " << aimax << ";\n";
+        out_ << "if (lane < " << s.splits << "u) {\n";
+        out_ << "const uint64_t* slot = reinterpret_cast<const uint64_t*>(scratch + " << offs[r] << "u);\n";
+        out_ << "const uint64_t bits = slot[row * " << s.splits << "u + lane];\n";
+        out_ << "__builtin_memcpy(&" << a.v << ", &bits, sizeof(" << a.v << "));\n";
+        if (am) out_ << a.i << " = (" << ait << ")slot[" << slots << "u + row * " << s.splits << "u + lane];\n";
+        out_ << "}\n";
+      }
+      wave_reduce(false);
+      out_ << "if (lane != 0) return;\n";
+    };
+    if (split && s.fused_combine) {
+      // Thread 0 stores this split's partials, publishes them with a
+      // device-scope release fence and counts the row's arrivals; the
+      // workgroup that arrives last (acquire fence) folds every split of the
+      // row with wavefront 0 and puts the counter back to zero for the next
+      // launch. No workgroup waits for another.
+      out_ << "__shared__ uint32_t last_arrival;\n";
+      out_ << "if (threadIdx.x == 0) {\n";
+      for (size_t r = 0; r < accs.size(); ++r) {
+        const Accum& a = accs[r];
+        out_ << "{ uint64_t* slot = reinterpret_cast<uint64_t*>(scratch + " << offs[r] << "u);\n";
+        out_ << "uint64_t bits = 0; __builtin_memcpy(&bits, &" << a.v << ", sizeof(" << a.v << "));\n";
+        out_ << "slot[row * " << s.splits << "u + split] = bits;\n";
+        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
+          out_ << "slot[" << slots << "u + row * " << s.splits << "u + split] = (uint64_t)" << a.i << ";\n";
+        out_ << "}\n";
+      }
+      out_ << "__threadfence();\n";
+      out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + row;\n";
+      out_ << "const uint32_t last = atomicAdd(ctr, 1u) == " << s.splits - 1 << "u;\n";
+      out_ << "if (last) atomicExch(ctr, 0u);\n";
+      out_ << "last_arrival = last;\n";
+      out_ << "}\n__syncthreads();\n";
+      out_ << "if (!last_arrival || threadIdx.x >= 64) return;\n";
+      out_ << "__threadfence();\n";
+      out_ << "const uint32_t lane = threadIdx.x;\n";
+      fold_partials();
+    } else if (split) {
       // Partials of this split go to scratch with plain stores; the
       // `<name>_combine` kernel (launched next on the same stream) folds
       // them. The kernel boundary publishes the stores, so no per-workgroup
@@ -1201,18 +1247,10 @@ void KernelGen::reduce(Step& s) {
       out_ << "const uint32_t lane = threadIdx.x & 63u;\n";
       for (size_t r = 0; r < accs.size(); ++r) {
         const Accum& a = accs[r];
-        const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
-        out_ << a.acc_t << " " << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
-        if (am) out_ << ait << " " << a.i << " = " << aimax << ";\n";
-        out_ << "if (lane < " << s.splits << "u) {\n";
-        out_ << "const uint64_t* slot = reinterpret_cast<const uint64_t*>(scratch + " << offs[r] << "u);\n";
-        out_ << "const uint64_t bits = slot[row * " << s.splits << "u + lane];\n";
-        out_ << "__builtin_memcpy(&" << a.v << ", &bits, sizeof(" << a.v << "));\n";
-        if (am) out_ << a.i << " = (" << ait << ")slot[" << slots << "u + row * " << s.splits << "u + lane];\n";
-        out_ << "}\n";
+        out_ << a.acc_t << " " << a.v << ";\n";
+        if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << ait << " " << a.i << ";\n";
       }
-      wave_reduce(false);
-      out_ << "if (lane != 0) return;\n";
+      fold_partials();
     } else {
       out_ << "if (threadIdx.x != 0) return;\n";
     }

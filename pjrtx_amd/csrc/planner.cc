@@ -1139,7 +1139,14 @@ void Planner::shape_reduce(Step* s) {
     size_t per_slot = 0;
     for (const ReduceSpec& r : s->reduces) per_slot += (r.kind == ReducerKind::kArgMax || r.kind == ReducerKind::kArgMin) ? 16 : 8;
     s->scratch_bytes = static_cast<size_t>(rows * splits) * per_slot;
-    s->combine_grid = static_cast<uint32_t>((rows + 3) / 4);
+    if (opts_.reduce_fused_combine) {
+      // One 32-bit arrival counter per row after the 8-byte slots.
+      s->fused_combine = true;
+      s->counter_offset = s->scratch_bytes;
+      s->scratch_bytes += static_cast<size_t>(rows) * 4;
+    } else {
+      s->combine_grid = static_cast<uint32_t>((rows + 3) / 4);
+    }
   }
 }
 
@@ -1239,7 +1246,8 @@ std::string Plan::describe(const Program& prog) const {
       o << ",\"reducers\":[";
       for (size_t k = 0; k < s.reduces.size(); ++k) o << (k ? "," : "") << "\"" << reducer_name(s.reduces[k].kind) << "\"";
       o << "],\"row_schedule\":" << (s.row_schedule ? "true" : "false") << ",\"rows\":" << s.rows
-        << ",\"row_len\":" << s.row_len << ",\"splits\":" << s.splits << ",\"chunk\":" << s.chunk;
+        << ",\"row_len\":" << s.row_len << ",\"splits\":" << s.splits << ",\"chunk\":" << s.chunk
+        << ",\"fused_combine\":" << (s.fused_combine ? "true" : "false");
     }
     if (s.kind == StepKind::kLibrary) {
       o << ",\"library\":\"" << lib_kind_name(s.lib) << "\",\"in_place\":" << (s.in_place ? "true" : "false");

@@ -76,6 +76,10 @@ struct Step {
   int unroll = 1;            // 256*vec-element sub-chunks loaded together per thread
   size_t scratch_bytes = 0;  // partial accumulators (splits > 1)
   uint32_t combine_grid = 0; // splits > 1: workgroups of `<name>_combine` (4 rows each)
+  // splits > 1 and no combine launch: the last workgroup of a row to finish
+  // folds the row's partials (per-row arrival counters after the slots).
+  bool fused_combine = false;
+  size_t counter_offset = 0; // fused_combine: byte offset of the counters in scratch
 
   // kLibrary / kAlias
   LibKind lib = LibKind::kCopy;
@@ -138,6 +142,13 @@ struct PlanOptions {
   // Target number of workgroups a reduction launch should reach.
   // (environment: PJRTX_REDUCE_TARGET_BLOCKS)
   int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 512);
+  // Split reductions fold their partials in the last workgroup of each row
+  // instead of a second launch (environment: PJRTX_REDUCE_FUSED_COMBINE=1).
+  // Off by default: each workgroup's device-scope release fence (an L2
+  // write-back, needed because the XCDs' L2s are not coherent) costs more
+  // than the launch it saves (64x128256 bf16 argmax + f16 reductions:
+  // 16.0 us fused vs 4.3 + 2.6 us with the combine kernel).
+  bool reduce_fused_combine = env_int("PJRTX_REDUCE_FUSED_COMBINE", 0) != 0;
   bool fuse_siblings = true;
   bool fuse_epilogues = true;
   // Row chains (reduce -> reduce/loop over the same rows) become one kernel

@@ -577,6 +577,14 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
       hip_check(hipModuleGetFunction(&L->combine_funcs[i], L->module, cname.c_str()), "hipModuleGetFunction");
     }
     if (s.scratch_bytes) L->scratch[i] = dev->allocate(s.scratch_bytes);
+    if (s.fused_combine) {
+      // Arrival counters start at zero; the last workgroup of each row puts
+      // its row's counter back to zero, so every later launch (and graph
+      // replay) finds them cleared without a memset in the execute path.
+      uint8_t* ctr = static_cast<uint8_t*>(L->scratch[i]->ptr) + s.counter_offset;
+      hip_check(hipMemsetAsync(ctr, 0, s.scratch_bytes - s.counter_offset, dev->stream()), "hipMemsetAsync(counters)");
+      hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    }
   }
   // Resident constants: uploaded once (reference: executable_constants.zig:32-83).
   for (int v : plan_.constants) {
@@ -643,7 +651,7 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       ptrs.reserve(s.inputs.size() + s.outputs.size() + 2);
       for (int v : s.inputs) ptrs.push_back(vals[v] ? vals[v]->ptr : nullptr);
       for (int v : s.outputs) ptrs.push_back(vals[v]->ptr);
-      if (s.combine_grid) ptrs.push_back(L->scratch[si]->ptr);
+      if (s.scratch_bytes) ptrs.push_back(L->scratch[si]->ptr);
       std::vector<void*> args(ptrs.size());
       for (size_t k = 0; k < ptrs.size(); ++k) args[k] = &ptrs[k];
       if (phase != 1) {
