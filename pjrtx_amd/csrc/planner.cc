@@ -1020,6 +1020,11 @@ void Planner::absorb_window_updates() {
         for (int v : steps[k].outputs) clear &= v != v0;
       }
       if (!clear) break;
+      // A kernel that reads the operand cannot also write the window into
+      // it: other workgroups may overwrite elements before they are read
+      // (a shift of the operand by one row, written back in place).
+      for (int v : L.inputs) clear &= v != v0 && v != r;
+      if (!clear) break;
       if (L.kind != StepKind::kLoop || L.loop_shape != ut.dims || L.window_out.size() >= 2) continue;
       if (ut.dims.back() % L.vec != 0) continue;
       const bool own = std::find(L.outputs.begin(), L.outputs.end(), u) != L.outputs.end();

@@ -38,3 +38,20 @@ def test_window_update_is_fused_and_clamped(client):
         q = min(max(p, 0), 7)
         want[:, q:q + 1, :] = x * 2.0
         np.testing.assert_array_equal(got, want)
+
+
+def test_shift_written_back_in_place_matches_numpy(client):
+    # c[0:7] = -c[1:8] into the donated c: the update kernel reads c, so the
+    # write must stay its own step (a fused window write would race).
+    b = Builder()
+    c_in = b.param((8, 16), "f32", donate=True)
+    u = b.negate(b.slice(c_in, [1, 0], [8, 16]))
+    z = b.constant(0, "s32")
+    exe = client.compile(b.build([b.dynamic_update_slice(c_in, u, [z, z])]))
+    steps = json.loads(exe.optimized_program())["steps"]
+    assert not any(s.get("window_outputs") for s in steps)
+    c = np.random.default_rng(1).standard_normal((8, 16)).astype(np.float32)
+    (got,) = exe(c)
+    want = c.copy()
+    want[0:7] = -c[1:8]
+    np.testing.assert_array_equal(got, want)

@@ -207,3 +207,21 @@ def test_residual_add_merges_into_decode_dot(plugin, monkeypatch):
     assert all(s.get("library") == "dot_general" for s in merged)
     monkeypatch.setenv("PJRTX_DOT_RESIDUAL", "0")
     assert not [s for s in plan(plugin, L.decode_program(L.FULL))["steps"] if "residual_add" in s]
+
+
+def _shift_in_place_program():
+    # c donated; c[0:7] = -c[1:8] written back into c (a roll-like shift).
+    b = Builder()
+    c = b.param((8, 16), "f32", donate=True)
+    u = b.negate(b.slice(c, [1, 0], [8, 16]))
+    z = b.constant(0, "s32")
+    return b.build([b.dynamic_update_slice(c, u, [z, z])])
+
+
+def test_window_write_not_absorbed_into_kernel_reading_operand(plugin):
+    # The kernel computing the update reads the operand at other rows than it
+    # would write: fusing the window write would race across workgroups.
+    steps = plan(plugin, _shift_in_place_program())["steps"]
+    assert not any(s.get("window_outputs") for s in steps)
+    dus = [s for s in steps if s.get("library") == "dynamic_update_slice"]
+    assert len(dus) == 1
