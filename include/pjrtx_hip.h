@@ -41,8 +41,10 @@ PJRTX_HIP_API int pjrtx_hip_device_count(int* count);
 PJRTX_HIP_API int pjrtx_hip_malloc(int device, size_t bytes, void** ptr);
 PJRTX_HIP_API int pjrtx_hip_free(int device, void* ptr);
 
-/* Stream-ordered copies on the device's single stream; each returns after
- * the copy completed. Replace buffer_from_host_typed (api.cc:1781-1852) and
+/* Stream-ordered copies on this ABI's stream of the device; each returns
+ * after the copy completed. pjrtx_hip_synchronize waits for all work queued
+ * on the device, on every stream (PJRT clients queue on streams of their
+ * own). Replace buffer_from_host_typed (api.cc:1781-1852) and
  * pjrtx_mlx_metal_buffer_copy_to_host (api.cc:5685-5731). */
 PJRTX_HIP_API int pjrtx_hip_copy_h2d(int device, void* dst, const void* src, size_t bytes);
 PJRTX_HIP_API int pjrtx_hip_copy_d2h(int device, void* dst, const void* src, size_t bytes);
@@ -50,18 +52,18 @@ PJRTX_HIP_API int pjrtx_hip_synchronize(int device);
 
 /* --------------------------------------------------- compiler (host only) */
 
-/* Parses a StableHLO text module, runs the fusion planner and code
- * generator, and writes a JSON description of the plan to `out` (at most
- * `cap` bytes; `*needed` gets the full size). Needs no GPU. Replaces the
- * compile-time half of pjrtx_metalcpp_executable_program_create
- * (metalcpp_api.cc:1296) together with the Zig planner
- * (program_build.zig:10-207). */
 /* Compile-cache counters of this process: compiles that reused a cached
  * parsed and planned program, compiles that built one, entries held (any
  * pointer may be NULL). Replaces the reference's executable-cache stats
  * (src/runtime/executable_cache.zig:9-25, hits / misses / resident_entries). */
 PJRTX_HIP_API int pjrtx_compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries);
 
+/* Parses a StableHLO text module, runs the fusion planner and code
+ * generator, and writes a JSON description of the plan to `out` (at most
+ * `cap` bytes; `*needed` gets the full size). Needs no GPU. Replaces the
+ * compile-time half of pjrtx_metalcpp_executable_program_create
+ * (metalcpp_api.cc:1296) together with the Zig planner
+ * (program_build.zig:10-207). */
 PJRTX_HIP_API int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed);
 
 /* As pjrtx_plan_json, and also compiles the generated fusion kernels with
@@ -98,6 +100,33 @@ PJRTX_HIP_API int pjrtx_executable_time_steps(struct PJRT_LoadedExecutable* exe,
  * execute_executable_program, metalcpp_api.cc:961-1161). */
 PJRTX_HIP_API int pjrtx_executable_run(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
                                        size_t num_args, int iters, double* ms_total);
+
+/* Allocation-free execute. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Runs a compiled,
+ * loaded executable (PJRT_Client_Compile loads it on device 0) on
+ * caller-owned device memory: args[i] and outputs[i] are device addresses of
+ * the i-th parameter / result, dense row-major, of the program's sizes.
+ * Every intermediate value, every copy of a parameter the plan writes in
+ * place (the caller's inputs are never modified), and every kernel scratch
+ * block (split-reduction partials, split-K partials, sort keys, scatter
+ * segments) is carved from one fixed device block per GPU of
+ * pjrtx_noalloc_scratch_bytes() bytes (64 MiB), held from the first call on
+ * that GPU until the process ends. A program whose needs exceed it fails with
+ * PJRT_Error_Code_RESOURCE_EXHAUSTED (outputs then unspecified); programs with
+ * a while loop fail with UNIMPLEMENTED. The call calls no hipMalloc or
+ * hipFree and no allocating library routine; the work is queued on the
+ * device's stream and the call returns without waiting
+ * (pjrtx_hip_synchronize waits). Every call on one GPU shares that GPU's
+ * block and finds the previous call's contents in it: calls queued from one
+ * thread are ordered on the device stream, but work that overlaps a call on
+ * the same GPU from another stream or process races on the block.
+ * `scratch_used` (may be NULL) gets the bytes of the block the call used. */
+PJRTX_HIP_API int pjrtx_executable_execute_noalloc(struct PJRT_LoadedExecutable* exe, int device,
+                                                   const void* const* args, size_t num_args,
+                                                   void* const* outputs, size_t num_outputs,
+                                                   size_t* scratch_used);
+PJRTX_HIP_API size_t pjrtx_noalloc_scratch_bytes(void);
 
 /* Names of the executable's launch units, in the order of
  * pjrtx_executable_time_steps, '\n'-separated: the kernel name, or

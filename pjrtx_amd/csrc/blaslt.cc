@@ -90,6 +90,9 @@ LtPlan make_plan(hipblasLtHandle_t h, const GemmParams& g, bool f16, bool b_kmaj
 
 bool blaslt_wanted(const GemmParams& g) {
   if (env_int("PJRTX_BLASLT", 1) == 0) return false;
+  // The allocation-free execute never enters the library (its handle and
+  // heuristics allocate).
+  if (thread_arena()) return false;
   // Products that fill the GPU with 256 x 256 tiles: the size where the
   // library's tuned kernels were measured ahead of the own ones.
   const int64_t tiles = static_cast<int64_t>((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;

@@ -8,6 +8,7 @@
 #include "../../include/pjrtx_hip.h"
 #include "pjrt_handles.h"
 #include "runtime.h"
+#include "kernels/noalloc.h"
 
 using namespace pjrtx;
 
@@ -112,7 +113,10 @@ int pjrtx_hip_copy_d2h(int device, void* dst, const void* src, size_t bytes) {
 int pjrtx_hip_synchronize(int device) {
   return guarded([&] {
     Device* d = abi_device(device);
-    hip_check(hipStreamSynchronize(d->stream()), "hipStreamSynchronize");
+    d->make_current();
+    // Every stream of the device: PJRT clients and this ABI queue on streams
+    // of their own.
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
   });
 }
 
@@ -184,6 +188,26 @@ int pjrtx_executable_run(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* args, s
     *ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   });
 }
+
+int pjrtx_executable_execute_noalloc(PJRT_LoadedExecutable* exe, int device, const void* const* args,
+                                     size_t num_args, void* const* outputs, size_t num_outputs,
+                                     size_t* scratch_used) {
+  return guarded([&] {
+    PJRTX_CHECK(exe && exe->exe, Code::kInvalidArgument, "execute_noalloc: null executable");
+    PJRTX_CHECK(!exe->deleted, Code::kFailedPrecondition, "execute_noalloc: executable was deleted");
+    PJRTX_CHECK((args || num_args == 0) && (outputs || num_outputs == 0), Code::kInvalidArgument,
+                "execute_noalloc: null argument or output array");
+    Device* dev = nullptr;
+    for (PJRT_Device* d : exe->devices)
+      if (d && d->dev && d->dev->ordinal() == device) dev = d->dev;
+    PJRTX_CHECK(dev != nullptr, Code::kInvalidArgument,
+                strformat("execute_noalloc: the executable is not addressable on device %d", device));
+    const size_t used = exe->exe->execute_noalloc(dev, args, num_args, outputs, num_outputs);
+    if (scratch_used) *scratch_used = used;
+  });
+}
+
+size_t pjrtx_noalloc_scratch_bytes(void) { return kNoallocScratchBytes; }
 
 int pjrtx_executable_step_names(PJRT_LoadedExecutable* exe, char* out, size_t cap, size_t* needed) {
   return guarded([&] {

@@ -1,6 +1,7 @@
 // Device runtime implementation. See runtime.h.
 #include "runtime.h"
 #include "kernels/library.h"
+#include "kernels/noalloc.h"
 
 #include <hip/hiprtc.h>
 #include <sys/stat.h>
@@ -28,8 +29,16 @@ void hip_check(hipError_t e, const char* what) {
 // ----------------------------------------------------------------- allocator
 
 DeviceMemory::~DeviceMemory() {
-  if (dev && ptr) dev->allocator().release(ptr, capacity);
+  if (dev && ptr && !borrowed) dev->allocator().release(ptr, capacity);
 }
+
+namespace {
+thread_local Arena* t_arena = nullptr;
+}  // namespace
+
+Arena* thread_arena() { return t_arena; }
+ArenaScope::ArenaScope(Arena* a) : prev_(t_arena) { t_arena = a; }
+ArenaScope::~ArenaScope() { t_arena = prev_; }
 
 Allocator::~Allocator() = default;
 
@@ -133,6 +142,19 @@ MemRef Device::allocate(size_t bytes) {
   m->dev = this;
   m->bytes = bytes;
   if (bytes == 0) return m;
+  if (Arena* a = t_arena; a && a->dev == this) {
+    const size_t off = (a->used + 255) & ~size_t(255);
+    PJRTX_CHECK(off <= a->cap && bytes <= a->cap - off, Code::kResourceExhausted,
+                strformat("allocation-free execute: the fixed device block of %zu bytes is too small (%zu bytes in "
+                          "use, %zu more requested)",
+                          a->cap, off, bytes));
+    m->ptr = a->base + off;
+    m->capacity = (bytes + 255) & ~size_t(255);
+    m->borrowed = true;
+    a->used = off + bytes;
+    if (a->used > a->peak) a->peak = a->used;
+    return m;
+  }
   make_current();
   m->ptr = alloc_.alloc(bytes, &m->capacity);
   if (capture_pins_) capture_pins_->push_back(m);
@@ -651,7 +673,20 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       ptrs.reserve(s.inputs.size() + s.outputs.size() + 2);
       for (int v : s.inputs) ptrs.push_back(vals[v] ? vals[v]->ptr : nullptr);
       for (int v : s.outputs) ptrs.push_back(vals[v]->ptr);
-      if (s.scratch_bytes) ptrs.push_back(L->scratch[si]->ptr);
+      MemRef arena_scratch;
+      if (s.scratch_bytes && thread_arena() && phase != 1) {
+        // Allocation-free execute: partial slots from the fixed block; the
+        // arrival counters of a one-launch fold must start at zero.
+        arena_scratch = dev->allocate(s.scratch_bytes);
+        if (s.fused_combine) {
+          const size_t lo = s.counter_offset & ~size_t(15);
+          const size_t hi = (s.scratch_bytes + 15) & ~size_t(15);
+          launch_noalloc_zero(dev->stream(), static_cast<uint8_t*>(arena_scratch->ptr) + lo, hi - lo);
+        }
+        ptrs.push_back(arena_scratch->ptr);
+      } else if (s.scratch_bytes) {
+        ptrs.push_back(L->scratch[si]->ptr);
+      }
       std::vector<void*> args(ptrs.size());
       for (size_t k = 0; k < ptrs.size(); ++k) args[k] = &ptrs[k];
       if (phase != 1) {
@@ -754,6 +789,73 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
   if (done) *done = ev;
   stats_.executions++;
   return outs;
+}
+
+size_t Executable::execute_noalloc(Device* dev, const void* const* args, size_t num_args, void* const* outs,
+                                   size_t num_outs) {
+  PJRTX_CHECK(num_args == prog_.params.size(), Code::kInvalidArgument,
+              strformat("execute_noalloc: program takes %zu arguments, got %zu", prog_.params.size(), num_args));
+  PJRTX_CHECK(num_outs == prog_.results.size(), Code::kInvalidArgument,
+              strformat("execute_noalloc: program has %zu results, got %zu output pointers", prog_.results.size(),
+                        num_outs));
+  PJRTX_CHECK(loops_.empty(), Code::kUnimplemented,
+              "execute_noalloc: programs with a while loop are not supported (their regions load on first use)");
+  Loaded* L = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = loaded_.find(dev->ordinal());
+    PJRTX_CHECK(it != loaded_.end(), Code::kFailedPrecondition,
+                strformat("execute_noalloc: the executable is not loaded on device %d (loading allocates)",
+                          dev->ordinal()));
+    L = it->second.get();
+  }
+  for (size_t i = 0; i < num_args; ++i)
+    PJRTX_CHECK(args[i] || prog_.type(prog_.params[i]).bytes() == 0, Code::kInvalidArgument,
+                strformat("execute_noalloc: argument %zu is null", i));
+  for (size_t i = 0; i < num_outs; ++i)
+    PJRTX_CHECK(outs[i] || prog_.type(prog_.results[i]).bytes() == 0, Code::kInvalidArgument,
+                strformat("execute_noalloc: output %zu is null", i));
+  std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  dev->make_current();
+  Arena arena;
+  arena.dev = dev;
+  arena.base = static_cast<uint8_t*>(noalloc_scratch(dev->ordinal()));
+  arena.cap = kNoallocScratchBytes;
+  ArenaScope scope(&arena);
+  std::vector<MemRef> vals(prog_.values.size());
+  for (size_t i = 0; i < num_args; ++i) {
+    auto m = std::make_shared<DeviceMemory>();
+    m->dev = dev;
+    m->ptr = const_cast<void*>(args[i]);
+    m->bytes = prog_.type(prog_.params[i]).bytes();
+    m->capacity = m->bytes;
+    m->borrowed = true;
+    vals[prog_.params[i]] = m;
+  }
+  for (int k : plan_.written_params) {
+    // The plan writes this parameter in place: work on a copy, the caller's
+    // input stays as it was.
+    const MemRef& src = vals[prog_.params[k]];
+    MemRef c = dev->allocate(src->bytes);
+    if (src->bytes)
+      hip_check(hipMemcpyAsync(c->ptr, src->ptr, src->bytes, hipMemcpyDeviceToDevice, dev->stream()),
+                "hipMemcpyAsync(written argument)");
+    vals[prog_.params[k]] = c;
+  }
+  for (auto& [v, m] : L->constants) vals[v] = m;
+  for (size_t si = 0; si < plan_.steps.size(); ++si) {
+    run_step(L, si, vals);
+    for (int v : plan_.steps[si].release_after) vals[v].reset();
+  }
+  for (size_t i = 0; i < num_outs; ++i) {
+    const MemRef& m = vals[prog_.results[i]];
+    PJRTX_CHECK(m != nullptr, Code::kInternal, "execute_noalloc: result value was not produced");
+    if (m->bytes && m->ptr != outs[i])
+      hip_check(hipMemcpyAsync(outs[i], m->ptr, m->bytes, hipMemcpyDeviceToDevice, dev->stream()),
+                "hipMemcpyAsync(result)");
+  }
+  stats_.executions++;
+  return arena.peak;
 }
 
 // ------------------------------------------------------------ graph replay

@@ -40,9 +40,33 @@ struct DeviceMemory {
   void* ptr = nullptr;
   size_t bytes = 0;     // requested
   size_t capacity = 0;  // allocated
+  bool borrowed = false;  // not the allocator's (an arena block or caller memory): never released
   ~DeviceMemory();
 };
 using MemRef = std::shared_ptr<DeviceMemory>;
+
+// A fixed device block that Device::allocate carves blocks from (bump order,
+// 256-byte aligned) instead of calling the caching allocator, while it is
+// installed on the calling thread for its device. Blocks are never handed
+// back one by one: the next call that installs the arena starts at zero.
+// Used by the allocation-free execute; exceeding `cap` fails with
+// RESOURCE_EXHAUSTED.
+struct Arena {
+  Device* dev = nullptr;
+  uint8_t* base = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+  size_t peak = 0;
+};
+Arena* thread_arena();
+class ArenaScope {
+ public:
+  explicit ArenaScope(Arena* a);
+  ~ArenaScope();
+
+ private:
+  Arena* prev_;
+};
 
 class Allocator {
  public:
@@ -183,6 +207,15 @@ class Executable {
   // argument is not donated is copied first.
   std::vector<BufferRef> execute(Device* dev, const std::vector<BufferRef>& args,
                                  std::shared_ptr<Event>* done, const std::vector<bool>* donate = nullptr);
+  // The same plan on caller-owned device memory with no allocation: args[i]
+  // and outs[i] are device addresses of the parameter / result sizes; every
+  // intermediate, copy of a parameter the plan writes, and kernel scratch
+  // block comes from the device's fixed no-allocation block (kernels/
+  // noalloc.h), whose contents the previous call left behind. Work is queued
+  // on the device stream (no graph capture, no completion event). The
+  // executable must already be loaded on `dev`. Returns the arena bytes used.
+  size_t execute_noalloc(Device* dev, const void* const* args, size_t num_args, void* const* outs,
+                         size_t num_outs);
   // Times each launch unit (a step; a split reduction counts as two units,
   // main pass then combine pass) by replaying it `iters` times between two
   // hipEvents on the device stream (inputs from `args`). Returns ms per unit

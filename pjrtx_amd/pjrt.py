@@ -216,10 +216,19 @@ class Plugin:
             "pjrtx_executable_run": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double)],
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_compile_cache_stats": [POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)],
+            "pjrtx_hip_malloc": [c_int, c_size_t, POINTER(c_void_p)],
+            "pjrtx_hip_free": [c_int, c_void_p],
+            "pjrtx_hip_copy_h2d": [c_int, c_void_p, c_void_p, c_size_t],
+            "pjrtx_hip_copy_d2h": [c_int, c_void_p, c_void_p, c_size_t],
+            "pjrtx_hip_synchronize": [c_int],
+            "pjrtx_executable_execute_noalloc": [c_void_p, c_int, POINTER(c_void_p), c_size_t, POINTER(c_void_p),
+                                                 c_size_t, POINTER(c_size_t)],
         }.items():
             f = getattr(L, name)
             f.argtypes = argtypes
             f.restype = c_int
+        L.pjrtx_noalloc_scratch_bytes.argtypes = []
+        L.pjrtx_noalloc_scratch_bytes.restype = c_size_t
 
     def hip_check(self, rc: int) -> None:
         if rc != 0:
@@ -470,6 +479,18 @@ class Executable:
         self.client.p.hip_check(L.pjrtx_executable_run(self.handle, arr, len(args), iters, ctypes.byref(ms)))
         return ms.value
 
+    def execute_noalloc(self, arg_ptrs: list[int], out_ptrs: list[int], device: int = 0) -> int:
+        """pjrtx_executable_execute_noalloc on raw device addresses (from
+        DeviceArray); queued on the device stream. Returns the bytes of the
+        fixed no-allocation block the call used."""
+        L = self.client.p.lib
+        a = (c_void_p * max(1, len(arg_ptrs)))(*arg_ptrs)
+        o = (c_void_p * max(1, len(out_ptrs)))(*out_ptrs)
+        used = c_size_t(0)
+        self.client.p.hip_check(L.pjrtx_executable_execute_noalloc(self.handle, device, a, len(arg_ptrs), o,
+                                                                   len(out_ptrs), ctypes.byref(used)))
+        return used.value
+
     def step_names(self) -> list[str]:
         L = self.client.p.lib
         need = c_size_t(0)
@@ -586,6 +607,37 @@ class Client:
             a.client = self.handle
             self.p.call("Client_Destroy", a)
             self.handle = None
+
+
+class DeviceArray:
+    """Raw device memory from pjrtx_hip_malloc (caller-owned, for the
+    allocation-free execute): `ptr` is the device address."""
+
+    def __init__(self, plugin_: Plugin, nbytes: int, device: int = 0):
+        self.p, self.nbytes, self.device = plugin_, int(nbytes), device
+        ptr = c_void_p(0)
+        self.p.hip_check(self.p.lib.pjrtx_hip_malloc(device, max(1, self.nbytes), ctypes.byref(ptr)))
+        self.ptr = ptr.value
+
+    @classmethod
+    def from_numpy(cls, plugin_: Plugin, a: np.ndarray, device: int = 0) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(plugin_, a.nbytes, device)
+        if a.nbytes:
+            d.p.hip_check(d.p.lib.pjrtx_hip_copy_h2d(device, d.ptr, a.ctypes.data, a.nbytes))
+        return d
+
+    def to_numpy(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert out.nbytes == self.nbytes
+        if out.nbytes:
+            self.p.hip_check(self.p.lib.pjrtx_hip_copy_d2h(self.device, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self.p.hip_check(self.p.lib.pjrtx_hip_free(self.device, self.ptr))
+            self.ptr = None
 
 
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:
