@@ -234,6 +234,19 @@ def scatter_rows_add(operand, idx, updates):
     return out
 
 
+def scatter_rows_add_bf16_bits(operand_bits, idx, update_bits):
+    """Row scatter-add on bf16 bit patterns in update order, each addition
+    done as XLA does bf16 arithmetic: widen both to f32, add in f32, round the
+    sum to bf16 (nearest-even)."""
+    out = bf16_bits_to_f32(np.asarray(operand_bits, np.uint16)).copy()
+    upd = bf16_bits_to_f32(np.asarray(update_bits, np.uint16))
+    idx = np.asarray(idx, dtype=np.int64)
+    for j in np.flatnonzero((idx >= 0) & (idx < out.shape[0])):
+        r = idx[j]
+        out[r] = bf16_bits_to_f32(f32_to_bf16_bits((out[r] + upd[j]).astype(np.float32)))
+    return f32_to_bf16_bits(out)
+
+
 def scatter_rows_add_int(operand, idx, updates):
     """Integer row scatter-add, vectorized: integer addition is associative,
     so per-row sums in any order (int64, then wrapped) equal the sequential

@@ -52,16 +52,36 @@ void launch_radix_sort(hipStream_t s, uint32_t* keys, uint32_t* vals, uint32_t* 
 // Combiner of the scatter region.
 enum class ScatterOp { kAdd, kSet, kMax, kMin, kMul };
 
-// Row mode, long segments: a segment (the updates of one operand row, in
-// update order) is cut into chunks of kScatterChunk updates. Chunk 0 folds
-// from the operand row, later chunks from their own first update; a row
-// with one chunk writes its result directly (the exact sequential fold),
-// otherwise the chunk partials are folded in chunk order.
-constexpr int kScatterChunk = 256;
-size_t scatter_chunk_scratch_bytes(int64_t rows, int64_t n, int64_t row_elems, DType t);
-void launch_scatter_chunked(hipStream_t s, int64_t rows, int64_t row_elems, int64_t n, int op, DType t,
-                            const void* operand, const void* updates, const uint32_t* perm,
-                            const uint32_t* seg_start, const uint32_t* seg_end, void* scratch, void* out);
+// Row mode: each operand row folds its updates in update order (bit-exact
+// against a sequential scatter loop for every type). Segments longer than
+// kHotMinUpdates are folded by 64-byte column slices on persistent
+// workgroups of their own (a list of hot rows, bucketed by
+// floor(log2(length)) so the longest start first), on the second stream
+// `aux` (joined back into `s` before return); the other rows one wave per row.
+// Integer add / max / min (exact in any order) fold hot rows in parallel
+// chunks merged with atomics instead. `h.counts` must be zero on entry (the
+// launcher lists the hot rows itself).
+constexpr int kHotMinUpdates = 256;
+constexpr int kHotSliceBytes = 64;
+
+struct ScatterHotList {
+  uint32_t* counts = nullptr;  // [32] rows per length class (zeroed before classify)
+  uint32_t* rows = nullptr;    // class k's rows at base[k] ..
+  int64_t base[32] = {};
+  int kmin = 0;                // lowest class that can hold a hot row
+};
+struct ScatterRowsParams {
+  int64_t rows = 0;
+  int64_t row_elems = 0;
+  int64_t hot_wgs = 0;  // persistent hot-slice workgroups (0: every row in bulk)
+};
+// Class layout for n updates; the list needs scatter_hot_list_words(n) words.
+ScatterHotList scatter_hot_list(int64_t n, uint32_t* counts, uint32_t* rows_list);
+size_t scatter_hot_list_words(int64_t n);
+void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join, int64_t rows,
+                         int64_t row_elems, int op, DType t, const void* operand, const void* updates,
+                         const uint32_t* perm, const uint32_t* seg_start, const uint32_t* seg_end,
+                         const ScatterHotList& h, int64_t hot_wgs, void* out);
 
 struct ScatterFoldParams {
   int64_t rows = 0;       // operand rows (element mode: operand elements)
@@ -72,9 +92,10 @@ struct ScatterFoldParams {
 
 void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* indices, uint32_t* keys,
                          uint32_t* vals);
-// seg_start/seg_end: `rows` uint32 each (zeroed by this launcher).
+// seg_start/seg_end: `rows` uint32 each; they and `extra_zero` words after
+// seg_end are zeroed by this launcher.
 void launch_scatter_segments(hipStream_t s, const uint32_t* sorted_keys, int64_t n, uint32_t invalid,
-                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows);
+                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows, int64_t extra_zero = 0);
 // out = fold(operand, updates in order) per target; `operand` may equal `out`.
 void launch_scatter_fold(hipStream_t s, const ScatterFoldParams& p, DType t, const void* operand,
                          const void* updates, const uint32_t* perm, const uint32_t* seg_start,

@@ -18,6 +18,8 @@
 // order; dimension numbers as in api.cc:3158-3236).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "kernels/scatter.h"
 
@@ -332,127 +334,386 @@ __global__ void __launch_bounds__(64) scatter_fold(ScatterFoldParams p, const ty
   out[t] = K::st(acc);
 }
 
-// ------------------------------------------------------- chunked row fold
-constexpr int kFoldDepth = 16;  // update rows in flight per lane
+// ------------------------------------------------------------ row fold
+//
+// Row mode: every operand row folds its updates strictly in update order, so
+// f32 results equal a sequential scatter loop bit for bit. Two kernels:
+//
+//  * bulk rows (segments of at most kHotMinUpdates updates, or every row when
+//    the sliced path is off): one wave per row folds the whole row, 16 bytes
+//    per lane, kFoldDepth update rows in flight.
+//  * hot slices (longer segments, e.g. the Zipf head with ~10^5 updates):
+//    a row is cut into 64-byte slices (16 f32 columns) and each slice is
+//    folded by one workgroup, so a row's sequential column chains run on
+//    many CUs at once. Waves 1-3 stream the slice's update rows through a
+//    register ring into double-buffered LDS blocks; wave 0's lanes run the
+//    column chains over each block. Hot workgroups are persistent over a
+//    list of (row, slice) items ordered longest segment class first, so the
+//    longest chain starts at once. This kernel runs on a second stream
+//    beside the bulk kernel.
+constexpr int kFoldDepth = 16;  // update rows in flight per lane (bulk rows)
 
 template <typename T, int VEC>
 struct alignas(sizeof(T) * VEC) VecOf {
   T v[VEC];
 };
 
-__global__ void __launch_bounds__(256) chunk_count(const uint32_t* __restrict__ seg_start,
-                                                   const uint32_t* __restrict__ seg_end, int64_t rows,
-                                                   uint32_t* __restrict__ cnt) {
+// Lists the hot rows by length class. With `init_src`, also copies each hot
+// row of the operand into the result (the integer chunk path accumulates
+// into it with atomics).
+__global__ void __launch_bounds__(256) scatter_hot_classify(const uint32_t* __restrict__ seg_start,
+                                                            const uint32_t* __restrict__ seg_end, int64_t rows,
+                                                            ScatterHotList h, const uint4* __restrict__ init_src,
+                                                            uint4* __restrict__ init_dst, int64_t row_u4) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (r >= rows) return;
   const uint32_t len = seg_end[r] - seg_start[r];
-  cnt[r] = len <= (uint32_t)kScatterChunk ? 1u : (len + kScatterChunk - 1) / kScatterChunk;
+  if (len <= (uint32_t)kHotMinUpdates) return;
+  const int k = 31 - __clz(len);
+  const uint32_t slot = atomicAdd(&h.counts[k], 1u);  // order inside a class does not change results
+  h.rows[h.base[k] + slot] = (uint32_t)r;
+  if (init_src)
+    for (int64_t j = 0; j < row_u4; ++j) init_dst[r * row_u4 + j] = init_src[r * row_u4 + j];
 }
 
-__global__ void __launch_bounds__(256) chunk_rows(const uint32_t* __restrict__ cnt, const uint32_t* __restrict__ off,
-                                                  int64_t rows, uint32_t* __restrict__ chunk_row,
-                                                  uint32_t* __restrict__ total) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
-  const uint32_t o = off[r], c = cnt[r];
-  for (uint32_t q = 0; q < c; ++q) chunk_row[o + q] = (uint32_t)r;
-  if (r == rows - 1) total[0] = o + c;
+// Integer add / max / min on hot rows: exact in any order, so a row's updates
+// are cut into chunks of kHotChunk folded by separate workgroups (registers,
+// then the 4 waves through LDS) and merged into the result with atomics.
+// Chunk items of class k: rows x ceil(2^(k+1) / kHotChunk) (empty chunks of
+// shorter rows exit at once); longest class first.
+constexpr int kHotChunk = 512;
+
+template <typename T, ScatterOp OP>
+__device__ __forceinline__ T int_fold(T a, T b) {
+  if constexpr (OP == ScatterOp::kAdd) return (T)((typename std::make_unsigned<T>::type)a + (typename std::make_unsigned<T>::type)b);
+  else if constexpr (OP == ScatterOp::kMax) return a > b ? a : b;
+  else return a < b ? a : b;
 }
 
-// One wave per chunk; 4 chunks per workgroup.
-template <typename Tag, int VEC>
-__global__ void __launch_bounds__(256) scatter_chunk_fold(
-    int64_t row_elems, ScatterOp op, const typename StorageOf<Tag>::T* __restrict__ operand,
+template <typename T, ScatterOp OP>
+__device__ __forceinline__ void int_atomic(T* p, T v) {
+  if constexpr (sizeof(T) == 4 && std::is_signed<T>::value) {
+    if constexpr (OP == ScatterOp::kAdd) atomicAdd(reinterpret_cast<int*>(p), (int)v);
+    else if constexpr (OP == ScatterOp::kMax) atomicMax(reinterpret_cast<int*>(p), (int)v);
+    else atomicMin(reinterpret_cast<int*>(p), (int)v);
+  } else if constexpr (sizeof(T) == 4) {
+    if constexpr (OP == ScatterOp::kAdd) atomicAdd(reinterpret_cast<unsigned*>(p), (unsigned)v);
+    else if constexpr (OP == ScatterOp::kMax) atomicMax(reinterpret_cast<unsigned*>(p), (unsigned)v);
+    else atomicMin(reinterpret_cast<unsigned*>(p), (unsigned)v);
+  } else {
+    if constexpr (OP == ScatterOp::kAdd) atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
+    else if constexpr (OP == ScatterOp::kMax) atomicMax(reinterpret_cast<long long*>(p), (long long)v);
+    else atomicMin(reinterpret_cast<long long*>(p), (long long)v);
+  }
+}
+
+template <typename T, ScatterOp OP>
+__global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, const T* __restrict__ updates,
+                                                          const uint32_t* __restrict__ perm,
+                                                          const uint32_t* __restrict__ seg_start,
+                                                          const uint32_t* __restrict__ seg_end, ScatterHotList h,
+                                                          T* __restrict__ out) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  typedef VecOf<T, VEC> V;
+  __shared__ V part[3][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int64_t total = 0;
+  for (int k = 31; k >= h.kmin; --k) total += (int64_t)h.counts[k] * (((int64_t(2) << k) + kHotChunk - 1) / kHotChunk);
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+    int64_t it = item;
+    uint32_t row = 0, chunk = 0;
+    for (int k = 31; k >= h.kmin; --k) {
+      const int64_t cpr = ((int64_t(2) << k) + kHotChunk - 1) / kHotChunk;
+      const int64_t c = (int64_t)h.counts[k] * cpr;
+      if (it < c) {
+        row = h.rows[h.base[k] + it / cpr];
+        chunk = (uint32_t)(it % cpr);
+        break;
+      }
+      it -= c;
+    }
+    const uint32_t lo = seg_start[row] + chunk * kHotChunk, hi = min(lo + (uint32_t)kHotChunk, seg_end[row]);
+    if (lo >= hi) continue;  // uniform over the workgroup
+    for (int64_t c0 = (int64_t)lane * VEC; c0 - lane * VEC < row_elems; c0 += 64 * VEC) {
+      const bool col_ok = c0 < row_elems;
+      V acc;
+      bool any = false;
+      for (uint32_t i = lo + wave; i < hi; i += 4 * kFoldDepth) {
+        V u[kFoldDepth];
+#pragma unroll
+        for (int q = 0; q < kFoldDepth; ++q) {
+          const uint32_t j = min(i + 4 * q, hi - 1);  // clamped: a repeat of the last row is never folded
+          u[q] = col_ok ? *reinterpret_cast<const V*>(updates + (int64_t)perm[j] * row_elems + c0) : V();
+        }
+#pragma unroll
+        for (int q = 0; q < kFoldDepth; ++q) {
+          if (i + 4 * q >= hi) break;
+          if (!any) {
+            acc = u[q];
+            any = true;
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc.v[e] = int_fold<T, OP>(acc.v[e], u[q].v[e]);
+          }
+        }
+      }
+      // waves 1-3 hand their partials to wave 0 (a wave with no row keeps `any` false)
+      __shared__ int has[3];
+      if (wave > 0) {
+        part[wave - 1][lane] = acc;
+        if (lane == 0) has[wave - 1] = any ? 1 : 0;
+      }
+      __syncthreads();
+      if (wave == 0 && col_ok) {
+#pragma unroll
+        for (int w = 0; w < 3; ++w) {
+          if (!has[w]) continue;
+          const V o = part[w][lane];
+          if (!any) {
+            acc = o;
+            any = true;
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc.v[e] = int_fold<T, OP>(acc.v[e], o.v[e]);
+          }
+        }
+        if (any)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) int_atomic<T, OP>(out + (int64_t)row * row_elems + c0 + e, acc.v[e]);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <typename Tag, ScatterOp OP>
+__device__ __forceinline__ typename Codec<Tag>::C fold1(typename Codec<Tag>::C acc, typename Codec<Tag>::C u) {
+  return Codec<Tag>::rnd(combine<typename Codec<Tag>::C>(OP, acc, u));
+}
+
+// Shape of a hot slice's pipeline (per element size): kHotSliceBytes of a
+// row per slice, 16-byte loads, update rows staged in LDS as
+// [row quad][column][4 rows] so a chain lane reads four rows of its column
+// with one load.
+template <typename T>
+struct HotShape {
+  static constexpr int COLS = kHotSliceBytes / (int)sizeof(T);  // columns per slice = chain lanes
+  static constexpr int EPL = 16 / (int)sizeof(T);               // elements per 16-byte lane load
+  static constexpr int LPR = COLS / EPL;                        // lanes per update row of a slice
+  static constexpr int RPI = 64 / LPR;                          // update rows per wave load
+  static constexpr int BROWS = 192;                             // update rows per LDS block (3 loader waves x 64)
+  static constexpr int NI = (BROWS / 3) / RPI;                  // loads per loader wave per block
+  static constexpr int DEPTH = (int)sizeof(T) == 2 ? 8 : ((int)sizeof(T) == 4 ? 4 : 2);  // blocks in flight
+  static constexpr int QS = COLS * 4 + 4 * EPL;                 // elements per row quad in LDS (padded)
+  static constexpr int BUF = (BROWS / 4) * QS;                  // elements per LDS block
+};
+
+// One (row, slice) item of the hot path. Wave 0 runs the column chains;
+// waves 1-3 stream the update rows through a register ring (data DEPTH
+// blocks ahead, perm indices 2*DEPTH blocks ahead) into two LDS blocks.
+// Both roles pass one barrier per block. The streamed arrays are not
+// __restrict__ here: the barrier then orders their loads, so each stays
+// issued where it is written instead of being sunk next to its use.
+template <typename Tag, ScatterOp OP>
+__device__ __forceinline__ void hot_slice_fold(int64_t row_elems, uint32_t row, int slice,
+                                               const typename StorageOf<Tag>::T* __restrict__ operand,
+                                               const typename StorageOf<Tag>::T* updates, const uint32_t* perm,
+                                               uint32_t lo, uint32_t len,
+                                               typename StorageOf<Tag>::T* __restrict__ out,
+                                               typename StorageOf<Tag>::T* lds) {
+  typedef Codec<Tag> K;
+  typedef typename K::C C;
+  typedef typename StorageOf<Tag>::T T;
+  typedef HotShape<T> S;
+  typedef VecOf<T, S::EPL> V;
+  typedef VecOf<T, 4> Q;
+  constexpr int D = S::DEPTH, NI = S::NI;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t c0 = (int64_t)slice * S::COLS;
+  const int nb = (int)((len + S::BROWS - 1) / S::BROWS);
+  const int nsteps = (nb + D - 1) / D * D;  // whole unrolled rounds: both roles pass the same barriers
+
+  if (wave == 0) {
+    // ---- chain role: lane c folds column c0 + c in update order.
+    const bool chain = lane < S::COLS && c0 + lane < row_elems;
+    C acc = C();
+    if (chain) acc = K::ld(operand[(int64_t)row * row_elems + c0 + lane]);
+    for (int b0 = 0; b0 < nsteps; b0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int b = b0 + d;
+        __syncthreads();  // block b is in LDS buffer d
+        const int here = b < nb ? (int)min((uint32_t)S::BROWS, len - (uint32_t)b * S::BROWS) : 0;
+        if (chain) {
+          const T* src = lds + d * S::BUF + lane * 4;
+          if (here == S::BROWS) {
+            // Half a block of quads into registers first: the reads queue
+            // back to back and the chain only waits for the oldest.
+            for (int q0 = 0; q0 < S::BROWS / 4; q0 += S::BROWS / 8) {
+              Q x[S::BROWS / 8];
+#pragma unroll
+              for (int j = 0; j < S::BROWS / 8; ++j) x[j] = *reinterpret_cast<const Q*>(src + (q0 + j) * S::QS);
+#pragma unroll
+              for (int j = 0; j < S::BROWS / 8; ++j) {
+                acc = fold1<Tag, OP>(acc, K::ld(x[j].v[0]));
+                acc = fold1<Tag, OP>(acc, K::ld(x[j].v[1]));
+                acc = fold1<Tag, OP>(acc, K::ld(x[j].v[2]));
+                acc = fold1<Tag, OP>(acc, K::ld(x[j].v[3]));
+              }
+            }
+          } else {
+            for (int r = 0; r < here; ++r) acc = fold1<Tag, OP>(acc, K::ld(src[(r >> 2) * S::QS + (r & 3)]));
+          }
+        }
+      }
+    }
+    if (chain) out[(int64_t)row * row_elems + c0 + lane] = K::st(acc);
+  } else {
+    // ---- load role: waves 1..3 each own 64 rows of a block.
+    const int lw = wave - 1;
+    const int g = lane % S::LPR, rr = lane / S::LPR;
+    // Column of this lane's 16-byte load; a group past the row end re-reads
+    // the row's first group and stores it into its quad's padding.
+    const bool g_ok = c0 + g * S::EPL < row_elems;
+    const int64_t lc = g_ok ? c0 + g * S::EPL : 0;
+    const int wcol = g_ok ? g * S::EPL * 4 : S::COLS * 4;
+    const uint32_t last = len - 1;
+    auto perm_of = [&](int b, int i) -> uint32_t {
+      const uint32_t r = (uint32_t)b * S::BROWS + (uint32_t)(lw * 64 + i * S::RPI + rr);
+      return perm[lo + (r < last ? r : last)];
+    };
+    uint32_t P[D][NI];  // perm of blocks b+D .. b+2D-1 (slot = block % D)
+    V R[D][NI];         // update data of blocks b .. b+D-1 (slot = block % D)
+    // Prologue in the loop's own issue order (per slot: perm of the block D
+    // further on, then the slot's data), so the loop sees the same queue of
+    // loads on entry as around its back edge.
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) P[d][i] = perm_of(d, i);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const V* a[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) a[i] = reinterpret_cast<const V*>(updates + (int64_t)P[d][i] * row_elems + lc);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) P[d][i] = perm_of(D + d, i);
+      __builtin_amdgcn_sched_barrier(0);  // keep the issue order: perm, then data, slot by slot
+#pragma unroll
+      for (int i = 0; i < NI; ++i) R[d][i] = *a[i];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int b0 = 0; b0 < nsteps; b0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int b = b0 + d;
+        T* buf = lds + (d & 1) * S::BUF;
+        // block b into LDS as [quad][column][4 rows]
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int rho = lw * 64 + i * S::RPI + rr;
+          T* dst = buf + (rho >> 2) * S::QS + wcol + (rho & 3);
+#pragma unroll
+          for (int e = 0; e < S::EPL; ++e) dst[e * 4] = R[d][i].v[e];
+        }
+        // addresses of block b+D from its perm (formed first, so the perm
+        // registers are free for the new perm loads and stay the same
+        // registers around the loop), then perm of b+2D, then the loads of
+        // b+D (after those perm loads: waiting for this block's data later
+        // also covers them)
+        const V* a[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) a[i] = reinterpret_cast<const V*>(updates + (int64_t)P[d][i] * row_elems + lc);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) P[d][i] = perm_of(b + 2 * D, i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) R[d][i] = *a[i];
+        __syncthreads();  // block b complete
+      }
+    }
+  }
+  __syncthreads();  // the next item reuses the LDS blocks
+}
+
+template <typename Tag, ScatterOp OP>
+__global__ void __launch_bounds__(256) scatter_hot_fold(
+    int64_t row_elems, const typename StorageOf<Tag>::T* __restrict__ operand,
+    const typename StorageOf<Tag>::T* updates, const uint32_t* perm, const uint32_t* __restrict__ seg_start,
+    const uint32_t* __restrict__ seg_end, ScatterHotList h, typename StorageOf<Tag>::T* __restrict__ out) {
+  typedef typename StorageOf<Tag>::T T;
+  typedef HotShape<T> S;
+  __shared__ __align__(16) T lds[2 * S::BUF];
+  const int64_t slices = (row_elems + S::COLS - 1) / S::COLS;
+  int64_t total = 0;
+  for (int k = 31; k >= h.kmin; --k) total += (int64_t)h.counts[k] * slices;
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+    int64_t it = item;
+    uint32_t row = 0;
+    int slice = 0;
+    for (int k = 31; k >= h.kmin; --k) {
+      const int64_t c = (int64_t)h.counts[k] * slices;
+      if (it < c) {
+        row = h.rows[h.base[k] + it / slices];
+        slice = (int)(it % slices);
+        break;
+      }
+      it -= c;
+    }
+    const uint32_t lo = seg_start[row];
+    hot_slice_fold<Tag, OP>(row_elems, row, slice, operand, updates, perm, lo, seg_end[row] - lo, out, lds);
+  }
+}
+
+template <typename Tag, ScatterOp OP, int VEC>
+__global__ void __launch_bounds__(256) scatter_rows_fold(
+    ScatterRowsParams p, const typename StorageOf<Tag>::T* __restrict__ operand,
     const typename StorageOf<Tag>::T* __restrict__ updates, const uint32_t* __restrict__ perm,
-    const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ seg_end, const uint32_t* __restrict__ cnt,
-    const uint32_t* __restrict__ off, const uint32_t* __restrict__ chunk_row, const uint32_t* __restrict__ total,
-    typename StorageOf<Tag>::T* __restrict__ partial, typename StorageOf<Tag>::T* __restrict__ out) {
+    const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ seg_end,
+    typename StorageOf<Tag>::T* __restrict__ out) {
   typedef Codec<Tag> K;
   typedef typename K::C C;
   typedef typename StorageOf<Tag>::T T;
   typedef VecOf<T, VEC> V;
+  // One wave per row, 4 rows per workgroup.
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint32_t j = blockIdx.x * 4 + wave;
-  if (j >= total[0]) return;
-  const uint32_t r = chunk_row[j];
-  const uint32_t q = j - off[r];
-  const uint32_t lo = seg_start[r] + q * kScatterChunk;
-  const uint32_t hi = min(lo + (uint32_t)kScatterChunk, seg_end[r]);
-  T* dst = cnt[r] == 1 ? out + (int64_t)r * row_elems : partial + (int64_t)j * row_elems;
-  for (int64_t c0 = (int64_t)lane * VEC; c0 < row_elems; c0 += 64 * VEC) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  if (r >= p.rows) return;
+  const uint32_t lo = seg_start[r], hi = seg_end[r];
+  if (p.hot_wgs > 0 && hi - lo > (uint32_t)kHotMinUpdates) return;  // a hot row: folded by slices
+  const T* xr = operand + r * p.row_elems;
+  T* dst = out + r * p.row_elems;
+  if (lo == hi) {
+    if (operand != out)
+      for (int64_t c0 = (int64_t)lane * VEC; c0 < p.row_elems; c0 += 64 * VEC)
+        *reinterpret_cast<V*>(dst + c0) = *reinterpret_cast<const V*>(xr + c0);
+    return;
+  }
+  for (int64_t c0 = (int64_t)lane * VEC; c0 < p.row_elems; c0 += 64 * VEC) {
     C acc[VEC];
-    uint32_t i = lo;
-    {
-      const V first = q == 0 ? *reinterpret_cast<const V*>(operand + (int64_t)r * row_elems + c0)
-                             : *reinterpret_cast<const V*>(updates + (int64_t)perm[lo] * row_elems + c0);
+    const V first = *reinterpret_cast<const V*>(xr + c0);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = K::ld(first.v[e]);
-      if (q != 0) ++i;
-    }
+    for (int e = 0; e < VEC; ++e) acc[e] = K::ld(first.v[e]);
+    uint32_t i = lo;
     for (; i + kFoldDepth <= hi; i += kFoldDepth) {
       V u[kFoldDepth];
 #pragma unroll
       for (int d = 0; d < kFoldDepth; ++d)
-        u[d] = *reinterpret_cast<const V*>(updates + (int64_t)perm[i + d] * row_elems + c0);
+        u[d] = *reinterpret_cast<const V*>(updates + (int64_t)perm[i + d] * p.row_elems + c0);
 #pragma unroll
       for (int d = 0; d < kFoldDepth; ++d)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u[d].v[e])));
+        for (int e = 0; e < VEC; ++e) acc[e] = fold1<Tag, OP>(acc[e], K::ld(u[d].v[e]));
     }
     for (; i < hi; ++i) {
-      const V u = *reinterpret_cast<const V*>(updates + (int64_t)perm[i] * row_elems + c0);
+      const V u = *reinterpret_cast<const V*>(updates + (int64_t)perm[i] * p.row_elems + c0);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u.v[e])));
+      for (int e = 0; e < VEC; ++e) acc[e] = fold1<Tag, OP>(acc[e], K::ld(u.v[e]));
     }
     V o;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) o.v[e] = K::st(acc[e]);
     *reinterpret_cast<V*>(dst + c0) = o;
-  }
-}
-
-// Rows with more than one chunk: fold the chunk partials in chunk order. One
-// wave per row, 4 rows per workgroup.
-template <typename Tag, int VEC>
-__global__ void __launch_bounds__(256) scatter_chunk_combine(int64_t rows, int64_t row_elems, ScatterOp op,
-                                                             const uint32_t* __restrict__ cnt,
-                                                             const uint32_t* __restrict__ off,
-                                                             const typename StorageOf<Tag>::T* __restrict__ partial,
-                                                             typename StorageOf<Tag>::T* __restrict__ out) {
-  typedef Codec<Tag> K;
-  typedef typename K::C C;
-  typedef typename StorageOf<Tag>::T T;
-  typedef VecOf<T, VEC> V;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
-  if (r >= rows) return;
-  const uint32_t n = cnt[r];
-  if (n <= 1) return;
-  const T* src = partial + (int64_t)off[r] * row_elems;
-  for (int64_t c0 = (int64_t)lane * VEC; c0 < row_elems; c0 += 64 * VEC) {
-    C acc[VEC];
-    const V first = *reinterpret_cast<const V*>(src + c0);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] = K::ld(first.v[e]);
-    uint32_t qi = 1;
-    for (; qi + kFoldDepth <= n; qi += kFoldDepth) {
-      V u[kFoldDepth];
-#pragma unroll
-      for (int d = 0; d < kFoldDepth; ++d) u[d] = *reinterpret_cast<const V*>(src + (int64_t)(qi + d) * row_elems + c0);
-#pragma unroll
-      for (int d = 0; d < kFoldDepth; ++d)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u[d].v[e])));
-    }
-    for (; qi < n; ++qi) {
-      const V u = *reinterpret_cast<const V*>(src + (int64_t)qi * row_elems + c0);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = K::rnd(combine<C>(op, acc[e], K::ld(u.v[e])));
-    }
-    V o;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) o.v[e] = K::st(acc[e]);
-    *reinterpret_cast<V*>(out + r * row_elems + c0) = o;
   }
 }
 
@@ -522,79 +783,124 @@ void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* i
 }
 
 void launch_scatter_segments(hipStream_t s, const uint32_t* sorted_keys, int64_t n, uint32_t invalid,
-                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows) {
+                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows, int64_t extra_zero) {
   // Zero with a kernel (not a memset node), so the sequence stays capturable.
-  hipLaunchKernelGGL(zero_u32, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, rows);
-  hipLaunchKernelGGL(zero_u32, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_end, rows);
+  if (seg_end == seg_start + rows) {
+    hipLaunchKernelGGL(zero_u32, dim3(blocks(2 * rows + extra_zero, 256)), dim3(256), 0, s, seg_start,
+                       2 * rows + extra_zero);
+  } else {
+    hipLaunchKernelGGL(zero_u32, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, rows);
+    hipLaunchKernelGGL(zero_u32, dim3(blocks(rows + extra_zero, 256)), dim3(256), 0, s, seg_end, rows + extra_zero);
+  }
   if (n == 0) return;
   hipLaunchKernelGGL(scatter_segments, dim3(blocks(n, 256)), dim3(256), 0, s, sorted_keys, n, invalid, seg_start,
                      seg_end);
   check("scatter_segments");
 }
 
-namespace {
-size_t align256(size_t b) { return (b + 255) / 256 * 256; }
-int64_t max_chunks(int64_t rows, int64_t n) { return rows + (n + kScatterChunk - 1) / kScatterChunk; }
-}  // namespace
 
-size_t scatter_chunk_scratch_bytes(int64_t rows, int64_t n, int64_t row_elems, DType t) {
-  const int64_t mc = max_chunks(rows, n);
-  return 3 * align256(rows * 4) + align256(mc * 4) + align256(256) + align256(kScanTile * 4) +
-         align256(mc * row_elems * dtype_size(t));
+
+ScatterHotList scatter_hot_list(int64_t n, uint32_t* counts, uint32_t* rows_list) {
+  ScatterHotList h;
+  h.counts = counts;
+  h.rows = rows_list;
+  h.kmin = 0;
+  while ((int64_t(1) << (h.kmin + 1)) <= kHotMinUpdates + 1) ++h.kmin;  // 2^kmin <= kHotMinUpdates + 1
+  int64_t base = 0;
+  for (int k = 31; k >= 0; --k) {
+    h.base[k] = base;
+    if (k >= h.kmin) base += n >> k;  // a class-k row holds at least 2^k updates
+  }
+  return h;
 }
 
-void launch_scatter_chunked(hipStream_t s, int64_t rows, int64_t row_elems, int64_t n, int op_i, DType t,
-                            const void* operand, const void* updates, const uint32_t* perm,
-                            const uint32_t* seg_start, const uint32_t* seg_end, void* scratch, void* out) {
+size_t scatter_hot_list_words(int64_t n) {
+  const ScatterHotList h = scatter_hot_list(n, nullptr, nullptr);
+  return static_cast<size_t>(h.base[h.kmin] + (n >> h.kmin));
+}
+
+void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join, int64_t rows,
+                         int64_t row_elems, int op_i, DType t, const void* operand, const void* updates,
+                         const uint32_t* perm, const uint32_t* seg_start, const uint32_t* seg_end,
+                         const ScatterHotList& h, int64_t hot_wgs, void* out) {
   if (rows == 0 || row_elems == 0) return;
   const ScatterOp op = static_cast<ScatterOp>(op_i);
-  const int64_t mc = max_chunks(rows, n);
-  char* b = static_cast<char*>(scratch);
-  uint32_t* cnt = reinterpret_cast<uint32_t*>(b);
-  b += align256(rows * 4);
-  uint32_t* off = reinterpret_cast<uint32_t*>(b);
-  b += align256(rows * 4);
-  b += align256(rows * 4);  // reserved
-  uint32_t* chunk_row = reinterpret_cast<uint32_t*>(b);
-  b += align256(mc * 4);
-  uint32_t* total = reinterpret_cast<uint32_t*>(b);
-  b += align256(256);
-  uint32_t* scan_tmp = reinterpret_cast<uint32_t*>(b);
-  b += align256(kScanTile * 4);
-  void* partial = b;
-  hipLaunchKernelGGL(chunk_count, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, seg_end, rows, cnt);
-  exclusive_scan(s, cnt, off, rows, scan_tmp);
-  hipLaunchKernelGGL(chunk_rows, dim3(blocks(rows, 256)), dim3(256), 0, s, cnt, off, rows, chunk_row, total);
-  check("scatter chunk plan");
   const size_t es = dtype_size(t);
   const bool vec = (row_elems * es) % 16 == 0 && (reinterpret_cast<uintptr_t>(operand) % 16 == 0) &&
                    (reinterpret_cast<uintptr_t>(updates) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
-  const dim3 g1(blocks(mc, 4)), g2(blocks(rows, 4)), blk(256);
-#define PJRTX_CHUNKED(TAG, VEC)                                                                                      \
-  do {                                                                                                               \
-    typedef StorageOf<TAG>::T T_;                                                                                    \
-    hipLaunchKernelGGL((scatter_chunk_fold<TAG, VEC>), g1, blk, 0, s, row_elems, op, (const T_*)operand,            \
-                       (const T_*)updates, perm, seg_start, seg_end, cnt, off, chunk_row, total, (T_*)partial,       \
-                       (T_*)out);                                                                                    \
-    hipLaunchKernelGGL((scatter_chunk_combine<TAG, VEC>), g2, blk, 0, s, rows, row_elems, op, cnt, off,             \
-                       (const T_*)partial, (T_*)out);                                                                \
+  ScatterRowsParams p;
+  p.rows = rows;
+  p.row_elems = row_elems;
+  p.hot_wgs = vec && aux ? hot_wgs : 0;
+  // Integer add / max / min: order-free, so hot rows fold in parallel
+  // chunks merged with atomics instead of sequential column chains.
+  const bool int_type = t == DType::kS32 || t == DType::kU32 || t == DType::kS64;
+  const bool chunked = int_type && (op == ScatterOp::kAdd || op == ScatterOp::kMax || op == ScatterOp::kMin);
+  if (p.hot_wgs > 0) {
+    const bool init = chunked && operand != out;
+    hipLaunchKernelGGL(scatter_hot_classify, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, seg_end, rows, h,
+                       init ? static_cast<const uint4*>(operand) : nullptr, init ? static_cast<uint4*>(out) : nullptr,
+                       row_elems * static_cast<int64_t>(es) / 16);
+    check("scatter_hot_classify");
+  }
+  if (p.hot_wgs > 0) {
+    // The hot slices run on the second stream, beside the bulk rows.
+    hcheck(hipEventRecord(fork, s), "hipEventRecord(scatter fork)");
+    hcheck(hipStreamWaitEvent(aux, fork, 0), "hipStreamWaitEvent(scatter fork)");
+  }
+  const dim3 gh(static_cast<unsigned>(p.hot_wgs)), gb(static_cast<unsigned>(blocks(rows, 4))), blk(256);
+#define PJRTX_HOT_OP(TAG, OPV)                                                                                        \
+  hipLaunchKernelGGL((scatter_hot_fold<TAG, OPV>), gh, blk, 0, aux, row_elems, (const StorageOf<TAG>::T*)operand,   \
+                     (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, h, (StorageOf<TAG>::T*)out)
+#define PJRTX_CHUNK_OP(TAG, OPV)                                                                                      \
+  do {                                                                                                                \
+    if constexpr (std::is_integral<StorageOf<TAG>::T>::value && OPV != ScatterOp::kSet && OPV != ScatterOp::kMul)     \
+      hipLaunchKernelGGL((scatter_hot_chunks<StorageOf<TAG>::T, OPV>), gh, blk, 0, aux, row_elems,                    \
+                         (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, h, (StorageOf<TAG>::T*)out);   \
   } while (0)
-#define PJRTX_CHUNKED_T(TAG, V16)            \
-  if (vec) PJRTX_CHUNKED(TAG, V16);          \
-  else PJRTX_CHUNKED(TAG, 1);
+#define PJRTX_ROWS_OP(TAG, V, OPV)                                                                                    \
+  do {                                                                                                                \
+    if (V * sizeof(StorageOf<TAG>::T) == 16 && p.hot_wgs > 0) {                                                      \
+      if (chunked) PJRTX_CHUNK_OP(TAG, OPV);                                                                         \
+      else PJRTX_HOT_OP(TAG, OPV);                                                                                    \
+    }                                                                                                                 \
+    hipLaunchKernelGGL((scatter_rows_fold<TAG, OPV, V>), gb, blk, 0, s, p, (const StorageOf<TAG>::T*)operand,        \
+                       (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, (StorageOf<TAG>::T*)out);        \
+  } while (0)
+#define PJRTX_ROWS_V(TAG, V)                                              \
+  switch (op) {                                                           \
+    case ScatterOp::kAdd: PJRTX_ROWS_OP(TAG, V, ScatterOp::kAdd); break;  \
+    case ScatterOp::kSet: PJRTX_ROWS_OP(TAG, V, ScatterOp::kSet); break;  \
+    case ScatterOp::kMax: PJRTX_ROWS_OP(TAG, V, ScatterOp::kMax); break;  \
+    case ScatterOp::kMin: PJRTX_ROWS_OP(TAG, V, ScatterOp::kMin); break;  \
+    case ScatterOp::kMul: PJRTX_ROWS_OP(TAG, V, ScatterOp::kMul); break;  \
+  }
+#define PJRTX_ROWS_T(TAG, V16)  \
+  if (vec) {                    \
+    PJRTX_ROWS_V(TAG, V16)      \
+  } else {                      \
+    PJRTX_ROWS_V(TAG, 1)        \
+  }
   switch (t) {
-    case DType::kF32: PJRTX_CHUNKED_T(float, 4) break;
-    case DType::kF64: PJRTX_CHUNKED_T(double, 2) break;
-    case DType::kBF16: PJRTX_CHUNKED_T(Bf16Tag, 8) break;
-    case DType::kF16: PJRTX_CHUNKED_T(F16Tag, 8) break;
-    case DType::kS32: PJRTX_CHUNKED_T(int32_t, 4) break;
-    case DType::kU32: PJRTX_CHUNKED_T(uint32_t, 4) break;
-    case DType::kS64: PJRTX_CHUNKED_T(int64_t, 2) break;
+    case DType::kF32: PJRTX_ROWS_T(float, 4) break;
+    case DType::kF64: PJRTX_ROWS_T(double, 2) break;
+    case DType::kBF16: PJRTX_ROWS_T(Bf16Tag, 8) break;
+    case DType::kF16: PJRTX_ROWS_T(F16Tag, 8) break;
+    case DType::kS32: PJRTX_ROWS_T(int32_t, 4) break;
+    case DType::kU32: PJRTX_ROWS_T(uint32_t, 4) break;
+    case DType::kS64: PJRTX_ROWS_T(int64_t, 2) break;
     default: fail(Code::kUnimplemented, std::string("scatter: element type not supported: ") + dtype_name(t));
   }
-#undef PJRTX_CHUNKED_T
-#undef PJRTX_CHUNKED
-  check("scatter_chunk_fold");
+#undef PJRTX_ROWS_T
+#undef PJRTX_ROWS_V
+#undef PJRTX_ROWS_OP
+#undef PJRTX_HOT_OP
+#undef PJRTX_CHUNK_OP
+  check("scatter_rows_fold");
+  if (p.hot_wgs > 0) {
+    hcheck(hipEventRecord(join, aux), "hipEventRecord(scatter join)");
+    hcheck(hipStreamWaitEvent(s, join, 0), "hipStreamWaitEvent(scatter join)");
+  }
 }
 
 void launch_scatter_fold(hipStream_t s, const ScatterFoldParams& p, DType t, const void* operand, const void* updates,

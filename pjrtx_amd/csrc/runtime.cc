@@ -102,6 +102,9 @@ void Allocator::trim() {
 Device::Device(int ordinal) : ordinal_(ordinal), alloc_(ordinal) {
   hip_check(hipSetDevice(ordinal), "hipSetDevice");
   hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  hip_check(hipStreamCreateWithFlags(&aux_stream_, hipStreamNonBlocking), "hipStreamCreate(aux)");
+  hip_check(hipEventCreateWithFlags(&fork_ev_, hipEventDisableTiming), "hipEventCreate(fork)");
+  hip_check(hipEventCreateWithFlags(&join_ev_, hipEventDisableTiming), "hipEventCreate(join)");
   hipDeviceProp_t prop;
   hip_check(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
   arch_ = prop.gcnArchName;

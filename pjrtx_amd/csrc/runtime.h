@@ -109,6 +109,12 @@ class Device {
   // one, and it returns here when the last Event holding it is destroyed.
   hipEvent_t take_event();
   void give_event(hipEvent_t e);
+  // A second stream (default priority) for work that runs beside the main
+  // stream inside one step, and the two events that fork it from and join it
+  // back into the main stream. Created with the device.
+  hipStream_t aux_stream() const { return aux_stream_; }
+  hipEvent_t fork_event() const { return fork_ev_; }
+  hipEvent_t join_event() const { return join_ev_; }
 
  private:
   std::vector<MemRef>* capture_pins_ = nullptr;
@@ -116,6 +122,8 @@ class Device {
   std::vector<hipEvent_t> ev_free_;
   int ordinal_;
   hipStream_t stream_ = nullptr;
+  hipStream_t aux_stream_ = nullptr;
+  hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
   Allocator alloc_;
   std::mutex exec_mu_;
   std::string arch_, name_;

@@ -153,7 +153,8 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   MemRef keys = dev->allocate(n * 4), vals_a = dev->allocate(n * 4);
   MemRef tkeys = dev->allocate(n * 4), tvals = dev->allocate(n * 4);
   MemRef scratch = dev->allocate(radix_sort_scratch_bytes(n));
-  MemRef seg = dev->allocate(static_cast<size_t>(rows) * 8);
+  // seg_start, seg_end, then the 32 hot-class counters: zeroed by one launch.
+  MemRef seg = dev->allocate(static_cast<size_t>(rows) * 8 + 32 * 4);
   uint32_t* K = static_cast<uint32_t*>(keys->ptr);
   uint32_t* V = static_cast<uint32_t*>(vals_a->ptr);
   launch_scatter_keys(s, p, I, K, V);
@@ -162,11 +163,25 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   launch_radix_sort(s, K, V, static_cast<uint32_t*>(tkeys->ptr), static_cast<uint32_t*>(tvals->ptr), scratch->ptr, n, bits);
   uint32_t* seg_start = static_cast<uint32_t*>(seg->ptr);
   uint32_t* seg_end = seg_start + rows;
-  launch_scatter_segments(s, K, n, p.invalid, seg_start, seg_end, rows);
+  uint32_t* hot_counts = seg_end + rows;
+  launch_scatter_segments(s, K, n, p.invalid, seg_start, seg_end, rows, 32);
   if (p.row_mode) {
-    MemRef cs = dev->allocate(scatter_chunk_scratch_bytes(rows, n, p.row_elems, xt.dtype));
-    launch_scatter_chunked(s, rows, p.row_elems, n, static_cast<int>(sop), xt.dtype, X, U, V, seg_start, seg_end,
-                           cs->ptr, out);
+    // Segments longer than kHotMinUpdates fold by column slices on
+    // persistent workgroups (two per CU) on the device's second stream; the
+    // hot list lives in the sort's temporary key array, free again after
+    // the sort.
+    int64_t hot_wgs = 0;
+    ScatterHotList h;
+    if (n > kHotMinUpdates && scatter_hot_list_words(n) <= static_cast<size_t>(n)) {
+      h = scatter_hot_list(n, hot_counts, static_cast<uint32_t*>(tkeys->ptr));
+      const int64_t cols = kHotSliceBytes / static_cast<int64_t>(dtype_size(xt.dtype));
+      const int64_t slices = (p.row_elems + cols - 1) / cols;
+      const int64_t max_items = (n / (kHotMinUpdates + 1)) * slices;
+      hot_wgs = std::min<int64_t>(max_items, 2 * static_cast<int64_t>(dev->compute_units()));
+    }
+    launch_scatter_rows(s, dev->aux_stream(), dev->fork_event(), dev->join_event(), rows, p.row_elems,
+                        static_cast<int>(sop), xt.dtype, X, U, V, seg_start, seg_end, h,
+                        hot_wgs, out);
     return;
   }
   ScatterFoldParams f;

@@ -148,3 +148,42 @@ def test_scatter_f64_and_segment_lengths():
             want[r] += u[j]
     np.testing.assert_array_equal(exact, want)
     np.testing.assert_allclose(ops.scatter_rows_add(x, idx, u), exact, rtol=1e-6)
+
+
+def _bf16_round_py(x: float) -> float:
+    """Nearest-even bf16 rounding of an f32 value, by integer arithmetic on its
+    bits (independent of the numpy helpers)."""
+    import struct
+    u = struct.unpack("<I", struct.pack("<f", x))[0]
+    lsb = (u >> 16) & 1
+    u = ((u + 0x7FFF + lsb) >> 16) << 16
+    return struct.unpack("<f", struct.pack("<I", u & 0xFFFFFFFF))[0]
+
+
+def test_scatter_bf16_sequential_matches_brute_force():
+    # Pure-Python loop: f32 add of the two widened values, then bf16 rounding,
+    # one update at a time in index order.
+    import struct
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 4)).astype(np.float32)
+    u = (0.3 * rng.standard_normal((40, 4))).astype(np.float32)
+    idx = rng.integers(-1, 4, 40).astype(np.int32)  # -1 and 3 are out of bounds
+    xb, ub = ops.f32_to_bf16_bits(x), ops.f32_to_bf16_bits(u)
+    got = ops.bf16_bits_to_f32(ops.scatter_rows_add_bf16_bits(xb, idx, ub))
+    want = ops.bf16_bits_to_f32(xb).astype(np.float64).tolist()
+    uf = ops.bf16_bits_to_f32(ub).tolist()
+    f32 = lambda v: struct.unpack("<f", struct.pack("<f", v))[0]
+    for j, r in enumerate(idx):
+        if 0 <= r < 3:
+            want[r] = [_bf16_round_py(f32(a + b)) for a, b in zip(want[r], uf[j])]
+    np.testing.assert_array_equal(got, np.array(want, np.float32))
+    # Small integers are exact in bf16: the sum is the closed form.
+    xi = ops.f32_to_bf16_bits(np.zeros((2, 3), np.float32))
+    ui = ops.f32_to_bf16_bits(np.ones((10, 3), np.float32))
+    out = ops.bf16_bits_to_f32(ops.scatter_rows_add_bf16_bits(xi, np.array([0] * 7 + [1] * 3), ui))
+    np.testing.assert_array_equal(out, [[7, 7, 7], [3, 3, 3]])
+    # Order matters once rounding bites: 256 + 1 + 1 rounds each +1 away.
+    a = ops.f32_to_bf16_bits(np.array([[256.0]], np.float32))
+    ones = ops.f32_to_bf16_bits(np.array([[1.0], [1.0], [256.0]], np.float32))
+    o1 = ops.bf16_bits_to_f32(ops.scatter_rows_add_bf16_bits(a, np.array([0, 0, 0]), ones))
+    assert o1[0, 0] == 512.0  # 256+1 -> 256, +1 -> 256, +256 -> 512
