@@ -361,6 +361,39 @@ def test_matmul_8192_sampled_rows(client):
     assert_bf16_close(out[rows], want)
 
 
+def test_matmul_8192_own_kernel_sampled_rows(client, monkeypatch):
+    """C3d at full size on the hand-written MFMA kernel (library GEMM off);
+    sampled rows against float64, both ends and tile boundaries."""
+    monkeypatch.setenv("PJRTX_BLASLT", "0")
+    n = 8192
+    rng = np.random.default_rng(9)
+    a = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
+    b_ = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
+    (out,) = run(client, programs.c3_matmul(n, n, n), a, b_, dtypes=["bf16", "bf16"])
+    rows = np.array([0, 1, 255, 256, 4095, 4096, 8190, 8191])
+    want = fb(a[rows]).astype(np.float64) @ fb(b_).astype(np.float64)
+    assert_bf16_close(out[rows], want)
+
+
+def test_attention_full_size_sampled_heads(client):
+    """C3 attention at [8,32,2048,128] (causal, bf16) through the fused
+    kernel; four (batch, head) pairs compared in full (every query tile, the
+    first and the last included) against the oracle's bf16 arithmetic."""
+    B, H, S, D = 8, 32, 2048, 128
+    from bench import randn_bits
+    q = randn_bits((B, H, S, D), 21, 1 / np.sqrt(D))
+    k = randn_bits((B, H, S, D), 22, 1 / np.sqrt(D))
+    v = randn_bits((B, H, S, D), 23, 1 / np.sqrt(D))
+    exe = client.compile(programs.c3_attention(B, H, S, D))
+    steps = json.loads(exe.optimized_program())["steps"]
+    assert any("attention" in str(s_.get("library", "")) for s_ in steps)
+    (out,) = exe(q, k, v, dtypes=["bf16"] * 3)
+    for b_, h in [(0, 0), (3, 17), (5, 31), (7, 31)]:
+        sl = (slice(b_, b_ + 1), slice(h, h + 1))
+        want = fb(ops.attention_bf16(q[sl], k[sl], v[sl], causal=True))
+        assert_bf16_close(out[sl], want)
+
+
 @pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 64), (2, 2, 512, 128)])
 def test_attention_small(client, b, h, s, d):
     rng = np.random.default_rng(s)

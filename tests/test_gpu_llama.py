@@ -36,16 +36,33 @@ def tiny(client):
     return L.LlamaRunner(client, L.TINY, w), O.weights_f32(L.TINY, w)
 
 
+def _first_flip_is_exempt(gpu_toks, ora_toks, ora_logits):
+    """Free-running greedy sequences must be equal; they may part only at a
+    step where the oracle's top-2 margin is within the logit bar (2 x TOL of
+    the logit range), and the comparison ends there (the histories differ
+    afterwards). Returns the step of the parting, or None."""
+    for i, (a, b) in enumerate(zip(gpu_toks, ora_toks)):
+        if int(a) != int(b):
+            ref = np.asarray(ora_logits[i], np.float64)
+            top = np.sort(ref)[::-1]
+            assert top[0] - top[1] <= 2 * TOL * np.abs(ref).max(), (i, a, b, top[:2])
+            return i
+    return None
+
+
 def test_tiny_greedy_decode_matches_oracle(tiny):
     runner, W = tiny
     cfg = L.TINY
-    prompt = L.prompt_tokens(cfg, seed=1)
-    toks, _, logits = runner.generate(prompt, cfg.new_tokens, keep_logits=True)
-    ora_toks, ora_logits = O.generate(cfg, W, prompt, cfg.new_tokens, forced=toks[:-1])
-    for i in range(cfg.new_tokens):
-        _check_step(O.bf16_bits_to_f32(logits[i])[0], ora_logits[i], int(toks[i]))
-    agree = np.mean(toks == ora_toks)
-    assert agree >= 0.9, (toks, ora_toks)
+    for seed in (1, 2, 3):
+        prompt = L.prompt_tokens(cfg, seed=seed)
+        toks, _, logits = runner.generate(prompt, cfg.new_tokens, keep_logits=True)
+        # teacher-forced logits, step by step
+        _, forced_logits = O.generate(cfg, W, prompt, cfg.new_tokens, forced=toks[:-1])
+        for i in range(cfg.new_tokens):
+            _check_step(O.bf16_bits_to_f32(logits[i])[0], forced_logits[i], int(toks[i]))
+        # free-running greedy tokens: equal, up to a margin-exempt parting
+        ora_toks, ora_logits = O.generate(cfg, W, prompt, cfg.new_tokens)
+        _first_flip_is_exempt(toks, ora_toks, ora_logits)
 
 
 def test_tiny_cache_donation(tiny, client):
@@ -126,6 +143,34 @@ def test_full_prefill_and_decode_match_oracle(full):
         top = np.sort(exact)[::-1]
         if top[0] - top[1] > 2 * TOL * scale:
             assert int(toks[i]) == int(np.argmax(exact))
+
+
+def test_full_decode_128_steps_teacher_forced(full):
+    """All 128 decode steps of C5 at full size, teacher-forced: at every step
+    the GPU's logits are within twice the bar of the bf16 restatement fed the
+    same tokens, the GPU's token is the argmax of its own logits, and it
+    differs from the restatement's argmax only where the restatement's top-2
+    margin is within that bar. The steps where it differs are printed (and
+    recorded in the design notes)."""
+    runner, wbits = full
+    cfg = L.FULL
+    W = O.weights_f32(cfg, wbits)
+    prompt = L.prompt_tokens(cfg, seed=1)
+    steps = cfg.new_tokens
+    toks, _, logits = runner.generate(prompt, steps, keep_logits=True)
+    _, ora_logits = O.generate(cfg, W, prompt, steps, forced=toks[:-1])
+    flips = []
+    for i in range(steps):
+        g = O.bf16_bits_to_f32(logits[i])[0].astype(np.float64)
+        ref = np.asarray(ora_logits[i], np.float64)
+        scale = float(np.abs(ref).max())
+        assert np.abs(g - ref).max() <= 2 * TOL * scale, (i, np.abs(g - ref).max(), scale)
+        assert int(toks[i]) == int(np.argmax(g))
+        if int(toks[i]) != int(np.argmax(ref)):
+            top = np.sort(ref)[::-1]
+            assert top[0] - top[1] <= 2 * TOL * scale, (i, top[:2])
+            flips.append(i)
+    print(f"C5 128-step teacher-forced greedy flips (margin-exempt): {flips}")
 
 
 def test_full_decode_step_equals_longer_prefill(full, client):
