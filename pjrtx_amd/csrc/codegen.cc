@@ -627,6 +627,7 @@ void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, boo
     ++o;
   }
   if (with_scratch) out_ << ", unsigned char* __restrict__ scratch";
+  if (with_scratch && s.fused_combine) out_ << ", const uint32_t fused_mode";
   out_ << ") {\n";
 }
 
@@ -762,9 +763,18 @@ void KernelGen::reduce(Step& s) {
   const int vec = s.vec;
 
   std::ostringstream head;  // before the element loop
+  bool epilogue_then_combine = false;  // fused combine: also emit the `_combine` fallback kernel
+  std::string combine_fallback_body;
   if (s.row_schedule) {
-    head << "const idx_t row = (idx_t)blockIdx.x / " << s.splits << "u;\n";
-    head << "const idx_t split = (idx_t)blockIdx.x - row * " << s.splits << "u;\n";
+    if (s.fused_combine) {
+      // Workgroup b runs on XCD b % 8 and rows % 8 == 0: with row = b % rows
+      // every split of a row lands on the same XCD (one L2).
+      head << "const idx_t row = (idx_t)blockIdx.x % " << s.rows << "u;\n";
+      head << "const idx_t split = (idx_t)blockIdx.x / " << s.rows << "u;\n";
+    } else {
+      head << "const idx_t row = (idx_t)blockIdx.x / " << s.splits << "u;\n";
+      head << "const idx_t split = (idx_t)blockIdx.x - row * " << s.splits << "u;\n";
+    }
     head << "const idx_t c0 = split * " << s.chunk << "u;\n";
     head << "const idx_t c1 = (c0 + " << s.chunk << "u < " << s.row_len << "u) ? c0 + " << s.chunk << "u : "
          << s.row_len << "u;\n";
@@ -1180,28 +1190,39 @@ void KernelGen::reduce(Step& s) {
     // Fold of a row's partials by one wavefront, lane k reading split k
     // (wavefront all-reduce over the lanes: a fixed order, so the result does
     // not depend on which workgroup folds or on the launch).
-    auto fold_partials = [&]() {
+    auto fold_partials = [&](bool coherent) {
+      // coherent: loads that skip this CU's L1 and read the XCD's L2, where
+      // the other workgroups' partial stores have landed.
+      auto ld = [&](const std::string& addr) {
+        return coherent ? "__hip_atomic_load(&" + addr + ", __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)" : addr;
+      };
       for (size_t r = 0; r < accs.size(); ++r) {
         const Accum& a = accs[r];
         const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
         out_ << a.v << " = " << identity_of(a.kind, a.vt, a.acc_t) << ";\n";
         if (am) out_ << a.i << " = " << aimax << ";\n";
         out_ << "if (lane < " << s.splits << "u) {\n";
-        out_ << "const uint64_t* slot = reinterpret_cast<const uint64_t*>(scratch + " << offs[r] << "u);\n";
-        out_ << "const uint64_t bits = slot[row * " << s.splits << "u + lane];\n";
+        out_ << "uint64_t* slot = reinterpret_cast<uint64_t*>(scratch + " << offs[r] << "u);\n";
+        out_ << "const uint64_t bits = " << ld("slot[row * " + std::to_string(s.splits) + "u + lane]") << ";\n";
         out_ << "__builtin_memcpy(&" << a.v << ", &bits, sizeof(" << a.v << "));\n";
-        if (am) out_ << a.i << " = (" << ait << ")slot[" << slots << "u + row * " << s.splits << "u + lane];\n";
+        if (am)
+          out_ << a.i << " = (" << ait << ")"
+               << ld("slot[" + std::to_string(slots) + "u + row * " + std::to_string(s.splits) + "u + lane]") << ";\n";
         out_ << "}\n";
       }
       wave_reduce(false);
       out_ << "if (lane != 0) return;\n";
     };
     if (split && s.fused_combine) {
-      // Thread 0 stores this split's partials, publishes them with a
-      // device-scope release fence and counts the row's arrivals; the
-      // workgroup that arrives last (acquire fence) folds every split of the
-      // row with wavefront 0 and puts the counter back to zero for the next
-      // launch. No workgroup waits for another.
+      // Thread 0 stores this split's partials. In fused mode (the device
+      // places workgroup b on XCD b % 8, probed at start-up) every split of
+      // the row runs on this XCD: once the stores are acknowledged by its L2
+      // (s_waitcnt), an L2 atomic counts the row's arrivals, and the
+      // workgroup that arrives last folds every split with wavefront 0,
+      // reading the slots past its L1, and puts the counter back to zero.
+      // No device-scope fence (an L2 write-back on this GPU) is needed, and
+      // no workgroup waits for another. Otherwise (fused_mode 0) the
+      // partials stay for the `_combine` kernel launched next.
       out_ << "__shared__ uint32_t last_arrival;\n";
       out_ << "if (threadIdx.x == 0) {\n";
       for (size_t r = 0; r < accs.size(); ++r) {
@@ -1213,16 +1234,38 @@ void KernelGen::reduce(Step& s) {
           out_ << "slot[" << slots << "u + row * " << s.splits << "u + split] = (uint64_t)" << a.i << ";\n";
         out_ << "}\n";
       }
-      out_ << "__threadfence();\n";
-      out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + row;\n";
-      out_ << "const uint32_t last = atomicAdd(ctr, 1u) == " << s.splits - 1 << "u;\n";
-      out_ << "if (last) atomicExch(ctr, 0u);\n";
+      out_ << "uint32_t last = 0u;\n";
+      out_ << "if (fused_mode) {\n";
+      out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
+      // one counter per 128-byte line: rows do not contend for a line
+      out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + row * 32u;\n";
+      out_ << "last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " << s.splits - 1
+           << "u;\n";
+      out_ << "if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+      out_ << "}\n";
       out_ << "last_arrival = last;\n";
       out_ << "}\n__syncthreads();\n";
       out_ << "if (!last_arrival || threadIdx.x >= 64) return;\n";
-      out_ << "__threadfence();\n";
       out_ << "const uint32_t lane = threadIdx.x;\n";
-      fold_partials();
+      fold_partials(true);
+      epilogue_then_combine = true;
+      {
+        // text of the fallback combine kernel's fold (emitted after the epilogue)
+        std::ostringstream saved;
+        saved << out_.str();
+        out_.str("");
+        out_.clear();
+        for (size_t r = 0; r < accs.size(); ++r) {
+          const Accum& a = accs[r];
+          out_ << a.acc_t << " " << a.v << ";\n";
+          if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << ait << " " << a.i << ";\n";
+        }
+        fold_partials(false);
+        combine_fallback_body = out_.str();
+        out_.str("");
+        out_.clear();
+        out_ << saved.str();
+      }
     } else if (split) {
       // Partials of this split go to scratch with plain stores; the
       // `<name>_combine` kernel (launched next on the same stream) folds
@@ -1250,7 +1293,7 @@ void KernelGen::reduce(Step& s) {
         out_ << a.acc_t << " " << a.v << ";\n";
         if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << ait << " " << a.i << ";\n";
       }
-      fold_partials();
+      fold_partials(false);
     } else {
       out_ << "if (threadIdx.x != 0) return;\n";
     }
@@ -1320,10 +1363,23 @@ void KernelGen::reduce(Step& s) {
   }
   std::vector<std::string> outs;
   for (int v : s.outputs) outs.push_back(e.value(v, oid));
-  out_ << "{\n" << fin.str() << e.body.str();
+  std::ostringstream epi;
+  epi << "{\n" << fin.str() << e.body.str();
   for (size_t o = 0; o < s.outputs.size(); ++o)
-    out_ << "out" << o << "[row] = " << to_storage(prog_.type(s.outputs[o]).dtype, outs[o]) << ";\n";
-  out_ << "}\n}\n\n";
+    epi << "out" << o << "[row] = " << to_storage(prog_.type(s.outputs[o]).dtype, outs[o]) << ";\n";
+  epi << "}\n}\n\n";
+  out_ << epi.str();
+  if (epilogue_then_combine) {
+    // The `_combine` kernel of the fallback (fused_mode 0): one wavefront per
+    // row, lane k reads split k; the same epilogue.
+    signature(s, &ptr_of, true, "_combine");
+    out_ << "typedef " << it << " idx_t;\n";
+    out_ << "const idx_t row = (idx_t)blockIdx.x * 4u + (threadIdx.x >> 6);\n";
+    out_ << "if (row >= " << s.rows << "u) return;\n";
+    out_ << "const uint32_t lane = threadIdx.x & 63u;\n";
+    out_ << combine_fallback_body;
+    out_ << epi.str();
+  }
 }
 
 // Row-fused kernel: one workgroup (or one wave) per row. Each reduce phase

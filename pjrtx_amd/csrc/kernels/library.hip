@@ -13,6 +13,8 @@
 // executable_metal_graph_generation.zig:8-135 concatenate).
 #include <hip/hip_runtime.h>
 
+#include <vector>
+
 #include <cstring>
 
 #include "common.h"
@@ -329,6 +331,36 @@ __global__ void __launch_bounds__(256) copy_segments_kernel(CopySegments c) {
   }
 }
 }  // namespace
+
+namespace {
+// Records the XCD (hardware register XCC_ID) each workgroup runs on.
+__global__ void __launch_bounds__(64) xcc_probe_kernel(uint32_t* __restrict__ out) {
+  if (threadIdx.x == 0) {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    out[blockIdx.x] = x & 0xfu;
+  }
+}
+}  // namespace
+
+bool probe_xcd_round_robin(hipStream_t s) {
+  constexpr int kProbeBlocks = 1024;
+  uint32_t* d = nullptr;
+  if (hipMalloc(&d, kProbeBlocks * sizeof(uint32_t)) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbeBlocks), dim3(64), 0, s, d);
+  std::vector<uint32_t> h(kProbeBlocks, 0xffffffffu);
+  bool ok = hipGetLastError() == hipSuccess &&
+            hipMemcpyAsync(h.data(), d, kProbeBlocks * sizeof(uint32_t), hipMemcpyDeviceToHost, s) == hipSuccess &&
+            hipStreamSynchronize(s) == hipSuccess;
+  (void)hipFree(d);
+  (void)hipGetLastError();
+  // Workgroups b and b % 8 must share an XCD (one XCD: trivially).
+  for (int b = 0; ok && b < kProbeBlocks; ++b) ok = h[b] == h[b % 8];
+  return ok;
+}
 
 void launch_copy_segments(hipStream_t s, const CopySegments& c) {
   if (c.n <= 0) return;

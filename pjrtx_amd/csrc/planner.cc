@@ -1144,13 +1144,18 @@ void Planner::shape_reduce(Step* s) {
     size_t per_slot = 0;
     for (const ReduceSpec& r : s->reduces) per_slot += (r.kind == ReducerKind::kArgMax || r.kind == ReducerKind::kArgMin) ? 16 : 8;
     s->scratch_bytes = static_cast<size_t>(rows * splits) * per_slot;
-    if (opts_.reduce_fused_combine) {
-      // One 32-bit arrival counter per row after the 8-byte slots.
+    // The `_combine` kernel folds the partials in a second launch; with a
+    // fused combine (rows a multiple of 8, so that every split of a row runs
+    // on one XCD) the last-arriving workgroup of each row folds them inside
+    // the same launch, and the combine kernel remains the fallback for a
+    // device that does not place workgroups round-robin on its XCDs.
+    s->combine_grid = static_cast<uint32_t>((rows + 3) / 4);
+    if (opts_.reduce_fused_combine && rows % 8 == 0) {
+      // One 32-bit arrival counter per row, each on a 128-byte line of its
+      // own, after the 8-byte slots.
       s->fused_combine = true;
-      s->counter_offset = s->scratch_bytes;
-      s->scratch_bytes += static_cast<size_t>(rows) * 4;
-    } else {
-      s->combine_grid = static_cast<uint32_t>((rows + 3) / 4);
+      s->counter_offset = (s->scratch_bytes + 127) / 128 * 128;
+      s->scratch_bytes = s->counter_offset + static_cast<size_t>(rows) * 128;
     }
   }
 }

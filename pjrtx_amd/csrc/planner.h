@@ -148,7 +148,7 @@ struct PlanOptions {
   // write-back, needed because the XCDs' L2s are not coherent) costs more
   // than the launch it saves (64x128256 bf16 argmax + f16 reductions:
   // 16.0 us fused vs 4.3 + 2.6 us with the combine kernel).
-  bool reduce_fused_combine = env_int("PJRTX_REDUCE_FUSED_COMBINE", 0) != 0;
+  bool reduce_fused_combine = env_int("PJRTX_REDUCE_FUSED_COMBINE", 1) != 0;
   bool fuse_siblings = true;
   bool fuse_epilogues = true;
   // Row chains (reduce -> reduce/loop over the same rows) become one kernel

@@ -105,6 +105,7 @@ Device::Device(int ordinal) : ordinal_(ordinal), alloc_(ordinal) {
   hip_check(hipStreamCreateWithFlags(&aux_stream_, hipStreamNonBlocking), "hipStreamCreate(aux)");
   hip_check(hipEventCreateWithFlags(&fork_ev_, hipEventDisableTiming), "hipEventCreate(fork)");
   hip_check(hipEventCreateWithFlags(&join_ev_, hipEventDisableTiming), "hipEventCreate(join)");
+  xcd_round_robin_ = env_int("PJRTX_XCD_LOCAL", 1) != 0 && probe_xcd_round_robin(stream_);
   hipDeviceProp_t prop;
   hip_check(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
   arch_ = prop.gcnArchName;
@@ -677,6 +678,10 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       for (int v : s.inputs) ptrs.push_back(vals[v] ? vals[v]->ptr : nullptr);
       for (int v : s.outputs) ptrs.push_back(vals[v]->ptr);
       MemRef arena_scratch;
+      // A fused combine folds the partials inside the main launch when the
+      // device places workgroups round-robin on its XCDs; otherwise the
+      // `_combine` kernel runs after it.
+      const uint32_t fused_mode = s.fused_combine && dev->xcd_round_robin() ? 1u : 0u;
       if (s.scratch_bytes && thread_arena() && phase != 1) {
         // Allocation-free execute: partial slots from the fixed block; the
         // arrival counters of a one-launch fold must start at zero.
@@ -692,13 +697,14 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       }
       std::vector<void*> args(ptrs.size());
       for (size_t k = 0; k < ptrs.size(); ++k) args[k] = &ptrs[k];
+      if (s.fused_combine) args.push_back(const_cast<uint32_t*>(&fused_mode));
       if (phase != 1) {
         hip_check(hipModuleLaunchKernel(L->funcs[si], s.grid, 1, 1, s.block, 1, 1, 0, dev->stream(), args.data(),
                                         nullptr),
                   "hipModuleLaunchKernel");
         stats_.kernel_launches++;
       }
-      if (s.combine_grid && phase != 0) {
+      if (s.combine_grid && phase != 0 && !fused_mode) {
         // Second pass of a split reduction: same arguments, one wave per row.
         hip_check(hipModuleLaunchKernel(L->combine_funcs[si], s.combine_grid, 1, 1, 256, 1, 1, 0, dev->stream(),
                                         args.data(), nullptr),
@@ -1033,7 +1039,7 @@ std::vector<std::string> Executable::unit_names() const {
       out.push_back("-");
     } else {
       out.push_back(st.name);
-      if (st.combine_grid) out.push_back(st.name + "_combine");
+      if (st.combine_grid && !st.fused_combine) out.push_back(st.name + "_combine");
     }
   }
   return out;
@@ -1062,7 +1068,7 @@ std::vector<double> Executable::time_steps(Device* dev, const std::vector<Buffer
   for (size_t si = 0; si < plan_.steps.size(); ++si) {
     const Step& st = plan_.steps[si];
     run_step(L, si, vals);  // warm and produce outputs for later steps
-    bool split = st.kind != StepKind::kLibrary && st.kind != StepKind::kAlias && st.combine_grid;
+    bool split = st.kind != StepKind::kLibrary && st.kind != StepKind::kAlias && st.combine_grid && !st.fused_combine;
     if (split) {
       timed(si, 0);
       timed(si, 1);

@@ -113,6 +113,9 @@ class Device {
   // stream inside one step, and the two events that fork it from and join it
   // back into the main stream. Created with the device.
   hipStream_t aux_stream() const { return aux_stream_; }
+  // Workgroup b of a launch runs on the XCD of workgroup b % 8 (probed when
+  // the device is opened).
+  bool xcd_round_robin() const { return xcd_round_robin_; }
   hipEvent_t fork_event() const { return fork_ev_; }
   hipEvent_t join_event() const { return join_ev_; }
 
@@ -124,6 +127,7 @@ class Device {
   hipStream_t stream_ = nullptr;
   hipStream_t aux_stream_ = nullptr;
   hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
+  bool xcd_round_robin_ = false;
   Allocator alloc_;
   std::mutex exec_mu_;
   std::string arch_, name_;

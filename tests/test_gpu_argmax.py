@@ -118,23 +118,24 @@ def test_c2_shape_winner_everywhere(client):
     check(client, bits, "max")
 
 
-def test_fused_combine_matches_combine_kernel(client, monkeypatch):
-    """Split rows folded by the last-arriving workgroup
-    (PJRTX_REDUCE_FUSED_COMBINE=1) give the same bits as the separate combine
-    kernel (the default),
-    on every one of several back-to-back executions and graph replays (the
-    per-row arrival counters are put back to zero by each launch), for the
-    argmax, f16 sum, max and min of the benchmark's program."""
+@pytest.mark.parametrize("rows,n", [(64, 128256), (24, 50000)])
+def test_fused_combine_matches_combine_kernel(client, monkeypatch, rows, n):
+    """Split rows folded by the last-arriving workgroup of each row (the
+    default when the row count is a multiple of 8: every split of a row runs
+    on one XCD) give the same bits as the separate combine kernel
+    (PJRTX_REDUCE_FUSED_COMBINE=0), on every one of several back-to-back
+    executions (the per-row arrival counters are put back to zero by each
+    launch), for the argmax, f16 sum, max and min of the benchmark's program."""
     from pjrtx_amd import programs
-    rows, n = 64, 128256
     bits = ops.f32_to_bf16_bits(np.random.default_rng(21).standard_normal((rows, n)).astype(np.float32))
     text = programs.c2_argmax_f16_reductions(rows, n)
     monkeypatch.setenv("PJRTX_REDUCE_FUSED_COMBINE", "0")
     sep = client.compile(text)
     want = sep(bits, dtypes=["bf16"])
-    monkeypatch.setenv("PJRTX_REDUCE_FUSED_COMBINE", "1")
+    monkeypatch.delenv("PJRTX_REDUCE_FUSED_COMBINE")
     fused = client.compile(text)
     assert "_combine" not in " ".join(fused.step_names())
+    assert "_combine" in " ".join(sep.step_names())
     want_idx = ops.argmax_rows(ops.bf16_bits_to_f32(bits))[1]
     np.testing.assert_array_equal(want[1], want_idx)
     for _ in range(6):
