@@ -131,6 +131,10 @@ class Writer {
   // them is the current row (the planner checks this), so they read as the
   // named variable.
   std::map<int, std::string> row_scalar;
+  // Values held in LDS by the enclosing kernel (a GEMV's results in its
+  // epilogue): the function maps a linear index into the value to the
+  // expression that reads it.
+  std::map<int, std::function<std::string(const std::string&)>> lds_value;
 
   int add_index(Idx idx) {
     idxs_.push_back(std::move(idx));
@@ -217,6 +221,12 @@ std::string Writer::value(int v, int id) {
   auto m = memo_.find(key);
   if (m != memo_.end()) return m->second;
   std::string out;
+  auto lv = lds_value.find(v);
+  if (lv != lds_value.end()) {
+    out = define(prog_.type(v).dtype, lv->second(lin_of(id)));
+    memo_[key] = out;
+    return out;
+  }
   auto p = ptr_of_.find(v);
   const DType t = prog_.type(v).dtype;
   if (p != ptr_of_.end()) {
@@ -594,6 +604,7 @@ class KernelGen {
   void loop(Step& s);
   void reduce(Step& s);
   void row_fused(Step& s);
+  void gemv(Step& s);
 
  private:
   const Program& prog_;
@@ -609,6 +620,12 @@ class KernelGen {
     return m < (int64_t(1) << 31) ? "uint32_t" : "uint64_t";
   }
   void signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch, const char* suffix = "");
+  struct RowTarget {
+    std::string lds;  // LDS float array receiving the row (empty: the kernel's outputs)
+    std::string row;  // row index expression when `lds` is set
+  };
+  void row_body(Step& s, std::map<int, std::string>& ptr_of, const RowTarget& t);
+  void gemv_epilogue(Step& s, const std::map<int, std::string>& ptr_of, const std::string& seg);
 };
 
 void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch, const char* suffix) {
@@ -1396,6 +1413,16 @@ constexpr int64_t kRowCacheSweeps = 16;
 void KernelGen::row_fused(Step& s) {
   std::map<int, std::string> ptr_of;
   signature(s, &ptr_of, false);
+  row_body(s, ptr_of, RowTarget());
+  out_ << "}\n\n";
+}
+
+// The phases of a row-fused step for one row. By default the row is the
+// workgroup's (or the wave's) and the outputs go to the kernel's `out`
+// pointers; with `t.lds` the row is `t.row`, the block is one workgroup of
+// 256 threads, and the final phase writes the row as float into the LDS
+// array `t.lds` at t.row * row_len (a GEMV prologue).
+void KernelGen::row_body(Step& s, std::map<int, std::string>& ptr_of, const RowTarget& t) {
   const std::string it = idx_type(s);
   out_ << "typedef " << it << " idx_t;\n";
   const Dims& shape = s.reduce_operand_shape;
@@ -1405,10 +1432,12 @@ void KernelGen::row_fused(Step& s) {
   const int vec = s.vec;
   const int64_t row_len = s.row_len;
   const int64_t n_all = num_elements(shape);
-  const bool wpr = s.wave_per_row;
+  const bool wpr = s.wave_per_row && t.lds.empty();
   const int span = (wpr ? 64 : 256) * vec;     // elements per sweep of the row
   const std::string tix = wpr ? "(threadIdx.x & 63u)" : "threadIdx.x";
-  if (wpr) {
+  if (!t.lds.empty()) {
+    out_ << "const idx_t row = (idx_t)(" << t.row << ");\n";
+  } else if (wpr) {
     out_ << "const idx_t row = (idx_t)blockIdx.x * 4u + (threadIdx.x >> 6);\n";
     out_ << "if (row >= " << s.rows << "u) return;\n";  // whole wave: no barriers follow
   } else {
@@ -1587,7 +1616,7 @@ void KernelGen::row_fused(Step& s) {
         scalars[v] = name;
       }
       out_ << decl.str() << "{\n" << fin.str() << e.body.str() << assign.str() << "}\n";
-      for (size_t o = 0; o < s.outputs.size(); ++o)
+      for (size_t o = 0; o < s.outputs.size() && t.lds.empty(); ++o)
         if (scalars.count(s.outputs[o]) && prog_.type(s.outputs[o]).dims == kept &&
             std::find(ph.outputs.begin(), ph.outputs.end(), s.outputs[o]) != ph.outputs.end())
           out_ << "if (" << tix << " == 0) out" << o << "[row] = "
@@ -1610,14 +1639,317 @@ void KernelGen::row_fused(Step& s) {
         out_ << "res" << o << "[j] = " << to_storage(prog_.type(s.outputs[o]).dtype, expr) << ";\n";
       out_ << "}\n";
       for (auto& [o, expr] : outs) {
-        const DType t = prog_.type(s.outputs[o]).dtype;
-        out_ << "stv<" << dtype_storage_ctype(t) << ", " << vec << ">(out" << o << ", row * " << row_len
+        const DType ot = prog_.type(s.outputs[o]).dtype;
+        if (!t.lds.empty()) {
+          out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) " << t.lds << "[row * " << row_len
+               << "u + c + j] = " << from_storage(ot, "res" + std::to_string(o) + "[j]") << ";\n";
+          continue;
+        }
+        out_ << "stv<" << dtype_storage_ctype(ot) << ", " << vec << ">(out" << o << ", row * " << row_len
              << "u + c, res" << o << ", 0u, true);\n";
       }
       sweep_close(out_);
     }
   }
+}
+
+// ----------------------------------------------------------------------------
+// Decode GEMV (kGemv): Y_g[m][n] = sum_k X[m][k] * W_g[k][n] for the members
+// g of the step, W_g [K][N_g] 16-bit with N contiguous, X [M][K].
+//
+// Workgroup b (256 threads) belongs to segment (b % 8) + 8 * ((b / 8) / wps)
+// and is the (b / 8) % wps-th of its segment's wps workgroups: all of a
+// segment's workgroups have the same b % 8, which the device maps to one XCD
+// (probed at start-up; `fused_mode` says so). A workgroup owns `cols`
+// columns of one member over one chunk of K rows. Lanes take 16-byte pieces
+// (8 columns) of a row, cols / 8 lanes per row, so a wave reads 64 / (cols / 8)
+// rows at once and each lane keeps `depth` rows in flight. X (or the prologue
+// that produces it) is staged in LDS as float. The tile's column sums fold
+// over the row lanes by xor shuffles and over the 4 waves in wave order.
+//
+// Unless a tile is the whole result (direct: one K chunk, no epilogue), wave
+// 0 stores the tile's partial sums to scratch, waits until its L2 has them,
+// and counts the segment's arrivals with an L2 atomic; the last workgroup of
+// the segment folds every partial in K-chunk order (reads past its L1), rounds
+// to the result type, adds the residual, stores the results that are read
+// elsewhere, keeps the segment's results in LDS, and evaluates the epilogue
+// loop's elements of the segment from them. The fold order is fixed, so the
+// result does not depend on which workgroup arrives last. Without the XCD
+// placement (fused_mode 0) agent-scope fences publish the partials instead.
+void KernelGen::gemv(Step& s) {
+  const GemvSpec& g = s.gemv;
+  std::map<int, std::string> ptr_of;
+  signature(s, &ptr_of, !g.direct);
+  const int G = static_cast<int>(g.dots.size());
+  const int M = g.M;
+  const int64_t K = g.K;
+  const int C = g.cols, LPR = C / 8, RPW = 64 / LPR, RS = 4 * RPW, D = g.depth;
+  const int64_t iters = (g.kchunk + RS * D - 1) / (RS * D);
+  const DType wt = prog_.type(prog_.ops[g.dots[0]].operands[1]).dtype;
+  const bool f16 = wt == DType::kF16;
+  const DType rt = prog_.type(g.result[0]).dtype;
+  const bool pro = !s.prologue.empty();
+  const int64_t XS = pro ? K : g.kchunk;
+  const int64_t S = g.seg_cols;
+  const int64_t tps = S / C;
+  std::vector<int64_t> N(G), tile0(G + 1, 0);
+  for (int m = 0; m < G; ++m) {
+    N[m] = prog_.type(g.result[m]).dims[1];
+    tile0[m + 1] = tile0[m] + (N[m] + C - 1) / C;
+  }
+  auto out_of = [&](int v) {
+    for (size_t o = 0; o < s.outputs.size(); ++o)
+      if (s.outputs[o] == v) return "out" + std::to_string(o);
+    return std::string();
+  };
+  auto by_member = [&](const std::function<std::string(int)>& f) {  // gv_g == 0 ? f(0) : ...
+    std::string e = f(G - 1);
+    for (int m = G - 2; m >= 0; --m) e = "(gv_g == " + std::to_string(m) + "u ? " + f(m) + " : " + e + ")";
+    return e;
+  };
+  out_ << "typedef uint32_t idx_t;\n";
+  out_ << "__shared__ float gv_xs[" << M * XS << "];\n";
+  out_ << "__shared__ float gv_red[4][" << M << "][" << C << "];\n";
+  if (g.joint) out_ << "__shared__ float gv_ys[" << G * M * S << "];\n";
+  if (!g.direct) out_ << "__shared__ uint32_t gv_last;\n";
+  out_ << "const uint32_t gv_lane = threadIdx.x & 63u, gv_wave = threadIdx.x >> 6;\n";
+  out_ << "const uint32_t gv_jj = blockIdx.x >> 3;\n";
+  out_ << "const uint32_t gv_seg = (blockIdx.x & 7u) + 8u * (gv_jj / " << g.wps << "u);\n";
+  out_ << "const uint32_t gv_w = gv_jj % " << g.wps << "u;\n";
+  out_ << "if (gv_seg >= " << g.nseg << "u) return;\n";
+  out_ << "const uint32_t gv_ks = gv_w % " << g.ksplit << "u;\n";
+  if (g.joint) {
+    out_ << "const uint32_t gv_tg = gv_w / " << g.ksplit << "u;\n";
+    out_ << "const uint32_t gv_g = gv_tg / " << tps << "u;\n";
+    out_ << "const uint32_t gv_col0 = gv_seg * " << S << "u + (gv_tg % " << tps << "u) * " << C << "u;\n";
+  } else {
+    out_ << "uint32_t gv_g = 0u;\n";
+    for (int m = 1; m < G; ++m) out_ << "if (gv_seg >= " << tile0[m] << "u) gv_g = " << m << "u;\n";
+    out_ << "const uint32_t gv_col0 = (gv_seg - " << by_member([&](int m) { return std::to_string(tile0[m]) + "u"; })
+         << ") * " << C << "u;\n";
+  }
+  out_ << "const uint32_t gv_N = " << by_member([&](int m) { return std::to_string(N[m]) + "u"; }) << ";\n";
+  out_ << "const uint16_t* gv_W = " << by_member([&](int m) { return ptr_of.at(prog_.ops[g.dots[m]].operands[1]); })
+       << ";\n";
+  out_ << "const uint32_t gv_k0 = gv_ks * " << g.kchunk << "u;\n";
+  out_ << "const uint32_t gv_k1 = gv_k0 + " << g.kchunk << "u < " << K << "u ? gv_k0 + " << g.kchunk << "u : " << K
+       << "u;\n";
+  out_ << "const uint32_t gv_rg = gv_lane / " << LPR << "u, gv_cc = gv_lane % " << LPR << "u;\n";
+  out_ << "const uint32_t gv_c = gv_col0 + gv_cc * 8u;\n";
+  out_ << "const bool gv_cok = gv_c < gv_N;\n";
+  out_ << "const uint32_t gv_r0 = gv_k0 + gv_wave * " << RPW << "u + gv_rg;\n";
+  out_ << "const uint16_t* gv_wp = gv_W + (size_t)gv_r0 * gv_N + gv_c;\n";
+  // First batch of weight rows in flight before X is staged.
+  auto load_batch = [&](const std::string& dst, const std::string& it) {
+    out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) {\n";
+    out_ << "const uint32_t r = gv_r0 + (" << it << " * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
+    out_ << dst << "[i] = (gv_cok && r < gv_k1) ? gv_load16(gv_wp + (size_t)(r - gv_r0) * gv_N) : gv_u32x4{0u, 0u, 0u, 0u};\n";
+    out_ << "}\n";
+  };
+  out_ << "gv_u32x4 gv_wv[" << D << "];\n";
+  load_batch("gv_wv", "0u");
+  if (pro) {
+    Step& P = s.prologue[0];
+    out_ << "for (uint32_t gv_prow = 0; gv_prow < " << M << "u; ++gv_prow) {\n";
+    RowTarget t;
+    t.lds = "gv_xs";
+    t.row = "gv_prow";
+    row_body(P, ptr_of, t);
+    out_ << "__syncthreads();\n}\n";
+  } else {
+    const std::string X = ptr_of.at(g.x);
+    out_ << "for (uint32_t i = threadIdx.x; i < " << M * g.kchunk << "u; i += 256u) {\n";
+    out_ << "const uint32_t m = i / " << g.kchunk << "u, k = gv_k0 + i % " << g.kchunk << "u;\n";
+    out_ << "gv_xs[i] = k < " << K << "u ? " << load_expr(wt, X, "m * " + std::to_string(K) + "u + k") << " : 0.0f;\n";
+    out_ << "}\n__syncthreads();\n";
+  }
+  out_ << "float gv_acc[" << M << "][8];\n";
+  out_ << "#pragma unroll\nfor (int m = 0; m < " << M << "; ++m)\n#pragma unroll\nfor (int e = 0; e < 8; ++e) gv_acc[m][e] = 0.0f;\n";
+  out_ << "#pragma unroll\nfor (uint32_t it = 0; it < " << iters << "u; ++it) {\n";
+  out_ << "gv_u32x4 gv_nx[" << D << "];\n";
+  out_ << "if (it + 1u < " << iters << "u) {\n";
+  load_batch("gv_nx", "(it + 1u)");
+  out_ << "}\n";
+  out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) {\n";
+  out_ << "const uint32_t r = gv_r0 + (it * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
+  out_ << "if (r < gv_k1) {\n";
+  out_ << "#pragma unroll\nfor (int m = 0; m < " << M << "; ++m) gv_fma8<" << (f16 ? "true" : "false")
+       << ">(gv_acc[m], gv_xs[m * " << XS << "u + r" << (pro ? "" : " - gv_k0") << "], gv_wv[i]);\n";
+  out_ << "}\n}\n";
+  out_ << "if (it + 1u < " << iters << "u) {\n#pragma unroll\nfor (int i = 0; i < " << D
+       << "; ++i) gv_wv[i] = gv_nx[i];\n}\n";
+  out_ << "}\n";
+  // Fold the row lanes (xor over the row-group bits), then the waves.
+  out_ << "#pragma unroll\nfor (int m = 0; m < " << M << "; ++m)\n#pragma unroll\nfor (int e = 0; e < 8; ++e) {\n";
+  out_ << "float v = gv_acc[m][e];\n";
+  for (int sh = LPR; sh < 64; sh <<= 1) out_ << "v += wave_shfl_xor(v, " << sh << ");\n";
+  out_ << "gv_acc[m][e] = v;\n}\n";
+  out_ << "if (gv_rg == 0u) {\n#pragma unroll\nfor (int m = 0; m < " << M
+       << "; ++m)\n#pragma unroll\nfor (int e = 0; e < 8; ++e) gv_red[gv_wave][m][gv_cc * 8u + e] = gv_acc[m][e];\n}\n";
+  out_ << "__syncthreads();\n";
+  auto member_value = [&](const std::string& m_expr, const std::string& col, const std::string& sum, int m) {
+    // rounded product, plus the residual when the member has one
+    std::string y = round_to(rt, sum);
+    if (g.add[m] >= 0) {
+      const std::string a = load_expr(rt, ptr_of.at(g.add[m]), m_expr + " * " + std::to_string(N[m]) + "u + " + col);
+      y = round_to(rt, a + " + " + y);
+    }
+    return y;
+  };
+  if (g.direct) {
+    out_ << "for (uint32_t i = threadIdx.x; i < " << M * C << "u; i += 256u) {\n";
+    out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u, col = gv_col0 + c;\n";
+    out_ << "if (col < gv_N) {\n";
+    out_ << "const float p = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
+    for (int m = 0; m < G; ++m) {
+      out_ << "if (gv_g == " << m << "u) { const float y = " << member_value("m", "col", "p", m) << "; " << out_of(g.result[m])
+           << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << "; }\n";
+    }
+    out_ << "}\n}\n}\n\n";
+    return;
+  }
+  out_ << "float* gv_part = reinterpret_cast<float*>(scratch);\n";
+  out_ << "if (gv_wave == 0u) {\n";
+  out_ << "for (uint32_t i = gv_lane; i < " << M * C << "u; i += 64u) {\n";
+  out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u;\n";
+  out_ << "gv_part[((size_t)(gv_seg * " << g.wps << "u + gv_w) * " << M << "u + m) * " << C
+       << "u + c] = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
+  out_ << "}\n";
+  out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
+  out_ << "if (!fused_mode) __threadfence();\n";
+  out_ << "if (gv_lane == 0u) {\n";
+  // one counter per 128-byte line
+  out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + gv_seg * 32u;\n";
+  out_ << "const uint32_t last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == "
+       << g.wps - 1 << "u;\n";
+  out_ << "if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+  out_ << "gv_last = last;\n}\n}\n";
+  out_ << "__syncthreads();\n";
+  out_ << "if (!gv_last) return;\n";
+  out_ << "if (!fused_mode) __threadfence();\n";
+  auto ld = [&](const std::string& addr) {
+    return "__hip_atomic_load(&" + addr + ", __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)";
+  };
+  if (g.joint) {
+    out_ << "for (uint32_t i = threadIdx.x; i < " << G * M * S << "u; i += 256u) {\n";
+    out_ << "const uint32_t gv_g = i / " << M * S << "u, rem = i % " << M * S << "u;\n";
+    out_ << "const uint32_t m = rem / " << S << "u, c = rem % " << S << "u;\n";
+    out_ << "const size_t base = (size_t)gv_seg * " << g.wps << "u + ((size_t)gv_g * " << tps << "u + c / " << C
+         << "u) * " << g.ksplit << "u;\n";
+    out_ << "float sum = 0.0f;\n";
+    out_ << "for (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
+         << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c % " +
+               std::to_string(C) + "u]")
+         << ";\n";
+    out_ << "const uint32_t col = gv_seg * " << S << "u + c;\n";
+    out_ << "float y = 0.0f;\n";
+    for (int m = 0; m < G; ++m) {
+      out_ << "if (gv_g == " << m << "u) {\n";
+      out_ << "y = " << member_value("m", "col", "sum", m) << ";\n";
+      if (g.store[m]) out_ << out_of(g.result[m]) << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << ";\n";
+      out_ << "}\n";
+    }
+    out_ << "gv_ys[i] = y;\n";
+    out_ << "}\n";
+  } else {
+    out_ << "for (uint32_t i = threadIdx.x; i < " << M * C << "u; i += 256u) {\n";
+    out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u, col = gv_col0 + c;\n";
+    out_ << "if (col < gv_N) {\n";
+    out_ << "const size_t base = (size_t)gv_seg * " << g.wps << "u;\n";
+    out_ << "float sum = 0.0f;\n";
+    out_ << "for (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
+         << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c]") << ";\n";
+    for (int m = 0; m < G; ++m) {
+      out_ << "if (gv_g == " << m << "u) { const float y = " << member_value("m", "col", "sum", m) << "; "
+           << out_of(g.result[m]) << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << "; }\n";
+    }
+    out_ << "}\n}\n";
+  }
+  if (!s.epilogue_loop.empty()) {
+    out_ << "__syncthreads();\n";
+    gemv_epilogue(s, ptr_of, "gv_seg");
+  }
   out_ << "}\n\n";
+}
+
+// The epilogue loop of a kGemv step over segment `seg`'s root elements
+// [seg * R, (seg + 1) * R), one element per thread and pass. Reads of the
+// step's results come from the segment's LDS copy (the planner checked that
+// they stay inside the segment's columns); its outputs are the step's
+// outputs after the stored results, window outputs written in place.
+void KernelGen::gemv_epilogue(Step& s, const std::map<int, std::string>& ptr_of, const std::string& seg) {
+  const GemvSpec& g = s.gemv;
+  Step& L = s.epilogue_loop[0];
+  const int G = static_cast<int>(g.dots.size());
+  const int64_t S = g.seg_cols, R = g.root_per_seg;
+  const int M = g.M;
+  size_t base = 0;
+  for (int m = 0; m < G; ++m) base += g.store[m] ? 1 : 0;
+  out_ << "{\n";
+  Writer w(prog_, ptr_of, "uint32_t");
+  for (int m = 0; m < G; ++m) {
+    const int64_t N = prog_.type(g.result[m]).dims[1];
+    const std::string off = std::to_string(static_cast<int64_t>(m) * M * S);
+    w.lds_value[g.result[m]] = [=](const std::string& lin) {
+      if (M == 1) return "gv_ys[" + off + "u + (" + lin + ") - " + seg + " * " + std::to_string(S) + "u]";
+      return "gv_ys[" + off + "u + ((" + lin + ") / " + std::to_string(N) + "u) * " + std::to_string(S) + "u + (" + lin +
+             ") % " + std::to_string(N) + "u - " + seg + " * " + std::to_string(S) + "u]";
+    };
+  }
+  Idx root;
+  root.key = "R";
+  root.shape = L.loop_shape;
+  root.lin = "lin";
+  root.identity = true;
+  const int rid = w.add_index(root);
+  std::vector<std::string> vals;
+  for (size_t o = 0; o < L.outputs.size(); ++o) {
+    auto ww = L.window_out.find(static_cast<int>(o));
+    vals.push_back(w.value(ww == L.window_out.end() ? L.outputs[o] : ww->second.update, rid));
+  }
+  for (auto& [o, ww] : L.window_out) {
+    const Dims& od = prog_.type(ww.operand).dims;
+    for (size_t d = 0; d < ww.starts.size(); ++d) {
+      const int sv = ww.starts[d];
+      std::string e;
+      auto pi = ptr_of.find(sv);
+      if (pi != ptr_of.end()) {
+        e = "(int64_t)" + pi->second + "[0]";
+      } else {
+        const Op* c = nullptr;
+        for (const Op& op : prog_.ops)
+          if (!op.results.empty() && op.results[0] == sv) c = &op;
+        PJRTX_CHECK(c && c->kind == OpKind::kConstant, Code::kInternal, "window start is neither an input nor a constant");
+        e = "(int64_t)(" + literal_expr(prog_, *c, 0) + ")";
+      }
+      const int64_t hi = od[d] - L.loop_shape[d];
+      out_ << "int64_t ws" << o << "_" << d << " = " << e << ";\n";
+      out_ << "ws" << o << "_" << d << " = ws" << o << "_" << d << " < 0 ? 0 : (ws" << o << "_" << d << " > " << hi
+           << " ? " << hi << " : ws" << o << "_" << d << ");\n";
+    }
+  }
+  out_ << "for (uint32_t lin = " << seg << " * " << R << "u + threadIdx.x; lin < (" << seg << " + 1u) * " << R
+       << "u; lin += 256u) {\n";
+  out_ << w.body.str();
+  for (size_t o = 0; o < L.outputs.size(); ++o) {
+    const DType t = prog_.type(L.outputs[o]).dtype;
+    const std::string outp = "out" + std::to_string(base + o);
+    auto ww = L.window_out.find(static_cast<int>(o));
+    if (ww == L.window_out.end()) {
+      out_ << outp << "[lin] = " << to_storage(t, vals[o]) << ";\n";
+      continue;
+    }
+    const Dims& od = prog_.type(ww->second.operand).dims;
+    out_ << "{ uint64_t rem = lin, dst = 0;\n";
+    int64_t stride = 1;
+    for (int d = static_cast<int>(od.size()) - 1; d >= 0; --d) {
+      out_ << "{ const uint64_t c = rem % " << L.loop_shape[d] << "u; rem /= " << L.loop_shape[d]
+           << "u; dst += (c + (uint64_t)ws" << o << "_" << d << ") * " << stride << "ull; }\n";
+      stride *= od[d];
+    }
+    out_ << outp << "[dst] = " << to_storage(t, vals[o]) << "; }\n";
+  }
+  out_ << "}\n}\n";
 }
 
 }  // namespace
@@ -1629,6 +1961,7 @@ std::string generate_kernels(const Program& prog, Plan& plan) {
     if (s.kind == StepKind::kLoop) gen.loop(s);
     else if (s.kind == StepKind::kReduce) gen.reduce(s);
     else if (s.kind == StepKind::kRowFused) gen.row_fused(s);
+    else if (s.kind == StepKind::kGemv) gen.gemv(s);
   }
   return out.str();
 }

@@ -268,6 +268,29 @@ PJRTX_DEV float min_r(float a, float b) { return __builtin_elementwise_minimum(a
 PJRTX_DEV float max_seq(float acc, float x) { return max_r(acc, x); }
 PJRTX_DEV float min_seq(float acc, float x) { return min_r(acc, x); }
 
+// ------------------------------------------------------------ decode GEMV
+typedef uint32_t gv_u32x4 __attribute__((ext_vector_type(4)));
+PJRTX_DEV gv_u32x4 gv_load16(const uint16_t* p) { return *reinterpret_cast<const gv_u32x4*>(p); }
+// acc[e] += x * w[e] for the eight 16-bit weights of one 16-byte piece, in
+// element order (bf16: the high half of each 32-bit word is the odd element).
+template <bool kF16>
+PJRTX_DEV void gv_fma8(float* acc, float x, const gv_u32x4& w) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t u = w[q];
+    float lo, hi;
+    if constexpr (kF16) {
+      lo = f16_to_f32((uint16_t)(u & 0xffffu));
+      hi = f16_to_f32((uint16_t)(u >> 16));
+    } else {
+      lo = __builtin_bit_cast(float, u << 16);
+      hi = __builtin_bit_cast(float, u & 0xffff0000u);
+    }
+    acc[2 * q] = __builtin_fmaf(x, lo, acc[2 * q]);
+    acc[2 * q + 1] = __builtin_fmaf(x, hi, acc[2 * q + 1]);
+  }
+}
+
 // ------------------------------------------------------ wavefront reductions
 // 64-lane wavefronts: xor-butterfly over lane offsets 32..1. Every lane ends
 // with the same value, combined in a fixed order (deterministic).

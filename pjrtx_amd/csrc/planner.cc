@@ -1187,6 +1187,7 @@ Plan Planner::run() {
   plan_.num_fusion_kernels = kernel_id;
   liveness();
   if (opts_.fuse_siblings) absorb_window_updates();
+  fuse_gemv_steps(prog_, &plan_, outputs_, opts_);
   return std::move(plan_);
 }
 
@@ -1204,7 +1205,8 @@ std::string Plan::describe(const Program& prog) const {
     const Step& s = steps[i];
     if (i) o << ",";
     const char* kind = s.kind == StepKind::kLoop ? "loop" : s.kind == StepKind::kReduce ? "reduce"
-                     : s.kind == StepKind::kAlias ? "alias" : s.kind == StepKind::kRowFused ? "rowfused" : "library";
+                     : s.kind == StepKind::kAlias ? "alias" : s.kind == StepKind::kRowFused ? "rowfused"
+                     : s.kind == StepKind::kGemv ? "gemv" : "library";
     o << "{\"kind\":\"" << kind << "\",\"name\":\"" << s.name << "\"";
     o << ",\"inputs\":" << list(s.inputs) << ",\"outputs\":" << list(s.outputs);
     auto bytes_of = [&](const std::vector<int>& vs) {
@@ -1233,6 +1235,11 @@ std::string Plan::describe(const Program& prog) const {
         for (size_t k = 2; k < d.operands.size(); ++k) alg += prog.type(d.operands[k]).bytes();
       }
     }
+    if (s.kind == StepKind::kGemv) {
+      // Window outputs move only their window (the update's elements).
+      for (auto& [k, w] : s.window_out)
+        alg += prog.type(w.update).bytes() - prog.type(s.outputs[k]).bytes();
+    }
     o << ",\"algorithmic_bytes\":" << alg;
     std::vector<std::string> names;
     o << ",\"ops\":[";
@@ -1252,6 +1259,29 @@ std::string Plan::describe(const Program& prog) const {
     if (s.kind == StepKind::kRowFused)
       o << ",\"phases\":" << s.phases.size() << ",\"rows\":" << s.rows << ",\"row_len\":" << s.row_len
         << ",\"wave_per_row\":" << (s.wave_per_row ? "true" : "false");
+    if (s.kind == StepKind::kGemv) {
+      const GemvSpec& g = s.gemv;
+      int64_t flops = 0;
+      std::string ns = "[";
+      for (size_t m = 0; m < g.dots.size(); ++m) {
+        const int64_t n = prog.type(g.result[m]).dims[1];
+        flops += 2 * g.M * g.K * n;
+        ns += (m ? "," : "") + std::to_string(n);
+      }
+      o << ",\"flops\":" << flops << ",\"members\":" << g.dots.size() << ",\"M\":" << g.M << ",\"K\":" << g.K
+        << ",\"N\":" << ns << "],\"cols\":" << g.cols << ",\"depth\":" << g.depth << ",\"ksplit\":" << g.ksplit
+        << ",\"kchunk\":" << g.kchunk << ",\"joint\":" << (g.joint ? "true" : "false")
+        << ",\"seg_cols\":" << g.seg_cols << ",\"segments\":" << g.nseg << ",\"wg_per_segment\":" << g.wps
+        << ",\"direct\":" << (g.direct ? "true" : "false") << ",\"fused_combine\":" << (s.fused_combine ? "true" : "false")
+        << ",\"prologue\":" << (s.prologue.empty() ? "null" : "\"" + std::string("rowfused") + "\"")
+        << ",\"epilogue_loop\":[";
+      if (!s.epilogue_loop.empty())
+        for (size_t k = 0; k < s.epilogue_loop[0].ops.size(); ++k)
+          o << (k ? "," : "") << "\"" << op_kind_name(prog.ops[s.epilogue_loop[0].ops[k]].kind) << "\"";
+      o << "]";
+      for (size_t m = 0; m < g.add.size(); ++m)
+        if (g.add[m] >= 0) o << ",\"residual_add\":" << g.add[m];
+    }
     if (s.kind == StepKind::kReduce) {
       o << ",\"reducers\":[";
       for (size_t k = 0; k < s.reduces.size(); ++k) o << (k ? "," : "") << "\"" << reducer_name(s.reduces[k].kind) << "\"";

@@ -45,12 +45,45 @@ struct ReduceSpec {
 // elementwise pass that consumes them, as one kernel with one workgroup per
 // row (softmax, RMSNorm, layer norm). `phases` holds the fused steps in
 // order; earlier phases' results are per-row scalars in later phases.
-enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused };
+//
+// kGemv: decode-shaped dot_generals ([M, K] x [K, N_i], M <= 4, 16-bit)
+// sharing one LHS, as one generated kernel that streams each weight once,
+// split over K with the partials folded by the last workgroup of each
+// column segment. It may absorb the row-fused step that produces its LHS
+// (e.g. RMSNorm: recomputed per workgroup into LDS) and one elementwise
+// loop step over its results (e.g. SwiGLU, RoPE with the KV-row writes),
+// evaluated segment by segment by those last workgroups.
+enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused, kGemv };
 
 enum class LibKind {
   kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup, kWhile, kSort
 };
 const char* lib_kind_name(LibKind k);
+
+struct Step;
+
+// Geometry and members of a kGemv step.
+struct GemvSpec {
+  int x = -1;               // LHS value [M, K]
+  int M = 1;
+  int64_t K = 0;
+  std::vector<int> dots;    // member dot_general ops
+  std::vector<int> result;  // per member: value holding its final value
+  std::vector<int> add;     // per member: residual addend (result = add + round(dot)) or -1
+  std::vector<bool> store;  // per member: the result is written to memory
+  int cols = 64;            // columns per tile (8 lanes of 8 elements per row at 64)
+  int depth = 8;            // weight rows in flight per lane
+  int64_t ksplit = 1;       // K chunks (workgroups per tile)
+  int64_t kchunk = 0;       // rows per K chunk
+  // Segments: the unit whose last workgroup folds the partials. Joint
+  // segments span the same `seg_cols` columns of every member (an epilogue
+  // reads several members); otherwise a segment is one tile of one member.
+  bool joint = false;
+  int64_t seg_cols = 0, nseg = 0, wps = 0;  // wps: workgroups per segment
+  int64_t root_per_seg = 0;                 // epilogue loop elements per segment
+  bool direct = false;                      // ksplit 1, no epilogue: tiles store their results
+  size_t partial_bytes = 0;                 // partial slots before the counters in scratch
+};
 
 struct Step {
   StepKind kind = StepKind::kLoop;
@@ -119,6 +152,11 @@ struct Step {
     std::vector<int> starts;
   };
   std::map<int, WindowWrite> window_out;  // output position -> window write
+
+  // kGemv
+  GemvSpec gemv;
+  std::vector<Step> prologue;       // 0 or 1 kRowFused step producing gemv.x
+  std::vector<Step> epilogue_loop;  // 0 or 1 kLoop step over member results
 };
 
 struct Plan {
@@ -161,6 +199,12 @@ struct PlanOptions {
   // A decode-shaped dot whose only reader is `add(dot, x)` writes the sum
   // itself (environment: PJRTX_DOT_RESIDUAL, 0 disables).
   bool dot_residual = env_int("PJRTX_DOT_RESIDUAL", 1) != 0;
+  // Decode-shaped dots become generated split-K GEMV kernels with fused
+  // prologues and epilogues (environment: PJRTX_GEMV_FUSION, 0 keeps the
+  // library GEMV steps).
+  bool gemv_fusion = env_int("PJRTX_GEMV_FUSION", 1) != 0;
+  // Target workgroups per GEMV launch (environment: PJRTX_GEMV_WGS).
+  int64_t gemv_target_wgs = env_int("PJRTX_GEMV_WGS", 768);
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
@@ -170,6 +214,12 @@ Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
 // (unless PJRTX_FUSED_ATTENTION=0) and drops ops left without users.
 // Unsupported custom-call targets fail with kUnimplemented.
 void rewrite_program(Program* prog);
+
+// Turns decode-shaped dot and dot-group library steps into kGemv steps and
+// absorbs their row-fused prologues and elementwise epilogues
+// (gemv_fusion.cc). Runs on a finished plan (after liveness); recomputes the
+// releases. `outputs` are the program's result values.
+void fuse_gemv_steps(const Program& prog, Plan* plan, const std::set<int>& outputs, const PlanOptions& opts);
 
 // Emits the HIP source of every generated step (codegen.cc).
 std::string generate_kernels(const Program& prog, Plan& plan);

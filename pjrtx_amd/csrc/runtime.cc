@@ -595,7 +595,8 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
   L->scratch.resize(plan_.steps.size());
   for (size_t i = 0; i < plan_.steps.size(); ++i) {
     const Step& s = plan_.steps[i];
-    if (s.kind == StepKind::kLoop || s.kind == StepKind::kReduce || s.kind == StepKind::kRowFused) {
+    if (s.kind == StepKind::kLoop || s.kind == StepKind::kReduce || s.kind == StepKind::kRowFused ||
+        s.kind == StepKind::kGemv) {
       hip_check(hipModuleGetFunction(&L->funcs[i], L->module, s.name.c_str()), "hipModuleGetFunction");
     }
     if (s.combine_grid) {
@@ -662,7 +663,8 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       return;
     case StepKind::kLoop:
     case StepKind::kReduce:
-    case StepKind::kRowFused: {
+    case StepKind::kRowFused:
+    case StepKind::kGemv: {
       if (phase != 1) {
         for (size_t k = 0; k < s.outputs.size(); ++k) {
           auto ww = s.window_out.find(static_cast<int>(k));

@@ -1,6 +1,7 @@
 """Dot groups (planner: decode-shaped dots sharing one LHS, the reference's
-dot group of executable_metal_graph_lowering_fusion.zig:394-424) run as one
-gemv_wide launch. Each member must equal float64 within the bf16/f16 bar and
+dot group of executable_metal_graph_lowering_fusion.zig:394-424) on the
+library path (PJRTX_GEMV_FUSION=0; the generated GEMVs are tested in
+test_gpu_gemv.py) run as one gemv_wide launch. Each member must equal float64 within the bf16/f16 bar and
 be bit-identical to the same dot planned alone (same kernel, same summation
 order)."""
 import json
@@ -38,6 +39,7 @@ def _f64(a, dt):
     (4, 8192, (2048, 2048), "bf16"),         # M*K past the LDS stage: members run one by one
 ])
 def test_dot_group_matches_oracle_and_single_dots(client, monkeypatch, M, K, Ns, dt):
+    monkeypatch.setenv("PJRTX_GEMV_FUSION", "0")
     rng = np.random.default_rng(K + sum(Ns) + M)
     x = _bits(rng, (M, K), dt)
     ws = [_bits(rng, (K, n), dt, 1 / np.sqrt(K)) for n in Ns]
@@ -72,6 +74,7 @@ def test_dot_group_matches_oracle_and_single_dots(client, monkeypatch, M, K, Ns,
 def test_residual_add_merged_into_dot(client, monkeypatch, M, K, N, dt):
     """x + dot(h, w) with the dot read only by the add: one launch writing
     the sum, bit-identical to the dot followed by the elementwise add."""
+    monkeypatch.setenv("PJRTX_GEMV_FUSION", "0")
     rng = np.random.default_rng(K + N)
     b = Builder()
     h, w, x = b.param((M, K), dt), b.param((K, N), dt), b.param((M, N), dt)

@@ -182,8 +182,12 @@ def test_generated_code_has_no_packed_f32(plugin):
 def test_decode_dots_sharing_an_lhs_form_groups(plugin, monkeypatch):
     from pjrtx_amd import llama_like as L
     steps = plan(plugin, L.decode_program(L.TINY))["steps"]
-    groups = [s["group_size"] for s in steps if s.get("library") == "dot_group"]
+    groups = [s["members"] for s in steps if s["kind"] == "gemv" and s["members"] > 1]
     assert groups == [3, 2] * L.TINY.layers  # q/k/v and gate/up of every layer
+    monkeypatch.setenv("PJRTX_GEMV_FUSION", "0")
+    steps = plan(plugin, L.decode_program(L.TINY))["steps"]
+    groups = [s["group_size"] for s in steps if s.get("library") == "dot_group"]
+    assert groups == [3, 2] * L.TINY.layers
     monkeypatch.setenv("PJRTX_DOT_GROUPS", "0")
     assert not [s for s in plan(plugin, L.decode_program(L.TINY))["steps"] if s.get("library") == "dot_group"]
 
@@ -204,9 +208,51 @@ def test_residual_add_merges_into_decode_dot(plugin, monkeypatch):
     steps = plan(plugin, L.decode_program(L.FULL))["steps"]
     merged = [s for s in steps if "residual_add" in s]
     assert len(merged) >= 2 * L.FULL.layers - 1  # o-proj and down-proj residuals
+    assert all(s["kind"] == "gemv" for s in merged)
+    monkeypatch.setenv("PJRTX_GEMV_FUSION", "0")
+    steps = plan(plugin, L.decode_program(L.FULL))["steps"]
+    merged = [s for s in steps if "residual_add" in s]
+    assert len(merged) >= 2 * L.FULL.layers - 1
     assert all(s.get("library") == "dot_general" for s in merged)
     monkeypatch.setenv("PJRTX_DOT_RESIDUAL", "0")
     assert not [s for s in plan(plugin, L.decode_program(L.FULL))["steps"] if "residual_add" in s]
+
+
+def test_decode_layer_is_five_launches(plugin):
+    """Per layer: q/k/v GEMV (RMSNorm prologue, RoPE and both KV-row writes
+    in its epilogue), attention, o-projection (+ residual), gate/up GEMV
+    (RMSNorm prologue, SwiGLU epilogue), down projection (+ residual)."""
+    from pjrtx_amd import llama_like as L
+    steps = plan(plugin, L.decode_program(L.FULL))["steps"]
+    units = [s for s in steps if s["kind"] != "alias"]
+    gemv = [s for s in steps if s["kind"] == "gemv"]
+    assert len(gemv) == 4 * L.FULL.layers + 1  # + lm_head
+    qkv = [s for s in gemv if s["members"] == 3]
+    assert len(qkv) == L.FULL.layers
+    for s in qkv:
+        assert s["prologue"] == "rowfused" and s["joint"] and s["seg_cols"] == L.FULL.head_dim
+        assert "concatenate" in s["epilogue_loop"] and len(s["window_outputs"]) == 2
+    up = [s for s in gemv if s["members"] == 2]
+    assert all(s["prologue"] == "rowfused" and "logistic" in s["epilogue_loop"] for s in up)
+    assert gemv[-1]["prologue"] == "rowfused" and gemv[-1]["N"] == [L.FULL.vocab]  # final norm + lm_head
+    assert len(units) <= 5 * L.FULL.layers + 5
+    # Every split GEMV folds in-launch (no combine kernel).
+    assert all(s["direct"] or s["fused_combine"] for s in gemv)
+
+
+def test_gemv_epilogue_must_stay_inside_segments(plugin):
+    """A loop that reads a result across the whole row (a reverse) cannot
+    run per segment: it stays its own launch."""
+    b = Builder()
+    x = b.param((1, 256), "bf16")
+    w = b.param((256, 1024), "bf16")
+    y = b.dot_general(x, w, contract=((1,), (0,)))
+    z = b.multiply(b.reverse(y, [1]), y)
+    steps = plan(plugin, b.build([z]))["steps"]
+    assert [s["kind"] for s in steps] == ["gemv", "loop"]
+    # Elementwise over the same index fuses.
+    steps = plan(plugin, b.build([b.multiply(y, y)]))["steps"]
+    assert [s["kind"] for s in steps] == ["gemv"] and steps[0]["epilogue_loop"] == ["multiply"]
 
 
 def _shift_in_place_program():
