@@ -485,6 +485,8 @@ AttnParams attention_params(const Program& prog, const Op& op) {
   return p;
 }
 
+static_assert(Device::kArrivalCounterBytes / 128 >= kAttnCounterRows, "one counter line per decode query row");
+
 void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
   AttnParams p = attention_params(prog, op);
   auto ptr = [&](int v) -> void* { return vals[v] ? vals[v]->ptr : nullptr; };
@@ -493,7 +495,8 @@ void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<M
   const size_t scratch_bytes = attention_scratch_bytes(p, t);
   MemRef scratch = scratch_bytes ? dev->allocate(scratch_bytes) : nullptr;
   launch_attention(dev->stream(), p, t, ptr(op.operands[0]), ptr(op.operands[1]), ptr(op.operands[2]),
-                   ptr(op.results[0]), scratch ? static_cast<float*>(scratch->ptr) : nullptr);
+                   ptr(op.results[0]), scratch ? static_cast<float*>(scratch->ptr) : nullptr, dev->arrival_counters(),
+                   dev->xcd_round_robin());
 }
 
 }  // namespace pjrtx

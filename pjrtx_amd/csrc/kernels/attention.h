@@ -46,8 +46,13 @@ AttnPath attention_path(const AttnParams& p, DType t, int* nsplit, int* keys_per
 // Device scratch the launch needs (split-key partials), 0 if none.
 size_t attention_scratch_bytes(const AttnParams& p, DType t);
 // Launches the kernels for element type t (bf16, f16 or f32; Q, K, V and out
-// share it). `scratch` holds attention_scratch_bytes(p, t) bytes.
+// share it). `scratch` holds attention_scratch_bytes(p, t) bytes. The split
+// decode kernel merges its splits in the same launch when `xcd_local` (the
+// device runs workgroup b on XCD b % 8) and `counters` (arrival counters, one
+// per 128 bytes, zero on entry and left zero) covers the query rows (at most
+// kAttnCounterRows); otherwise a second kernel merges them.
+constexpr int64_t kAttnCounterRows = 8192;
 void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
-                      void* out, float* scratch);
+                      void* out, float* scratch, uint32_t* counters, bool xcd_local);
 
 }  // namespace pjrtx

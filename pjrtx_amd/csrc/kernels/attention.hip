@@ -442,147 +442,219 @@ __global__ void __launch_bounds__(256) attn_rows(AttnParams p, const T* __restri
 
 // --------------------------------------------------------------- decode
 
-// Few queries per (batch, head): grid (query rows, key splits). Each of the
-// 4 waves takes 64 keys per step: lane j scores key j (its K row read as
-// 16-byte chunks, all in flight together; q from LDS), the wave folds the
-// online softmax, then the lanes regroup as (16-byte head-dim chunk c, key
-// group g) for P.V so that each V row is read as one coalesced span. The
-// workgroup merges its waves (and key groups) through LDS in a fixed order;
-// with one split that is the output, otherwise (m, l, O) partials go to
-// `part` and attn_combine merges the splits in split order.
+// Few queries per (batch, head): the keys of each query row are split into
+// chunks of `keys_per_split` (a multiple of 64), one workgroup per (row,
+// chunk), so a decode step launches rows x splits workgroups. A workgroup
+// walks its chunk 64 keys per pass with both loads in flight at once: for
+// the scores 4 lanes share a key (each a quarter of its K row, folded by two
+// xor shuffles), for P.V a lane owns one 16-byte head-dim piece of a group of
+// keys (each V row read as one coalesced span). The pass max and sum fold
+// over the waves through LDS in wave order (online softmax). The key groups
+// of P.V fold through LDS in group order. Splits past the row's last allowed
+// key exit at once.
+//
+// One split: the workgroup writes the row. Otherwise each split writes
+// (m, l, unnormalized O) to `part`; with `fused` (workgroup b runs on XCD
+// b % 8 and the row's splits were placed on one XCD) the split counts its
+// arrival on the row's L2 counter once its stores are acknowledged by that
+// L2, and the last to arrive merges the splits in split order (reading past
+// its L1) and puts the counter back to zero; without it attn_combine, launched
+// next, merges them the same way. The merge order is fixed, so the result
+// does not depend on which split arrives last.
 constexpr int DK = 64;
+constexpr int kCounterStride = 32;  // uint32 per arrival counter: one 128-byte line each
+
+template <typename T>
+__device__ __forceinline__ int active_splits(const AttnParams& p, int q, int keys_per_split) {
+  const int nkeys = key_limit(p, read_offset(p), q) + 1;
+  return nkeys <= 0 ? 1 : (nkeys + keys_per_split - 1) / keys_per_split;
+}
+
+// Merges splits 0..nact-1 (nact <= 64) of a row's partials `pr` (per split:
+// m, l, then D unnormalized outputs) into out[d] for d < D, by the block's
+// first D threads (D <= blockDim.x). The splits' (m, l) go through LDS first,
+// one load per thread; each output then folds its splits in split order,
+// eight loads in flight at a time. kCoherent: loads that skip this CU's L1
+// (other workgroups of this XCD wrote the partials).
+template <bool kCoherent, typename T>
+__device__ __forceinline__ void merge_splits(const float* pr, int nact, int D, T* out, float* msh, float* lsh) {
+  auto ld = [](const float* a) {
+    if constexpr (kCoherent) return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *a;
+  };
+  const int tid = threadIdx.x;
+  if (tid < nact) {
+    msh[tid] = ld(pr + (int64_t)tid * (D + 2));
+    lsh[tid] = ld(pr + (int64_t)tid * (D + 2) + 1);
+  }
+  __syncthreads();
+  if (tid >= D) return;
+  float mall = -INFINITY;
+  for (int s = 0; s < nact; ++s) mall = fmaxf(mall, msh[s]);
+  const float mref = mall == -INFINITY ? 0.f : mall;
+  float lsum = 0.f, acc = 0.f;
+  for (int s0 = 0; s0 < nact; s0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = s0 + u < nact ? ld(pr + (int64_t)(s0 + u) * (D + 2) + 2 + tid) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + u < nact) {
+        const float f = expf(msh[s0 + u] - mref);
+        lsum += lsh[s0 + u] * f;
+        acc += v[u] * f;
+      }
+    }
+  }
+  out[tid] = Elem<T>::put(acc / lsum);
+}
 
 template <typename T, int NCH>
 __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __restrict__ Q, const T* __restrict__ K,
-                                                   const T* __restrict__ V, T* __restrict__ O,
-                                                   float* __restrict__ part, int keys_per_split) {
-  constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk
+                                                   const T* __restrict__ V, T* __restrict__ O, float* __restrict__ part,
+                                                   int keys_per_split, int nsplit, uint32_t* __restrict__ counters,
+                                                   int fused) {
+  constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte piece
   constexpr int D = NCH * EPC;
-  constexpr int G = 64 / NCH;          // key groups in the P.V pass
+  constexpr int CPT = NCH / 4;         // pieces of a K row per lane (4 lanes per key)
+  constexpr int G = 256 / NCH;         // key groups in P.V
   constexpr int KG = DK / G;           // keys per group
-  __shared__ float qs[D];
-  __shared__ float ow[4][64][EPC];
-  __shared__ float mw[4], lw[4];
-  const int row = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
+  __shared__ float ps[DK];
+  __shared__ float wred[2][4];
+  __shared__ float ow[G][D];
+  __shared__ float msh[64], lsh[64];
+  __shared__ uint32_t last_s;
+  const int rows = p.B * p.Hq * p.Sq;
+  // The row's splits share b % 8 (one XCD): row = (b % 8) + 8 * ((b / 8) / nsplit).
+  const int xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const int row = xcd + 8 * (jj / nsplit);
+  const int split = jj % nsplit;
+  if (row >= rows) return;
   const int q = row % p.Sq;
   const int bh = row / p.Sq;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
+  const int nkeys = key_limit(p, read_offset(p), q) + 1;
+  const int nact = nkeys <= 0 ? 1 : (nkeys + keys_per_split - 1) / keys_per_split;
+  if (split >= nact) return;
   const T* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
   const T* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
+  const T* Qp = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h + (int64_t)q * p.q_s;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  if (tid < D) qs[tid] = Elem<T>::get(Q[(int64_t)b * p.q_b + (int64_t)h * p.q_h + (int64_t)q * p.q_s + tid]);
-  __syncthreads();
-  const int nkeys = key_limit(p, read_offset(p), q) + 1;
+  const int quarter = tid & 3, kslot = tid >> 2;      // scores: key slot, quarter of the row
+  const int c = tid % NCH, g = tid / NCH;             // P.V: head-dim piece, key group
+  float qv[CPT * EPC];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(Qp + (quarter * CPT + i) * EPC);
+    const T* e8 = reinterpret_cast<const T*>(&w);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) qv[i * EPC + e] = Elem<T>::get(e8[e]);
+  }
   const int k0 = split * keys_per_split;
   const int k1 = std::min(nkeys, k0 + keys_per_split);
-  const int c = lane % NCH, grp = lane / NCH;
   float m = -INFINITY, l = 0.f, o[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) o[e] = 0.f;
-  for (int kb = k0 + wave * DK; kb < k1; kb += 4 * DK) {
-    const int key = kb + lane;
-    float sc = -INFINITY;
-    if (key < k1) {
-      const T* kr = Kp + (int64_t)key * p.k_s;
-      u32x4 kv[NCH];
+  for (int kb = k0; kb < k1; kb += DK) {
+    const int key = kb + kslot;
+    u32x4 kv[CPT];
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) kv[i] = *reinterpret_cast<const u32x4*>(kr + i * EPC);
-      float acc = 0.f;
-#pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const T* e8 = reinterpret_cast<const T*>(&kv[i]);
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) acc += qs[i * EPC + e] * Elem<T>::get(e8[e]);
-      }
-      if (p.round_scores) acc = Elem<T>::get(Elem<T>::put(acc));
-      sc = acc * p.scale;
-    }
-    float mx = sc;
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
-    const float mnew = fmaxf(m, mx);
-    const float mref = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = expf(m - mref);
-    const float pe = expf(sc - mref);
-    float ps = pe;
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) ps += __shfl_xor(ps, k);
-    l = l * alpha + ps;
-    m = mnew;
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) o[e] *= alpha;
-    // P.V: lane (c, grp) reads chunk c of keys kb + grp*KG + i; keys past k1
-    // weigh 0 and read the last allowed row instead.
+    for (int i = 0; i < CPT; ++i)
+      kv[i] = key < k1 ? *reinterpret_cast<const u32x4*>(Kp + (int64_t)key * p.k_s + (quarter * CPT + i) * EPC)
+                       : u32x4{0u, 0u, 0u, 0u};
+    // keys past k1 weigh 0 and read the last allowed row instead
     u32x4 vv[KG];
 #pragma unroll
     for (int i = 0; i < KG; ++i) {
-      const int kk = std::min(kb + grp * KG + i, k1 - 1);
+      const int kk = std::min(kb + g * KG + i, k1 - 1);
       vv[i] = *reinterpret_cast<const u32x4*>(Vp + (int64_t)kk * p.v_s + c * EPC);
     }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const T* e8 = reinterpret_cast<const T*>(&kv[i]);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) acc += qv[i * EPC + e] * Elem<T>::get(e8[e]);
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    if (p.round_scores) acc = Elem<T>::get(Elem<T>::put(acc));
+    const float sc = key < k1 ? acc * p.scale : -INFINITY;
+    float mx = sc;
+#pragma unroll
+    for (int k = 32; k >= 4; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
+    if (lane == 0) wred[0][wave] = mx;
+    __syncthreads();
+    const float mnew = fmaxf(m, fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3])));
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = expf(m - mref);
+    const float pe = expf(sc - mref);
+    if (quarter == 0) ps[kslot] = pe;
+    float sum = quarter == 0 ? pe : 0.f;
+#pragma unroll
+    for (int k = 32; k >= 4; k >>= 1) sum += __shfl_xor(sum, k);
+    if (lane == 0) wred[1][wave] = sum;
+    __syncthreads();
+    l = l * alpha + (((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3]);
+    m = mnew;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) o[e] *= alpha;
 #pragma unroll
     for (int i = 0; i < KG; ++i) {
-      const float pj = __shfl(pe, grp * KG + i);
+      const float pj = ps[g * KG + i];
       const T* e8 = reinterpret_cast<const T*>(&vv[i]);
 #pragma unroll
       for (int e = 0; e < EPC; ++e) o[e] += pj * Elem<T>::get(e8[e]);
     }
-  }
-  if (lane == 0) {
-    mw[wave] = m;
-    lw[wave] = l;
+    __syncthreads();  // ps and wred are rewritten by the next pass
   }
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) ow[wave][lane][e] = o[e];
+  for (int e = 0; e < EPC; ++e) ow[g][c * EPC + e] = o[e];
   __syncthreads();
-  if (tid >= D) return;
-  const int cc = tid / EPC, ee = tid % EPC;
-  const float mall = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
-  const float mref = mall == -INFINITY ? 0.f : mall;
-  float lsum = 0.f, acc = 0.f;
+  float acc = 0.f;
+  if (tid < D) {
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float f = expf(mw[w] - mref);
-    lsum += lw[w] * f;
-    float ow_sum = 0.f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) ow_sum += ow[w][g * NCH + cc][ee];
-    acc += ow_sum * f;
+    for (int gg = 0; gg < G; ++gg) acc += ow[gg][tid];
   }
-  if (nsplit == 1) {
-    O[(int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s + tid] = Elem<T>::put(acc / lsum);
+  T* orow = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s;
+  if (nact == 1) {
+    if (tid < D) orow[tid] = Elem<T>::put(acc / l);
     return;
   }
-  float* pr = part + ((int64_t)row * nsplit + split) * (D + 2);
-  pr[2 + tid] = acc;
+  float* pr = part + (int64_t)row * nsplit * (D + 2);
+  if (tid < D) pr[(int64_t)split * (D + 2) + 2 + tid] = acc;
   if (tid == 0) {
-    pr[0] = mall;
-    pr[1] = lsum;
+    pr[(int64_t)split * (D + 2)] = m;
+    pr[(int64_t)split * (D + 2) + 1] = l;
   }
+  if (!fused) return;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are in the L2
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* ctr = counters + (int64_t)row * kCounterStride;
+    const uint32_t last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                          (uint32_t)(nact - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_s = last;
+  }
+  __syncthreads();
+  if (!last_s) return;
+  merge_splits<true>(pr, nact, D, orow, msh, lsh);
 }
 
 template <typename T>
-__global__ void __launch_bounds__(256) attn_combine(AttnParams p, const float* __restrict__ part, int nsplit,
-                                                    T* __restrict__ O) {
+__global__ void __launch_bounds__(512) attn_combine(AttnParams p, const float* __restrict__ part, int nsplit,
+                                                    int keys_per_split, T* __restrict__ O) {
   const int row = blockIdx.x;
   const int q = row % p.Sq;
   const int bh = row / p.Sq;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
-  const int D = p.D;
-  const float* pr = part + (int64_t)row * nsplit * (D + 2);
-  float mall = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mall = fmaxf(mall, pr[(int64_t)s * (D + 2)]);
-  const float mref = mall == -INFINITY ? 0.f : mall;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float lsum = 0.f, acc = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* ps = pr + (int64_t)s * (D + 2);
-      const float f = expf(ps[0] - mref);
-      lsum += ps[1] * f;
-      acc += ps[2 + d] * f;
-    }
-    O[(int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s + d] = Elem<T>::put(acc / lsum);
-  }
+  const int nact = active_splits<T>(p, q, keys_per_split);
+  if (nact == 1) return;  // the split kernel wrote the row
+  __shared__ float msh[64], lsh[64];
+  const float* pr = part + (int64_t)row * nsplit * (p.D + 2);
+  merge_splits<false>(pr, nact, p.D, O + (int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s, msh, lsh);
 }
 
 template <typename T>
@@ -591,24 +663,27 @@ bool decode_fits(const AttnParams& p) {
   if (p.D % EPC != 0) return false;
   const int nch = p.D / EPC;
   if (nch != 4 && nch != 8 && nch != 16 && nch != 32) return false;
-  for (int64_t st : {p.k_b, p.k_h, p.k_s, p.v_b, p.v_h, p.v_s})
+  for (int64_t st : {p.q_b, p.q_h, p.q_s, p.k_b, p.k_h, p.k_s, p.v_b, p.v_h, p.v_s})
     if (st % EPC != 0) return false;
   return true;
 }
 
 template <typename T>
 void launch_decode(hipStream_t s, const AttnParams& p, const T* q, const T* k, const T* v, T* o, float* part,
-                   int nsplit, int keys_per_split) {
+                   int nsplit, int keys_per_split, uint32_t* counters, bool fused) {
   constexpr int EPC = 16 / sizeof(T);
-  const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(p.B) * p.Hq * p.Sq), static_cast<uint32_t>(nsplit));
-  const dim3 block(256);
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+  const dim3 grid(static_cast<uint32_t>(8 * ((rows + 7) / 8) * nsplit)), block(256);
+  const int f = fused ? 1 : 0;
   switch (p.D / EPC) {
-    case 4: hipLaunchKernelGGL((attn_decode<T, 4>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
-    case 8: hipLaunchKernelGGL((attn_decode<T, 8>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
-    case 16: hipLaunchKernelGGL((attn_decode<T, 16>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
-    default: hipLaunchKernelGGL((attn_decode<T, 32>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split); break;
+    case 4: hipLaunchKernelGGL((attn_decode<T, 4>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
+    case 8: hipLaunchKernelGGL((attn_decode<T, 8>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
+    case 16: hipLaunchKernelGGL((attn_decode<T, 16>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
+    default: hipLaunchKernelGGL((attn_decode<T, 32>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
   }
-  if (nsplit > 1) hipLaunchKernelGGL((attn_combine<T>), dim3(grid.x), dim3(128), 0, s, p, part, nsplit, o);
+  if (nsplit > 1 && !fused)
+    hipLaunchKernelGGL((attn_combine<T>), dim3(static_cast<uint32_t>(rows)), dim3(std::max(64, p.D)), 0, s, p, part,
+                       nsplit, keys_per_split, o);
 }
 
 template <typename T>
@@ -645,11 +720,14 @@ AttnPath attention_path(const AttnParams& p, DType t, int* nsplit, int* keys_per
   const bool fits = t == DType::kF32 ? decode_fits<float>(p) : t == DType::kBF16 ? decode_fits<uint16_t>(p)
                     : t == DType::kF16 ? decode_fits<_Float16>(p) : false;
   if (!fits) return AttnPath::kRows;
-  // Splits of whole 256-key steps (4 waves x 64 keys), at most 64 of them.
-  const int steps = std::max(1, (p.Skv + 4 * DK - 1) / (4 * DK));
-  const int n = std::min(steps, 64);
-  const int per = (steps + n - 1) / n;
-  *keys_per_split = per * 4 * DK;
+  // Splits of whole 64-key passes: enough splits for about 512 workgroups
+  // over the rows, at most 64 per row.
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+  const int passes = std::max(1, (p.Skv + DK - 1) / DK);
+  const int want = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(64, (512 + rows - 1) / rows)));
+  const int n = std::min(passes, want);
+  const int per = (passes + n - 1) / n;
+  *keys_per_split = per * DK;
   *nsplit = (p.Skv + *keys_per_split - 1) / *keys_per_split;
   if (*nsplit < 1) *nsplit = 1;
   return AttnPath::kDecode;
@@ -662,7 +740,7 @@ size_t attention_scratch_bytes(const AttnParams& p, DType t) {
 }
 
 void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
-                      void* out, float* scratch) {
+                      void* out, float* scratch, uint32_t* counters, bool xcd_local) {
   PJRTX_CHECK(p.B >= 1 && p.Hq >= 1 && p.Hkv >= 1 && p.Hq % p.Hkv == 0 && p.D >= 1 && p.Sq >= 0 && p.Skv >= 0,
               Code::kInvalidArgument, "attention: bad shape");
   PJRTX_CHECK(p.D <= 512, Code::kUnimplemented, "attention: head dim above 512");
@@ -674,15 +752,19 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     PJRTX_CHECK(static_cast<int64_t>(p.B) * p.Hq * p.Sq < (int64_t(1) << 31), Code::kUnimplemented,
                 "attention: too many query rows");
     PJRTX_CHECK(nsplit == 1 || scratch != nullptr, Code::kInternal, "attention: split decode needs scratch");
+    const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+    const bool fused = xcd_local && counters != nullptr && rows <= kAttnCounterRows;
     if (t == DType::kF32)
       launch_decode<float>(s, p, static_cast<const float*>(Q), static_cast<const float*>(K),
-                           static_cast<const float*>(V), static_cast<float*>(out), scratch, nsplit, per);
+                           static_cast<const float*>(V), static_cast<float*>(out), scratch, nsplit, per, counters, fused);
     else if (t == DType::kBF16)
       launch_decode<uint16_t>(s, p, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
-                              static_cast<const uint16_t*>(V), static_cast<uint16_t*>(out), scratch, nsplit, per);
+                              static_cast<const uint16_t*>(V), static_cast<uint16_t*>(out), scratch, nsplit, per,
+                              counters, fused);
     else
       launch_decode<_Float16>(s, p, static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
-                              static_cast<const _Float16*>(V), static_cast<_Float16*>(out), scratch, nsplit, per);
+                              static_cast<const _Float16*>(V), static_cast<_Float16*>(out), scratch, nsplit, per,
+                              counters, fused);
   } else if (path == AttnPath::kTiles) {
     const int64_t grid = static_cast<int64_t>(p.B) * p.Hq * ((p.Sq + FQ - 1) / FQ);
     PJRTX_CHECK(grid < (int64_t(1) << 31), Code::kUnimplemented, "attention: too many query tiles");

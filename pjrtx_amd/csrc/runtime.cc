@@ -106,6 +106,9 @@ Device::Device(int ordinal) : ordinal_(ordinal), alloc_(ordinal) {
   hip_check(hipEventCreateWithFlags(&fork_ev_, hipEventDisableTiming), "hipEventCreate(fork)");
   hip_check(hipEventCreateWithFlags(&join_ev_, hipEventDisableTiming), "hipEventCreate(join)");
   xcd_round_robin_ = env_int("PJRTX_XCD_LOCAL", 1) != 0 && probe_xcd_round_robin(stream_);
+  hip_check(hipMalloc(reinterpret_cast<void**>(&counters_), kArrivalCounterBytes), "hipMalloc(counters)");
+  hip_check(hipMemsetAsync(counters_, 0, kArrivalCounterBytes, stream_), "hipMemsetAsync(counters)");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
   hipDeviceProp_t prop;
   hip_check(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
   arch_ = prop.gcnArchName;

@@ -117,6 +117,13 @@ class Device {
   // the device is opened).
   bool xcd_round_robin() const { return xcd_round_robin_; }
   hipEvent_t fork_event() const { return fork_ev_; }
+  // Arrival counters for library kernels whose last workgroup finishes a
+  // launch (one per 128-byte line, kArrivalCounterBytes in all): zeroed when
+  // the device is opened; a kernel that counts on a line puts it back to
+  // zero before it ends. Launches on the device are ordered on its stream, so
+  // they share the lines.
+  static constexpr size_t kArrivalCounterBytes = 1 << 20;
+  uint32_t* arrival_counters() const { return counters_; }
   hipEvent_t join_event() const { return join_ev_; }
 
  private:
@@ -128,6 +135,7 @@ class Device {
   hipStream_t aux_stream_ = nullptr;
   hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
   bool xcd_round_robin_ = false;
+  uint32_t* counters_ = nullptr;
   Allocator alloc_;
   std::mutex exec_mu_;
   std::string arch_, name_;

@@ -123,3 +123,29 @@ def test_fused_pattern_matches_unfused(client, monkeypatch, b_, h, s, d, dt, cau
     assert_close16(from_bits(got, dt), from_bits(plain, dt))
     if causal:
         np.testing.assert_array_equal(np.asarray(got)[:, :, 0], np.asarray(v)[:, :, 0])
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_decode_split_merge_paths_agree(client, run_fresh, dt):
+    """Decode attention splits the keys over workgroups. Merged in the same
+    launch by the row's last split (XCD-local counters) or by the separate
+    merge kernel (PJRTX_XCD_LOCAL=0, a fresh process): same merge order,
+    same bits; both match the float64 oracle."""
+    qs, kvs, tok = (1, 1, 16, 128), (1, 640, 16, 128), 517
+    rng = np.random.default_rng(11)
+    conv = (lambda x: to_bits(x, dt)) if dt != "f32" else (lambda x: np.asarray(x, np.float32))
+    q, k, v = conv(rng.standard_normal(qs)), conv(rng.standard_normal(kvs)), conv(rng.standard_normal(kvs))
+    b = Builder()
+    pq, pk, pv, t = b.param(qs, dt), b.param(kvs, dt), b.param(kvs, dt), b.param((), "s32")
+    text = b.build([b.custom_call(SDPA, [pq, pk, pv, t], qs, dt)])
+    dts = [dt, dt, dt, None] if dt != "f32" else [None] * 4
+    args = [q, k, v, np.array(tok, np.int32)]
+    (got,) = client.compile(text)(*args, dtypes=dts)
+    (other,) = run_fresh(text, args, dts, {"PJRTX_XCD_LOCAL": "0"})
+    np.testing.assert_array_equal(got, other)
+    want = A.sdpa_f64(from_bits(q, dt) if dt != "f32" else q, from_bits(k, dt) if dt != "f32" else k,
+                      from_bits(v, dt) if dt != "f32" else v, np.int32(tok))
+    if dt == "f32":
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    else:
+        assert_close16(from_bits(got, dt), want)

@@ -6,10 +6,6 @@ the same bits on every run (fixed fold order), and be the same bits when
 the partials are published by device-scope fences instead of the XCD-local
 path (PJRTX_XCD_LOCAL=0, in a subprocess: the device probe runs once)."""
 import json
-import os
-import subprocess
-import sys
-import textwrap
 
 import numpy as np
 import pytest
@@ -19,8 +15,6 @@ from oracle import ops
 from pjrtx_amd.hlo import Builder
 
 pytestmark = pytest.mark.gpu
-
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _bits(rng, shape, dt, scale=1.0):
@@ -135,19 +129,7 @@ def test_rmsnorm_prologue_swiglu_epilogue(client, monkeypatch, d, f):
     assert np.abs(gf - act).max() <= 2e-2 * np.abs(act).max()
 
 
-_FALLBACK = textwrap.dedent("""
-    import sys, numpy as np
-    sys.path.insert(0, sys.argv[1])
-    from pjrtx_amd.pjrt import Client
-    d = np.load(sys.argv[2])
-    c = Client()
-    exe = c.compile(open(sys.argv[3]).read())
-    outs = exe(*[d[f"a{i}"] for i in range(int(d["n"]))], dtypes=[str(t) for t in d["dtypes"]])
-    np.savez(sys.argv[4], *outs)
-""")
-
-
-def test_fence_path_gives_the_same_bits(client, tmp_path):
+def test_fence_path_gives_the_same_bits(client, run_fresh):
     """With the XCD placement unavailable (PJRTX_XCD_LOCAL=0) the partials
     are published with agent-scope fences; the fold order is the same, so
     are the bits."""
@@ -157,11 +139,5 @@ def test_fence_path_gives_the_same_bits(client, tmp_path):
             _bits(rng, (d, f), "bf16", 0.02)]
     text = _norm_swiglu_program(d, f)
     (got,) = client.compile(text)(*args, dtypes=["bf16"] * 4)
-    (tmp_path / "p.mlir").write_text(text)
-    np.savez(tmp_path / "in.npz", n=len(args), dtypes=np.array(["bf16"] * 4), **{f"a{i}": a for i, a in enumerate(args)})
-    env = dict(os.environ, PJRTX_XCD_LOCAL="0")
-    r = subprocess.run([sys.executable, "-c", _FALLBACK, ROOT, str(tmp_path / "in.npz"), str(tmp_path / "p.mlir"),
-                        str(tmp_path / "out.npz")], env=env, capture_output=True, text=True, timeout=300)
-    assert r.returncode == 0, r.stderr[-2000:]
-    other = np.load(tmp_path / "out.npz")["arr_0"]
+    (other,) = run_fresh(text, args, ["bf16"] * 4, {"PJRTX_XCD_LOCAL": "0"})
     np.testing.assert_array_equal(got, other)
