@@ -623,6 +623,13 @@ class KernelGen {
   struct RowTarget {
     std::string lds;  // LDS float array receiving the row (empty: the kernel's outputs)
     std::string row;  // row index expression when `lds` is set
+    // Emitted right after the row's inputs are requested, before they are
+    // used (a GEMV issues its weight loads there, so that waiting for the
+    // row's inputs does not wait for the weights).
+    std::function<void()> after_preload;
+    // Inputs already staged in LDS by the caller (value -> array of its
+    // storage elements): read from there, never from global memory.
+    std::map<int, std::string> lds_inputs;
   };
   void row_body(Step& s, std::map<int, std::string>& ptr_of, const RowTarget& t);
   void gemv_epilogue(Step& s, const std::map<int, std::string>& ptr_of, const std::string& seg);
@@ -1477,9 +1484,10 @@ void KernelGen::row_body(Step& s, std::map<int, std::string>& ptr_of, const RowT
   // tix*vec + k*span .. +vec (vec divides row_len, so a sweep that starts
   // inside the row is whole).
   const int64_t sweeps = (row_len + span - 1) / span;
+  auto row_shaped = [&](int v) { return prog_.type(v).elements() == n_all && !t.lds_inputs.count(v); };
   int64_t cache_regs = 0;
   for (int v : s.inputs)
-    if (prog_.type(v).elements() == n_all)
+    if (row_shaped(v))
       cache_regs += sweeps * vec * static_cast<int64_t>(std::max<size_t>(dtype_size(prog_.type(v).dtype), 4)) / 4;
   const bool cached = sweeps <= kRowCacheSweeps && cache_regs <= kRowCacheRegs;
   const bool ragged = row_len % span != 0;
@@ -1495,22 +1503,31 @@ void KernelGen::row_body(Step& s, std::map<int, std::string>& ptr_of, const RowT
   auto sweep_close = [&](std::ostream& o) { o << ((cached && ragged) ? "}\n}\n" : "}\n"); };
   if (cached) {
     for (int v : s.inputs) {
-      if (prog_.type(v).elements() != n_all) continue;
+      if (!row_shaped(v)) continue;
       const std::string st = dtype_storage_ctype(prog_.type(v).dtype);
       out_ << st << " pre_" << ptr_of[v] << "[" << sweeps << "][" << vec << "];\n";
     }
     sweep_open(out_);
     for (int v : s.inputs) {
-      if (prog_.type(v).elements() != n_all) continue;
+      if (!row_shaped(v)) continue;
       const std::string st = dtype_storage_ctype(prog_.type(v).dtype);
       out_ << "ldv<" << st << ", " << vec << ">(pre_" << ptr_of[v] << "[k], " << ptr_of[v] << ", row * " << row_len
            << "u + c, 0u, true);\n";
     }
     sweep_close(out_);
   }
+  if (t.after_preload) t.after_preload();
+  auto stage_hooks = [&](Writer& w) {
+    for (auto& [v, name] : t.lds_inputs) {
+      const DType dt = prog_.type(v).dtype;
+      const std::string nm = name;
+      w.lds_value[v] = [=](const std::string& lin) { return from_storage(dt, nm + "[" + lin + "]"); };
+    }
+  };
   auto preloads = [&](Writer& w, std::ostream& decl, std::ostream& load) {
+    stage_hooks(w);
     for (int v : s.inputs) {
-      if (prog_.type(v).elements() != n_all) continue;
+      if (!row_shaped(v)) continue;
       const std::string name = "pre_" + ptr_of[v];
       if (cached) {
         w.preload[v] = name + "[k]";
@@ -1581,6 +1598,7 @@ void KernelGen::row_body(Step& s, std::map<int, std::string>& ptr_of, const RowT
       }
       // Fold the init values, round, and evaluate this phase's outputs.
       Writer e(prog_, ptr_of, it);
+      stage_hooks(e);
       e.row_scalar = scalars;
       Idx oroot;
       oroot.key = "O";
@@ -1657,25 +1675,31 @@ void KernelGen::row_body(Step& s, std::map<int, std::string>& ptr_of, const RowT
 // Decode GEMV (kGemv): Y_g[m][n] = sum_k X[m][k] * W_g[k][n] for the members
 // g of the step, W_g [K][N_g] 16-bit with N contiguous, X [M][K].
 //
-// Workgroup b (256 threads) belongs to segment (b % 8) + 8 * ((b / 8) / wps)
-// and is the (b / 8) % wps-th of its segment's wps workgroups: all of a
-// segment's workgroups have the same b % 8, which the device maps to one XCD
-// (probed at start-up; `fused_mode` says so). A workgroup owns `cols`
-// columns of one member over one chunk of K rows. Lanes take 16-byte pieces
-// (8 columns) of a row, cols / 8 lanes per row, so a wave reads 64 / (cols / 8)
-// rows at once and each lane keeps `depth` rows in flight. X (or the prologue
-// that produces it) is staged in LDS as float. The tile's column sums fold
-// over the row lanes by xor shuffles and over the 4 waves in wave order.
+// Work items: one item is `cols` columns of one member over one chunk of
+// `kchunk` K rows; a segment (the unit whose partial sums are folded
+// together) has wps items. Segment s belongs to XCD s % 8, and workgroup b
+// runs on XCD b % 8 (the device places workgroups round-robin, probed at
+// start-up; `fused_mode` says so): workgroup b takes items b / 8, b / 8 + P,
+// b / 8 + 2P, ... of its XCD's list (P workgroups per XCD), segment by
+// segment, so segments complete early and their folds overlap the streaming
+// of later items; the next item's weight rows are loaded while the current
+// one is reduced. Lanes take 16-byte pieces (8 columns) of a row, cols / 8
+// lanes per row, so a wave reads 64 / (cols / 8) rows at once and each lane
+// keeps `depth` rows in flight. X (or the prologue that produces it) is
+// staged in LDS as float, whole or the one chunk a single-item workgroup
+// needs. An item's column sums fold over the row lanes by xor shuffles and
+// over the 4 waves in wave order.
 //
-// Unless a tile is the whole result (direct: one K chunk, no epilogue), wave
-// 0 stores the tile's partial sums to scratch, waits until its L2 has them,
-// and counts the segment's arrivals with an L2 atomic; the last workgroup of
-// the segment folds every partial in K-chunk order (reads past its L1), rounds
-// to the result type, adds the residual, stores the results that are read
-// elsewhere, keeps the segment's results in LDS, and evaluates the epilogue
-// loop's elements of the segment from them. The fold order is fixed, so the
-// result does not depend on which workgroup arrives last. Without the XCD
-// placement (fused_mode 0) agent-scope fences publish the partials instead.
+// Unless an item is the whole result (direct: one K chunk, no epilogue), wave
+// 0 stores the item's partial sums to scratch, waits until its L2 has them,
+// and counts the segment's arrivals with an L2 atomic; the workgroup that
+// completes a segment folds every partial in K-chunk order (reads past its
+// L1), rounds to the result type, adds the residual, stores the results that
+// are read elsewhere, keeps the segment's results in LDS, and evaluates the
+// epilogue loop's elements of the segment from them. The fold order is fixed,
+// so the result does not depend on which workgroup completes the segment.
+// Without the XCD placement (fused_mode 0) agent-scope fences publish the
+// partials instead.
 void KernelGen::gemv(Step& s) {
   const GemvSpec& g = s.gemv;
   std::map<int, std::string> ptr_of;
@@ -1689,9 +1713,11 @@ void KernelGen::gemv(Step& s) {
   const bool f16 = wt == DType::kF16;
   const DType rt = prog_.type(g.result[0]).dtype;
   const bool pro = !s.prologue.empty();
-  const int64_t XS = pro ? K : g.kchunk;
+  const bool all_x = g.stage_all_x;
+  const int64_t XS = all_x ? K : g.kchunk;
   const int64_t S = g.seg_cols;
   const int64_t tps = S / C;
+  const int64_t P = g.wgs / 8;  // workgroups per XCD
   std::vector<int64_t> N(G), tile0(G + 1, 0);
   for (int m = 0; m < G; ++m) {
     N[m] = prog_.type(g.result[m]).dims[1];
@@ -1702,9 +1728,9 @@ void KernelGen::gemv(Step& s) {
       if (s.outputs[o] == v) return "out" + std::to_string(o);
     return std::string();
   };
-  auto by_member = [&](const std::function<std::string(int)>& f) {  // gv_g == 0 ? f(0) : ...
+  auto by_member = [&](const std::string& gv, const std::function<std::string(int)>& f) {  // gv == 0 ? f(0) : ...
     std::string e = f(G - 1);
-    for (int m = G - 2; m >= 0; --m) e = "(gv_g == " + std::to_string(m) + "u ? " + f(m) + " : " + e + ")";
+    for (int m = G - 2; m >= 0; --m) e = "(" + gv + " == " + std::to_string(m) + "u ? " + f(m) + " : " + e + ")";
     return e;
   };
   out_ << "typedef uint32_t idx_t;\n";
@@ -1713,79 +1739,166 @@ void KernelGen::gemv(Step& s) {
   if (g.joint) out_ << "__shared__ float gv_ys[" << G * M * S << "];\n";
   if (!g.direct) out_ << "__shared__ uint32_t gv_last;\n";
   out_ << "const uint32_t gv_lane = threadIdx.x & 63u, gv_wave = threadIdx.x >> 6;\n";
-  out_ << "const uint32_t gv_jj = blockIdx.x >> 3;\n";
-  out_ << "const uint32_t gv_seg = (blockIdx.x & 7u) + 8u * (gv_jj / " << g.wps << "u);\n";
-  out_ << "const uint32_t gv_w = gv_jj % " << g.wps << "u;\n";
-  out_ << "if (gv_seg >= " << g.nseg << "u) return;\n";
-  out_ << "const uint32_t gv_ks = gv_w % " << g.ksplit << "u;\n";
-  if (g.joint) {
-    out_ << "const uint32_t gv_tg = gv_w / " << g.ksplit << "u;\n";
-    out_ << "const uint32_t gv_g = gv_tg / " << tps << "u;\n";
-    out_ << "const uint32_t gv_col0 = gv_seg * " << S << "u + (gv_tg % " << tps << "u) * " << C << "u;\n";
-  } else {
-    out_ << "uint32_t gv_g = 0u;\n";
-    for (int m = 1; m < G; ++m) out_ << "if (gv_seg >= " << tile0[m] << "u) gv_g = " << m << "u;\n";
-    out_ << "const uint32_t gv_col0 = (gv_seg - " << by_member([&](int m) { return std::to_string(tile0[m]) + "u"; })
-         << ") * " << C << "u;\n";
-  }
-  out_ << "const uint32_t gv_N = " << by_member([&](int m) { return std::to_string(N[m]) + "u"; }) << ";\n";
-  out_ << "const uint16_t* gv_W = " << by_member([&](int m) { return ptr_of.at(prog_.ops[g.dots[m]].operands[1]); })
-       << ";\n";
-  out_ << "const uint32_t gv_k0 = gv_ks * " << g.kchunk << "u;\n";
-  out_ << "const uint32_t gv_k1 = gv_k0 + " << g.kchunk << "u < " << K << "u ? gv_k0 + " << g.kchunk << "u : " << K
-       << "u;\n";
+  out_ << "const uint32_t gv_x = blockIdx.x & 7u, gv_lb = blockIdx.x >> 3;\n";
+  // items of this XCD: its segments x, x + 8, ... times wps
+  out_ << "const uint32_t gv_nx = ((" << g.nseg << "u + 7u - gv_x) / 8u) * " << g.wps << "u;\n";
+  out_ << "if (gv_lb >= gv_nx) return;\n";
   out_ << "const uint32_t gv_rg = gv_lane / " << LPR << "u, gv_cc = gv_lane % " << LPR << "u;\n";
-  out_ << "const uint32_t gv_c = gv_col0 + gv_cc * 8u;\n";
-  out_ << "const bool gv_cok = gv_c < gv_N;\n";
-  out_ << "const uint32_t gv_r0 = gv_k0 + gv_wave * " << RPW << "u + gv_rg;\n";
-  out_ << "const uint16_t* gv_wp = gv_W + (size_t)gv_r0 * gv_N + gv_c;\n";
-  // First batch of weight rows in flight before X is staged.
-  auto load_batch = [&](const std::string& dst, const std::string& it) {
-    out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) {\n";
-    out_ << "const uint32_t r = gv_r0 + (" << it << " * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
-    out_ << dst << "[i] = (gv_cok && r < gv_k1) ? gv_load16(gv_wp + (size_t)(r - gv_r0) * gv_N) : gv_u32x4{0u, 0u, 0u, 0u};\n";
-    out_ << "}\n";
+  // The item being consumed (c_*) and the next one (n_*): plain registers
+  // (a struct or a lambda taking pointers would put them on the stack and
+  // turn the weight loads into flat loads).
+  const char* fields[] = {"seg", "w", "g", "col0", "N", "k0", "k1", "r0"};
+  for (const char* pre : {"c_", "n_"}) {
+    out_ << "uint32_t";
+    for (int f = 0; f < 8; ++f) out_ << (f ? ", " : " ") << pre << fields[f];
+    out_ << ";\nconst uint16_t* " << pre << "W;\n";
+  }
+  auto assign_item = [&](const std::string& p, const std::string& it) {
+    out_ << p << "seg = gv_x + 8u * ((" << it << ") / " << g.wps << "u);\n";
+    out_ << p << "w = (" << it << ") % " << g.wps << "u;\n";
+    out_ << "{\nconst uint32_t ks = " << p << "w % " << g.ksplit << "u;\n";
+    if (g.joint) {
+      out_ << "const uint32_t tg = " << p << "w / " << g.ksplit << "u;\n";
+      out_ << p << "g = tg / " << tps << "u;\n";
+      out_ << p << "col0 = " << p << "seg * " << S << "u + (tg % " << tps << "u) * " << C << "u;\n";
+    } else {
+      out_ << p << "g = 0u;\n";
+      for (int m = 1; m < G; ++m) out_ << "if (" << p << "seg >= " << tile0[m] << "u) " << p << "g = " << m << "u;\n";
+      out_ << p << "col0 = (" << p << "seg - " << by_member(p + "g", [&](int m) { return std::to_string(tile0[m]) + "u"; })
+           << ") * " << C << "u;\n";
+    }
+    out_ << p << "N = " << by_member(p + "g", [&](int m) { return std::to_string(N[m]) + "u"; }) << ";\n";
+    out_ << p << "W = " << by_member(p + "g", [&](int m) { return ptr_of.at(prog_.ops[g.dots[m]].operands[1]); })
+         << ";\n";
+    out_ << p << "k0 = ks * " << g.kchunk << "u;\n";
+    out_ << p << "k1 = " << p << "k0 + " << g.kchunk << "u < " << K << "u ? " << p << "k0 + " << g.kchunk << "u : " << K
+         << "u;\n";
+    out_ << p << "r0 = " << p << "k0 + gv_wave * " << RPW << "u + gv_rg;\n}\n";
   };
+  // Batch b of an item: rows r0 + (b * depth + i) * RS for i < depth. The
+  // loads are unconditional (no branch between them, all in flight at once):
+  // rows past the chunk read its last row and columns past N read the last
+  // piece; the FMA loop skips those rows and the stores skip those columns.
+  auto load_batch = [&](const std::string& p, const std::string& b, const std::string& dst) {
+    out_ << "{\nconst uint32_t c0 = " << p << "col0 + gv_cc * 8u;\n";
+    out_ << "const uint32_t c = c0 < " << p << "N ? c0 : " << p << "N - 8u;\n";
+    out_ << "const uint16_t* wp = " << p << "W + c;\n";
+    out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) {\n";
+    out_ << "const uint32_t r = " << p << "r0 + ((" << b << ") * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
+    out_ << "const uint32_t rr = r < " << p << "k1 ? r : " << p << "k1 - 1u;\n";
+    out_ << dst << "[i] = gv_load16(wp + (size_t)rr * " << p << "N);\n";
+    out_ << "}\n}\n";
+  };
+  assign_item("c_", "gv_lb");
   out_ << "gv_u32x4 gv_wv[" << D << "];\n";
-  load_batch("gv_wv", "0u");
+  // X is requested before the first weight rows, so that the wait for X
+  // (loads complete in order) does not include the weights.
   if (pro) {
-    Step& P = s.prologue[0];
-    out_ << "for (uint32_t gv_prow = 0; gv_prow < " << M << "u; ++gv_prow) {\n";
+    Step& Pst = s.prologue[0];
     RowTarget t;
     t.lds = "gv_xs";
-    t.row = "gv_prow";
-    row_body(P, ptr_of, t);
-    out_ << "__syncthreads();\n}\n";
+    // The prologue's inputs (a few KB: the row and the norm weights) are
+    // copied to LDS with 16-byte loads issued before the weight rows, so the
+    // prologue never waits on a global load issued after them.
+    int64_t staged_bytes = 0;
+    bool stageable = true;
+    for (int v : Pst.inputs) {
+      staged_bytes += prog_.type(v).bytes();
+      stageable &= prog_.type(v).bytes() % 16 == 0;
+    }
+    if (stageable && staged_bytes <= 32768) {
+      int k = 0;
+      std::vector<std::pair<int, int64_t>> pieces;  // value, 16-byte pieces
+      for (int v : Pst.inputs) {
+        const std::string name = "gv_pin" + std::to_string(k++);
+        out_ << "__shared__ __attribute__((aligned(16))) " << dtype_storage_ctype(prog_.type(v).dtype) << " " << name
+             << "[" << prog_.type(v).elements() << "];\n";
+        t.lds_inputs[v] = name;
+        pieces.push_back({v, prog_.type(v).bytes() / 16});
+      }
+      for (size_t q = 0; q < pieces.size(); ++q) {
+        const int64_t per = (pieces[q].second + 255) / 256;
+        out_ << "gv_u32x4 gv_pr" << q << "[" << per << "];\n";
+        out_ << "#pragma unroll\nfor (int j = 0; j < " << per << "; ++j) {\n";
+        out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)j;\n";
+        out_ << "if (i < " << pieces[q].second << "u) gv_pr" << q << "[j] = reinterpret_cast<const gv_u32x4*>("
+             << ptr_of.at(pieces[q].first) << ")[i];\n}\n";
+      }
+      load_batch("c_", "0u", "gv_wv");
+      for (size_t q = 0; q < pieces.size(); ++q) {
+        const int64_t per = (pieces[q].second + 255) / 256;
+        out_ << "#pragma unroll\nfor (int j = 0; j < " << per << "; ++j) {\n";
+        out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)j;\n";
+        out_ << "if (i < " << pieces[q].second << "u) reinterpret_cast<gv_u32x4*>(" << t.lds_inputs[pieces[q].first]
+             << ")[i] = gv_pr" << q << "[j];\n}\n";
+      }
+      out_ << "__syncthreads();\n";
+      t.row = "gv_prow";
+      out_ << "for (uint32_t gv_prow = 0; gv_prow < " << M << "u; ++gv_prow) {\n";
+      row_body(Pst, ptr_of, t);
+      out_ << "__syncthreads();\n}\n";
+    } else if (M == 1) {
+      t.row = "0u";
+      t.after_preload = [&]() { load_batch("c_", "0u", "gv_wv"); };
+      out_ << "{\n";
+      row_body(Pst, ptr_of, t);
+      out_ << "__syncthreads();\n}\n";
+    } else {
+      load_batch("c_", "0u", "gv_wv");
+      t.row = "gv_prow";
+      out_ << "for (uint32_t gv_prow = 0; gv_prow < " << M << "u; ++gv_prow) {\n";
+      row_body(Pst, ptr_of, t);
+      out_ << "__syncthreads();\n}\n";
+    }
   } else {
     const std::string X = ptr_of.at(g.x);
-    out_ << "for (uint32_t i = threadIdx.x; i < " << M * g.kchunk << "u; i += 256u) {\n";
-    out_ << "const uint32_t m = i / " << g.kchunk << "u, k = gv_k0 + i % " << g.kchunk << "u;\n";
-    out_ << "gv_xs[i] = k < " << K << "u ? " << load_expr(wt, X, "m * " + std::to_string(K) + "u + k") << " : 0.0f;\n";
-    out_ << "}\n__syncthreads();\n";
+    const int64_t nx = all_x ? M * K : M * g.kchunk;
+    const int64_t per = (nx + 255) / 256;
+    out_ << "float gv_xr[" << per << "];\n";
+    out_ << "#pragma unroll\nfor (int j = 0; j < " << per << "; ++j) {\n";
+    out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)j;\n";
+    if (all_x) {
+      out_ << "gv_xr[j] = i < " << nx << "u ? " << load_expr(wt, X, "i") << " : 0.0f;\n";
+    } else {
+      out_ << "const uint32_t m = i / " << g.kchunk << "u, k = c_k0 + i % " << g.kchunk << "u;\n";
+      out_ << "gv_xr[j] = (i < " << nx << "u && k < " << K << "u) ? "
+           << load_expr(wt, X, "m * " + std::to_string(K) + "u + k") << " : 0.0f;\n";
+    }
+    out_ << "}\n";
+    load_batch("c_", "0u", "gv_wv");
+    out_ << "#pragma unroll\nfor (int j = 0; j < " << per << "; ++j) {\n";
+    out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)j;\n";
+    out_ << "if (i < " << nx << "u) gv_xs[i] = gv_xr[j];\n}\n";
+    out_ << "__syncthreads();\n";
   }
   out_ << "float gv_acc[" << M << "][8];\n";
   out_ << "#pragma unroll\nfor (int m = 0; m < " << M << "; ++m)\n#pragma unroll\nfor (int e = 0; e < 8; ++e) gv_acc[m][e] = 0.0f;\n";
-  out_ << "#pragma unroll\nfor (uint32_t it = 0; it < " << iters << "u; ++it) {\n";
-  out_ << "gv_u32x4 gv_nx[" << D << "];\n";
-  out_ << "if (it + 1u < " << iters << "u) {\n";
-  load_batch("gv_nx", "(it + 1u)");
-  out_ << "}\n";
+  out_ << "uint32_t gv_it = gv_lb, gv_b = 0u;\n";
+  out_ << "while (true) {\n";
+  out_ << "uint32_t gv_nit = gv_it, gv_nb = gv_b + 1u;\n";
+  out_ << "if (gv_nb == " << iters << "u) { gv_nit = gv_it + " << P << "u; gv_nb = 0u; }\n";
+  out_ << "const bool gv_more = gv_nit < gv_nx;\n";
+  out_ << "if (gv_more && gv_nb == 0u) {\n";
+  assign_item("n_", "gv_nit");
+  out_ << "} else {\n";
+  for (const char* f : fields) out_ << "n_" << f << " = c_" << f << "; ";
+  out_ << "n_W = c_W;\n}\n";
+  out_ << "gv_u32x4 gv_nv[" << D << "];\n";
+  out_ << "if (gv_more) ";
+  load_batch("n_", "gv_nb", "gv_nv");
   out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) {\n";
-  out_ << "const uint32_t r = gv_r0 + (it * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
-  out_ << "if (r < gv_k1) {\n";
+  out_ << "const uint32_t r = c_r0 + (gv_b * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
+  out_ << "if (r < c_k1) {\n";
   out_ << "#pragma unroll\nfor (int m = 0; m < " << M << "; ++m) gv_fma8<" << (f16 ? "true" : "false")
-       << ">(gv_acc[m], gv_xs[m * " << XS << "u + r" << (pro ? "" : " - gv_k0") << "], gv_wv[i]);\n";
+       << ">(gv_acc[m], gv_xs[m * " << XS << "u + r" << (all_x ? "" : " - c_k0") << "], gv_wv[i]);\n";
   out_ << "}\n}\n";
-  out_ << "if (it + 1u < " << iters << "u) {\n#pragma unroll\nfor (int i = 0; i < " << D
-       << "; ++i) gv_wv[i] = gv_nx[i];\n}\n";
-  out_ << "}\n";
-  // Fold the row lanes (xor over the row-group bits), then the waves.
+  out_ << "if (gv_b + 1u == " << iters << "u) {\n";
+  // ---- item done: fold the row lanes (xor over the row-group bits), then the waves
   out_ << "#pragma unroll\nfor (int m = 0; m < " << M << "; ++m)\n#pragma unroll\nfor (int e = 0; e < 8; ++e) {\n";
   out_ << "float v = gv_acc[m][e];\n";
   for (int sh = LPR; sh < 64; sh <<= 1) out_ << "v += wave_shfl_xor(v, " << sh << ");\n";
-  out_ << "gv_acc[m][e] = v;\n}\n";
-  out_ << "if (gv_rg == 0u) {\n#pragma unroll\nfor (int m = 0; m < " << M
-       << "; ++m)\n#pragma unroll\nfor (int e = 0; e < 8; ++e) gv_red[gv_wave][m][gv_cc * 8u + e] = gv_acc[m][e];\n}\n";
+  out_ << "gv_acc[m][e] = 0.0f;\n";
+  out_ << "if (gv_rg == 0u) gv_red[gv_wave][m][gv_cc * 8u + e] = v;\n}\n";
   out_ << "__syncthreads();\n";
   auto member_value = [&](const std::string& m_expr, const std::string& col, const std::string& sum, int m) {
     // rounded product, plus the residual when the member has one
@@ -1796,79 +1909,88 @@ void KernelGen::gemv(Step& s) {
     }
     return y;
   };
-  if (g.direct) {
-    out_ << "for (uint32_t i = threadIdx.x; i < " << M * C << "u; i += 256u) {\n";
-    out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u, col = gv_col0 + c;\n";
-    out_ << "if (col < gv_N) {\n";
-    out_ << "const float p = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
-    for (int m = 0; m < G; ++m) {
-      out_ << "if (gv_g == " << m << "u) { const float y = " << member_value("m", "col", "p", m) << "; " << out_of(g.result[m])
-           << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << "; }\n";
-    }
-    out_ << "}\n}\n}\n\n";
-    return;
-  }
-  out_ << "float* gv_part = reinterpret_cast<float*>(scratch);\n";
-  out_ << "if (gv_wave == 0u) {\n";
-  out_ << "for (uint32_t i = gv_lane; i < " << M * C << "u; i += 64u) {\n";
-  out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u;\n";
-  out_ << "gv_part[((size_t)(gv_seg * " << g.wps << "u + gv_w) * " << M << "u + m) * " << C
-       << "u + c] = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
-  out_ << "}\n";
-  out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
-  out_ << "if (!fused_mode) __threadfence();\n";
-  out_ << "if (gv_lane == 0u) {\n";
-  // one counter per 128-byte line
-  out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + gv_seg * 32u;\n";
-  out_ << "const uint32_t last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == "
-       << g.wps - 1 << "u;\n";
-  out_ << "if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
-  out_ << "gv_last = last;\n}\n}\n";
-  out_ << "__syncthreads();\n";
-  out_ << "if (!gv_last) return;\n";
-  out_ << "if (!fused_mode) __threadfence();\n";
   auto ld = [&](const std::string& addr) {
     return "__hip_atomic_load(&" + addr + ", __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)";
   };
-  if (g.joint) {
-    out_ << "for (uint32_t i = threadIdx.x; i < " << G * M * S << "u; i += 256u) {\n";
-    out_ << "const uint32_t gv_g = i / " << M * S << "u, rem = i % " << M * S << "u;\n";
-    out_ << "const uint32_t m = rem / " << S << "u, c = rem % " << S << "u;\n";
-    out_ << "const size_t base = (size_t)gv_seg * " << g.wps << "u + ((size_t)gv_g * " << tps << "u + c / " << C
-         << "u) * " << g.ksplit << "u;\n";
-    out_ << "float sum = 0.0f;\n";
-    out_ << "for (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
-         << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c % " +
-               std::to_string(C) + "u]")
-         << ";\n";
-    out_ << "const uint32_t col = gv_seg * " << S << "u + c;\n";
-    out_ << "float y = 0.0f;\n";
-    for (int m = 0; m < G; ++m) {
-      out_ << "if (gv_g == " << m << "u) {\n";
-      out_ << "y = " << member_value("m", "col", "sum", m) << ";\n";
-      if (g.store[m]) out_ << out_of(g.result[m]) << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << ";\n";
-      out_ << "}\n";
-    }
-    out_ << "gv_ys[i] = y;\n";
-    out_ << "}\n";
-  } else {
+  if (g.direct) {
     out_ << "for (uint32_t i = threadIdx.x; i < " << M * C << "u; i += 256u) {\n";
-    out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u, col = gv_col0 + c;\n";
-    out_ << "if (col < gv_N) {\n";
-    out_ << "const size_t base = (size_t)gv_seg * " << g.wps << "u;\n";
-    out_ << "float sum = 0.0f;\n";
-    out_ << "for (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
-         << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c]") << ";\n";
+    out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u, col = c_col0 + c;\n";
+    out_ << "if (col < c_N) {\n";
+    out_ << "const float p = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
     for (int m = 0; m < G; ++m) {
-      out_ << "if (gv_g == " << m << "u) { const float y = " << member_value("m", "col", "sum", m) << "; "
+      out_ << "if (c_g == " << m << "u) { const float y = " << member_value("m", "col", "p", m) << "; "
            << out_of(g.result[m]) << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << "; }\n";
     }
     out_ << "}\n}\n";
-  }
-  if (!s.epilogue_loop.empty()) {
+    out_ << "__syncthreads();\n";  // gv_red is rewritten by the next item
+  } else {
+    out_ << "float* gv_part = reinterpret_cast<float*>(scratch);\n";
+    out_ << "if (gv_wave == 0u) {\n";
+    out_ << "for (uint32_t i = gv_lane; i < " << M * C << "u; i += 64u) {\n";
+    out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u;\n";
+    out_ << "gv_part[((size_t)(c_seg * " << g.wps << "u + c_w) * " << M << "u + m) * " << C
+         << "u + c] = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
+    out_ << "}\n";
+    out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
+    out_ << "if (!fused_mode) __threadfence();\n";
+    out_ << "if (gv_lane == 0u) {\n";
+    // one counter per 128-byte line
+    out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + c_seg * 32u;\n";
+    out_ << "const uint32_t last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == "
+         << g.wps - 1 << "u;\n";
+    out_ << "if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
+    out_ << "gv_last = last;\n}\n}\n";
     out_ << "__syncthreads();\n";
-    gemv_epilogue(s, ptr_of, "gv_seg");
+    out_ << "if (gv_last) {\n";
+    out_ << "if (!fused_mode) __threadfence();\n";
+    if (g.joint) {
+      out_ << "for (uint32_t i = threadIdx.x; i < " << G * M * S << "u; i += 256u) {\n";
+      out_ << "const uint32_t gv_g = i / " << M * S << "u, rem = i % " << M * S << "u;\n";
+      out_ << "const uint32_t m = rem / " << S << "u, c = rem % " << S << "u;\n";
+      out_ << "const size_t base = (size_t)c_seg * " << g.wps << "u + ((size_t)gv_g * " << tps << "u + c / " << C
+           << "u) * " << g.ksplit << "u;\n";
+      out_ << "float sum = 0.0f;\n";
+      out_ << "#pragma unroll\nfor (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
+           << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c % " +
+                 std::to_string(C) + "u]")
+           << ";\n";
+      out_ << "const uint32_t col = c_seg * " << S << "u + c;\n";
+      out_ << "float y = 0.0f;\n";
+      for (int m = 0; m < G; ++m) {
+        out_ << "if (gv_g == " << m << "u) {\n";
+        out_ << "y = " << member_value("m", "col", "sum", m) << ";\n";
+        if (g.store[m]) out_ << out_of(g.result[m]) << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << ";\n";
+        out_ << "}\n";
+      }
+      out_ << "gv_ys[i] = y;\n";
+      out_ << "}\n";
+    } else {
+      out_ << "for (uint32_t i = threadIdx.x; i < " << M * C << "u; i += 256u) {\n";
+      out_ << "const uint32_t m = i / " << C << "u, c = i % " << C << "u, col = c_col0 + c;\n";
+      out_ << "if (col < c_N) {\n";
+      out_ << "const size_t base = (size_t)c_seg * " << g.wps << "u;\n";
+      out_ << "float sum = 0.0f;\n";
+      out_ << "#pragma unroll\nfor (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
+           << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c]") << ";\n";
+      for (int m = 0; m < G; ++m) {
+        out_ << "if (c_g == " << m << "u) { const float y = " << member_value("m", "col", "sum", m) << "; "
+             << out_of(g.result[m]) << "[m * " << N[m] << "u + col] = " << to_storage(rt, "y") << "; }\n";
+      }
+      out_ << "}\n}\n";
+    }
+    if (!s.epilogue_loop.empty()) {
+      out_ << "__syncthreads();\n";
+      gemv_epilogue(s, ptr_of, "c_seg");
+    }
+    out_ << "}\n";  // gv_last
   }
+  out_ << "}\n";  // item done
+  out_ << "if (!gv_more) break;\n";
+  out_ << "gv_it = gv_nit; gv_b = gv_nb;\n";
+  for (const char* f : fields) out_ << "c_" << f << " = n_" << f << "; ";
+  out_ << "c_W = n_W;\n";
+  out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) gv_wv[i] = gv_nv[i];\n";
+  out_ << "}\n";
   out_ << "}\n\n";
 }
 

@@ -377,7 +377,7 @@ class GemvFuser {
           written_between(prog_, steps_, i, l, ww.operand))
         return;
     }
-    const int cols = tile_cols();
+    const int cols = tile_cols(N * static_cast<int64_t>(G.gemv.dots.size()));
     if (N % cols != 0) return;
     const int64_t S = segment_width(G, L, N, cols);
     if (S == 0) return;
@@ -416,14 +416,26 @@ class GemvFuser {
     steps_.erase(steps_.begin() + l);
   }
 
-  int tile_cols() const {
-    const int64_t c = env_int("PJRTX_GEMV_COLS", 64);
-    return (c == 32 || c == 128) ? static_cast<int>(c) : 64;
+  // Tile width: PJRTX_GEMV_COLS (32, 64 or 128) when set, else 128 columns
+  // for wide products (8192 columns and more over the members) and 64 for the
+  // rest (measured on cold weights: 128 is 4-8% faster on the 5632 x 2 gate/up
+  // and 32000-column lm_head products, slower on 2048-column ones).
+  int tile_cols(int64_t total_n = 0) const {
+    const int64_t c = env_int("PJRTX_GEMV_COLS", 0);
+    if (c == 32 || c == 64 || c == 128) return static_cast<int>(c);
+    return total_n >= 8192 ? 128 : 64;
   }
 
   void shape(Step* s) {
     GemvSpec& g = s->gemv;
-    g.cols = tile_cols();
+    int64_t total_n = 0;
+    for (int dd : g.dots) total_n += prog_.type(prog_.ops[dd].results[0]).dims[1];
+    // Joint segments were sized for the tile width chosen when the epilogue
+    // was absorbed; keep tiles within a segment.
+    g.cols = tile_cols(total_n);
+    if (g.joint) {
+      while (g.cols > 32 && g.seg_cols % g.cols != 0) g.cols /= 2;
+    }
     const int64_t d = env_int("PJRTX_GEMV_DEPTH", 8);
     g.depth = (d == 4 || d == 16) ? static_cast<int>(d) : 8;
     const int64_t rows_per_step = 4 * (64 / (g.cols / 8));  // 256 threads
@@ -441,18 +453,35 @@ class GemvFuser {
       }
       tiles = g.nseg;
     }
-    const int64_t target = std::max<int64_t>(opts_.gemv_target_wgs, 1);
-    int64_t ksplit = std::max<int64_t>(1, (target + tiles / 2) / tiles);
-    ksplit = std::min<int64_t>(ksplit, std::max<int64_t>(1, g.K / rows_per_step));
-    int64_t kchunk = (g.K + ksplit - 1) / ksplit;
-    kchunk = (kchunk + rows_per_step - 1) / rows_per_step * rows_per_step;
-    // Without a prologue the chunk of X is staged in LDS.
+    // One item per workgroup, the K split aiming at PJRTX_GEMV_WGS workgroups
+    // (768). With PJRTX_GEMV_PERSIST=1, one batch of `depth` rows per lane is
+    // one item and PJRTX_GEMV_PWGS workgroups (512) walk the items,
+    // prefetching the next while folding the last: slower on this GPU (the
+    // wait for a partial's stores before its arrival count also waits for the
+    // prefetched loads, which complete in order), so off by default.
+    const bool persist = env_int("PJRTX_GEMV_PERSIST", 0) != 0 && g.M * g.K <= kMaxLdsFloats;
+    int64_t kchunk;
+    if (persist) {
+      kchunk = rows_per_step * g.depth;
+    } else {
+      const int64_t target = std::max<int64_t>(opts_.gemv_target_wgs, 1);
+      int64_t ksplit = std::max<int64_t>(1, (target + tiles / 2) / tiles);
+      ksplit = std::min<int64_t>(ksplit, std::max<int64_t>(1, g.K / rows_per_step));
+      kchunk = (g.K + ksplit - 1) / ksplit;
+      kchunk = (kchunk + rows_per_step - 1) / rows_per_step * rows_per_step;
+    }
+    // A workgroup that stages only its chunk of X keeps it within the LDS cap.
     const int64_t xs_cap = kMaxLdsFloats / g.M / rows_per_step * rows_per_step;
     if (s->prologue.empty()) kchunk = std::min(kchunk, xs_cap);
     g.kchunk = kchunk;
     g.ksplit = (g.K + kchunk - 1) / kchunk;
     g.wps = (g.joint ? members * (g.seg_cols / g.cols) : 1) * g.ksplit;
     g.direct = g.ksplit == 1 && !g.joint;
+    const int64_t items_x = (g.nseg + 7) / 8 * g.wps;  // items of the busiest XCD
+    int64_t per_xcd = items_x;
+    if (persist) per_xcd = std::min<int64_t>(items_x, std::max<int64_t>(1, env_int("PJRTX_GEMV_PWGS", 512) / 8));
+    g.wgs = 8 * per_xcd;
+    g.stage_all_x = !s->prologue.empty() || per_xcd < items_x;
     g.partial_bytes = g.direct ? 0 : static_cast<size_t>(g.nseg * g.wps * g.M * g.cols) * 4;
     g.partial_bytes = (g.partial_bytes + 255) / 256 * 256;
     if (!g.direct) {
@@ -460,7 +489,7 @@ class GemvFuser {
       s->counter_offset = g.partial_bytes;
       s->scratch_bytes = g.partial_bytes + static_cast<size_t>(g.nseg) * 128;
     }
-    s->grid = static_cast<uint32_t>(8 * ((g.nseg + 7) / 8) * g.wps);
+    s->grid = static_cast<uint32_t>(g.wgs);
     s->block = 256;
   }
 

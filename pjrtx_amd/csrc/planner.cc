@@ -1271,7 +1271,8 @@ std::string Plan::describe(const Program& prog) const {
       o << ",\"flops\":" << flops << ",\"members\":" << g.dots.size() << ",\"M\":" << g.M << ",\"K\":" << g.K
         << ",\"N\":" << ns << "],\"cols\":" << g.cols << ",\"depth\":" << g.depth << ",\"ksplit\":" << g.ksplit
         << ",\"kchunk\":" << g.kchunk << ",\"joint\":" << (g.joint ? "true" : "false")
-        << ",\"seg_cols\":" << g.seg_cols << ",\"segments\":" << g.nseg << ",\"wg_per_segment\":" << g.wps
+        << ",\"seg_cols\":" << g.seg_cols << ",\"segments\":" << g.nseg << ",\"items_per_segment\":" << g.wps << ",\"workgroups\":" << g.wgs
+        << ",\"stage_all_x\":" << (g.stage_all_x ? "true" : "false")
         << ",\"direct\":" << (g.direct ? "true" : "false") << ",\"fused_combine\":" << (s.fused_combine ? "true" : "false")
         << ",\"prologue\":" << (s.prologue.empty() ? "null" : "\"" + std::string("rowfused") + "\"")
         << ",\"epilogue_loop\":[";

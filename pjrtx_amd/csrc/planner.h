@@ -83,6 +83,8 @@ struct GemvSpec {
   int64_t root_per_seg = 0;                 // epilogue loop elements per segment
   bool direct = false;                      // ksplit 1, no epilogue: tiles store their results
   size_t partial_bytes = 0;                 // partial slots before the counters in scratch
+  int64_t wgs = 0;                          // workgroups launched (8 per XCD round)
+  bool stage_all_x = false;                 // whole X in LDS (else each workgroup's one chunk)
 };
 
 struct Step {
