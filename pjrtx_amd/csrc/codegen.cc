@@ -790,11 +790,17 @@ void KernelGen::reduce(Step& s) {
   bool epilogue_then_combine = false;  // fused combine: also emit the `_combine` fallback kernel
   std::string combine_fallback_body;
   if (s.row_schedule) {
-    if (s.fused_combine) {
+    if (s.fused_combine && s.rows % 8 == 0) {
       // Workgroup b runs on XCD b % 8 and rows % 8 == 0: with row = b % rows
       // every split of a row lands on the same XCD (one L2).
       head << "const idx_t row = (idx_t)blockIdx.x % " << s.rows << "u;\n";
       head << "const idx_t split = (idx_t)blockIdx.x / " << s.rows << "u;\n";
+    } else if (s.fused_combine) {
+      // Padded grid: row (b % 8) + 8 * ((b / 8) / splits) keeps a row's
+      // splits on XCD b % 8; workgroups past the last row exit.
+      head << "const idx_t row = (idx_t)(blockIdx.x & 7u) + 8u * ((idx_t)(blockIdx.x >> 3) / " << s.splits << "u);\n";
+      head << "const idx_t split = (idx_t)(blockIdx.x >> 3) % " << s.splits << "u;\n";
+      head << "if (row >= " << s.rows << "u) return;\n";
     } else {
       head << "const idx_t row = (idx_t)blockIdx.x / " << s.splits << "u;\n";
       head << "const idx_t split = (idx_t)blockIdx.x - row * " << s.splits << "u;\n";

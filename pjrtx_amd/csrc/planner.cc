@@ -295,6 +295,10 @@ class Planner {
   void shape_loop(Step* s);
 };
 
+// Total inlined ops below which an expensive value is recomputed under a
+// broadcast instead of being materialized.
+constexpr int64_t kRecomputeBroadcastOps = int64_t(1) << 20;
+
 void Planner::decide_materialization() {
   for (int p : prog_.params) mat_.insert(p);
   for (int r : prog_.results) outputs_.insert(r);
@@ -347,8 +351,11 @@ void Planner::decide_materialization() {
     if (op.kind == OpKind::kBroadcastInDim && !op.operands.empty()) {
       const int u = op.operands[0];
       const bool expands = prog_.type(op.results[0]).elements() > prog_.type(u).elements();
-      if (expands && !mat_.count(u) && cost[u] > 8 && prog_.type(u).elements() > 1) {
-        // Avoid recomputing an expensive value once per broadcast element.
+      if (expands && !mat_.count(u) && cost[u] > 8 && prog_.type(u).elements() > 1 &&
+          prog_.type(op.results[0]).elements() * cost[u] > kRecomputeBroadcastOps) {
+        // Avoid recomputing an expensive value once per broadcast element
+        // (unless the whole broadcast is small: a decode step's RoPE tables,
+        // recomputed per head, cost less than the launch that would hold them).
         mat_.insert(u);
         c -= cost[u];
       }
@@ -369,8 +376,12 @@ void Planner::decide_materialization() {
     const int v = op.results[0];
     int64_t rbytes = 0;
     for (int w : rd) rbytes += prog_.type(w).bytes();
+    // Small values (the whole recomputation under 2^20 ops) are recomputed
+    // whatever their per-element cost.
+    const bool costly = c > opts_.recompute_limit &&
+                        prog_.type(v).elements() * c * static_cast<int64_t>(users_[v].size()) > kRecomputeBroadcastOps;
     if (users_[v].size() > 1 && !is_splat_constant(prog_, op) &&
-        (c > opts_.recompute_limit || (rd.size() > 1 && 2 * rbytes > 3 * prog_.type(v).bytes()))) {
+        (costly || (rd.size() > 1 && 2 * rbytes > 3 * prog_.type(v).bytes()))) {
       mat_.insert(v);
       c = 0;
       rd.clear();
@@ -1150,10 +1161,14 @@ void Planner::shape_reduce(Step* s) {
     // the same launch, and the combine kernel remains the fallback for a
     // device that does not place workgroups round-robin on its XCDs.
     s->combine_grid = static_cast<uint32_t>((rows + 3) / 4);
-    if (opts_.reduce_fused_combine && rows % 8 == 0) {
+    if (opts_.reduce_fused_combine) {
       // One 32-bit arrival counter per row, each on a 128-byte line of its
-      // own, after the 8-byte slots.
+      // own, after the 8-byte slots. With rows a multiple of 8, row = b %
+      // rows keeps a row's splits on one XCD; otherwise the grid is padded to
+      // 8 * ceil(rows / 8) * splits workgroups, row (b % 8) + 8 * ((b / 8) /
+      // splits) (the rest exit at once).
       s->fused_combine = true;
+      if (rows % 8 != 0) s->grid = static_cast<uint32_t>(8 * ((rows + 7) / 8) * splits);
       s->counter_offset = (s->scratch_bytes + 127) / 128 * 128;
       s->scratch_bytes = s->counter_offset + static_cast<size_t>(rows) * 128;
     }
