@@ -473,6 +473,15 @@ std::string Writer::emit_op(const Op& op, int v, int id) {
       return define(R, std::string("(") + ct + ")(__clz((int32_t)(uint32_t)(" + unsigned_of(A) + ")" + a[0] + ") - " +
                            std::to_string(32 - bits) + ")");
     }
+    case OpKind::kReducePrecision: {
+      PJRTX_CHECK(op.exponent_bits >= 1 && op.mantissa_bits >= 0, Code::kInvalidArgument,
+                  "reduce_precision: exponent_bits must be >= 1 and mantissa_bits >= 0");
+      const char* fn = R == DType::kF32 ? "rp_f32" : R == DType::kF64 ? "rp_f64" : R == DType::kBF16 ? "rp_bf16"
+                     : R == DType::kF16 ? "rp_f16" : nullptr;
+      PJRTX_CHECK(fn != nullptr, Code::kUnimplemented, "reduce_precision: element type must be a float");
+      return define(R, std::string(fn) + "(" + a[0] + ", " + std::to_string(op.exponent_bits) + ", " +
+                           std::to_string(op.mantissa_bits) + ")");
+    }
     case OpKind::kConvert: {
       const std::string x = a[0];
       if (R == DType::kPred) return define(R, x + " != 0");

@@ -26,6 +26,8 @@ enum class OpKind {
   kAbs, kNegate, kExp, kExpm1, kLog, kLog1p, kLogistic, kSqrt, kRsqrt, kCbrt,
   kTanh, kSine, kCosine, kTan, kFloor, kCeil, kRoundAfz, kRoundEven, kSign,
   kNot, kIsFinite, kPopcnt, kClz, kConvert, kBitcastConvert,
+  // rounds to `mantissa_bits` / clamps to `exponent_bits` in the same type
+  kReducePrecision,
   // elementwise binary
   kAdd, kSubtract, kMultiply, kDivide, kRemainder, kPower, kMaximum, kMinimum,
   kAnd, kOr, kXor, kShiftLeft, kShiftRightArithmetic, kShiftRightLogical,
@@ -38,6 +40,10 @@ enum class OpKind {
   kConcatenate, kPad, kDynamicSlice, kDynamicUpdateSlice,
   // reductions and library ops
   kReduce, kDotGeneral, kGather, kScatter,
+  // windowed reduction: regions[0] the reducer; window in `sizes`, strides in
+  // `strides`, dilations in base_dilations / window_dilations, padding in
+  // pad_low / pad_high
+  kReduceWindow,
   // control flow: regions[0] = cond (state -> pred), regions[1] = body
   // (state -> state); operands = initial state, results = final state
   kWhile,
@@ -98,6 +104,10 @@ struct Op {
   // dynamic_slice sizes / gather slice_sizes
   Dims sizes;
 
+  // reduce_precision
+  int64_t exponent_bits = -1, mantissa_bits = -1;
+  // reduce_window dilations
+  Dims base_dilations, window_dilations;
   // dot_general dimension numbers
   Dims lhs_batch, rhs_batch, lhs_contract, rhs_contract;
 
@@ -147,6 +157,7 @@ struct Program {
   std::vector<int> param_alias;
   int num_partitions = 1;
   int num_replicas = 1;
+  int64_t mesh_devices = 1;  // largest `sdy.mesh` declared (shardings are ignored)
 
   const TensorType& type(int v) const { return values.at(v).type; }
   std::string describe() const;  // one line per op, for diagnostics

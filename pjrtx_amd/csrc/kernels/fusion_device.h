@@ -51,6 +51,48 @@ PJRTX_DEV float add_f16v(float acc, float x) {
   return r;
 }
 
+// stablehlo.reduce_precision on the bits of a float with E exponent and Mn
+// mantissa bits: the mantissa rounds to m bits (to nearest, ties to even;
+// a carry moves into the exponent), then exponents beyond e bits' range go
+// to +-inf (overflow) or +-0 (underflow, which includes the source's
+// subnormals when e < E). A NaN input stays that NaN when m > 0.
+template <typename U, int E, int Mn>
+PJRTX_DEV U rp_bits(U u, int e, int m) {
+  constexpr int W = 1 + E + Mn;
+  const U sign = (U)((U)1 << (W - 1));
+  const U expm = (U)((((U)1 << E) - 1) << Mn);
+  const U manm = (U)(((U)1 << Mn) - 1);
+  const bool nan = (U)(u & expm) == expm && (U)(u & manm) != 0;
+  const U x = u;
+  if (m < Mn) {
+    const int sh = Mn - m;
+    const U last = (U)((U)1 << sh);
+    const U bias = (U)((last >> 1) - 1 + ((u & last) >> sh));
+    u = (U)((U)(u + bias) & (U)~(U)(last - 1));
+  }
+  if (e < E) {
+    const U b = (U)(((U)1 << (E - 1)) - 1);
+    const U rb = (U)(((U)1 << (e - 1)) - 1);
+    const U xe = (U)(u & expm);
+    const bool over = xe > (U)((U)(b + rb) << Mn);
+    const bool under = xe <= (U)((U)(b - rb) << Mn);
+    const U sz = (U)(u & sign);
+    u = over ? (U)(sz | expm) : (under ? sz : u);
+  }
+  return (m > 0 && nan) ? x : u;
+}
+PJRTX_DEV float rp_f32(float x, int e, int m) {
+  return __builtin_bit_cast(float, rp_bits<uint32_t, 8, 23>(__builtin_bit_cast(uint32_t, x), e, m));
+}
+PJRTX_DEV double rp_f64(double x, int e, int m) {
+  return __builtin_bit_cast(double, rp_bits<uint64_t, 11, 52>(__builtin_bit_cast(uint64_t, x), e, m));
+}
+// 16-bit types arrive as the float of their value (exact).
+PJRTX_DEV float rp_bf16(float x, int e, int m) {
+  return bf16_to_f32(rp_bits<uint16_t, 8, 7>((uint16_t)(__builtin_bit_cast(uint32_t, x) >> 16), e, m));
+}
+PJRTX_DEV float rp_f16(float x, int e, int m) { return f16_to_f32(rp_bits<uint16_t, 5, 10>(f32_to_f16(x), e, m)); }
+
 // Storage <-> compute for each element kind.
 PJRTX_DEV float ld_f32(const float* p, uint32_t i) { return p[i]; }
 PJRTX_DEV float ld_bf16(const uint16_t* p, uint32_t i) { return bf16_to_f32(p[i]); }

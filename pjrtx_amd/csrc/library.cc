@@ -1,6 +1,7 @@
 // Dispatch of library steps: StableHLO ops that materialize their result
 // through a precompiled kernel instead of a generated fusion.
 #include "kernels/library.h"
+#include "kernels/reduce_window.h"
 
 #include <cstring>
 
@@ -188,6 +189,32 @@ void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<M
 void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops, std::vector<MemRef>& vals);
 void run_dot_residual(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, int add, int out);
 
+// stablehlo.reduce_window (the planner checked the supported forms).
+// Replaces pjrtx_mlx_metal_buffer_reduce_window (reference:
+// src/backend/mlx_metal/api.cc:4324-4437).
+void run_reduce_window(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
+  ReduceWindowParams p;
+  const TensorType& in = prog.type(op.operands[0]);
+  const TensorType& out = prog.type(op.results[0]);
+  p.rank = static_cast<int>(in.dims.size());
+  switch (classify_reducer(prog, op)) {
+    case ReducerKind::kProd: p.op = 1; break;
+    case ReducerKind::kMax: p.op = 2; break;
+    case ReducerKind::kMin: p.op = 3; break;
+    default: p.op = 0; break;
+  }
+  for (int d = 0; d < p.rank; ++d) {
+    p.in_dims[d] = in.dims[d];
+    p.out_dims[d] = out.dims[d];
+    p.window[d] = op.sizes[d];
+    p.stride[d] = op.strides[d];
+    p.dilation[d] = op.window_dilations[d];
+    p.pad_low[d] = op.pad_low[d];
+  }
+  launch_reduce_window(dev->stream(), p, in.dtype, ptr(vals, op.operands[0]), ptr(vals, op.operands[1]),
+                       ptr(vals, op.results[0]));
+}
+
 void run_library_step(Device* dev, const Program& prog, const Step& step, std::vector<MemRef>& vals) {
   const Op& op = prog.ops.at(step.lib_op);
   switch (step.lib) {
@@ -224,6 +251,9 @@ void run_library_step(Device* dev, const Program& prog, const Step& step, std::v
       return;
     case LibKind::kSort:
       run_sort(dev, prog, op, vals);
+      return;
+    case LibKind::kReduceWindow:
+      run_reduce_window(dev, prog, op, vals);
       return;
     default:
       fail(Code::kUnimplemented, std::string("library op not available: ") + lib_kind_name(step.lib));

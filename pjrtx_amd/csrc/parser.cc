@@ -125,6 +125,7 @@ const OpInfo kOpTable[] = {
     {"count_leading_zeros", OpKind::kClz},
     {"convert", OpKind::kConvert},
     {"bitcast_convert", OpKind::kBitcastConvert},
+    {"reduce_precision", OpKind::kReducePrecision},
     {"add", OpKind::kAdd},
     {"subtract", OpKind::kSubtract},
     {"multiply", OpKind::kMultiply},
@@ -154,6 +155,7 @@ const OpInfo kOpTable[] = {
     {"dynamic_slice", OpKind::kDynamicSlice},
     {"dynamic_update_slice", OpKind::kDynamicUpdateSlice},
     {"reduce", OpKind::kReduce},
+    {"reduce_window", OpKind::kReduceWindow},
     {"dot_general", OpKind::kDotGeneral},
     {"dot", OpKind::kDotGeneral},
     {"gather", OpKind::kGather},
@@ -456,6 +458,8 @@ class Parser {
   // Calls recorded as ops with kind kReturn and `name` = "call:@callee".
 
   void parse_module();
+  void parse_mesh();
+  bool try_identity_op(const std::vector<std::string>& names);
   void parse_func();
   void parse_block(std::vector<Op>* ops, std::vector<int>* ret_values, bool top_level);
   Op parse_op(const std::vector<std::string>& result_names, int result_count_hint,
@@ -473,6 +477,80 @@ class Parser {
   void inline_into(const std::string& fname, const std::vector<int>& args, std::vector<int>* results,
                    std::vector<Op>* out, int depth);
 };
+
+// `sdy.mesh @name = <["x"=2, ...]>` (Shardy): the program runs whole on one
+// device, so meshes and the shardings that name them are accepted and
+// ignored; the mesh's device count is kept for diagnostics.
+void Parser::parse_mesh() {
+  symbol();
+  expect("=");
+  ws();
+  const std::string body = balanced();
+  int64_t devices = 1;
+  for (size_t i = body.find('='); i != std::string::npos; i = body.find('=', i + 1)) {
+    const long long n = std::strtoll(body.c_str() + i + 1, nullptr, 10);
+    if (n > 0) devices *= n;
+  }
+  prog_.mesh_devices = std::max<int64_t>(prog_.mesh_devices, devices);
+}
+
+// Identity ops: stablehlo.optimization_barrier (results are its operands,
+// the reference lowers it to an alias, lowering_rules.zig:136) and
+// sdy.sharding_constraint (a no-op on one device). Binds the result names
+// to the operand values; no op is emitted. Returns false (input untouched)
+// when the next op is not one of them.
+bool Parser::try_identity_op(const std::vector<std::string>& names) {
+  const size_t save = p_;
+  ws();
+  std::string nm;
+  if (peek() == '"') nm = string_lit();
+  else if (is_ident_start(peek())) nm = ident();
+  if (nm != "stablehlo.optimization_barrier" && nm != "mhlo.optimization_barrier" &&
+      nm != "sdy.sharding_constraint") {
+    p_ = save;
+    return false;
+  }
+  std::vector<int> vals;
+  while (true) {
+    ws();
+    const char c = peek();
+    if (c == ':') break;
+    if (c == '\0') error("unexpected end of input in " + nm);
+    if (c == ',' || c == '(' || c == ')') {
+      ++p_;
+      continue;
+    }
+    if (c == '%') {
+      vals.push_back(lookup(ssa_name()));
+      continue;
+    }
+    if (c == '<' || c == '{' || c == '[') {
+      balanced();
+      continue;
+    }
+    error("unexpected token in " + nm);
+  }
+  expect(":");
+  ws();
+  if (peek() == '(') {
+    balanced();
+    if (try_lit("->")) type_list_maybe_parens();
+  } else {
+    do {
+      type();
+    } while (try_lit(","));
+  }
+  std::vector<std::string> rn;
+  if (names.size() == 1 && vals.size() > 1) {
+    for (size_t i = 0; i < vals.size(); ++i) rn.push_back(names[0] + "#" + std::to_string(i));
+    bind(names[0], vals[0]);
+  } else {
+    rn = names;
+  }
+  if (rn.size() != vals.size()) error(nm + ": result count does not match its operands");
+  for (size_t i = 0; i < vals.size(); ++i) bind(rn[i], vals[i]);
+  return true;
+}
 
 Program Parser::run() {
   scopes_.emplace_back();
@@ -493,10 +571,20 @@ Program Parser::run() {
     expect("{");
     while (!try_lit("}")) {
       if (eof()) error("unexpected end of module");
+      if (try_word("sdy.mesh")) {
+        parse_mesh();
+        continue;
+      }
       parse_func();
     }
   } else {
-    while (!eof()) parse_func();
+    while (!eof()) {
+      if (try_word("sdy.mesh")) {
+        parse_mesh();
+        continue;
+      }
+      parse_func();
+    }
   }
   if (!funcs_.count("main")) error("module has no @main function");
   // Inline everything into main.
@@ -717,6 +805,7 @@ void Parser::parse_block(std::vector<Op>* ops, std::vector<int>* ret_values, boo
       ops->push_back(ret);
       continue;
     }
+    if (try_identity_op(names)) continue;
     std::vector<std::string> out_names;
     Op op = parse_op(names, count_hint, &out_names);
     ops->push_back(std::move(op));
@@ -863,6 +952,47 @@ void Parser::parse_generic_attrs(const std::string& dict, Op* op) {
           {"LE", CmpDir::kLE}, {"GT", CmpDir::kGT}, {"GE", CmpDir::kGE}};
       for (auto& dd : dirs)
         if (d == dd.first) op->cmp_dir = dd.second;
+    } else if (key == "exponent_bits") {
+      op->exponent_bits = std::stoll(val.substr(0, val.find(':')));
+    } else if (key == "mantissa_bits") {
+      op->mantissa_bits = std::stoll(val.substr(0, val.find(':')));
+    } else if (key == "window_dimensions") {
+      parse_dims_attr(val, &op->sizes);
+    } else if (key == "window_strides") {
+      parse_dims_attr(val, &op->strides);
+    } else if (key == "base_dilations") {
+      parse_dims_attr(val, &op->base_dilations);
+    } else if (key == "window_dilations") {
+      parse_dims_attr(val, &op->window_dilations);
+    } else if (key == "padding") {
+      // dense<[[lo, hi], ...]> : tensor<Nx2xi64>, or dense<0> (splat)
+      Dims flat;
+      const size_t lt = val.find('<');
+      const size_t colon = val.rfind(':');
+      std::string body = lt == std::string::npos ? val : val.substr(lt + 1, (colon == std::string::npos ? val.size() : colon) - lt - 1);
+      for (char& ch : body)
+        if (ch == '[' || ch == ']' || ch == '>' || ch == '<') ch = ' ';
+      size_t i = 0;
+      while (i < body.size()) {
+        while (i < body.size() && (body[i] == ' ' || body[i] == ',')) ++i;
+        if (i >= body.size()) break;
+        char* end = nullptr;
+        long long v = std::strtoll(body.c_str() + i, &end, 10);
+        if (end == body.c_str() + i) break;
+        flat.push_back(v);
+        i = end - body.c_str();
+      }
+      op->pad_low.clear();
+      op->pad_high.clear();
+      if (flat.size() == 1) {  // splat: filled in once the rank is known
+        op->pad_low.push_back(flat[0]);
+        op->pad_high.push_back(-(flat[0] + 1));  // marker
+      } else {
+        for (size_t k = 0; k + 1 < flat.size(); k += 2) {
+          op->pad_low.push_back(flat[k]);
+          op->pad_high.push_back(flat[k + 1]);
+        }
+      }
     } else if (key == "call_target_name") {
       const size_t q0 = val.find('"'), q1 = val.rfind('"');
       if (q0 != std::string::npos && q1 > q0) op->target = val.substr(q0 + 1, q1 - q0 - 1);
@@ -1328,6 +1458,12 @@ Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint
           op.lhs_contract = int_list();
           expect("x");
           op.rhs_contract = int_list();
+        } else if (word == "format") {  // reduce_precision: e<exponent>m<mantissa>
+          const std::string f = ident();
+          const size_t mpos = f.find('m');
+          if (f.empty() || f[0] != 'e' || mpos == std::string::npos) error("bad reduce_precision format " + f);
+          op.exponent_bits = std::stoll(f.substr(1, mpos - 1));
+          op.mantissa_bits = std::stoll(f.substr(mpos + 1));
         } else if (word == "precision" || word == "algorithm") {
           if (peek() == '[' || peek() == '<' || peek() == '#') balanced();
           else ident();
@@ -1427,6 +1563,38 @@ Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint
     op.results.push_back(id);
   }
   if (out_names) *out_names = names;
+  if (op.kind == OpKind::kReduceWindow && !op.operands.empty()) {
+    // Defaults of the optional window attributes, and a splat padding.
+    const size_t r = prog_.values[op.operands[0]].type.dims.size();
+    auto ones = [&](Dims* d) {
+      if (d->empty()) d->assign(r, 1);
+    };
+    ones(&op.strides);
+    ones(&op.base_dilations);
+    ones(&op.window_dilations);
+    if (op.pad_low.size() == 1 && op.pad_high.size() == 1 && op.pad_high[0] == -(op.pad_low[0] + 1)) {
+      op.pad_high.assign(r, op.pad_low[0]);
+      op.pad_low.assign(r, op.pad_low[0]);
+    }
+    if (op.pad_low.empty()) op.pad_low.assign(r, 0);
+    if (op.pad_high.empty()) op.pad_high.assign(r, 0);
+  }
+  if (op.kind == OpKind::kReduceWindow && !op.operands.empty()) {
+    // Defaults of the optional window attributes, and a splat padding.
+    const size_t r = prog_.values[op.operands[0]].type.dims.size();
+    auto ones = [&](Dims* d) {
+      if (d->empty()) d->assign(r, 1);
+    };
+    ones(&op.strides);
+    ones(&op.base_dilations);
+    ones(&op.window_dilations);
+    if (op.pad_low.size() == 1 && op.pad_high.size() == 1 && op.pad_high[0] == -(op.pad_low[0] + 1)) {
+      op.pad_high.assign(r, op.pad_low[0]);
+      op.pad_low.assign(r, op.pad_low[0]);
+    }
+    if (op.pad_low.empty()) op.pad_low.assign(r, 0);
+    if (op.pad_high.empty()) op.pad_high.assign(r, 0);
+  }
 
   // Deferred pieces that need the result type.
   if (have_dense) {

@@ -40,6 +40,7 @@ const char* lib_kind_name(LibKind k) {
     case LibKind::kDotGroup: return "dot_group";
     case LibKind::kWhile: return "while";
     case LibKind::kSort: return "sort";
+    case LibKind::kReduceWindow: return "reduce_window";
   }
   return "?";
 }
@@ -95,6 +96,40 @@ ReducerKind classify_reducer(const Program& prog, const Op& op) {
   }
 }
 
+// reduce_window forms the library kernel runs (kernels/reduce_window.hip):
+// one operand, a sum / product / max / min region, base dilation 1,
+// non-negative padding, positive strides and window dilations, rank <= 8.
+// Anything else fails closed at compile time (the reference accepts sum and
+// max with base dilation 1, api.cc:4324-4360).
+void check_reduce_window_supported(const Program& prog, const Op& op) {
+  PJRTX_CHECK(op.operands.size() == 2 && op.results.size() == 1, Code::kUnimplemented,
+              "reduce_window: only single-operand windows are supported");
+  const ReducerKind k = classify_reducer(prog, op);
+  PJRTX_CHECK(k == ReducerKind::kSum || k == ReducerKind::kProd || k == ReducerKind::kMax || k == ReducerKind::kMin,
+              Code::kUnimplemented, "reduce_window: the region must be add, multiply, maximum or minimum");
+  const TensorType& in = prog.type(op.operands[0]);
+  const TensorType& out = prog.type(op.results[0]);
+  const size_t r = in.dims.size();
+  PJRTX_CHECK(r >= 1 && r <= 8, Code::kUnimplemented, "reduce_window: rank must be 1..8");
+  PJRTX_CHECK(op.sizes.size() == r && op.strides.size() == r && op.base_dilations.size() == r &&
+                  op.window_dilations.size() == r && op.pad_low.size() == r && op.pad_high.size() == r,
+              Code::kInvalidArgument, "reduce_window: window attributes do not match the operand rank");
+  const DType t = in.dtype;
+  PJRTX_CHECK(t == DType::kF32 || t == DType::kF64 || t == DType::kBF16 || t == DType::kF16 || t == DType::kS32 ||
+                  t == DType::kS64,
+              Code::kUnimplemented, std::string("reduce_window: element type ") + dtype_name(t) + " is not supported");
+  for (size_t d = 0; d < r; ++d) {
+    PJRTX_CHECK(op.base_dilations[d] == 1, Code::kUnimplemented, "reduce_window: base dilation must be 1");
+    PJRTX_CHECK(op.sizes[d] >= 1 && op.strides[d] >= 1 && op.window_dilations[d] >= 1 && op.pad_low[d] >= 0 &&
+                    op.pad_high[d] >= 0,
+                Code::kUnimplemented, "reduce_window: windows, strides and dilations must be positive, padding >= 0");
+    const int64_t padded = op.pad_low[d] + in.dims[d] + op.pad_high[d];
+    const int64_t span = (op.sizes[d] - 1) * op.window_dilations[d] + 1;
+    const int64_t want = padded < span ? 0 : (padded - span) / op.strides[d] + 1;
+    PJRTX_CHECK(out.dims[d] == want, Code::kInvalidArgument, "reduce_window: result shape does not match the window");
+  }
+}
+
 namespace {
 
 bool is_splat_constant(const Program& prog, const Op& op) {
@@ -120,6 +155,8 @@ int op_cost(OpKind k) {
     case OpKind::kExp: case OpKind::kExpm1: case OpKind::kLog: case OpKind::kLog1p: case OpKind::kLogistic:
     case OpKind::kTanh: case OpKind::kCbrt: case OpKind::kDivide: case OpKind::kRemainder:
       return 4;
+    case OpKind::kReducePrecision:
+      return 2;
     default:
       return 1;
   }
@@ -130,7 +167,7 @@ bool is_library(const Op& op) {
   return k == OpKind::kDotGeneral || k == OpKind::kGather || k == OpKind::kScatter ||
          k == OpKind::kDynamicSlice || k == OpKind::kDynamicUpdateSlice ||
          (k == OpKind::kConcatenate && !fusible_concat(op)) || k == OpKind::kPad || k == OpKind::kAttention ||
-         k == OpKind::kWhile || k == OpKind::kSort || k == OpKind::kTopK;
+         k == OpKind::kWhile || k == OpKind::kSort || k == OpKind::kTopK || k == OpKind::kReduceWindow;
 }
 
 LibKind lib_kind_of(OpKind k) {
@@ -146,6 +183,7 @@ LibKind lib_kind_of(OpKind k) {
     case OpKind::kWhile: return LibKind::kWhile;
     case OpKind::kSort:
     case OpKind::kTopK: return LibKind::kSort;
+    case OpKind::kReduceWindow: return LibKind::kReduceWindow;
     default: return LibKind::kCopy;
   }
 }
@@ -539,6 +577,7 @@ void Planner::build_steps(std::vector<Step>* steps) {
       s.outputs = op.results;
       if (op.kind == OpKind::kWhile) s.while_trips = static_trip_count(prog_, prog_.ops, op);
       if (s.lib == LibKind::kSort) check_sort_supported(prog_, op);
+      if (s.lib == LibKind::kReduceWindow) check_reduce_window_supported(prog_, op);
       steps->push_back(std::move(s));
       continue;
     }

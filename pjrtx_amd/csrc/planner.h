@@ -56,7 +56,8 @@ struct ReduceSpec {
 enum class StepKind { kLoop, kReduce, kAlias, kLibrary, kRowFused, kGemv };
 
 enum class LibKind {
-  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup, kWhile, kSort
+  kCopy, kDot, kGather, kScatter, kDynamicSlice, kDynamicUpdateSlice, kConcatenate, kPad, kAttention, kDotGroup, kWhile, kSort,
+  kReduceWindow
 };
 const char* lib_kind_name(LibKind k);
 

@@ -70,8 +70,12 @@ def _literal(value, dtype: str) -> str:
 class Builder:
     """Accumulates one ``@main`` function; ``build()`` returns module text."""
 
-    def __init__(self, name: str = "jit_f"):
+    def __init__(self, name: str = "jit_f", mesh: str | None = None):
+        """`mesh`: an `sdy.mesh` body such as '["x"=1]' to declare (Shardy
+        prefix of a jax.jit module on one device); the arguments then carry
+        replicated `sdy.sharding` attributes."""
         self.name = name
+        self.mesh = mesh
         self.params: list[T] = []
         self.donated: set[str] = set()
         self.lines: list[str] = []
@@ -180,6 +184,59 @@ class Builder:
     def popcnt(self, x): return self._unary("popcnt", x)
     def clz(self, x): return self._unary("count_leading_zeros", x)
     def is_finite(self, x): return self._unary("is_finite", x, "pred")
+
+    def reduce_precision(self, x: T, exponent_bits: int, mantissa_bits: int, generic: bool = False) -> T:
+        if generic:
+            return self._emit(f'"stablehlo.reduce_precision"({x.name}) <{{exponent_bits = {exponent_bits} : i32, '
+                              f'mantissa_bits = {mantissa_bits} : i32}}> : ({x.type}) -> {x.type}', x.shape, x.dtype)
+        return self._emit(f"stablehlo.reduce_precision {x.name}, format = e{exponent_bits}m{mantissa_bits} : {x.type}",
+                          x.shape, x.dtype)
+
+    def optimization_barrier(self, xs: list[T]) -> list[T]:
+        """stablehlo.optimization_barrier: its results are its operands."""
+        name = self._fresh()
+        names = ", ".join(x.name for x in xs)
+        types = ", ".join(x.type for x in xs)
+        if len(xs) == 1:
+            self.lines.append(f"    {name} = stablehlo.optimization_barrier {names} : {types}")
+            return [T(name, xs[0].shape, xs[0].dtype)]
+        self.lines.append(f'    {name}:{len(xs)} = "stablehlo.optimization_barrier"({names}) : ({types}) -> ({types})')
+        return [T(f"{name}#{i}", x.shape, x.dtype) for i, x in enumerate(xs)]
+
+    def sharding_constraint(self, x: T) -> T:
+        """sdy.sharding_constraint to a replicated sharding (needs a mesh)."""
+        rep = ", ".join("{}" for _ in x.shape)
+        return self._emit(f"sdy.sharding_constraint {x.name} <@mesh, [{rep}]> : {x.type}", x.shape, x.dtype)
+
+    def reduce_window(self, x: T, init: T, op: str, window, strides=None, window_dilations=None, padding=None,
+                      base_dilations=None) -> T:
+        """stablehlo.reduce_window (generic form, as jax.lax.reduce_window
+        prints it) with a one-op region (add / maximum / minimum / multiply)."""
+        r = len(x.shape)
+        strides = list(strides or [1] * r)
+        wd = list(window_dilations or [1] * r)
+        bd = list(base_dilations or [1] * r)
+        pad = [list(p) for p in (padding or [(0, 0)] * r)]
+        shape = []
+        for d in range(r):
+            padded = pad[d][0] + (x.shape[d] - 1) * bd[d] + 1 + pad[d][1] if x.shape[d] else pad[d][0] + pad[d][1]
+            span = (window[d] - 1) * wd[d] + 1
+            shape.append(0 if padded < span else (padded - span) // strides[d] + 1)
+        name = self._fresh()
+        b = name[1:]
+        sv = tensor_type((), x.dtype)
+        arr = lambda v: "array<i64: " + ", ".join(str(int(e)) for e in v) + ">"  # noqa: E731
+        pads = ", ".join(f"[{lo}, {hi}]" for lo, hi in pad)
+        self.lines += [
+            f'    {name} = "stablehlo.reduce_window"({x.name}, {init.name}) ({{',
+            f"    ^bb0(%w{b}_a: {sv}, %w{b}_b: {sv}):",
+            f"      %w{b}_c = stablehlo.{op} %w{b}_a, %w{b}_b : {sv}",
+            f"      stablehlo.return %w{b}_c : {sv}",
+            f"    }}) {{base_dilations = {arr(bd)}, padding = dense<[{pads}]> : tensor<{r}x2xi64>, "
+            f"window_dimensions = {arr(window)}, window_dilations = {arr(wd)}, window_strides = {arr(strides)}}} : "
+            f"({x.type}, {init.type}) -> {tensor_type(shape, x.dtype)}",
+        ]
+        return T(name, tuple(shape), x.dtype)
 
     def convert(self, x: T, dtype: str) -> T:
         return self._emit(f"stablehlo.convert {x.name} : ({x.type}) -> {tensor_type(x.shape, dtype)}", x.shape, dtype)
@@ -490,6 +547,10 @@ class Builder:
                 else:
                     claimed.add(match)
                     attr = f" {{tf.aliasing_output = {match} : i32}}"
+            if self.mesh is not None:
+                rep = ", ".join("{}" for _ in p.shape)
+                shard = f"sdy.sharding = #sdy.sharding<@mesh, [{rep}]>"
+                attr = f" {{{shard}}}" if not attr else attr[:-1] + f", {shard}}}"
             parts.append(f"{p.name}: {p.type}{attr}")
         args = ", ".join(parts)
         if len(outputs) == 1:
@@ -500,6 +561,7 @@ class Builder:
         ret_types = ", ".join(o.type for o in outputs)
         return "\n".join([
             f"module @{self.name} attributes {{mhlo.num_partitions = 1 : i32, mhlo.num_replicas = 1 : i32}} {{",
+            *([f"  sdy.mesh @mesh = <{self.mesh}>"] if self.mesh is not None else []),
             f"  func.func public @main({args}) -> {res} {{",
             *self.lines,
             f"    return {ret_names} : {ret_types}",
