@@ -1050,6 +1050,125 @@ typedef struct PJRT_Buffer_CopyToMemory_Args {
 #define PJRT_Buffer_CopyToMemory_Args_STRUCT_SIZE PJRT_STRUCT_SIZE(PJRT_Buffer_CopyToMemory_Args, dst_buffer)
 typedef PJRT_Error* PJRT_Buffer_CopyToMemory(PJRT_Buffer_CopyToMemory_Args* args);
 
+/* ------------------------- async host-to-device ------------------------- */
+/* A transfer manager owns one device buffer per shape spec; the host fills  */
+/* each with TransferData chunks (any order, any sizes); a buffer is ready   */
+/* once the call flagged is_last_transfer has been made for it.              */
+
+typedef struct PJRT_ShapeSpec {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  const int64_t* dims;
+  size_t num_dims;
+  PJRT_Buffer_Type element_type;
+} PJRT_ShapeSpec;
+#define PJRT_ShapeSpec_STRUCT_SIZE PJRT_STRUCT_SIZE(PJRT_ShapeSpec, element_type)
+
+typedef struct PJRT_Client_CreateBuffersForAsyncHostToDevice_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_Client* client;
+  PJRT_ShapeSpec* shape_specs;
+  size_t num_shape_specs;
+  PJRT_Buffer_MemoryLayout** device_layouts; /* optional */
+  size_t num_device_layouts;
+  PJRT_Memory* memory;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager; /* out */
+} PJRT_Client_CreateBuffersForAsyncHostToDevice_Args;
+#define PJRT_Client_CreateBuffersForAsyncHostToDevice_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_Client_CreateBuffersForAsyncHostToDevice_Args, transfer_manager)
+typedef PJRT_Error* PJRT_Client_CreateBuffersForAsyncHostToDevice(PJRT_Client_CreateBuffersForAsyncHostToDevice_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_Destroy_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+} PJRT_AsyncHostToDeviceTransferManager_Destroy_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_Destroy_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_Destroy_Args, transfer_manager)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_Destroy(PJRT_AsyncHostToDeviceTransferManager_Destroy_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_TransferData_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  int buffer_index;
+  const void* data;
+  int64_t offset;
+  int64_t transfer_size;
+  bool is_last_transfer;
+  PJRT_Event* done_with_h2d_transfer; /* out */
+} PJRT_AsyncHostToDeviceTransferManager_TransferData_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_TransferData_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_TransferData_Args, done_with_h2d_transfer)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_TransferData(PJRT_AsyncHostToDeviceTransferManager_TransferData_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  int buffer_index;
+  PJRT_Buffer* buffer_out; /* out */
+} PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args, buffer_out)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer(PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_Device_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  PJRT_Device* device_out; /* out */
+} PJRT_AsyncHostToDeviceTransferManager_Device_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_Device_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_Device_Args, device_out)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_Device(PJRT_AsyncHostToDeviceTransferManager_Device_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  size_t buffer_count; /* out */
+} PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args, buffer_count)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_BufferCount(PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  int buffer_index;
+  size_t buffer_size; /* out */
+} PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args, buffer_size)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_BufferSize(PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  int buffer_index;
+  PJRT_Error_Code error_code;
+  const char* error_message;
+  size_t error_message_size;
+} PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args, error_message_size)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_SetBufferError(PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args* args);
+
+typedef struct PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_AsyncHostToDeviceTransferManager* transfer_manager;
+  const PJRT_NamedValue* transfer_metadata;
+  size_t num_metadata;
+} PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args;
+#define PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args, num_metadata)
+typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_AddMetadata(PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args* args);
+
 /* --------------------- Families outside the hot path --------------------- */
 /* Slots keep their table position; the plugin answers UNIMPLEMENTED.       */
 
@@ -1119,24 +1238,6 @@ typedef struct PJRT_ExecuteContext_Destroy_Args PJRT_ExecuteContext_Destroy_Args
 typedef PJRT_Error* PJRT_ExecuteContext_Destroy(PJRT_ExecuteContext_Destroy_Args* args);
 typedef struct PJRT_Buffer_CopyRawToHost_Args PJRT_Buffer_CopyRawToHost_Args;
 typedef PJRT_Error* PJRT_Buffer_CopyRawToHost(PJRT_Buffer_CopyRawToHost_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_Destroy_Args PJRT_AsyncHostToDeviceTransferManager_Destroy_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_Destroy(PJRT_AsyncHostToDeviceTransferManager_Destroy_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_TransferData_Args PJRT_AsyncHostToDeviceTransferManager_TransferData_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_TransferData(PJRT_AsyncHostToDeviceTransferManager_TransferData_Args* args);
-typedef struct PJRT_Client_CreateBuffersForAsyncHostToDevice_Args PJRT_Client_CreateBuffersForAsyncHostToDevice_Args;
-typedef PJRT_Error* PJRT_Client_CreateBuffersForAsyncHostToDevice(PJRT_Client_CreateBuffersForAsyncHostToDevice_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer(PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_Device_Args PJRT_AsyncHostToDeviceTransferManager_Device_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_Device(PJRT_AsyncHostToDeviceTransferManager_Device_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_BufferCount(PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_BufferSize(PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_SetBufferError(PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args* args);
-typedef struct PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args;
-typedef PJRT_Error* PJRT_AsyncHostToDeviceTransferManager_AddMetadata(PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args* args);
 typedef struct PJRT_Client_DmaMap_Args PJRT_Client_DmaMap_Args;
 typedef PJRT_Error* PJRT_Client_DmaMap(PJRT_Client_DmaMap_Args* args);
 typedef struct PJRT_Client_DmaUnmap_Args PJRT_Client_DmaUnmap_Args;

@@ -58,6 +58,31 @@ PJRTX_HIP_API int pjrtx_hip_synchronize(int device);
  * (src/runtime/executable_cache.zig:9-25, hits / misses / resident_entries). */
 PJRTX_HIP_API int pjrtx_compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries);
 
+/* Host bytes the compile cache holds (program texts and constant literals)
+ * and entries it evicted; the cap is PJRTX_COMPILE_CACHE_BYTES (default
+ * 256 MiB) and 32 entries. Replaces the reference's cache byte accounting
+ * (src/runtime/executable_cache.zig:9-25, resident_bytes / evictions). */
+PJRTX_HIP_API int pjrtx_compile_cache_usage(int64_t* bytes, int64_t* evictions);
+
+/* The compile-cache key of a program text under the current PJRTX_*
+ * environment ("pjrtx-" and 32 hex digits). Replaces
+ * executable_fingerprint.zig:9-24 (alloc). */
+PJRTX_HIP_API int pjrtx_compile_fingerprint(const char* text, size_t len, char* out, size_t cap, size_t* needed);
+
+/* Device residency budget: the cap, in bytes, on the device memory that
+ * loaded executables hold (code objects, resident constants, kernel
+ * scratch); 0 removes it (the default, or PJRTX_MAX_RESIDENT_BYTES).
+ * Loading past the cap first evicts idle executables, largest first, then
+ * least recently used; an evicted executable loads again when next run.
+ * Replaces Residency.setMaxResidentBytes (executable_cache.zig:118-122,
+ * 233-300) and client_residency.zig:58-92. */
+PJRTX_HIP_API int pjrtx_set_max_resident_bytes(int device, int64_t bytes);
+
+/* out = {resident bytes, peak resident bytes, resident executables,
+ * evictions, evicted bytes, cap} of the device's residency budget.
+ * Replaces executable_cache.zig:9-25 (Stats). */
+PJRTX_HIP_API int pjrtx_residency_stats(int device, int64_t out[6]);
+
 /* Parses a StableHLO text module, runs the fusion planner and code
  * generator, and writes a JSON description of the plan to `out` (at most
  * `cap` bytes; `*needed` gets the full size). Needs no GPU. Replaces the

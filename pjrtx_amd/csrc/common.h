@@ -64,6 +64,7 @@ struct TensorType {
 // Error codes follow PJRT_Error_Code numbering.
 enum class Code : int {
   kOk = 0,
+  kCancelled = 1,
   kInvalidArgument = 3,
   kNotFound = 5,
   kResourceExhausted = 8,

@@ -124,6 +124,34 @@ int pjrtx_compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries) 
   return guarded([&] { compile_cache_stats(hits, misses, entries); });
 }
 
+int pjrtx_compile_cache_usage(int64_t* bytes, int64_t* evictions) {
+  return guarded([&] { compile_cache_usage(bytes, evictions); });
+}
+
+int pjrtx_compile_fingerprint(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
+  return guarded([&] { copy_out(compile_fingerprint(std::string(text, len)), out, cap, needed); });
+}
+
+int pjrtx_set_max_resident_bytes(int device, int64_t bytes) {
+  return guarded([&] {
+    PJRTX_CHECK(bytes >= 0, Code::kInvalidArgument, "set_max_resident_bytes: negative cap");
+    set_max_resident_bytes(abi_device(device)->ordinal(), bytes);
+  });
+}
+
+int pjrtx_residency_stats(int device, int64_t out[6]) {
+  return guarded([&] {
+    PJRTX_CHECK(out != nullptr, Code::kInvalidArgument, "residency_stats: null output");
+    const ResidencyStats st = residency_stats(abi_device(device)->ordinal());
+    out[0] = st.resident_bytes;
+    out[1] = st.peak_resident_bytes;
+    out[2] = st.entries;
+    out[3] = st.evictions;
+    out[4] = st.evicted_bytes;
+    out[5] = st.max_resident_bytes;
+  });
+}
+
 int pjrtx_plan_json(const char* text, size_t len, char* out, size_t cap, size_t* needed) {
   return guarded([&] {
     Program prog = parse_stablehlo(std::string(text, len));

@@ -524,6 +524,115 @@ static PJRT_Error* Client_BufferFromHostBuffer(PJRT_Client_BufferFromHostBuffer_
   });
 }
 
+// ----------------------------------------------------- async host transfers
+// (reference: src/plugin/async_h2d.zig:196-437, client.zig:420-440)
+
+static PJRT_AsyncHostToDeviceTransferManager* manager_of(PJRT_AsyncHostToDeviceTransferManager* m) {
+  PJRTX_CHECK(m != nullptr && m->t != nullptr, Code::kInvalidArgument, "transfer manager is null");
+  return m;
+}
+
+static size_t transfer_index(PJRT_AsyncHostToDeviceTransferManager* m, int i) {
+  PJRTX_CHECK(i >= 0 && static_cast<size_t>(i) < m->t->count(), Code::kInvalidArgument,
+              "async transfer buffer index is out of range");
+  return static_cast<size_t>(i);
+}
+
+static PJRT_Error* Client_CreateBuffersForAsyncHostToDevice(PJRT_Client_CreateBuffersForAsyncHostToDevice_Args* args) {
+  return guarded("PJRT_Client_CreateBuffersForAsyncHostToDevice", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_Client_CreateBuffersForAsyncHostToDevice_Args, transfer_manager);
+    PJRTX_CHECK(args->shape_specs != nullptr || args->num_shape_specs == 0, Code::kInvalidArgument,
+                "shape specs are null");
+    for (size_t i = 0; i < args->num_device_layouts; ++i)
+      PJRTX_CHECK(args->device_layouts == nullptr || args->device_layouts[i] == nullptr, Code::kUnimplemented,
+                  "async transfers take the default (dense row-major) layout only");
+    PJRT_Device* d = args->memory ? args->memory->device : args->client->devices.at(0);
+    std::vector<TensorType> types;
+    for (size_t i = 0; i < args->num_shape_specs; ++i) {
+      const PJRT_ShapeSpec& sp = args->shape_specs[i];
+      PJRTX_CHECK(sp.dims != nullptr || sp.num_dims == 0, Code::kInvalidArgument, "shape spec dimensions are null");
+      TensorType t;
+      t.dtype = dtype_from_pjrt(sp.element_type);
+      t.dims.assign(sp.dims, sp.dims + sp.num_dims);
+      for (int64_t x : t.dims) PJRTX_CHECK(x >= 0, Code::kInvalidArgument, "negative dimension");
+      types.push_back(t);
+    }
+    auto* m = new PJRT_AsyncHostToDeviceTransferManager();
+    m->t = std::make_unique<AsyncTransfer>(d->dev, types);
+    m->client = args->client;
+    m->device = d;
+    args->transfer_manager = m;
+  });
+}
+
+static PJRT_Error* Transfer_Destroy(PJRT_AsyncHostToDeviceTransferManager_Destroy_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_Destroy", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_Destroy_Args, transfer_manager);
+    delete args->transfer_manager;  // retrieved buffers keep their memory
+  });
+}
+
+static PJRT_Error* Transfer_TransferData(PJRT_AsyncHostToDeviceTransferManager_TransferData_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_TransferData", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_TransferData_Args, done_with_h2d_transfer);
+    auto* m = manager_of(args->transfer_manager);
+    const size_t i = transfer_index(m, args->buffer_index);
+    auto done = m->t->write(i, args->offset, args->data, args->transfer_size, args->is_last_transfer);
+    args->done_with_h2d_transfer = new PJRT_Event{done};
+  });
+}
+
+static PJRT_Error* Transfer_RetrieveBuffer(PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args, buffer_out);
+    auto* m = manager_of(args->transfer_manager);
+    auto* pb = new PJRT_Buffer();
+    pb->buf = m->t->buffer(transfer_index(m, args->buffer_index));
+    pb->client = m->client;
+    pb->device = m->device;
+    args->buffer_out = pb;
+  });
+}
+
+static PJRT_Error* Transfer_Device(PJRT_AsyncHostToDeviceTransferManager_Device_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_Device", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_Device_Args, device_out);
+    args->device_out = manager_of(args->transfer_manager)->device;
+  });
+}
+
+static PJRT_Error* Transfer_BufferCount(PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_BufferCount", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args, buffer_count);
+    args->buffer_count = manager_of(args->transfer_manager)->t->count();
+  });
+}
+
+static PJRT_Error* Transfer_BufferSize(PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_BufferSize", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args, buffer_size);
+    auto* m = manager_of(args->transfer_manager);
+    args->buffer_size = m->t->bytes(transfer_index(m, args->buffer_index));
+  });
+}
+
+static PJRT_Error* Transfer_SetBufferError(PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_SetBufferError", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args, error_message_size);
+    auto* m = manager_of(args->transfer_manager);
+    const std::string msg = args->error_message ? std::string(args->error_message, args->error_message_size)
+                                                : std::string("async transfer buffer failed");
+    m->t->fail(transfer_index(m, args->buffer_index), static_cast<Code>(args->error_code), msg);
+  });
+}
+
+static PJRT_Error* Transfer_AddMetadata(PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args* args) {
+  return guarded("PJRT_AsyncHostToDeviceTransferManager_AddMetadata", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args, num_metadata);
+    manager_of(args->transfer_manager);  // metadata is informational here
+  });
+}
+
 // ------------------------------------------------------- device description
 
 static PJRT_Error* DeviceDescription_Id(PJRT_DeviceDescription_Id_Args* args) {
@@ -1023,6 +1132,7 @@ static PJRT_Error* Buffer_CopyToDevice(PJRT_Buffer_CopyToDevice_Args* args) {
   return guarded("PJRT_Buffer_CopyToDevice", [&] {
     PJRTX_ARGS_CHECK(args, PJRT_Buffer_CopyToDevice_Args, dst_buffer);
     const Buffer& src = *args->buffer->buf;
+    if (src.ready) src.ready->wait_resolved();  // an async transfer still filling it
     PJRT_Device* d = args->dst_device;
     auto b = std::make_shared<Buffer>();
     b->dev = d->dev;
@@ -1219,15 +1329,15 @@ extern "C" __attribute__((visibility("default"))) const PJRT_Api* GetPjrtApi(voi
     a.PJRT_ExecuteContext_Create = Unimplemented<PJRT_ExecuteContext_Create_Args>;
     a.PJRT_ExecuteContext_Destroy = Unimplemented<PJRT_ExecuteContext_Destroy_Args>;
     a.PJRT_Buffer_CopyRawToHost = Unimplemented<PJRT_Buffer_CopyRawToHost_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_Destroy = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_Destroy_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_TransferData = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_TransferData_Args>;
-    a.PJRT_Client_CreateBuffersForAsyncHostToDevice = Unimplemented<PJRT_Client_CreateBuffersForAsyncHostToDevice_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_Device = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_Device_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_BufferCount = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_BufferCount_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_BufferSize = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_BufferSize_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_SetBufferError = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_SetBufferError_Args>;
-    a.PJRT_AsyncHostToDeviceTransferManager_AddMetadata = Unimplemented<PJRT_AsyncHostToDeviceTransferManager_AddMetadata_Args>;
+    a.PJRT_AsyncHostToDeviceTransferManager_Destroy = Transfer_Destroy;
+    a.PJRT_AsyncHostToDeviceTransferManager_TransferData = Transfer_TransferData;
+    a.PJRT_Client_CreateBuffersForAsyncHostToDevice = Client_CreateBuffersForAsyncHostToDevice;
+    a.PJRT_AsyncHostToDeviceTransferManager_RetrieveBuffer = Transfer_RetrieveBuffer;
+    a.PJRT_AsyncHostToDeviceTransferManager_Device = Transfer_Device;
+    a.PJRT_AsyncHostToDeviceTransferManager_BufferCount = Transfer_BufferCount;
+    a.PJRT_AsyncHostToDeviceTransferManager_BufferSize = Transfer_BufferSize;
+    a.PJRT_AsyncHostToDeviceTransferManager_SetBufferError = Transfer_SetBufferError;
+    a.PJRT_AsyncHostToDeviceTransferManager_AddMetadata = Transfer_AddMetadata;
     a.PJRT_Client_DmaMap = Unimplemented<PJRT_Client_DmaMap_Args>;
     a.PJRT_Client_DmaUnmap = Unimplemented<PJRT_Client_DmaUnmap_Args>;
     return a;

@@ -78,3 +78,8 @@ struct PJRT_LoadedExecutable {
   bool deleted = false;
 };
 
+struct PJRT_AsyncHostToDeviceTransferManager {
+  std::unique_ptr<pjrtx::AsyncTransfer> t;
+  PJRT_Client* client = nullptr;
+  PJRT_Device* device = nullptr;
+};

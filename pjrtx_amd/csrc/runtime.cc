@@ -234,6 +234,40 @@ std::shared_ptr<Event> Event::record(Device* dev) {
   return e;
 }
 
+std::shared_ptr<Event> Event::pending() {
+  auto e = std::shared_ptr<Event>(new Event());
+  e->pending_ = true;
+  return e;
+}
+
+void Event::resolve(std::shared_ptr<Event> then) {
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (!pending_) return;
+    then_ = std::move(then);
+    pending_ = false;
+  }
+  cv_.notify_all();
+}
+
+void Event::resolve_failed(Code code, const std::string& msg) {
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (!pending_) return;
+    pending_ = false;
+    done_ = true;
+    code_ = code;
+    msg_ = msg;
+  }
+  cv_.notify_all();
+}
+
+void Event::wait_resolved() {
+  std::unique_lock<std::mutex> lk(mu_);
+  cv_.wait(lk, [&] { return !pending_; });
+  if (done_ && code_ != Code::kOk) throw Error(code_, msg_);
+}
+
 bool Event::materialize_locked() {
   if (ev_ || !lazy_) return true;
   dev_->make_current();
@@ -255,8 +289,21 @@ Event::~Event() {
 }
 
 bool Event::is_ready() {
-  std::lock_guard<std::mutex> lk(mu_);
+  std::unique_lock<std::mutex> lk(mu_);
   if (done_) return true;
+  if (pending_) return false;
+  if (then_) {
+    std::shared_ptr<Event> t = then_;
+    lk.unlock();
+    const bool r = t->is_ready();
+    lk.lock();
+    if (r) {
+      done_ = true;
+      code_ = t->error_code();
+      msg_ = t->error_message();
+    }
+    return done_;
+  }
   if (lazy_ && !ev_) {
     // An idle stream has finished this work; otherwise record now.
     dev_->make_current();
@@ -280,8 +327,19 @@ bool Event::is_ready() {
 void Event::await() {
   hipEvent_t ev = nullptr;
   {
-    std::lock_guard<std::mutex> lk(mu_);
+    std::unique_lock<std::mutex> lk(mu_);
+    cv_.wait(lk, [&] { return !pending_; });
     if (done_) return;
+    if (then_) {
+      std::shared_ptr<Event> t = then_;
+      lk.unlock();
+      t->await();
+      lk.lock();
+      done_ = true;
+      code_ = t->error_code();
+      msg_ = t->error_message();
+      return;
+    }
     if (!materialize_locked()) return;
     ev = ev_;
   }
@@ -337,6 +395,7 @@ void buffer_to_host(const Buffer& b, void* dst, size_t dst_size) {
   const size_t bytes = b.type.bytes();
   PJRTX_CHECK(dst_size >= bytes, Code::kInvalidArgument,
               strformat("ToHostBuffer: destination holds %zu bytes, buffer needs %zu", dst_size, bytes));
+  if (b.ready) b.ready->wait_resolved();  // an async transfer still filling it, or its error
   if (!bytes) return;
   b.dev->make_current();
   hip_check(hipMemcpyAsync(dst, b.mem->ptr, bytes, hipMemcpyDeviceToHost, b.dev->stream()), "hipMemcpyAsync(D2H)");
@@ -497,9 +556,161 @@ int64_t Executable::while_trips(size_t si) const {
   return it == loops_.end() ? -1 : it->second->trips;
 }
 
+// ------------------------------------------------------------- residency
+
+namespace {
+
+struct ResidentEntry {
+  Executable* exe = nullptr;
+  int64_t bytes = 0;
+  uint64_t last_use = 0;
+  int busy = 0;
+};
+
+struct Residency {
+  std::mutex mu;
+  std::map<int, std::map<Executable*, ResidentEntry>> by_device;
+  std::map<int, ResidencyStats> stats;
+  uint64_t clock = 0;
+};
+
+Residency& residency() {
+  static Residency* r = new Residency();
+  return *r;
+}
+
+int64_t default_max_resident_bytes() { return env_int("PJRTX_MAX_RESIDENT_BYTES", 0); }
+
+ResidencyStats& stats_locked(Residency& r, int ord) {
+  auto it = r.stats.find(ord);
+  if (it == r.stats.end()) {
+    ResidencyStats st;
+    st.max_resident_bytes = default_max_resident_bytes();
+    it = r.stats.emplace(ord, st).first;
+  }
+  return it->second;
+}
+
+// Marks an executable busy on a device for a scope (not evictable).
+class BusyScope {
+ public:
+  BusyScope(Executable* e, int ord) : e_(e), ord_(ord) {
+    Residency& r = residency();
+    std::lock_guard<std::mutex> lk(r.mu);
+    ResidentEntry& en = r.by_device[ord][e];
+    en.exe = e;
+    en.busy++;
+    en.last_use = ++r.clock;
+  }
+  ~BusyScope() {
+    Residency& r = residency();
+    std::lock_guard<std::mutex> lk(r.mu);
+    auto d = r.by_device.find(ord_);
+    if (d == r.by_device.end()) return;
+    auto it = d->second.find(e_);
+    if (it != d->second.end()) it->second.busy--;
+  }
+
+ private:
+  Executable* e_;
+  int ord_;
+};
+
+// Evicts idle executables (not `keep`) until `incoming` more bytes fit under
+// the cap. Caller holds the device's execute lock, so no idle executable can
+// start executing on this device meanwhile.
+void make_room(int ord, Executable* keep, int64_t incoming) {
+  std::vector<Executable*> victims;
+  {
+    Residency& r = residency();
+    std::lock_guard<std::mutex> lk(r.mu);
+    ResidencyStats& st = stats_locked(r, ord);
+    if (st.max_resident_bytes <= 0) return;
+    auto& entries = r.by_device[ord];
+    int64_t total = st.resident_bytes;
+    std::set<Executable*> chosen;
+    while (total + incoming > st.max_resident_bytes) {
+      const ResidentEntry* best = nullptr;
+      for (auto& [e, en] : entries) {
+        if (e == keep || en.busy > 0 || en.bytes <= 0 || chosen.count(e)) continue;
+        if (!best || en.bytes > best->bytes || (en.bytes == best->bytes && en.last_use < best->last_use)) best = &en;
+      }
+      if (!best) break;  // everything left is busy: load past the cap
+      total -= best->bytes;
+      st.evictions++;
+      st.evicted_bytes += best->bytes;
+      chosen.insert(best->exe);
+      victims.push_back(best->exe);
+    }
+  }
+  for (Executable* e : victims) e->evict(ord);
+}
+
+void register_resident(int ord, Executable* e, int64_t bytes) {
+  Residency& r = residency();
+  std::lock_guard<std::mutex> lk(r.mu);
+  ResidencyStats& st = stats_locked(r, ord);
+  ResidentEntry& en = r.by_device[ord][e];
+  en.exe = e;
+  st.resident_bytes += bytes - en.bytes;
+  if (en.bytes == 0) st.entries++;
+  en.bytes = bytes;
+  en.last_use = ++r.clock;
+  st.peak_resident_bytes = std::max(st.peak_resident_bytes, st.resident_bytes);
+}
+
+// Takes an executable's bytes on a device out of the total; `erase` also
+// forgets the entry (the executable is being destroyed).
+void unregister_resident(int ord, Executable* e, bool erase) {
+  Residency& r = residency();
+  std::lock_guard<std::mutex> lk(r.mu);
+  auto d = r.by_device.find(ord);
+  if (d == r.by_device.end()) return;
+  auto it = d->second.find(e);
+  if (it == d->second.end()) return;
+  ResidencyStats& st = stats_locked(r, ord);
+  if (it->second.bytes > 0) {
+    st.resident_bytes -= it->second.bytes;
+    st.entries--;
+  }
+  it->second.bytes = 0;
+  if (erase) d->second.erase(it);
+}
+
+// Drops every device's entry for a destroyed executable.
+void forget_resident(Executable* e) {
+  Residency& r = residency();
+  std::lock_guard<std::mutex> lk(r.mu);
+  for (auto& [ord, entries] : r.by_device) {
+    auto it = entries.find(e);
+    if (it == entries.end()) continue;
+    ResidencyStats& st = stats_locked(r, ord);
+    if (it->second.bytes > 0) {
+      st.resident_bytes -= it->second.bytes;
+      st.entries--;
+    }
+    entries.erase(it);
+  }
+}
+
+}  // namespace
+
+ResidencyStats residency_stats(int ordinal) {
+  Residency& r = residency();
+  std::lock_guard<std::mutex> lk(r.mu);
+  return stats_locked(r, ordinal);
+}
+
+void set_max_resident_bytes(int ordinal, int64_t bytes) {
+  Residency& r = residency();
+  std::lock_guard<std::mutex> lk(r.mu);
+  stats_locked(r, ordinal).max_resident_bytes = std::max<int64_t>(0, bytes);
+}
+
 std::vector<MemRef> Executable::run_values(Device* dev, const std::vector<MemRef>& args) {
   PJRTX_CHECK(args.size() == prog_.params.size(), Code::kInternal, "run_values: argument count");
-  Loaded* L = loaded_for(dev);
+  BusyScope busy(this, dev->ordinal());
+  Loaded* L = loaded_for(dev, true);
   std::vector<MemRef> vals(prog_.values.size());
   for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i];
   for (auto& [v, m] : L->constants) vals[v] = m;
@@ -574,15 +785,56 @@ void Executable::run_while(Loaded* L, size_t si, std::vector<MemRef>& vals) {
   stats_.library_calls++;
 }
 
+void Executable::evict(int ordinal) {
+  std::unique_ptr<Loaded> gone;
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = loaded_.find(ordinal);
+    if (it != loaded_.end()) {
+      gone = std::move(it->second);
+      loaded_.erase(it);
+    }
+    graphs_.erase(ordinal);
+  }
+  if (gone) {
+    // Kernels this executable queued may still run: drain the device's
+    // stream before the module and its memory go.
+    gone->dev->make_current();
+    hip_check(hipStreamSynchronize(gone->dev->stream()), "hipStreamSynchronize(evict)");
+    if (gone->module) (void)hipModuleUnload(gone->module);
+  }
+  for (auto& [si, loop] : loops_) {
+    if (loop->cond) loop->cond->evict(ordinal);
+    if (loop->body) loop->body->evict(ordinal);
+  }
+  unregister_resident(ordinal, this, false);
+}
+
 Executable::~Executable() {
   for (auto& [ord, L] : loaded_) {
     if (L->module) (void)hipModuleUnload(L->module);
   }
+  forget_resident(this);
 }
 
-void Executable::load(Device* dev) { loaded_for(dev); }
+void Executable::load(Device* dev) {
+  std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  BusyScope busy(this, dev->ordinal());
+  loaded_for(dev, true);
+}
 
-Executable::Loaded* Executable::loaded_for(Device* dev) {
+Executable::Loaded* Executable::loaded_for(Device* dev, bool may_evict) {
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = loaded_.find(dev->ordinal());
+    if (it != loaded_.end()) return it->second.get();
+  }
+  if (may_evict) {
+    int64_t incoming = static_cast<int64_t>(code_.size());
+    for (const Step& st : plan_.steps) incoming += static_cast<int64_t>(st.scratch_bytes);
+    for (int v : plan_.constants) incoming += prog_.type(v).bytes();
+    make_room(dev->ordinal(), this, incoming);
+  }
   std::lock_guard<std::mutex> lk(mu_);
   auto it = loaded_.find(dev->ordinal());
   if (it != loaded_.end()) return it->second.get();
@@ -640,7 +892,13 @@ Executable::Loaded* Executable::loaded_for(Device* dev) {
   }
   hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
   Loaded* raw = L.get();
+  int64_t resident = static_cast<int64_t>(code_.size());
+  for (const MemRef& m : L->scratch)
+    if (m) resident += static_cast<int64_t>(m->bytes);
+  for (auto& [v, m] : L->constants)
+    if (m) resident += static_cast<int64_t>(m->bytes);
   loaded_[dev->ordinal()] = std::move(L);
+  register_resident(dev->ordinal(), this, resident);
   return raw;
 }
 
@@ -732,9 +990,13 @@ std::vector<BufferRef> Executable::execute(Device* dev, const std::vector<Buffer
                 strformat("execute: argument %zu has type %s, program expects %s", i, args[i]->type.str().c_str(),
                           want.str().c_str()));
     PJRTX_CHECK(args[i]->dev == dev, Code::kInvalidArgument, strformat("execute: argument %zu is on another device", i));
+    // An argument still receiving an async host transfer: wait for its last
+    // chunk (the chunks are queued on this device's stream, ahead of us).
+    if (args[i]->ready) args[i]->ready->wait_resolved();
   }
-  Loaded* L = loaded_for(dev);
   std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  BusyScope busy(this, dev->ordinal());
+  Loaded* L = loaded_for(dev, true);
   dev->make_current();
   // Repeated executions with the same large arguments replay a captured
   // graph (second call captures, later calls replay).
@@ -1073,8 +1335,9 @@ std::vector<std::string> Executable::unit_names() const {
 }
 
 std::vector<double> Executable::time_steps(Device* dev, const std::vector<BufferRef>& args, int iters) {
-  Loaded* L = loaded_for(dev);
   std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  BusyScope busy(this, dev->ordinal());
+  Loaded* L = loaded_for(dev, true);
   dev->make_current();
   std::vector<MemRef> vals(prog_.values.size());
   for (size_t i = 0; i < args.size(); ++i) vals[prog_.params[i]] = args[i]->mem;

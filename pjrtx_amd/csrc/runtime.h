@@ -151,6 +151,16 @@ class Event : public std::enable_shared_from_this<Event> {
   // Marks the stream's current tail. The hipEvent itself is recorded only
   // when readiness is first asked for (see Event::record).
   static std::shared_ptr<Event> record(Device* dev);
+  // Resolved by the host later (an async host-to-device transfer that has
+  // not received all its data): not ready, and await() blocks, until
+  // resolve(then) (it then follows `then`) or resolve_failed().
+  static std::shared_ptr<Event> pending();
+  void resolve(std::shared_ptr<Event> then);
+  void resolve_failed(Code code, const std::string& msg);
+  // Blocks until a pending event is resolved (device work it then follows
+  // is not waited for; stream order covers it). Throws the failure of an
+  // event resolved as failed.
+  void wait_resolved();
   ~Event();
   bool is_ready();
   void await();  // blocks until done
@@ -165,6 +175,9 @@ class Event : public std::enable_shared_from_this<Event> {
   // error stored, if recording failed.
   bool materialize_locked();
   std::mutex mu_;
+  std::condition_variable cv_;
+  bool pending_ = false;          // host-resolved and not yet resolved
+  std::shared_ptr<Event> then_;   // what a resolved pending event follows
   hipEvent_t ev_ = nullptr;
   Device* dev_ = nullptr;
   bool lazy_ = false;
@@ -192,6 +205,53 @@ struct CompiledProgram {
 };
 std::shared_ptr<const CompiledProgram> compile_program_cached(const std::string& text);
 void compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries);
+void compile_cache_usage(int64_t* bytes, int64_t* evictions);
+// The cache key of a program text under the current PJRTX_* environment.
+std::string compile_fingerprint(const std::string& text);
+
+// Device residency budget (the reference's executable residency cache:
+// src/runtime/executable_cache.zig:85-300, client_residency.zig:58-92):
+// every loaded executable's device bytes (code, resident constants, kernel
+// scratch) count against a per-device cap (PJRTX_MAX_RESIDENT_BYTES, or
+// set_max_resident_bytes; 0 = none). Loading past the cap evicts idle
+// executables, the largest first, then the least recently used; an
+// executable is busy while it executes.
+struct ResidencyStats {
+  int64_t resident_bytes = 0, peak_resident_bytes = 0, entries = 0, evictions = 0, evicted_bytes = 0,
+          max_resident_bytes = 0;
+};
+ResidencyStats residency_stats(int ordinal);
+void set_max_resident_bytes(int ordinal, int64_t bytes);
+
+// PJRT's asynchronous host-to-device transfer (the reference's async H2D
+// manager, src/plugin/async_h2d.zig:196-437): device buffers of fixed
+// shapes filled by the host in chunks of any size and order. A chunk is
+// copied on the device stream (large ones through the pinned staging ring),
+// so executions queued later read it; a buffer becomes ready once its chunk
+// flagged `last` has been copied. Until then its readiness event is pending
+// (await blocks, an execution taking it waits for it).
+class AsyncTransfer {
+ public:
+  AsyncTransfer(Device* dev, const std::vector<TensorType>& types);
+  size_t count() const { return bufs_.size(); }
+  size_t bytes(size_t i) const;
+  BufferRef buffer(size_t i) const;
+  Device* device() const { return dev_; }
+  // Copies `size` bytes to [offset, offset + size) of buffer i. Returns the
+  // event after which the host may reuse `data`.
+  std::shared_ptr<Event> write(size_t i, int64_t offset, const void* data, int64_t size, bool last);
+  void fail(size_t i, Code code, const std::string& msg);
+  // Buffers still waiting for their last chunk become errors, so that
+  // nothing waits on them for ever.
+  ~AsyncTransfer();
+
+ private:
+  Device* dev_;
+  std::mutex mu_;
+  std::vector<BufferRef> bufs_;
+  std::vector<std::shared_ptr<Event>> pending_;  // each buffer's readiness until resolved
+  std::vector<bool> finished_;
+};
 
 // Large host-to-device copies through a pinned staging ring on a copy
 // stream (transfer.cc); returns when the data is on the device.
@@ -256,6 +316,10 @@ class Executable {
   const std::string& name() const { return name_; }
   size_t code_size() const { return code_.size(); }
   ExecStats stats() const { return stats_; }
+  // Drops this executable's device state on `ordinal` (code, resident
+  // constants, kernel scratch, captured graphs); the next execution there
+  // loads it again. Called by the residency budget on an idle executable.
+  void evict(int ordinal);
 
  private:
   struct Loaded {
@@ -305,7 +369,9 @@ class Executable {
   };
   std::map<int, GraphState> graphs_;  // by device ordinal
 
-  Loaded* loaded_for(Device* dev);
+  // `may_evict`: the caller holds the device's execute lock, so idle
+  // executables may be evicted to keep within the residency budget.
+  Loaded* loaded_for(Device* dev, bool may_evict = false);
   GraphState& graph_state(int ordinal);
   bool graph_candidate(const std::vector<BufferRef>& args, const std::vector<bool>* donate) const;
   std::vector<const void*> graph_key(const std::vector<BufferRef>& args) const;

@@ -104,4 +104,72 @@ void staged_upload(Device* dev, void* dst, const void* src, size_t bytes) {
   for (bool& b : st.busy) b = false;
 }
 
+// ------------------------------------------------------- async transfers
+
+AsyncTransfer::AsyncTransfer(Device* dev, const std::vector<TensorType>& types) : dev_(dev) {
+  for (const TensorType& t : types) {
+    auto b = std::make_shared<Buffer>();
+    b->dev = dev;
+    b->type = t;
+    b->mem = dev->allocate(t.bytes());
+    auto ev = Event::pending();
+    b->ready = ev;
+    bufs_.push_back(b);
+    pending_.push_back(ev);
+    finished_.push_back(false);
+  }
+}
+
+size_t AsyncTransfer::bytes(size_t i) const {
+  PJRTX_CHECK(i < bufs_.size(), Code::kInvalidArgument, "async transfer buffer index is out of range");
+  return bufs_[i]->type.bytes();
+}
+
+BufferRef AsyncTransfer::buffer(size_t i) const {
+  PJRTX_CHECK(i < bufs_.size(), Code::kInvalidArgument, "async transfer buffer index is out of range");
+  return bufs_[i];
+}
+
+std::shared_ptr<Event> AsyncTransfer::write(size_t i, int64_t offset, const void* data, int64_t size, bool last) {
+  std::lock_guard<std::mutex> lk(mu_);
+  PJRTX_CHECK(i < bufs_.size(), Code::kInvalidArgument, "async transfer buffer index is out of range");
+  PJRTX_CHECK(offset >= 0 && size >= 0, Code::kInvalidArgument, "async transfer offset and size must be non-negative");
+  PJRTX_CHECK(data != nullptr || size == 0, Code::kInvalidArgument, "async transfer data is null");
+  const size_t total = bufs_[i]->type.bytes();
+  PJRTX_CHECK(static_cast<uint64_t>(offset) + static_cast<uint64_t>(size) <= total, Code::kInvalidArgument,
+              "async transfer range exceeds buffer size");
+  PJRTX_CHECK(!finished_[i], Code::kFailedPrecondition, "async transfer buffer already received its last chunk");
+  dev_->make_current();
+  std::shared_ptr<Event> done = Event::ready();
+  if (size > 0) {
+    char* dst = static_cast<char*>(bufs_[i]->mem->ptr) + offset;
+    if (staged_upload_wanted(static_cast<size_t>(size))) {
+      staged_upload(dev_, dst, data, static_cast<size_t>(size));  // returns once on the device
+    } else {
+      hip_check(hipMemcpyAsync(dst, data, static_cast<size_t>(size), hipMemcpyHostToDevice, dev_->stream()),
+                "hipMemcpyAsync(async transfer)");
+      done = Event::record(dev_);
+    }
+  }
+  if (last) {
+    finished_[i] = true;
+    pending_[i]->resolve(Event::record(dev_));
+  }
+  return done;
+}
+
+AsyncTransfer::~AsyncTransfer() {
+  std::lock_guard<std::mutex> lk(mu_);
+  for (size_t i = 0; i < bufs_.size(); ++i)
+    if (!finished_[i])
+      pending_[i]->resolve_failed(Code::kCancelled, "async transfer manager destroyed before the buffer's last chunk");
+}
+
+void AsyncTransfer::fail(size_t i, Code code, const std::string& msg) {
+  std::lock_guard<std::mutex> lk(mu_);
+  PJRTX_CHECK(i < bufs_.size(), Code::kInvalidArgument, "async transfer buffer index is out of range");
+  finished_[i] = true;
+  pending_[i]->resolve_failed(code, msg);
+}
+
 }  // namespace pjrtx

@@ -123,6 +123,22 @@ EventAwaitArgs = _args("EventAwaitArgs", [("event", c_void_p)])
 EventDestroyArgs = _args("EventDestroyArgs", [("event", c_void_p)])
 EventIsReadyArgs = _args("EventIsReadyArgs", [("event", c_void_p), ("is_ready", c_bool)])
 DeviceMemoryStatsArgs = _args("DeviceMemoryStatsArgs", [("device", c_void_p), ("bytes_in_use", c_int64)])
+ShapeSpec = _args("ShapeSpec", [("dims", POINTER(c_int64)), ("num_dims", c_size_t), ("element_type", c_int)])
+AsyncCreateArgs = _args("AsyncCreateArgs", [
+    ("client", c_void_p), ("shape_specs", POINTER(ShapeSpec)), ("num_shape_specs", c_size_t),
+    ("device_layouts", c_void_p), ("num_device_layouts", c_size_t), ("memory", c_void_p), ("transfer_manager", c_void_p)])
+AsyncManagerArgs = _args("AsyncManagerArgs", [("transfer_manager", c_void_p)])
+AsyncTransferDataArgs = _args("AsyncTransferDataArgs", [
+    ("transfer_manager", c_void_p), ("buffer_index", c_int), ("data", c_void_p), ("offset", c_int64),
+    ("transfer_size", c_int64), ("is_last_transfer", c_bool), ("done_with_h2d_transfer", c_void_p)])
+AsyncRetrieveArgs = _args("AsyncRetrieveArgs", [("transfer_manager", c_void_p), ("buffer_index", c_int),
+                                                ("buffer_out", c_void_p)])
+AsyncCountArgs = _args("AsyncCountArgs", [("transfer_manager", c_void_p), ("buffer_count", c_size_t)])
+AsyncSizeArgs = _args("AsyncSizeArgs", [("transfer_manager", c_void_p), ("buffer_index", c_int),
+                                        ("buffer_size", c_size_t)])
+AsyncSetErrorArgs = _args("AsyncSetErrorArgs", [
+    ("transfer_manager", c_void_p), ("buffer_index", c_int), ("error_code", c_int), ("error_message", c_char_p),
+    ("error_message_size", c_size_t)])
 
 # PJRT_Api function-pointer order (include/pjrt_c_api.h).
 API_FIELDS = """
@@ -216,6 +232,10 @@ class Plugin:
             "pjrtx_executable_run": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double)],
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_compile_cache_stats": [POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)],
+            "pjrtx_compile_cache_usage": [POINTER(c_int64), POINTER(c_int64)],
+            "pjrtx_compile_fingerprint": [c_char_p, c_size_t, c_char_p, c_size_t, POINTER(c_size_t)],
+            "pjrtx_set_max_resident_bytes": [c_int, c_int64],
+            "pjrtx_residency_stats": [c_int, POINTER(c_int64)],
             "pjrtx_hip_malloc": [c_int, c_size_t, POINTER(c_void_p)],
             "pjrtx_hip_free": [c_int, c_void_p],
             "pjrtx_hip_copy_h2d": [c_int, c_void_p, c_void_p, c_size_t],
@@ -305,7 +325,27 @@ class Plugin:
         """{"hits", "misses", "entries"} of the process's compile cache."""
         h, m, e = c_int64(0), c_int64(0), c_int64(0)
         self.hip_check(self.lib.pjrtx_compile_cache_stats(ctypes.byref(h), ctypes.byref(m), ctypes.byref(e)))
-        return {"hits": h.value, "misses": m.value, "entries": e.value}
+        b, ev = c_int64(0), c_int64(0)
+        self.hip_check(self.lib.pjrtx_compile_cache_usage(ctypes.byref(b), ctypes.byref(ev)))
+        return {"hits": h.value, "misses": m.value, "entries": e.value, "bytes": b.value, "evictions": ev.value}
+
+    def compile_fingerprint(self, text: str) -> str:
+        """The compile-cache key of `text` under the current PJRTX_* environment."""
+        raw = text.encode()
+        buf = ctypes.create_string_buffer(64)
+        need = c_size_t(0)
+        self.hip_check(self.lib.pjrtx_compile_fingerprint(raw, len(raw), buf, 64, ctypes.byref(need)))
+        return buf.value.decode()
+
+    def set_max_resident_bytes(self, device: int, nbytes: int) -> None:
+        """Caps the device memory loaded executables hold (0: no cap)."""
+        self.hip_check(self.lib.pjrtx_set_max_resident_bytes(device, nbytes))
+
+    def residency_stats(self, device: int = 0) -> dict:
+        out = (c_int64 * 6)()
+        self.hip_check(self.lib.pjrtx_residency_stats(device, out))
+        keys = ("resident_bytes", "peak_resident_bytes", "entries", "evictions", "evicted_bytes", "max_resident_bytes")
+        return dict(zip(keys, list(out)))
 
 
 def plugin() -> Plugin:
@@ -595,6 +635,9 @@ class Client:
         self.p.call("Client_Compile", a)
         return Executable(self, a.executable, text)
 
+    def async_transfer(self, specs: list[tuple[tuple, str]]) -> AsyncTransfer:
+        return AsyncTransfer(self, specs)
+
     def bytes_in_use(self) -> int:
         a = _mk(DeviceMemoryStatsArgs())
         a.device = self.devices[0]
@@ -607,6 +650,91 @@ class Client:
             a.client = self.handle
             self.p.call("Client_Destroy", a)
             self.handle = None
+
+
+class AsyncTransfer:
+    """PJRT_Client_CreateBuffersForAsyncHostToDevice and the transfer
+    manager's calls: device buffers of the given (shape, dtype) filled by
+    `transfer` chunks in any order."""
+
+    def __init__(self, client: "Client", specs: list[tuple[tuple, str]]):
+        self.client = client
+        self._dims = [(c_int64 * max(1, len(shape)))(*shape) for shape, _ in specs]
+        arr = (ShapeSpec * max(1, len(specs)))()
+        for i, (shape, dt) in enumerate(specs):
+            _mk(arr[i])
+            arr[i].dims = self._dims[i]
+            arr[i].num_dims = len(shape)
+            arr[i].element_type = DTYPES[dt]
+        a = _mk(AsyncCreateArgs())
+        a.client = client.handle
+        a.shape_specs = arr
+        a.num_shape_specs = len(specs)
+        client.p.call("Client_CreateBuffersForAsyncHostToDevice", a)
+        self.handle = a.transfer_manager
+
+    def count(self) -> int:
+        a = _mk(AsyncCountArgs())
+        a.transfer_manager = self.handle
+        self.client.p.call("AsyncHostToDeviceTransferManager_BufferCount", a)
+        return a.buffer_count
+
+    def size(self, i: int) -> int:
+        a = _mk(AsyncSizeArgs())
+        a.transfer_manager = self.handle
+        a.buffer_index = i
+        self.client.p.call("AsyncHostToDeviceTransferManager_BufferSize", a)
+        return a.buffer_size
+
+    def buffer(self, i: int) -> Buffer:
+        a = _mk(AsyncRetrieveArgs())
+        a.transfer_manager = self.handle
+        a.buffer_index = i
+        self.client.p.call("AsyncHostToDeviceTransferManager_RetrieveBuffer", a)
+        return Buffer(self.client, a.buffer_out)
+
+    def transfer(self, i: int, data: bytes | np.ndarray, offset: int, last: bool) -> None:
+        """Copies `data` to bytes [offset, offset + len) of buffer i and
+        waits until the host copy may be reused."""
+        raw = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, bytes) else data).view(np.uint8)
+        a = _mk(AsyncTransferDataArgs())
+        a.transfer_manager = self.handle
+        a.buffer_index = i
+        a.data = raw.ctypes.data if raw.size else None
+        a.offset = offset
+        a.transfer_size = raw.size
+        a.is_last_transfer = last
+        self.client.p.call("AsyncHostToDeviceTransferManager_TransferData", a)
+        if a.done_with_h2d_transfer:
+            w = _mk(EventAwaitArgs())
+            w.event = a.done_with_h2d_transfer
+            self.client.p.call("Event_Await", w)
+            d = _mk(EventDestroyArgs())
+            d.event = a.done_with_h2d_transfer
+            self.client.p.call("Event_Destroy", d)
+
+    def set_error(self, i: int, code: int, message: str) -> None:
+        msg = message.encode()
+        a = _mk(AsyncSetErrorArgs())
+        a.transfer_manager = self.handle
+        a.buffer_index = i
+        a.error_code = code
+        a.error_message = msg
+        a.error_message_size = len(msg)
+        self.client.p.call("AsyncHostToDeviceTransferManager_SetBufferError", a)
+
+    def close(self) -> None:
+        if self.handle:
+            a = _mk(AsyncManagerArgs())
+            a.transfer_manager = self.handle
+            self.client.p.call("AsyncHostToDeviceTransferManager_Destroy", a)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class DeviceArray:

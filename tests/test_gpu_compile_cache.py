@@ -53,3 +53,27 @@ def test_cached_decode_compile(client, plugin):
     second = time.perf_counter() - t0
     print(f"decode program compile: first {first * 1e3:.1f} ms, again {second * 1e3:.1f} ms")
     assert plugin.compile_cache_stats()["hits"] == hits + 1
+
+
+def test_byte_cap_evicts_least_recent(client, plugin, monkeypatch):
+    """PJRTX_COMPILE_CACHE_BYTES caps the host bytes the cache holds: with
+    room for one program, compiling a second evicts the first (compiling it
+    again is a miss), and the held bytes stay under the cap."""
+    a, b = _prog(f"capA{os.getpid()}"), _prog(f"capB{os.getpid()}")
+    monkeypatch.setenv("PJRTX_COMPILE_CACHE_BYTES", str(len(a) + len(a) // 2))
+    client.compile(a)
+    s0 = plugin.compile_cache_stats()
+    client.compile(b)
+    s1 = plugin.compile_cache_stats()
+    assert s1["evictions"] > s0["evictions"] and s1["bytes"] <= len(a) + len(a) // 2
+    client.compile(a)
+    assert plugin.compile_cache_stats()["misses"] == s1["misses"] + 1
+
+
+def test_fingerprint_names_the_entry(plugin, monkeypatch):
+    text = _prog("fp")
+    f1 = plugin.compile_fingerprint(text)
+    assert f1.startswith("pjrtx-") and len(f1) == 38 and f1 == plugin.compile_fingerprint(text)
+    assert plugin.compile_fingerprint(_prog("fp2")) != f1
+    monkeypatch.setenv("PJRTX_REDUCE_TARGET_BLOCKS", "64")
+    assert plugin.compile_fingerprint(text) != f1
