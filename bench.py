@@ -45,6 +45,27 @@ def host_threads() -> int:
     return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
 
 
+def host_facts() -> dict:
+    """The host the CPU baseline ran on: logical CPUs, the CPUs this process
+    may run on, the CPU model; and why the reference's own CPU figure (JAX's
+    CPU backend) is not measured beside it."""
+    model = None
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity, "cpu_model": model,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "jax_cpu": "JAX CPU baseline unavailable: jax is not installed in this image and there is no network"}
+
+
 def randn_bits(shape, seed: int, scale: float = 1.0):
     """Seeded N(0,1)*scale as bf16 bit patterns, filled in independently
     seeded 2^22-element blocks on a thread pool."""
@@ -265,6 +286,7 @@ def cpu_baseline(W: Workload, inputs, budget_s: float = 10.0) -> dict:
     out["value"] = round(W.flops / step_s / 1e12, 4) if W.flops else round(W.bytes / step_s / 1e9, 3)
     if "BLAS" not in sample:
         out["cores"] = 1  # numpy elementwise / indexing runs on one thread
+    out["host"] = host_facts()
     return out
 
 
@@ -291,24 +313,65 @@ def launch_units(plan: dict) -> list[dict]:
     return units
 
 
-def roofline(units, unit_ms, names, dtype: str) -> dict:
+def profile_unit_us(workload: str, unit: str):
+    """The rocprofv3 figure for `unit` that the committed kernel-stats summary
+    of this workload records (its `rocprof_unit_us <unit> <us> <file>` line:
+    the unit's kernels' total duration over the run divided by the unit's
+    calls), so that `frac` can be recomputed from the profile."""
+    for p in sorted((ROOT / "profiles").glob(f"*.{workload}.kernel_stats.md")):
+        for ln in p.read_text().splitlines():
+            parts = ln.strip().strip("`").split()
+            if len(parts) >= 3 and parts[0] == "rocprof_unit_us" and parts[1] == unit:
+                return {"file": f"profiles/{p.name}", "kernel_us": float(parts[2])}
+    return None
+
+
+_MEASURED_PEAK = {}
+
+
+def measured_mfma_peak() -> float | None:
+    """Dense bf16 MFMA TFLOP/s this GPU sustains (pjrtx_mfma_peak_tflops,
+    v_mfma_f32_32x32x16_bf16 on every SIMD), measured once per process."""
+    if "bf16" not in _MEASURED_PEAK:
+        from pjrtx_amd.pjrt import plugin
+        try:
+            _MEASURED_PEAK["bf16"] = round(max(plugin().mfma_peak_tflops(0, 1) for _ in range(2)), 1)
+        except Exception:
+            _MEASURED_PEAK["bf16"] = None
+    return _MEASURED_PEAK["bf16"]
+
+
+def roofline(units, unit_ms, names, dtype: str, workload: str | None = None) -> dict:
     """Roofline of the dominant launch unit: HBM-bound unless its arithmetic
-    intensity is past the MFMA ridge point."""
+    intensity is past the MFMA ridge point. `kernel_us` is the HIP-event time
+    of the unit replayed back to back on the plugin's stream; `rocprof` is the
+    committed profile's figure for the same unit, with the fraction it gives."""
     k = max(range(len(unit_ms)), key=lambda i: unit_ms[i] if units[i]["bytes"] else -1)
     u, sec = units[k], unit_ms[k] / 1e3
     peak_tf = MFMA_PEAK_TFLOPS.get(dtype, MFMA_PEAK_TFLOPS["bf16"])
     ridge = peak_tf * 1e12 / (HBM_PEAK_GBPS * 1e9)
     out = {"kernel": names[k], "kernel_us": round(unit_ms[k] * 1e3, 3), "kernel_algorithmic_bytes": u["bytes"]}
+    prof = profile_unit_us(workload, names[k]) if workload else None
     if u["flops"] and u["flops"] / max(u["bytes"], 1) > ridge:
         ach = u["flops"] / sec / 1e12
         out.update({"bound": "mfma", "achieved": round(ach, 2), "peak": peak_tf, "unit": "TFLOP/s",
                     "frac": round(ach / peak_tf, 4), "kernel_flops": u["flops"]})
+        mp = measured_mfma_peak() if dtype in ("bf16", "f16") else None
+        if mp:
+            out["measured_peak"] = mp
+            out["frac_of_measured_peak"] = round(ach / mp, 4)
+        if prof:
+            prof["frac"] = round(u["flops"] / (prof["kernel_us"] * 1e-6) / 1e12 / peak_tf, 4)
     else:
         ach = u["bytes"] / sec / 1e9
         out.update({"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(ach / HBM_PEAK_GBPS, 4)})
         if u["flops"]:
             out["kernel_tflops"] = round(u["flops"] / sec / 1e12, 2)
+        if prof:
+            prof["frac"] = round(u["bytes"] / (prof["kernel_us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)
+    if prof:
+        out["rocprof"] = prof
     keys = ["bound", "achieved", "peak", "unit", "frac"]
     return {**{kk: out[kk] for kk in keys}, "traffic": None, **{kk: v for kk, v in out.items() if kk not in keys}}
 
@@ -371,7 +434,7 @@ def bench_program(a, W: Workload) -> dict:
     unit_ms = exe.time_steps(bufs, iters=max(10, min(50, a.steps)))
     names = exe.step_names()
     assert len(units) == len(unit_ms) == len(names), (len(units), len(unit_ms), len(names))
-    rf = roofline(units, unit_ms, names, W.dtype)
+    rf = roofline(units, unit_ms, names, W.dtype, W.workload)
     rf["traffic"] = traffic_from_profiles(W.workload, rf["kernel"])
     sec = ms_per_step / 1e3
     if W.flops:
@@ -445,17 +508,27 @@ def bench_c5(a) -> dict:
     tokens = [int(x.to_numpy()[0]) for x in toks]
 
     graph_stats = runner.decode.graph_stats()
-    # The same decode loop with graph replay off, for comparison.
-    os.environ["PJRTX_GRAPHS"] = "0"
-    tok_e, _, caches_e = runner.start(prompt)
-    tok_e.block_until_ready()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        tok_e, _, caches_e = runner.step_with(tok_e, pos_bufs[i], caches_e)
-    tok_e.block_until_ready()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
-    os.environ.pop("PJRTX_GRAPHS")
-    del caches_e
+    # The same decode loop with every execute replayed as a hipGraph
+    # (PJRTX_GRAPHS=2), for comparison: the default captures only launch-bound
+    # plans, and this one runs eagerly. Skipped when the caller set
+    # PJRTX_GRAPHS (profiling runs keep graphs off).
+    graph_ms = None
+    if "PJRTX_GRAPHS" not in os.environ:
+        os.environ["PJRTX_GRAPHS"] = "2"
+        try:
+            tok_e, _, caches_e = runner.start(prompt)
+            for i in range(min(3, steps)):
+                tok_e, _, caches_e = runner.step_with(tok_e, pos_bufs[i], caches_e)
+            tok_e, _, caches_e = runner.start(prompt)
+            tok_e.block_until_ready()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                tok_e, _, caches_e = runner.step_with(tok_e, pos_bufs[i], caches_e)
+            tok_e.block_until_ready()
+            graph_ms = round((time.perf_counter() - t0) * 1e3 / steps, 4)
+            del caches_e
+        finally:
+            os.environ.pop("PJRTX_GRAPHS")
 
     # All decode steps in one execute: the step inside an on-device while
     # loop over a constant count (compiled and warmed before timing).
@@ -479,8 +552,9 @@ def bench_c5(a) -> dict:
     assert len(units) == len(unit_ms) == len(names), (len(units), len(unit_ms), len(names))
     by_kind: dict[str, float] = {}
     for u, ms in zip(units, unit_ms):
-        key = u["name"] if u["name"].startswith("lib:") else ("fusion_combine" if u["name"].endswith("_combine")
-                                                               else "fusion")
+        n = u["name"]
+        key = (n if n.startswith("lib:") else "gemv" if n.startswith("pjrtx_gemv") else
+               "fusion_combine" if n.endswith("_combine") else "fusion")
         by_kind[key] = by_kind.get(key, 0.0) + ms * 1e3
     weight_bytes = 2 * L.num_params(cfg) - 2 * cfg.vocab * cfg.d_model + 2 * cfg.d_model  # one embedding row
     kv_bytes = 2 * cfg.layers * 2 * cfg.heads * cfg.head_dim * (cfg.max_len + 1)  # cache read + new row
@@ -499,9 +573,10 @@ def bench_c5(a) -> dict:
                    "launch_units_per_step": sum(1 for n in names if n != "-"),
                    "gpu_us_per_step_by_kind": {kk: round(v, 2) for kk, v in sorted(by_kind.items())},
                    "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2), "first_tokens": tokens[:8],
-                   "graph": graph_stats, "eager_ms_per_step": round(eager_ms, 4),
+                   "graph": graph_stats, "all_graphs_ms_per_step": graph_ms,
                    "one_execute_ms_per_step": round(loop_ms, 4), "one_execute_tokens_match": loop_match},
-        "roofline": roofline(units, unit_ms, names, "bf16"),
+        "roofline": roofline(units, unit_ms, names, "bf16",
+                             "llama_like_decode_8L_d2048_h16x128_ffn5632_v32000_prompt512"),
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_c5(cfg, weights, prompt, tokens)
@@ -525,7 +600,7 @@ def cpu_baseline_c5(cfg, weights, prompt, tokens, budget_s: float = 15.0) -> dic
     el = time.perf_counter() - t0
     return {"value": round(n / el, 3), "unit": "tokens/s", "cores": host_threads(), "kind": "port",
             "sample": f"{n} decode steps of the numpy oracle after the 512-token prefill "
-                      f"({el / n * 1e3:.0f} ms/token, numpy matmul on all host threads)"}
+                      f"({el / n * 1e3:.0f} ms/token, numpy matmul on all host threads)", "host": host_facts()}
 
 
 def main() -> int:

@@ -50,6 +50,14 @@ PJRTX_HIP_API int pjrtx_hip_copy_h2d(int device, void* dst, const void* src, siz
 PJRTX_HIP_API int pjrtx_hip_copy_d2h(int device, void* dst, const void* src, size_t bytes);
 PJRTX_HIP_API int pjrtx_hip_synchronize(int device);
 
+/* Calibration: the dense bf16 matrix-core throughput the device sustains,
+ * in TFLOP/s (two waves per SIMD on every CU issuing independent
+ * v_mfma_f32_16x16x32_bf16 for shape 0, v_mfma_f32_32x32x16_bf16 for
+ * shape 1; best of five timed runs). Lets MFMA-bound roofline fractions be
+ * quoted against a measured peak beside the published one. No counterpart
+ * in the reference (its benchmarks quote Apple GPU figures). */
+PJRTX_HIP_API int pjrtx_mfma_peak_tflops(int device, int shape, double* tflops);
+
 /* --------------------------------------------------- compiler (host only) */
 
 /* Compile-cache counters of this process: compiles that reused a cached

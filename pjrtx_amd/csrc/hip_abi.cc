@@ -8,6 +8,7 @@
 #include "../../include/pjrtx_hip.h"
 #include "pjrt_handles.h"
 #include "runtime.h"
+#include "kernels/library.h"
 #include "kernels/noalloc.h"
 
 using namespace pjrtx;
@@ -122,6 +123,16 @@ int pjrtx_hip_synchronize(int device) {
 
 int pjrtx_compile_cache_stats(int64_t* hits, int64_t* misses, int64_t* entries) {
   return guarded([&] { compile_cache_stats(hits, misses, entries); });
+}
+
+int pjrtx_mfma_peak_tflops(int device, int shape, double* tflops) {
+  return guarded([&] {
+    PJRTX_CHECK(tflops != nullptr, Code::kInvalidArgument, "mfma_peak_tflops: null output");
+    Device* d = abi_device(device);
+    d->make_current();
+    std::lock_guard<std::mutex> lk(d->exec_mutex());
+    *tflops = measure_mfma_peak_tflops(d->stream(), shape, d->compute_units());
+  });
 }
 
 int pjrtx_compile_cache_usage(int64_t* bytes, int64_t* evictions) {

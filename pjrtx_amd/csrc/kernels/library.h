@@ -81,4 +81,10 @@ struct CopySegments {
 };
 void launch_copy_segments(hipStream_t s, const CopySegments& c);
 
+// Dense bf16 MFMA throughput this GPU sustains (TFLOP/s): two waves per SIMD
+// on every CU issuing independent v_mfma_f32_16x16x32_bf16 (shape 0) or
+// v_mfma_f32_32x32x16_bf16 (shape 1), best of five timed runs. Synchronizes
+// the stream.
+double measure_mfma_peak_tflops(hipStream_t s, int shape, int compute_units);
+
 }  // namespace pjrtx

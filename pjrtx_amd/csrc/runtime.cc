@@ -794,15 +794,18 @@ void Executable::evict(int ordinal) {
       gone = std::move(it->second);
       loaded_.erase(it);
     }
-    graphs_.erase(ordinal);
   }
   if (gone) {
-    // Kernels this executable queued may still run: drain the device's
-    // stream before the module and its memory go.
+    // Kernels and graphs this executable queued may still run: drain the
+    // device's stream before the graphs, the module and its memory go.
     gone->dev->make_current();
     hip_check(hipStreamSynchronize(gone->dev->stream()), "hipStreamSynchronize(evict)");
-    if (gone->module) (void)hipModuleUnload(gone->module);
   }
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    graphs_.erase(ordinal);
+  }
+  if (gone && gone->module) (void)hipModuleUnload(gone->module);
   for (auto& [si, loop] : loops_) {
     if (loop->cond) loop->cond->evict(ordinal);
     if (loop->body) loop->body->evict(ordinal);
@@ -1260,8 +1263,10 @@ Executable::GraphEntry* Executable::capture_graph(Device* dev, Loaded* L, const 
   if (gs.entries.size() >= kGraphEntriesPerDevice) {
     auto lru = std::min_element(gs.entries.begin(), gs.entries.end(),
                                 [](const auto& a, const auto& b) { return a->last_use < b->last_use; });
-    // Work already queued on the stream that uses its blocks runs before any
-    // later user of them (single in-order stream).
+    // Its graph may still be queued: drain the stream before the executable
+    // graph is destroyed (its blocks alone would be safe to hand back, since
+    // reuse is ordered on the one stream).
+    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize(graph evict)");
     gs.entries.erase(lru);
   }
   gs.entries.push_back(std::move(g));

@@ -233,6 +233,7 @@ class Plugin:
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_compile_cache_stats": [POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)],
             "pjrtx_compile_cache_usage": [POINTER(c_int64), POINTER(c_int64)],
+            "pjrtx_mfma_peak_tflops": [c_int, c_int, POINTER(c_double)],
             "pjrtx_compile_fingerprint": [c_char_p, c_size_t, c_char_p, c_size_t, POINTER(c_size_t)],
             "pjrtx_set_max_resident_bytes": [c_int, c_int64],
             "pjrtx_residency_stats": [c_int, POINTER(c_int64)],
@@ -336,6 +337,12 @@ class Plugin:
         need = c_size_t(0)
         self.hip_check(self.lib.pjrtx_compile_fingerprint(raw, len(raw), buf, 64, ctypes.byref(need)))
         return buf.value.decode()
+
+    def mfma_peak_tflops(self, device: int = 0, shape: int = 0) -> float:
+        """Measured dense bf16 MFMA throughput (shape 0: 16x16x32, 1: 32x32x16)."""
+        out = c_double(0.0)
+        self.hip_check(self.lib.pjrtx_mfma_peak_tflops(device, shape, ctypes.byref(out)))
+        return out.value
 
     def set_max_resident_bytes(self, device: int, nbytes: int) -> None:
         """Caps the device memory loaded executables hold (0: no cap)."""
