@@ -13,6 +13,9 @@
 //    the whole walk. Workgroups take the heaviest (latest) query tiles first;
 //    when B*H is a multiple of 8, one head's query tiles run on one XCD so
 //    its K and V are served from that XCD's L2.
+//  * attn_pipe (head dim 128, the default for it): the same work split with
+//    K and V loaded straight into LDS, V^T fragments from transposing LDS
+//    reads and a leaner softmax (see its comment below).
 //  * attn_rows (any element type, head dim <= 512): one workgroup per query
 //    row, its 4 waves splitting the keys in blocks of 64 (one key per lane
 //    for the scores, then lanes across the head dim for P.V), combined at the
@@ -31,6 +34,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels/attention.h"
@@ -329,6 +333,289 @@ __global__ void __launch_bounds__(256, 2) attn_tiles(AttnParams p, const uint16_
       const f32x4 o = oacc[dt][qt];
       *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) =
           u32x2{pack2<kF16>(o[0] / l[qt], o[1] / l[qt]), pack2<kF16>(o[2] / l[qt], o[3] / l[qt])};
+    }
+  }
+}
+
+// ------------------------------------------------------ DMA tiles
+// attn_pipe (head dim 128): the tile kernel's work split (128 queries per
+// workgroup, 32 per wave, 64-key blocks, S^T = K.Q^T so a lane holds 16
+// scores of one query) with the memory and the VALU work laid out for
+// gfx950:
+//  * K and V blocks go from global memory straight into LDS (buffer loads
+//    with the LDS destination, 16 bytes a lane), two LDS stages each, one
+//    barrier per block; no register staging.
+//  * V stays row-major in LDS; the V^T fragments of O^T += V^T.P^T come from
+//    transposing LDS reads (ds_read_b64_tr_b16: lane j of a 16-lane group
+//    gets element j & 3 of the rows that lanes 4e + (j >> 2) address, e =
+//    0..3), so one read gives 4 consecutive keys of one head-dim column.
+//  * Softmax VALU kept small: NaN-propagating max3 (no operand
+//    canonicalization), the max taken on the unrounded scores (rounding is
+//    monotone), one packed convert per two scores for the rounding, the row
+//    sums from the P.V MFMAs (a row of ones beside V^T), and the running max
+//    raised only when it grows by more than 2^8 in the exponential, so most
+//    blocks skip the output rescale.
+// LDS: K stage [64 keys][128] with 16-byte chunk c of row r at c ^ (r & 15)
+// (the 16 rows of a fragment read fall in distinct banks); V stage [64][128]
+// with chunk c of row r at c ^ 2 (r & 7) (the 8 rows a half-wave of
+// transposing reads touches fall in distinct banks). The buffer loads place
+// lane L's 16 bytes at slot L of the wave's 1 KB, so the swizzle is applied
+// on the global side: the lane filling slot (r, s) fetches chunk s ^ f(r).
+typedef __attribute__((address_space(3))) void* attn_lds_ptr;
+typedef short attn_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) attn_v4i16 attn_lds_v4i16;
+
+constexpr int PK = 64;          // keys per block
+constexpr int PSTAGE = PK * 128;  // elements per K or V stage
+
+__device__ __forceinline__ int pk_swz(int row, int ch) { return row * 128 + ((ch ^ (row & 15)) << 3); }
+__device__ __forceinline__ int pv_swz(int row, int ch) { return row * 128 + ((ch ^ ((row & 7) << 1)) << 3); }
+constexpr int attn_vmcnt0() { return (7 << 4) | (15 << 8); }  // s_waitcnt vmcnt(0) alone
+
+template <bool kF16, bool kRound>
+__global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t* __restrict__ Q,
+                                                    const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+                                                    uint16_t* __restrict__ O) {
+  constexpr int D = 128, NDS = 4, NDT = 8;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * PSTAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * PSTAGE];
+
+  const int nq = (p.Sq + FQ - 1) / FQ;
+  const int BH = p.B * p.Hq;
+  const int bid = blockIdx.x;
+  int bh, qtile;
+  if (BH % 8 == 0) {
+    const int x = bid & 7, n = bid >> 3;
+    bh = (n / nq) * 8 + x;
+    qtile = nq - 1 - n % nq;
+  } else {
+    bh = bid % BH;
+    qtile = nq - 1 - bid / BH;
+  }
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int q0 = qtile * FQ;
+  const uint16_t* Qp = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h;
+  const uint16_t* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
+  const uint16_t* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
+  uint16_t* Op = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  u32x4 qf[2][NDS];
+  int lim[2];
+  const int64_t off = read_offset(p);
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = q0 + wave * 32 + qt * 16 + c16;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+      qf[qt][ds] = q < p.Sq ? *reinterpret_cast<const u32x4*>(Qp + (int64_t)q * p.q_s + ds * 32 + g * 8) : zero;
+    lim[qt] = key_limit(p, off, q);
+  }
+  const int kend = key_limit(p, off, std::min(q0 + FQ, p.Sq) - 1) + 1;
+  const int free_end = key_limit(p, off, q0) + 1;
+  const int nblocks = (kend + PK - 1) / PK;
+
+  // Buffer resources over this head's keys: rows past Skv read as zero.
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Skv - 1) * p.k_s + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Skv - 1) * p.v_s + D) * 2);
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Kp), 0, p.Skv > 0 ? (int)k_bytes : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Vp), 0, p.Skv > 0 ? (int)v_bytes : 0, 0x00020000);
+  // Wave w fills rows 16w .. 16w+15 of a stage, four rows per load; the
+  // lane part of each load's offset is fixed, the block part is scalar.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int lrow = lane >> 4, lslot = lane & 15;
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = wave_u * 16 + i * 4 + lrow;
+    koff[i] = (uint32_t)(((int64_t)row * p.k_s + ((lslot ^ (row & 15)) * 8)) * 2);
+    voff[i] = (uint32_t)(((int64_t)row * p.v_s + ((lslot ^ ((row & 7) << 1)) * 8)) * 2);
+  }
+  auto dma_k = [&](int kb, int stage) {
+    const uint32_t sblk = (uint32_t)((int64_t)kb * PK * p.k_s * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (attn_lds_ptr)(Ks + stage * PSTAGE + (wave_u * 16 + i * 4) * 128),
+                                               16, koff[i], sblk, 0, 0);
+  };
+  auto dma_v = [&](int kb, int stage) {
+    const uint32_t sblk = (uint32_t)((int64_t)kb * PK * p.v_s * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (attn_lds_ptr)(Vs + stage * PSTAGE + (wave_u * 16 + i * 4) * 128),
+                                               16, voff[i], sblk, 0, 0);
+  };
+
+  const float c2 = p.scale * 1.44269504088896340736f;
+  float m[2] = {-INFINITY, -INFINITY};
+  f32x4 oacc[NDT][2];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) oacc[dt][0] = oacc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Row sums: O^T rows of an all-ones V^T tile (every element of a lane's
+  // accumulator holds its query's sum).
+  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const uint32_t one2 = kF16 ? 0x3c003c00u : 0x3f803f80u;
+  const u32x4 ones = {one2, one2, one2, one2};
+
+  // S^T[key][query] of block kb for the wave's 32 queries, from K stage `stage`.
+  auto scores = [&](int stage, f32x4 (&sacc)[4][2]) {
+    const uint16_t* ks = Ks + stage * PSTAGE;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) sacc[kt][0] = sacc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[pk_swz(kt * 16 + c16, ds * 4 + g)]);
+        sacc[kt][0] = mfma16<kF16>(a, qf[0][ds], sacc[kt][0]);
+        sacc[kt][1] = mfma16<kF16>(a, qf[1][ds], sacc[kt][1]);
+      }
+    }
+  };
+  // Softmax of block kb's scores into P^T fragments; running max, sum and
+  // output rescale.
+  // Keys past a query's limit: only blocks that reach past the first
+  // query's limit have any (a branch of its own, so unmasked blocks pay
+  // nothing per score).
+  auto mask = [&](int kb, f32x4 (&sacc)[4][2]) {
+    if (kb * PK + PK <= free_end) return;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kb * PK + kt * 16 + g * 4 + r > lim[qt]) sacc[kt][qt][r] = -INFINITY;
+  };
+  // Running max: raised only when a block's max exceeds it by more than
+  // 2^8 in the exponential (then the output and sum are rescaled), so the
+  // exponentials stay below 2^8 and most blocks skip the rescale. The row
+  // sums come from the P.V products (a row of ones beside V), so the softmax
+  // itself is max, round, exponential and pack.
+  auto softmax = [&](int kb, f32x4 (&sacc)[4][2], u32x4 (&pf)[2][2]) {
+    (void)kb;
+    float alpha[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float s[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[kt][r] = sacc[kt][qt][r];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        mx = __builtin_elementwise_maximum(
+            mx, __builtin_elementwise_maximum(__builtin_elementwise_maximum(s[kt][0], s[kt][1]),
+                                              __builtin_elementwise_maximum(s[kt][2], s[kt][3])));
+      mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 16));
+      mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32));
+      if constexpr (kRound) mx = round16<kF16>(mx);
+      const bool raise = mx * c2 > m[qt] * c2 + 8.f;
+      const float mnew = raise ? mx : m[qt];
+      const float mc = (mnew == -INFINITY ? 0.f : mnew) * c2;
+      alpha[qt] = __builtin_amdgcn_exp2f(m[qt] * c2 - mc);
+      m[qt] = mnew;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          float x0 = s[kt][r], x1 = s[kt][r + 1];
+          if constexpr (kRound) {
+            const uint32_t pk = pack2<kF16>(x0, x1);
+            if constexpr (kF16) {
+              x0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(pk & 0xffffu));
+              x1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(pk >> 16));
+            } else {
+              x0 = __builtin_bit_cast(float, pk << 16);
+              x1 = __builtin_bit_cast(float, pk & 0xffff0000u);
+            }
+          }
+          s[kt][r] = __builtin_amdgcn_exp2f(fmaf(x0, c2, -mc));
+          s[kt][r + 1] = __builtin_amdgcn_exp2f(fmaf(x1, c2, -mc));
+        }
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        pf[qt][st] = u32x4{pack2<kF16>(s[2 * st][0], s[2 * st][1]), pack2<kF16>(s[2 * st][2], s[2 * st][3]),
+                           pack2<kF16>(s[2 * st + 1][0], s[2 * st + 1][1]),
+                           pack2<kF16>(s[2 * st + 1][2], s[2 * st + 1][3])};
+    }
+    if (!__all(alpha[0] == 1.f && alpha[1] == 1.f)) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt][qt] *= alpha[qt];
+        lacc[qt][0] *= alpha[qt];
+      }
+    }
+  };
+  // O^T[d][query] += V^T[d][key] . P^T[key][query] from V stage `stage`.
+  auto pv = [&](int stage, const u32x4 (&pf)[2][2]) {
+    const uint16_t* vs = Vs + stage * PSTAGE;
+    const int i = lane & 15;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int r0 = st * 32 + 4 * g + (i >> 2), r1 = r0 + 16;
+        const int ch = 2 * dt + ((i & 3) >> 1), sub = 4 * (i & 1);
+        const attn_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (attn_lds_v4i16*)((__attribute__((address_space(3))) uint16_t*)(vs + pv_swz(r0, ch) + sub)));
+        const attn_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (attn_lds_v4i16*)((__attribute__((address_space(3))) uint16_t*)(vs + pv_swz(r1, ch) + sub)));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
+        oacc[dt][0] = mfma16<kF16>(a, pf[0][st], oacc[dt][0]);
+        oacc[dt][1] = mfma16<kF16>(a, pf[1][st], oacc[dt][1]);
+      }
+      lacc[0] = mfma16<kF16>(ones, pf[0][st], lacc[0]);
+      lacc[1] = mfma16<kF16>(ones, pf[1][st], lacc[1]);
+    }
+  };
+
+  f32x4 sA[4][2];
+  u32x4 pf[2][2];
+  // Block kb from stage kb & 1 while block kb + 1 loads into the other
+  // (read in the step before); two workgroups per CU overlap one's MFMAs
+  // with the other's softmax. A wave whose 32 queries allow none of a
+  // block's keys (the diagonal blocks past its last query) only takes part
+  // in the loads and barriers.
+  const int wave_last = key_limit(p, off, std::min(q0 + wave * 32 + 31, p.Sq - 1));
+  if (nblocks > 0) {
+    dma_k(0, 0);
+    dma_v(0, 0);
+  }
+  for (int kb = 0; kb < nblocks; ++kb) {
+    __builtin_amdgcn_s_waitcnt(attn_vmcnt0());
+    __syncthreads();
+    if (kb + 1 < nblocks) {
+      dma_k(kb + 1, (kb + 1) & 1);
+      dma_v(kb + 1, (kb + 1) & 1);
+    }
+    if (kb * PK > wave_last) continue;
+    scores(kb & 1, sA);
+    mask(kb, sA);
+    softmax(kb, sA, pf);
+    pv(kb & 1, pf);
+  }
+
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = q0 + wave * 32 + qt * 16 + c16;
+    if (q >= p.Sq) continue;
+    uint16_t* orow = Op + (int64_t)q * p.o_s;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const f32x4 o = oacc[dt][qt];
+      const float lq = lacc[qt][0];
+      *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) =
+          u32x2{pack2<kF16>(o[0] / lq, o[1] / lq), pack2<kF16>(o[2] / lq, o[3] / lq)};
     }
   }
 }
@@ -775,8 +1062,17 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     uint16_t* o = static_cast<uint16_t*>(out);
     const dim3 g(static_cast<uint32_t>(grid)), block(256);
 #define PJRTX_ATTN(F16, DIM, RND) hipLaunchKernelGGL((attn_tiles<F16, DIM, RND>), g, block, 0, s, p, q, k, v, o)
+#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), g, block, 0, s, p, q, k, v, o)
     const bool rnd = p.round_scores != 0;
-    if (p.D == 128 && f16 && rnd) PJRTX_ATTN(true, 128, true);
+    // The DMA kernel addresses K and V through 32-bit buffer offsets;
+    // PJRTX_ATTN_PIPE=0 keeps the register-staged tile kernel.
+    const bool dma = p.D == 128 && env_int("PJRTX_ATTN_PIPE", 1) != 0 &&
+                     ((int64_t)std::max(p.Skv, 1) + PK) * std::max(p.k_s, p.v_s) * 2 < (int64_t(1) << 31);
+    if (dma && f16 && rnd) PJRTX_PIPE(true, true);
+    else if (dma && f16) PJRTX_PIPE(true, false);
+    else if (dma && rnd) PJRTX_PIPE(false, true);
+    else if (dma) PJRTX_PIPE(false, false);
+    else if (p.D == 128 && f16 && rnd) PJRTX_ATTN(true, 128, true);
     else if (p.D == 128 && f16) PJRTX_ATTN(true, 128, false);
     else if (p.D == 128 && rnd) PJRTX_ATTN(false, 128, true);
     else if (p.D == 128) PJRTX_ATTN(false, 128, false);
@@ -785,6 +1081,7 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     else if (rnd) PJRTX_ATTN(false, 64, true);
     else PJRTX_ATTN(false, 64, false);
 #undef PJRTX_ATTN
+#undef PJRTX_PIPE
   } else {
     PJRTX_CHECK(static_cast<int64_t>(p.B) * p.Hq * p.Sq < (int64_t(1) << 31), Code::kUnimplemented,
                 "attention: too many query rows");
