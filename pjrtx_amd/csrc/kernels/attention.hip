@@ -796,17 +796,20 @@ __device__ __forceinline__ void merge_splits(const float* pr, int nact, int D, T
   out[tid] = Elem<T>::put(acc / lsum);
 }
 
-template <typename T, int NCH>
+template <typename T, int NCH, int DKT>
 __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __restrict__ Q, const T* __restrict__ K,
                                                    const T* __restrict__ V, T* __restrict__ O, float* __restrict__ part,
                                                    int keys_per_split, int nsplit, uint32_t* __restrict__ counters,
                                                    int fused) {
   constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte piece
   constexpr int D = NCH * EPC;
-  constexpr int CPT = NCH / 4;         // pieces of a K row per lane (4 lanes per key)
+  constexpr int LPK = 256 / DKT;       // lanes per key in the scores (4 for 64-key passes, 8 for 32)
+  static_assert(NCH % LPK == 0 || DKT == 64, "a K row splits evenly over a key's lanes");
+  constexpr int CPT = NCH >= LPK ? NCH / LPK : 1;  // pieces of a K row per lane
   constexpr int G = 256 / NCH;         // key groups in P.V
-  constexpr int KG = DK / G;           // keys per group
-  __shared__ float ps[DK];
+  constexpr int KG = DKT / G;          // keys per group
+  static_assert(KG >= 1, "at least one key per P.V group");
+  __shared__ float ps[DKT];
   __shared__ float wred[2][4];
   __shared__ float ow[G][D];
   __shared__ float msh[64], lsh[64];
@@ -828,7 +831,7 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
   const T* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
   const T* Qp = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h + (int64_t)q * p.q_s;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int quarter = tid & 3, kslot = tid >> 2;      // scores: key slot, quarter of the row
+  const int quarter = tid % LPK, kslot = tid / LPK;  // scores: key slot, share of the row
   const int c = tid % NCH, g = tid / NCH;             // P.V: head-dim piece, key group
   float qv[CPT * EPC];
 #pragma unroll
@@ -843,7 +846,7 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
   float m = -INFINITY, l = 0.f, o[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) o[e] = 0.f;
-  for (int kb = k0; kb < k1; kb += DK) {
+  for (int kb = k0; kb < k1; kb += DKT) {
     const int key = kb + kslot;
     u32x4 kv[CPT];
 #pragma unroll
@@ -864,13 +867,13 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
 #pragma unroll
       for (int e = 0; e < EPC; ++e) acc += qv[i * EPC + e] * Elem<T>::get(e8[e]);
     }
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
+#pragma unroll
+    for (int k = 1; k < LPK; k <<= 1) acc += __shfl_xor(acc, k);
     if (p.round_scores) acc = Elem<T>::get(Elem<T>::put(acc));
     const float sc = key < k1 ? acc * p.scale : -INFINITY;
     float mx = sc;
 #pragma unroll
-    for (int k = 32; k >= 4; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
+    for (int k = 32; k >= LPK; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
     if (lane == 0) wred[0][wave] = mx;
     __syncthreads();
     const float mnew = fmaxf(m, fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3])));
@@ -880,7 +883,7 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
     if (quarter == 0) ps[kslot] = pe;
     float sum = quarter == 0 ? pe : 0.f;
 #pragma unroll
-    for (int k = 32; k >= 4; k >>= 1) sum += __shfl_xor(sum, k);
+    for (int k = 32; k >= LPK; k >>= 1) sum += __shfl_xor(sum, k);
     if (lane == 0) wred[1][wave] = sum;
     __syncthreads();
     l = l * alpha + (((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3]);
@@ -962,12 +965,18 @@ void launch_decode(hipStream_t s, const AttnParams& p, const T* q, const T* k, c
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
   const dim3 grid(static_cast<uint32_t>(8 * ((rows + 7) / 8) * nsplit)), block(256);
   const int f = fused ? 1 : 0;
+  // 32-key passes for splits that are not whole 64-key passes (K rows of at
+  // least 8 pieces, so a key's 8 lanes each take whole pieces).
+  const bool half = keys_per_split % DK != 0;
+#define PJRTX_DEC(NC, DKT) \
+  hipLaunchKernelGGL((attn_decode<T, NC, DKT>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f)
   switch (p.D / EPC) {
-    case 4: hipLaunchKernelGGL((attn_decode<T, 4>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
-    case 8: hipLaunchKernelGGL((attn_decode<T, 8>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
-    case 16: hipLaunchKernelGGL((attn_decode<T, 16>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
-    default: hipLaunchKernelGGL((attn_decode<T, 32>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f); break;
+    case 4: PJRTX_DEC(4, 64); break;
+    case 8: if (half) PJRTX_DEC(8, 32); else PJRTX_DEC(8, 64); break;
+    case 16: if (half) PJRTX_DEC(16, 32); else PJRTX_DEC(16, 64); break;
+    default: if (half) PJRTX_DEC(32, 32); else PJRTX_DEC(32, 64); break;
   }
+#undef PJRTX_DEC
   if (nsplit > 1 && !fused)
     hipLaunchKernelGGL((attn_combine<T>), dim3(static_cast<uint32_t>(rows)), dim3(std::max(64, p.D)), 0, s, p, part,
                        nsplit, keys_per_split, o);
@@ -1007,14 +1016,20 @@ AttnPath attention_path(const AttnParams& p, DType t, int* nsplit, int* keys_per
   const bool fits = t == DType::kF32 ? decode_fits<float>(p) : t == DType::kBF16 ? decode_fits<uint16_t>(p)
                     : t == DType::kF16 ? decode_fits<_Float16>(p) : false;
   if (!fits) return AttnPath::kRows;
-  // Splits of whole 64-key passes: enough splits for about 512 workgroups
-  // over the rows, at most 64 per row.
+  // Splits of whole 64-key passes (32-key ones with
+  // PJRTX_ATTN_DECODE_KEYS=32, head dims of 8 pieces or more; slower on the
+  // decode workload, where each workgroup's fixed cost dominates): enough
+  // splits for about PJRTX_ATTN_DECODE_WGS (512) workgroups over the rows,
+  // at most 64 per row.
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-  const int passes = std::max(1, (p.Skv + DK - 1) / DK);
-  const int want = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(64, (512 + rows - 1) / rows)));
+  const int64_t epc = t == DType::kF32 ? 4 : 8;
+  const int unit = p.D / epc >= 8 && env_int("PJRTX_ATTN_DECODE_KEYS", 64) == 32 ? 32 : DK;
+  const int64_t target = std::max<int64_t>(1, env_int("PJRTX_ATTN_DECODE_WGS", 512));
+  const int passes = std::max(1, (p.Skv + unit - 1) / unit);
+  const int want = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(64, (target + rows - 1) / rows)));
   const int n = std::min(passes, want);
   const int per = (passes + n - 1) / n;
-  *keys_per_split = per * DK;
+  *keys_per_split = per * unit;
   *nsplit = (p.Skv + *keys_per_split - 1) / *keys_per_split;
   if (*nsplit < 1) *nsplit = 1;
   return AttnPath::kDecode;
