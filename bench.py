@@ -315,13 +315,18 @@ def launch_units(plan: dict) -> list[dict]:
 
 def profile_unit_us(workload: str, unit: str):
     """The rocprofv3 figure for `unit` that the committed kernel-stats summary
-    of this workload records (its `rocprof_unit_us <unit> <us> <file>` line:
+    of this workload records (its `rocprof_unit_us <unit> <us> [route]` line:
     the unit's kernels' total duration over the run divided by the unit's
-    calls), so that `frac` can be recomputed from the profile."""
+    calls), so that `frac` can be recomputed from the profile. A plain GEMM
+    has two routes (hipBLASLt unless PJRTX_BLASLT=0, else the own kernels),
+    each with its own summary."""
+    route = "own" if os.environ.get("PJRTX_BLASLT", "1") == "0" else "blaslt"
     for p in sorted((ROOT / "profiles").glob(f"*.{workload}.kernel_stats.md")):
         for ln in p.read_text().splitlines():
             parts = ln.strip().strip("`").split()
             if len(parts) >= 3 and parts[0] == "rocprof_unit_us" and parts[1] == unit:
+                if len(parts) >= 4 and parts[3] != route:
+                    continue
                 return {"file": f"profiles/{p.name}", "kernel_us": float(parts[2])}
     return None
 
