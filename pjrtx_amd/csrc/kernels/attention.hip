@@ -375,7 +375,7 @@ constexpr int attn_vmcnt0() { return (7 << 4) | (15 << 8); }  // s_waitcnt vmcnt
 template <bool kF16, bool kRound>
 __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t* __restrict__ Q,
                                                     const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                                                    uint16_t* __restrict__ O) {
+                                                    uint16_t* __restrict__ O, int order) {
   constexpr int D = 128, NDS = 4, NDT = 8;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * PSTAGE];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * PSTAGE];
@@ -385,9 +385,24 @@ __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t
   const int bid = blockIdx.x;
   int bh, qtile;
   if (BH % 8 == 0) {
+    // One (batch, head)'s query tiles on one XCD (its K and V from that
+    // XCD's L2). order 0: a head's tiles in a row, latest first; order g > 0:
+    // heads in groups of g per XCD, each group's tiles latest first across
+    // its heads, so the heaviest tiles of the last group start early and
+    // light ones end the launch.
     const int x = bid & 7, n = bid >> 3;
-    bh = (n / nq) * 8 + x;
-    qtile = nq - 1 - n % nq;
+    if (order > 0) {
+      const int hx = BH / 8;
+      const int gsz = std::min(order, hx);
+      const int span = gsz * nq;
+      const int grp = n / span, w = n - grp * span;
+      const int gfirst = grp * gsz, gcount = std::min(gsz, hx - gfirst);
+      qtile = nq - 1 - w / gcount;
+      bh = (gfirst + w % gcount) * 8 + x;
+    } else {
+      bh = (n / nq) * 8 + x;
+      qtile = nq - 1 - n % nq;
+    }
   } else {
     bh = bid % BH;
     qtile = nq - 1 - bid / BH;
@@ -1077,7 +1092,8 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     uint16_t* o = static_cast<uint16_t*>(out);
     const dim3 g(static_cast<uint32_t>(grid)), block(256);
 #define PJRTX_ATTN(F16, DIM, RND) hipLaunchKernelGGL((attn_tiles<F16, DIM, RND>), g, block, 0, s, p, q, k, v, o)
-#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), g, block, 0, s, p, q, k, v, o)
+    const int order = static_cast<int>(env_int("PJRTX_ATTN_ORDER", 8));
+#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), g, block, 0, s, p, q, k, v, o, order)
     const bool rnd = p.round_scores != 0;
     // The DMA kernel addresses K and V through 32-bit buffer offsets;
     // PJRTX_ATTN_PIPE=0 keeps the register-staged tile kernel.
