@@ -375,15 +375,18 @@ constexpr int attn_vmcnt0() { return (7 << 4) | (15 << 8); }  // s_waitcnt vmcnt
 template <bool kF16, bool kRound>
 __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t* __restrict__ Q,
                                                     const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                                                    uint16_t* __restrict__ O, int order) {
+                                                    uint16_t* __restrict__ O, int order, int pair) {
   constexpr int D = 128, NDS = 4, NDT = 8;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * PSTAGE];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * PSTAGE];
 
   const int nq = (p.Sq + FQ - 1) / FQ;
+  // pair: a workgroup takes query tiles nq-1-j and j (the heaviest with the
+  // lightest), so every workgroup has the same number of key blocks.
+  const int nslots = pair ? (nq + 1) / 2 : nq;
   const int BH = p.B * p.Hq;
   const int bid = blockIdx.x;
-  int bh, qtile;
+  int bh, slot;
   if (BH % 8 == 0) {
     // One (batch, head)'s query tiles on one XCD (its K and V from that
     // XCD's L2). order 0: a head's tiles in a row, latest first; order g > 0:
@@ -394,26 +397,32 @@ __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t
     if (order > 0) {
       const int hx = BH / 8;
       const int gsz = std::min(order, hx);
-      const int span = gsz * nq;
+      const int span = gsz * nslots;
       const int grp = n / span, w = n - grp * span;
       const int gfirst = grp * gsz, gcount = std::min(gsz, hx - gfirst);
-      qtile = nq - 1 - w / gcount;
+      slot = w / gcount;
       bh = (gfirst + w % gcount) * 8 + x;
     } else {
-      bh = (n / nq) * 8 + x;
-      qtile = nq - 1 - n % nq;
+      bh = (n / nslots) * 8 + x;
+      slot = n % nslots;
     }
   } else {
     bh = bid % BH;
-    qtile = nq - 1 - bid / BH;
+    slot = bid / BH;
   }
+  const int tile0 = nq - 1 - slot;
+  const int tile1 = pair && slot < tile0 ? slot : -1;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
-  const int q0 = qtile * FQ;
   const uint16_t* Qp = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h;
   const uint16_t* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
   const uint16_t* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
   uint16_t* Op = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h;
+  for (int ti = 0; ti < 2; ++ti) {
+  const int qtile = ti == 0 ? tile0 : tile1;
+  if (qtile < 0) break;
+  if (ti > 0) __syncthreads();  // the first tile's last LDS reads are done
+  const int q0 = qtile * FQ;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -632,6 +641,7 @@ __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t
       *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) =
           u32x2{pack2<kF16>(o[0] / lq, o[1] / lq), pack2<kF16>(o[2] / lq, o[3] / lq)};
     }
+  }
   }
 }
 
@@ -1093,7 +1103,10 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     const dim3 g(static_cast<uint32_t>(grid)), block(256);
 #define PJRTX_ATTN(F16, DIM, RND) hipLaunchKernelGGL((attn_tiles<F16, DIM, RND>), g, block, 0, s, p, q, k, v, o)
     const int order = static_cast<int>(env_int("PJRTX_ATTN_ORDER", 8));
-#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), g, block, 0, s, p, q, k, v, o, order)
+    const int pair = p.causal && env_int("PJRTX_ATTN_PAIR", 1) != 0 ? 1 : 0;
+    const dim3 gp(static_cast<uint32_t>(static_cast<int64_t>(p.B) * p.Hq *
+                                        (pair ? ((p.Sq + FQ - 1) / FQ + 1) / 2 : (p.Sq + FQ - 1) / FQ)));
+#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), gp, block, 0, s, p, q, k, v, o, order, pair)
     const bool rnd = p.round_scores != 0;
     // The DMA kernel addresses K and V through 32-bit buffer offsets;
     // PJRTX_ATTN_PIPE=0 keeps the register-staged tile kernel.
