@@ -416,6 +416,7 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
   constexpr int VEC = 16 / (int)sizeof(T);
   typedef VecOf<T, VEC> V;
   __shared__ V part[3][64];
+  __shared__ uint32_t pidx[kHotChunk];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int64_t total = 0;
   for (int k = 31; k >= h.kmin; --k) total += (int64_t)h.counts[k] * (((int64_t(2) << k) + kHotChunk - 1) / kHotChunk);
@@ -434,20 +435,30 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
     }
     const uint32_t lo = seg_start[row] + chunk * kHotChunk, hi = min(lo + (uint32_t)kHotChunk, seg_end[row]);
     if (lo >= hi) continue;  // uniform over the workgroup
+    // The chunk's update indices go to LDS first (one coalesced read), so
+    // the update-row loads below need no dependent index load.
+    const int n = (int)(hi - lo);
+    __syncthreads();  // the previous item's readers of pidx are done
+    for (int t = threadIdx.x; t < n; t += 256) pidx[t] = perm[lo + t];
+    __syncthreads();
     for (int64_t c0 = (int64_t)lane * VEC; c0 - lane * VEC < row_elems; c0 += 64 * VEC) {
       const bool col_ok = c0 < row_elems;
       V acc;
       bool any = false;
-      for (uint32_t i = lo + wave; i < hi; i += 4 * kFoldDepth) {
-        V u[kFoldDepth];
+      // Wave w folds rows w, w + 4, ...; kFoldDepth of them per batch, the
+      // next batch's loads issued before the current batch is folded.
+      V ua[kFoldDepth], ub[kFoldDepth];
+      auto issue = [&](V (&u)[kFoldDepth], int base) {
 #pragma unroll
         for (int q = 0; q < kFoldDepth; ++q) {
-          const uint32_t j = min(i + 4 * q, hi - 1);  // clamped: a repeat of the last row is never folded
-          u[q] = col_ok ? *reinterpret_cast<const V*>(updates + (int64_t)perm[j] * row_elems + c0) : V();
+          const int j = min(base + 4 * q, n - 1);  // clamped: a repeat of the last row is never folded
+          u[q] = col_ok ? *reinterpret_cast<const V*>(updates + (int64_t)pidx[j] * row_elems + c0) : V();
         }
+      };
+      auto fold = [&](const V (&u)[kFoldDepth], int base) {
 #pragma unroll
         for (int q = 0; q < kFoldDepth; ++q) {
-          if (i + 4 * q >= hi) break;
+          if (base + 4 * q >= n) break;
           if (!any) {
             acc = u[q];
             any = true;
@@ -456,6 +467,18 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
             for (int e = 0; e < VEC; ++e) acc.v[e] = int_fold<T, OP>(acc.v[e], u[q].v[e]);
           }
         }
+      };
+      int base = wave;
+      if (base < n) issue(ua, base);
+      while (base < n) {
+        const int b1 = base + 4 * kFoldDepth;
+        if (b1 < n) issue(ub, b1);
+        fold(ua, base);
+        if (b1 >= n) break;
+        const int b2 = b1 + 4 * kFoldDepth;
+        if (b2 < n) issue(ua, b2);
+        fold(ub, b1);
+        base = b2;
       }
       // waves 1-3 hand their partials to wave 0 (a wave with no row keeps `any` false)
       __shared__ int has[3];
