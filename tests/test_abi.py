@@ -64,3 +64,25 @@ def test_unimplemented_slot_returns_error(plugin):
     with pytest.raises(PjrtError) as e:
         plugin.call("Executable_Serialize", _mk(Args()))
     assert e.value.code == 12
+
+
+def test_compile_fingerprint_needs_no_gpu(plugin, monkeypatch):
+    """The compile-cache key: stable for a text, different for another text
+    or another PJRTX_* environment (the switches change plans)."""
+    from pjrtx_amd.hlo import Builder
+    b = Builder("jit_fp")
+    x = b.param((8, 16), "f32")
+    text = b.build([b.sum(x, [1])])
+    f1 = plugin.compile_fingerprint(text)
+    assert f1.startswith("pjrtx-") and len(f1) == 38 and f1 == plugin.compile_fingerprint(text)
+    assert plugin.compile_fingerprint(text + " ") != f1
+    monkeypatch.setenv("PJRTX_GEMV_FUSION", "0")
+    assert plugin.compile_fingerprint(text) != f1
+
+
+def test_residency_setters_reject_bad_devices(plugin):
+    """Without a GPU the residency calls fail with an error code, not a crash."""
+    if plugin.device_count() > 0:
+        pytest.skip("covered by the GPU residency tests")
+    with pytest.raises(Exception):
+        plugin.set_max_resident_bytes(0, 1 << 20)

@@ -76,3 +76,11 @@ def test_destroyed_executables_leave_the_budget(client, uncapped):
     del exe
     gc.collect()
     assert p.residency_stats(0)["resident_bytes"] == before
+
+
+def test_measured_mfma_peak_is_plausible(plugin):
+    """The calibration kernel behind roofline.measured_peak: dense bf16 MFMA
+    on every SIMD sustains most of the published 2.5 PFLOP/s and never more."""
+    for shape in (0, 1):
+        tf = plugin.mfma_peak_tflops(0, shape)
+        assert 800.0 < tf < 2600.0, (shape, tf)
