@@ -100,28 +100,32 @@ __global__ void __launch_bounds__(256) scatter_keys(ScatterKeyParams p, const vo
 }
 
 // ------------------------------------------------------------- radix sort
+template <int BITS>
 __global__ void __launch_bounds__(64) radix_hist(const uint32_t* __restrict__ keys, int64_t n, int shift,
                                                  uint32_t* __restrict__ hist, int nblocks) {
-  __shared__ uint32_t h[256];
+  constexpr uint32_t BINS = 1u << BITS;
+  __shared__ uint32_t h[BINS];
   const int lane = threadIdx.x;
-  for (int i = lane; i < 256; i += 64) h[i] = 0;
+  for (uint32_t i = lane; i < BINS; i += 64) h[i] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kTile;
 #pragma unroll 4
   for (int j = 0; j < kItems; ++j) {
     const int64_t e = base + j * 64 + lane;
-    if (e < n) atomicAdd(&h[(keys[e] >> shift) & 255u], 1u);
+    if (e < n) atomicAdd(&h[(keys[e] >> shift) & (BINS - 1)], 1u);
   }
   __syncthreads();
-  for (int i = lane; i < 256; i += 64) hist[(int64_t)i * nblocks + blockIdx.x] = h[i];
+  for (uint32_t i = lane; i < BINS; i += 64) hist[(int64_t)i * nblocks + blockIdx.x] = h[i];
 }
 
+template <int BITS>
 __global__ void __launch_bounds__(64) radix_scatter(const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
                                                     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n,
                                                     int shift, const uint32_t* __restrict__ offsets, int nblocks) {
-  __shared__ uint32_t cnt[256];
+  constexpr uint32_t BINS = 1u << BITS;
+  __shared__ uint32_t cnt[BINS];
   const int lane = threadIdx.x;
-  for (int i = lane; i < 256; i += 64) cnt[i] = offsets[(int64_t)i * nblocks + blockIdx.x];
+  for (uint32_t i = lane; i < BINS; i += 64) cnt[i] = offsets[(int64_t)i * nblocks + blockIdx.x];
   __syncthreads();
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int64_t base = (int64_t)blockIdx.x * kTile;
@@ -130,11 +134,11 @@ __global__ void __launch_bounds__(64) radix_scatter(const uint32_t* __restrict__
     const bool valid = e < n;
     const uint32_t k = valid ? kin[e] : 0u;
     const uint32_t v = valid ? vin[e] : 0u;
-    const uint32_t d = (k >> shift) & 255u;
-    // Lanes holding the same digit: intersect the 8 per-bit ballots.
+    const uint32_t d = (k >> shift) & (BINS - 1);
+    // Lanes holding the same digit: intersect the per-bit ballots.
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < BITS; ++b) {
       const uint64_t m = __ballot((d >> b) & 1u);
       peers &= ((d >> b) & 1u) ? m : ~m;
     }
@@ -769,7 +773,7 @@ void exclusive_scan(hipStream_t s, const uint32_t* in, uint32_t* out, int64_t n,
 
 size_t radix_sort_scratch_bytes(int64_t n) {
   const int64_t nblocks = (n + kTile - 1) / kTile;
-  return static_cast<size_t>(256 * nblocks * 2 + kScanTile) * 4;
+  return static_cast<size_t>(512 * nblocks * 2 + kScanTile) * 4;
 }
 
 void launch_radix_sort(hipStream_t s, uint32_t* keys, uint32_t* vals, uint32_t* tmp_keys, uint32_t* tmp_vals,
@@ -777,18 +781,31 @@ void launch_radix_sort(hipStream_t s, uint32_t* keys, uint32_t* vals, uint32_t* 
   if (n <= 1) return;
   const int64_t nblocks = (n + kTile - 1) / kTile;
   PJRTX_CHECK(256 * nblocks <= int64_t(kScanTile) * kScanTile, Code::kUnimplemented, "radix sort: too many elements");
+  // 9-bit digits when that saves a pass (17 or 18 key bits: two passes
+  // instead of three, and no copy back), 8-bit ones otherwise.
+  const bool nine = (bits + 8) / 9 < (bits + 7) / 8 && 512 * nblocks <= int64_t(kScanTile) * kScanTile;
+  const int width = nine ? 9 : 8;
+  const int64_t bins = int64_t(1) << width;
   uint32_t* hist = static_cast<uint32_t*>(scratch);
-  uint32_t* offs = hist + 256 * nblocks;
-  uint32_t* tmp = offs + 256 * nblocks;
+  uint32_t* offs = hist + bins * nblocks;
+  uint32_t* tmp = offs + bins * nblocks;
   uint32_t *ki = keys, *vi = vals, *ko = tmp_keys, *vo = tmp_vals;
-  const int passes = (bits + 7) / 8;
+  const int passes = (bits + width - 1) / width;
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = pass * 8;
-    hipLaunchKernelGGL(radix_hist, dim3(static_cast<unsigned>(nblocks)), dim3(64), 0, s, ki, n, shift, hist,
-                       static_cast<int>(nblocks));
-    exclusive_scan(s, hist, offs, 256 * nblocks, tmp);
-    hipLaunchKernelGGL(radix_scatter, dim3(static_cast<unsigned>(nblocks)), dim3(64), 0, s, ki, vi, ko, vo, n, shift,
-                       offs, static_cast<int>(nblocks));
+    const int shift = pass * width;
+    if (nine)
+      hipLaunchKernelGGL(radix_hist<9>, dim3(static_cast<unsigned>(nblocks)), dim3(64), 0, s, ki, n, shift, hist,
+                         static_cast<int>(nblocks));
+    else
+      hipLaunchKernelGGL(radix_hist<8>, dim3(static_cast<unsigned>(nblocks)), dim3(64), 0, s, ki, n, shift, hist,
+                         static_cast<int>(nblocks));
+    exclusive_scan(s, hist, offs, bins * nblocks, tmp);
+    if (nine)
+      hipLaunchKernelGGL(radix_scatter<9>, dim3(static_cast<unsigned>(nblocks)), dim3(64), 0, s, ki, vi, ko, vo, n,
+                         shift, offs, static_cast<int>(nblocks));
+    else
+      hipLaunchKernelGGL(radix_scatter<8>, dim3(static_cast<unsigned>(nblocks)), dim3(64), 0, s, ki, vi, ko, vo, n,
+                         shift, offs, static_cast<int>(nblocks));
     std::swap(ki, ko);
     std::swap(vi, vo);
   }
