@@ -77,6 +77,8 @@ PJRTX_HIP_API int pjrtx_compile_cache_usage(int64_t* bytes, int64_t* evictions);
  * executable_fingerprint.zig:9-24 (alloc). */
 PJRTX_HIP_API int pjrtx_compile_fingerprint(const char* text, size_t len, char* out, size_t cap, size_t* needed);
 
+/* ------------------------------------------- residency (needs a device) */
+
 /* Device residency budget: the cap, in bytes, on the device memory that
  * loaded executables hold (code objects, resident constants, kernel
  * scratch); 0 removes it (the default, or PJRTX_MAX_RESIDENT_BYTES).
@@ -90,6 +92,8 @@ PJRTX_HIP_API int pjrtx_set_max_resident_bytes(int device, int64_t bytes);
  * evictions, evicted bytes, cap} of the device's residency budget.
  * Replaces executable_cache.zig:9-25 (Stats). */
 PJRTX_HIP_API int pjrtx_residency_stats(int device, int64_t out[6]);
+
+/* --------------------------------------------------- plans (host only) */
 
 /* Parses a StableHLO text module, runs the fusion planner and code
  * generator, and writes a JSON description of the plan to `out` (at most
