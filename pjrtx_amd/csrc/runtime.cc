@@ -397,6 +397,10 @@ void buffer_to_host(const Buffer& b, void* dst, size_t dst_size) {
               strformat("ToHostBuffer: destination holds %zu bytes, buffer needs %zu", dst_size, bytes));
   if (b.ready) b.ready->wait_resolved();  // an async transfer still filling it, or its error
   if (!bytes) return;
+  if (staged_download_wanted(bytes)) {
+    staged_download(b.dev, dst, b.mem->ptr, bytes);
+    return;
+  }
   b.dev->make_current();
   hip_check(hipMemcpyAsync(dst, b.mem->ptr, bytes, hipMemcpyDeviceToHost, b.dev->stream()), "hipMemcpyAsync(D2H)");
   hip_check(hipStreamSynchronize(b.dev->stream()), "hipStreamSynchronize");

@@ -257,6 +257,10 @@ class AsyncTransfer {
 // stream (transfer.cc); returns when the data is on the device.
 bool staged_upload_wanted(size_t bytes);
 void staged_upload(Device* dev, void* dst, const void* src, size_t bytes);
+// Large device-to-host copies through the same ring; returns when the data
+// is in `dst`.
+bool staged_download_wanted(size_t bytes);
+void staged_download(Device* dev, void* dst, const void* src, size_t bytes);
 void buffer_to_host(const Buffer& b, void* dst, size_t dst_size);
 
 // hiprtc compile of generated kernel source for the device arch, cached in

@@ -1,5 +1,6 @@
-// Host-to-device uploads through pinned staging (the reference's async H2D
-// manager: src/plugin/async_h2d.zig, src/runtime/async_host_transfer.zig).
+// Host-to-device uploads (and large device-to-host readbacks) through pinned
+// staging (the reference's async H2D manager: src/plugin/async_h2d.zig,
+// src/runtime/async_host_transfer.zig).
 //
 // A pageable host array is copied in chunks into a ring of pinned buffers
 // by a few host threads while the DMA engine moves the previous chunk to
@@ -101,6 +102,42 @@ void staged_upload(Device* dev, void* dst, const void* src, size_t bytes) {
     st.busy[k] = true;
   }
   hip_check(hipStreamSynchronize(st.stream), "hipStreamSynchronize(copy)");
+  for (bool& b : st.busy) b = false;
+}
+
+bool staged_download_wanted(size_t bytes) {
+  static const int on = env_int("PJRTX_STAGED_D2H", 1);
+  return on != 0 && bytes >= (64u << 20);
+}
+
+// Device-to-host through the same ring: the DMA engine fills pinned chunk
+// k+1.. while the host threads copy chunk k out to the caller's (pageable)
+// memory. The copy stream first waits for the compute stream, which may
+// still be producing the source.
+void staged_download(Device* dev, void* dst, const void* src, size_t bytes) {
+  Stager& st = stager_for(dev->ordinal());
+  std::lock_guard<std::mutex> lk(st.mu);
+  dev->make_current();
+  if (!st.ready) init(st);
+  hip_check(hipEventRecord(st.after_compute, dev->stream()), "hipEventRecord");
+  hip_check(hipStreamWaitEvent(st.stream, st.after_compute, 0), "hipStreamWaitEvent");
+  const size_t nchunks = (bytes + kChunk - 1) / kChunk;
+  size_t issued = 0, copied = 0;
+  while (copied < nchunks) {
+    while (issued < nchunks && issued - copied < static_cast<size_t>(kRing)) {
+      const size_t off = issued * kChunk, n = std::min(kChunk, bytes - off);
+      const int k = static_cast<int>(issued % kRing);
+      hip_check(hipMemcpyAsync(st.pinned[k], static_cast<const char*>(src) + off, n, hipMemcpyDeviceToHost, st.stream),
+                "hipMemcpyAsync(staged D2H)");
+      hip_check(hipEventRecord(st.done[k], st.stream), "hipEventRecord");
+      ++issued;
+    }
+    const size_t off = copied * kChunk, n = std::min(kChunk, bytes - off);
+    const int k = static_cast<int>(copied % kRing);
+    hip_check(hipEventSynchronize(st.done[k]), "hipEventSynchronize(staging)");
+    host_copy(static_cast<char*>(dst) + off, st.pinned[k], n);
+    ++copied;
+  }
   for (bool& b : st.busy) b = false;
 }
 
