@@ -249,6 +249,10 @@ class AsyncTransfer {
   Device* dev_;
   std::mutex mu_;
   std::vector<BufferRef> bufs_;
+  // The buffers' device memory, owned here too until each buffer's last
+  // chunk: a buffer deleted by its holder mid-transfer keeps its block
+  // while a copy into it may still be queued.
+  std::vector<MemRef> mems_;
   std::vector<std::shared_ptr<Event>> pending_;  // each buffer's readiness until resolved
   std::vector<bool> finished_;
 };

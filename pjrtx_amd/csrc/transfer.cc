@@ -151,6 +151,7 @@ AsyncTransfer::AsyncTransfer(Device* dev, const std::vector<TensorType>& types) 
     b->mem = dev->allocate(t.bytes());
     auto ev = Event::pending();
     b->ready = ev;
+    mems_.push_back(b->mem);
     bufs_.push_back(b);
     pending_.push_back(ev);
     finished_.push_back(false);
@@ -176,10 +177,11 @@ std::shared_ptr<Event> AsyncTransfer::write(size_t i, int64_t offset, const void
   PJRTX_CHECK(static_cast<uint64_t>(offset) + static_cast<uint64_t>(size) <= total, Code::kInvalidArgument,
               "async transfer range exceeds buffer size");
   PJRTX_CHECK(!finished_[i], Code::kFailedPrecondition, "async transfer buffer already received its last chunk");
+  PJRTX_CHECK(!bufs_[i]->deleted, Code::kFailedPrecondition, "async transfer buffer was deleted");
   dev_->make_current();
   std::shared_ptr<Event> done = Event::ready();
   if (size > 0) {
-    char* dst = static_cast<char*>(bufs_[i]->mem->ptr) + offset;
+    char* dst = static_cast<char*>(mems_[i]->ptr) + offset;
     if (staged_upload_wanted(static_cast<size_t>(size))) {
       staged_upload(dev_, dst, data, static_cast<size_t>(size));  // returns once on the device
     } else {
@@ -191,6 +193,7 @@ std::shared_ptr<Event> AsyncTransfer::write(size_t i, int64_t offset, const void
   if (last) {
     finished_[i] = true;
     pending_[i]->resolve(Event::record(dev_));
+    mems_[i].reset();  // the buffer alone owns its memory from here
   }
   return done;
 }
@@ -207,6 +210,7 @@ void AsyncTransfer::fail(size_t i, Code code, const std::string& msg) {
   PJRTX_CHECK(i < bufs_.size(), Code::kInvalidArgument, "async transfer buffer index is out of range");
   finished_[i] = true;
   pending_[i]->resolve_failed(code, msg);
+  mems_[i].reset();
 }
 
 }  // namespace pjrtx

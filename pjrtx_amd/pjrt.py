@@ -427,12 +427,23 @@ class Buffer:
     def is_deleted(self) -> bool:
         """PJRT_Buffer_IsDeleted: true after Delete or after the buffer was
         donated to an execution."""
+        if not self.handle:
+            return True
         a = _mk(BufferIsDeletedArgs())
         a.buffer = self.handle
         self.client.p.call("Buffer_IsDeleted", a)
         return bool(a.is_deleted)
 
+    def delete_memory(self) -> None:
+        """PJRT_Buffer_Delete: gives the device memory back; the handle
+        stays valid (is_deleted() turns true) until delete()."""
+        if self.handle:
+            a = _mk(BufferDestroyArgs())   # same layout as PJRT_Buffer_Delete_Args
+            a.buffer = self.handle
+            self.client.p.call("Buffer_Delete", a)
+
     def delete(self) -> None:
+        """PJRT_Buffer_Destroy: releases the handle (and its memory)."""
         if self.handle:
             a = _mk(BufferDestroyArgs())
             a.buffer = self.handle

@@ -120,3 +120,23 @@ def test_errors(client):
     t.close()   # buffer 2 never received its last chunk
     with pytest.raises(PjrtError, match="destroyed before"):
         b2.to_numpy()
+
+
+def test_buffer_deleted_mid_transfer(client):
+    """The holder deletes a buffer before its last chunk: the next chunk for
+    it is refused (no write into memory the buffer gave back), the other
+    buffers of the manager still fill."""
+    t = client.async_transfer([((1024,), "f32"), ((1024,), "f32")])
+    b0, b1 = t.buffer(0), t.buffer(1)
+    t.transfer(0, np.ones(512, np.float32), 0, False)
+    b0.delete_memory()
+    assert b0.is_deleted()
+    with pytest.raises(PjrtError, match="was deleted"):
+        t.transfer(0, np.ones(512, np.float32), 2048, True)
+    with pytest.raises(PjrtError, match="was deleted"):
+        b0.to_numpy()
+    t.transfer(1, np.full(1024, 3, np.float32), 0, True)
+    np.testing.assert_array_equal(b1.to_numpy(), np.full(1024, 3, np.float32))
+    t.close()
+    b0.delete()
+    assert b0.is_deleted()
