@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels/dot.h"
@@ -230,26 +231,51 @@ __global__ void __launch_bounds__(256) mfma_gemm(GemmParams p, const uint16_t* _
 }
 
 // ------------------------------------------------------------- large GEMM
-// gemm_nt_big: C[b] = A[b] (M x K, K contiguous) * B[b]^T (N x K, K
-// contiguous) for M, N >= 256. 256 x 256 block tile, BK = 64, 512 threads in
-// 2 x 4 waves of 128 x 64 (8 x 4 MFMA 16x16x32 subtiles each, 128 f32
-// accumulators per lane). Operands go global -> registers -> LDS (double
-// buffered, one barrier per K step; the next tile's global loads are in
-// flight while the current one is multiplied). LDS rows are 64 elements
-// (eight 16-byte chunks) with chunk c of row r stored at c ^ ((r >> 1) & 7),
-// so the 16-byte fragment reads of 16 consecutive rows hit distinct banks
-// without padding. The C tile is staged per wave through LDS (same swizzle)
-// and written with 16-byte stores.
+// gemm_nt_256: C[b] = A[b] (M x K, K contiguous) * B[b]^T (N x K, K
+// contiguous) for products with enough 256 x 256 tiles to fill the GPU.
+//  * 256 x 256 block tile, 64-deep k-tiles, 512 threads: 2 x 4 waves of
+//    128 x 64 (4 x 2 blocks of v_mfma_f32_32x32x16, 128 f32 accumulators a
+//    lane), two waves per SIMD.
+//  * A and B k-tiles go from global memory straight into LDS (buffer loads
+//    with the LDS destination, 16 bytes a lane, eight 128-byte row pieces per
+//    instruction); two stages. Waves 0-3 issue all of the loads, so on every
+//    SIMD one of the two waves never waits on a load issue.
+//  * One barrier per k-tile, placed before the tile's last 16-deep slab: by
+//    then every wave holds its last-slab fragments in registers and has read
+//    all of the tile, so the barrier both publishes tile kt+1 (loaded during
+//    tile kt) and frees tile kt's stage for tile kt+2.
+//  * LDS rows are 64 elements (eight 16-byte chunks), chunk c of row r stored
+//    at c ^ ((r >> 1) & 7): the fragment reads of 16 consecutive rows hit
+//    distinct banks. A load places lane L's 16 bytes in slot L of its 1 KB,
+//    so the swizzle is applied on the global side (the lane filling slot
+//    (r, c) fetches chunk c ^ f(r)).
+//  * Rows past M or N and 8-element k chunks past K read as zero: the whole
+//    offset of every load is in its lane part, which the buffer range check
+//    covers, and chunks past K get an offset beyond the range.
 constexpr int GBM = 256, GBN = 256, GBK = 64, GTHREADS = 512;
+constexpr int kGemmLoadWaves = 4;  // waves 0..3 issue the LDS loads
+constexpr int kGemmLoadsPerWave = (GBM + GBN) / 8 / kGemmLoadWaves;  // 1 KB loads a load wave issues per tile
+
+typedef __attribute__((address_space(3))) void* gemm_lds_ptr;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int gswz(int row, int chunk) { return row * GBK + ((chunk ^ ((row >> 1) & 7)) << 3); }
+constexpr int gemm_vmcnt0() { return (7 << 4) | (15 << 8); }  // s_waitcnt vmcnt(0) alone
+
+template <bool kF16>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                   0);
+}
 
 template <bool kF16, int kOutBytes>
-__global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_big(GemmParams p, const uint16_t* __restrict__ A,
+__global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const uint16_t* __restrict__ A,
                                                             const uint16_t* __restrict__ B, void* __restrict__ C) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GBM + GBN) * GBK];
-  uint16_t* As = smem;                    // [2][GBM * GBK]
-  uint16_t* Bs = smem + 2 * GBM * GBK;    // [2][GBN * GBK]
+  constexpr int STAGE = (GBM + GBN) * GBK;  // elements per stage
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
 
   const int tiles_m = (p.M + GBM - 1) / GBM, tiles_n = (p.N + GBN - 1) / GBN;
   const int per_batch = tiles_m * tiles_n;
@@ -258,7 +284,7 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_big(GemmParams p, const u
   if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;  // contiguous tile runs per XCD
   const int b = bid / per_batch;
   const int t = bid - b * per_batch;
-  const int group = 4;  // walk 4 tile-rows at a time so B tiles are reused from L2
+  const int group = 8;  // walk 8 tile-rows at a time so B k-tiles are reused from L2
   const int gsize = group * tiles_n;
   const int g = t / gsize;
   const int first_m = g * group;
@@ -266,82 +292,156 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_big(GemmParams p, const u
   const int tm = first_m + (t - g * gsize) % gm;
   const int tn = (t - g * gsize) / gm;
   const int m0 = tm * GBM, n0 = tn * GBN;
-  const uint16_t* Ab = A + (int64_t)b * p.a_batch_stride;
-  const uint16_t* Bb = B + (int64_t)b * p.b_batch_stride;
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  u32x4 ra[4], rb[4];
 
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = tid + GTHREADS * j;
-      const int row = c >> 3, k = k0 + (c & 7) * 8;
-      const int m = m0 + row, n = n0 + row;
-      ra[j] = (m < p.M && k < p.K) ? *reinterpret_cast<const u32x4*>(Ab + (int64_t)m * p.lda + k) : zero;
-      rb[j] = (n < p.N && k < p.K) ? *reinterpret_cast<const u32x4*>(Bb + (int64_t)n * p.ldb + k) : zero;
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = tid + GTHREADS * j;
-      const int row = c >> 3, ch = c & 7;
-      *reinterpret_cast<u32x4*>(&As[buf * GBM * GBK + gswz(row, ch)]) = ra[j];
-      *reinterpret_cast<u32x4*>(&Bs[buf * GBN * GBK + gswz(row, ch)]) = rb[j];
-    }
-  };
+  // Buffer resources over this tile's row panels; the range ends with the
+  // last valid row's K elements.
+  const uint16_t* Ap = A + (int64_t)b * p.a_batch_stride + (int64_t)m0 * p.lda;
+  const uint16_t* Bp = B + (int64_t)b * p.b_batch_stride + (int64_t)n0 * p.ldb;
+  const int rows_a = min(GBM, p.M - m0), rows_b = min(GBN, p.N - n0);
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Ap), 0, (int)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Bp), 0, (int)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2), 0x00020000);
+  const int nk = (p.K + GBK - 1) / GBK;
+  const int ktail = p.K - (nk - 1) * GBK;  // valid elements of the last k-tile
 
-  f32x4 acc[8][4];
+  // Load lanes: load i of load wave w fills stage rows (4 i + w) * 8 + L / 8,
+  // slot L % 8; its global chunk is (L % 8) ^ f(row), and f depends only on
+  // row % 16 = 8 (w % 2) + L / 8.
+  const int lrow = lane >> 3, lslot = lane & 7;
+  const int lchunk = lslot ^ ((((wave & 1) * 8 + lrow) >> 1) & 7);
+  const uint32_t tail_oob = lchunk * 8 >= ktail ? 0x80000000u : 0u;  // beyond the range of any resource
+  uint32_t aoff[kGemmLoadsPerWave / 2], boff[kGemmLoadsPerWave / 2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int kt_count = (p.K + GBK - 1) / GBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < kt_count; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < kt_count) gload((kt + 1) * GBK);
-    const uint16_t* as = As + buf * GBM * GBK;
-    const uint16_t* bs = Bs + buf * GBN * GBK;
-#pragma unroll
-    for (int kk = 0; kk < GBK; kk += 32) {
-      const int ch = (kk >> 3) + (lane >> 4);
-      u32x4 af[8], bfr[4];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        af[i] = *reinterpret_cast<const u32x4*>(&as[gswz(wm * 128 + i * 16 + (lane & 15), ch)]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bfr[j] = *reinterpret_cast<const u32x4*>(&bs[gswz(wn * 64 + j * 16 + (lane & 15), ch)]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<kF16>(af[i], bfr[j], acc[i][j]);
-    }
-    if (kt + 1 < kt_count) lstore(buf ^ 1);
-    __syncthreads();
+  for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
+    const int row = (i * kGemmLoadWaves + wave) * 8 + lrow;
+    aoff[i] = (uint32_t)(row * p.lda * 2 + lchunk * 16);
+    boff[i] = (uint32_t)(row * p.ldb * 2 + lchunk * 16);
   }
+  auto load_tile = [&](int kt, int stage) {
+    uint16_t* st = smem + stage * STAGE;
+    const uint32_t kb = (uint32_t)(kt * GBK * 2);
+    const uint32_t oob = kt == nk - 1 ? tail_oob : 0u;
+#pragma unroll
+    for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
+      const int row = (i * kGemmLoadWaves + wave) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (gemm_lds_ptr)(st + row * GBK), 16, (aoff[i] + kb) | oob, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
+      const int row = (i * kGemmLoadWaves + wave) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (gemm_lds_ptr)(st + (GBM + row) * GBK), 16, (boff[i] + kb) | oob,
+                                               0, 0, 0);
+    }
+  };
 
-  // Epilogue: lane holds rows (lane/16)*4 + r, column lane%16 of each 16x16
-  // subtile of the wave's 128 x 64 tile.
+  // Fragments of v_mfma_f32_32x32x16: lane L holds row L % 32 of a 32-row
+  // block, k chunk 2 s + L / 32 of slab s; f(row) = f(L % 32).
+  const int fr = lane & 31, fh = lane >> 5;
+  int loff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) loff[s] = gswz(fr, 2 * s + fh);
+  u32x4 fa[2][4], fb[2][2];
+  auto read_slab = [&](int stage, int s, int buf) {
+    const uint16_t* as = smem + stage * STAGE + (wm * 128) * GBK;
+    const uint16_t* bs = smem + stage * STAGE + (GBM + wn * 64) * GBK;
+    // In the order the MFMAs first use them.
+    fa[buf][0] = *reinterpret_cast<const u32x4*>(as + loff[s]);
+    fb[buf][0] = *reinterpret_cast<const u32x4*>(bs + loff[s]);
+    fb[buf][1] = *reinterpret_cast<const u32x4*>(bs + 32 * GBK + loff[s]);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(as + i * 32 * GBK + loff[s]);
+  };
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<kF16>(fa[buf][i], fb[buf][j], acc[i][j]);
+  };
+  // One MFMA, then one fragment read, six times; then the remaining MFMAs.
+  auto interleave_reads = [&]() {
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  };
+
+  // Tile kt: slabs 0..2 read the next slab's fragments while multiplying;
+  // then the barrier; then tile kt+1's first slab is read and tile kt+2's
+  // loads issued while the last slab multiplies. Tile indices past the last
+  // reload it into the free stage, so the load waves' counts stay uniform.
+  auto tile_body = [&](int kt, bool last, auto loader) {
+    constexpr bool kLoads = decltype(loader)::value;
+    const int cur = kt & 1;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      read_slab(cur, s + 1, (s + 1) & 1);
+      mma(s & 1);
+      interleave_reads();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!last) {
+      // Own loads of tile kt+1 landed and own reads of tile kt done, then
+      // everyone's.
+      __builtin_amdgcn_s_waitcnt(gemm_vmcnt0() & ~(15 << 8));
+      __builtin_amdgcn_s_barrier();
+      read_slab(cur ^ 1, 0, 0);
+      if constexpr (kLoads) load_tile(min(kt + 2, nk - 1), cur);
+    }
+    mma(1);
+    interleave_reads();
+    if constexpr (kLoads) {
+#pragma unroll
+      for (int q = 0; q < kGemmLoadsPerWave; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto run = [&](auto loader) {
+    constexpr bool kLoads = decltype(loader)::value;
+    if constexpr (kLoads) {
+      load_tile(0, 0);
+      load_tile(min(1, nk - 1), 1);
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | (kGemmLoadsPerWave & 15) | ((kGemmLoadsPerWave >> 4) << 14));
+    }
+    __builtin_amdgcn_s_barrier();
+    read_slab(0, 0, 0);
+    for (int kt = 0; kt < nk - 1; ++kt) tile_body(kt, false, loader);
+    tile_body(nk - 1, true, loader);
+  };
+  if (wave < kGemmLoadWaves) run(std::true_type{});
+  else run(std::false_type{});
+  __builtin_amdgcn_s_waitcnt(gemm_vmcnt0());
+  __syncthreads();
+
+  // Epilogue: lane L holds rows 8 (r / 4) + 4 (L / 32) + r % 4, column L % 32
+  // of each 32 x 32 block.
   const int wrow0 = m0 + wm * 128, wcol0 = n0 + wn * 64;
   if constexpr (kOutBytes == 2) {
     uint16_t* cs = smem + wave * 128 * GBK;  // this wave's 128 x 64 staging tile
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = i * 16 + (lane >> 4) * 4 + r;
-          const int col = j * 16 + (lane & 15);
+        for (int r = 0; r < 16; ++r) {
+          const int row = i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+          const int col = j * 32 + fr;
           const float v = acc[i][j][r];
           cs[gswz(row, col >> 3) + (col & 7)] = kF16 ? f32_to_f16_bits(v) : f32_to_bf16_rne(v);
         }
@@ -364,13 +464,13 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_big(GemmParams p, const u
   } else {
     float* Cb = reinterpret_cast<float*>(C) + (int64_t)b * p.M * p.ldc;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = wrow0 + i * 16 + (lane >> 4) * 4 + r;
-          const int n = wcol0 + j * 16 + (lane & 15);
+        for (int r = 0; r < 16; ++r) {
+          const int m = wrow0 + i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+          const int n = wcol0 + j * 32 + fr;
           if (m < p.M && n < p.N) Cb[(int64_t)m * p.ldc + n] = acc[i][j][r];
         }
   }
@@ -730,8 +830,12 @@ bool use_big_gemm(const GemmParams& p) {
   // better (environment: PJRTX_BIG_GEMM_MIN_TILES).
   const int64_t min_tiles = env_int("PJRTX_BIG_GEMM_MIN_TILES", 256);
   const int64_t tiles = (int64_t)((p.M + GBM - 1) / GBM) * ((p.N + GBN - 1) / GBN) * p.batch;
-  return p.M >= GBM && p.N >= GBN && p.K % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
-         p.a_batch_stride % 8 == 0 && p.b_batch_stride % 8 == 0 && tiles >= min_tiles && tiles < (int64_t(1) << 31);
+  // Every load offset (a 256-row panel) must stay below 2^31 bytes.
+  const int64_t panel_limit = int64_t(1) << 30;
+  return p.M >= GBM && p.N >= GBN && p.K > 0 && p.K % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
+         p.lda >= p.K && p.ldb >= p.K && p.a_batch_stride % 8 == 0 && p.b_batch_stride % 8 == 0 &&
+         tiles >= min_tiles && tiles < (int64_t(1) << 31) && (int64_t)GBM * p.lda < panel_limit &&
+         (int64_t)GBN * p.ldb < panel_limit;
 }
 
 void launch_transpose16(hipStream_t s, const void* in, void* out, int64_t batch, int64_t rows, int64_t cols,
@@ -752,13 +856,13 @@ void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const v
     const uint16_t* a = static_cast<const uint16_t*>(A);
     const uint16_t* b = static_cast<const uint16_t*>(B);
     if (out_bytes == 2) {
-      if (f16) hipLaunchKernelGGL((gemm_nt_big<true, 2>), grid, block, 0, s, p, a, b, C);
-      else hipLaunchKernelGGL((gemm_nt_big<false, 2>), grid, block, 0, s, p, a, b, C);
+      if (f16) hipLaunchKernelGGL((gemm_nt_256<true, 2>), grid, block, 0, s, p, a, b, C);
+      else hipLaunchKernelGGL((gemm_nt_256<false, 2>), grid, block, 0, s, p, a, b, C);
     } else {
-      if (f16) hipLaunchKernelGGL((gemm_nt_big<true, 4>), grid, block, 0, s, p, a, b, C);
-      else hipLaunchKernelGGL((gemm_nt_big<false, 4>), grid, block, 0, s, p, a, b, C);
+      if (f16) hipLaunchKernelGGL((gemm_nt_256<true, 4>), grid, block, 0, s, p, a, b, C);
+      else hipLaunchKernelGGL((gemm_nt_256<false, 4>), grid, block, 0, s, p, a, b, C);
     }
-    check("gemm_nt_big");
+    check("gemm_nt_256");
     return;
   }
   const int64_t tiles = (int64_t)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN) * p.batch;
