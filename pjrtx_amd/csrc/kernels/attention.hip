@@ -375,7 +375,7 @@ constexpr int attn_vmcnt0() { return (7 << 4) | (15 << 8); }  // s_waitcnt vmcnt
 template <bool kF16, bool kRound>
 __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t* __restrict__ Q,
                                                     const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                                                    uint16_t* __restrict__ O, int order, int pair) {
+                                                    uint16_t* __restrict__ O, int order, int pair, int prio) {
   constexpr int D = 128, NDS = 4, NDT = 8;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * PSTAGE];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * PSTAGE];
@@ -623,10 +623,18 @@ __global__ void __launch_bounds__(256, 2) attn_pipe(AttnParams p, const uint16_t
       dma_v(kb + 1, (kb + 1) & 1);
     }
     if (kb * PK > wave_last) continue;
+    // With `prio`, the matrix-core phases run at raised wave priority: on a
+    // SIMD whose other wave is in its softmax, the MFMAs issue first
+    // (environment: PJRTX_ATTN_PRIO=0 disables; 360-365 vs 368-370 us on
+    // [8,32,2048,128] causal bf16).
+    if (prio) __builtin_amdgcn_s_setprio(1);
     scores(kb & 1, sA);
+    if (prio) __builtin_amdgcn_s_setprio(0);
     mask(kb, sA);
     softmax(kb, sA, pf);
+    if (prio) __builtin_amdgcn_s_setprio(1);
     pv(kb & 1, pf);
+    if (prio) __builtin_amdgcn_s_setprio(0);
   }
 
 #pragma unroll
@@ -1106,7 +1114,8 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
     const int pair = p.causal && env_int("PJRTX_ATTN_PAIR", 1) != 0 ? 1 : 0;
     const dim3 gp(static_cast<uint32_t>(static_cast<int64_t>(p.B) * p.Hq *
                                         (pair ? ((p.Sq + FQ - 1) / FQ + 1) / 2 : (p.Sq + FQ - 1) / FQ)));
-#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), gp, block, 0, s, p, q, k, v, o, order, pair)
+    const int prio = static_cast<int>(env_int("PJRTX_ATTN_PRIO", 1));
+#define PJRTX_PIPE(F16, RND) hipLaunchKernelGGL((attn_pipe<F16, RND>), gp, block, 0, s, p, q, k, v, o, order, pair, prio)
     const bool rnd = p.round_scores != 0;
     // The DMA kernel addresses K and V through 32-bit buffer offsets;
     // PJRTX_ATTN_PIPE=0 keeps the register-staged tile kernel.
