@@ -218,13 +218,14 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
           blaslt_gemm(dev, g, A, B, out, f16, b_kmajor, out_kind == 2 ? 4 : 2))
         return;
       MemRef bt;
-      if (!b_kmajor) {
-        // The large-tile kernel takes B K-contiguous: transpose an N-contiguous
-        // B ([K][N] per batch) once, at HBM speed, when that kernel applies.
+      if (!b_kmajor && !use_big_gemm(g, false)) {
+        // The large-tile kernel reads an N-contiguous B directly when its
+        // rows allow (N a multiple of 8); otherwise transpose B ([K][N] per
+        // batch) once, at HBM speed, when the kernel applies to the result.
         GemmParams t = g;
         t.ldb = K;
         t.b_batch_stride = N * K;
-        if (use_big_gemm(t) && g.ldb == N && (batch == 1 || b.bs == K * N)) {
+        if (use_big_gemm(t, true) && g.ldb == N && (batch == 1 || b.bs == K * N)) {
           bt = dev->allocate(static_cast<size_t>(batch * N * K) * 2);
           launch_transpose16(dev->stream(), B, bt->ptr, batch, K, N, K * N, N * K);
           B = bt->ptr;

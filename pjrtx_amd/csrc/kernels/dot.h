@@ -20,8 +20,9 @@ struct GemmParams {
 void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const void* B, void* C, bool f16, bool b_kmajor,
                       int out_bytes);
 // True when the 256 x 256 tile kernel applies (M, N >= 256, 16-byte aligned
-// K-contiguous rows, enough tiles to fill the GPU); it needs B K-contiguous.
-bool use_big_gemm(const GemmParams& p);
+// rows, K a multiple of 8 and, for an N-contiguous B, N too; enough tiles to
+// fill the GPU). It takes B in either layout.
+bool use_big_gemm(const GemmParams& p, bool b_kmajor);
 // out[b] = transpose(in[b]) for 16-bit elements: in [rows][cols] -> out
 // [cols][rows], batch strides in elements.
 void launch_transpose16(hipStream_t s, const void* in, void* out, int64_t batch, int64_t rows, int64_t cols,

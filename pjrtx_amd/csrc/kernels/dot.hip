@@ -271,7 +271,15 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                    0);
 }
 
-template <bool kF16, int kOutBytes>
+// kBN: B is N-contiguous ([K][N], row stride ldb) instead of K-contiguous.
+// Its k-tile is then stored as 64 rows of 256 columns (512 bytes, chunk c of
+// row k at c ^ 4 (k & 3): the 32 lanes of a transposing read, 4 rows x 64
+// bytes, hit 64 distinct banks), and the B fragments come from transposing LDS
+// reads (ds_read_b64_tr_b16: lane j of a 16-lane group gets element j & 3
+// of the 8-byte pieces lanes 4 e + (j >> 2) address, e = 0..3; lanes
+// addressing 4 consecutive k rows x 16 columns return 4 consecutive k of
+// one column, half a fragment), so no transposed copy of B is made.
+template <bool kF16, int kOutBytes, bool kBN>
 __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const uint16_t* __restrict__ A,
                                                             const uint16_t* __restrict__ B, void* __restrict__ C) {
   constexpr int STAGE = (GBM + GBN) * GBK;  // elements per stage
@@ -300,12 +308,16 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const u
   // Buffer resources over this tile's row panels; the range ends with the
   // last valid row's K elements.
   const uint16_t* Ap = A + (int64_t)b * p.a_batch_stride + (int64_t)m0 * p.lda;
-  const uint16_t* Bp = B + (int64_t)b * p.b_batch_stride + (int64_t)n0 * p.ldb;
+  const uint16_t* Bp = B + (int64_t)b * p.b_batch_stride + (kBN ? (int64_t)n0 : (int64_t)n0 * p.ldb);
   const int rows_a = min(GBM, p.M - m0), rows_b = min(GBN, p.N - n0);
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(Ap), 0, (int)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2), 0x00020000);
+  // N-contiguous B: the range ends with row K-1's last valid column, so k
+  // rows past K read as zero; columns past N are masked per load below.
   const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(Bp), 0, (int)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2), 0x00020000);
+      const_cast<uint16_t*>(Bp), 0,
+      kBN ? (int)(((int64_t)(p.K - 1) * p.ldb + rows_b) * 2) : (int)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2),
+      0x00020000);
   const int nk = (p.K + GBK - 1) / GBK;
   const int ktail = p.K - (nk - 1) * GBK;  // valid elements of the last k-tile
 
@@ -320,7 +332,16 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const u
   for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
     const int row = (i * kGemmLoadWaves + wave) * 8 + lrow;
     aoff[i] = (uint32_t)(row * p.lda * 2 + lchunk * 16);
-    boff[i] = (uint32_t)(row * p.ldb * 2 + lchunk * 16);
+    if constexpr (kBN) {
+      // Load i of load wave w fills k rows 2 (4 i + w) + L / 32, slot L % 32
+      // (global chunk (L % 32) ^ 4 (k & 3)); chunks past N get an offset
+      // beyond the range.
+      const int krow = (i * kGemmLoadWaves + wave) * 2 + (lane >> 5);
+      const int chunk = (lane & 31) ^ ((krow & 3) << 2);
+      boff[i] = (uint32_t)(krow * p.ldb * 2 + chunk * 16) | (chunk * 8 >= rows_b ? 0x80000000u : 0u);
+    } else {
+      boff[i] = (uint32_t)(row * p.ldb * 2 + lchunk * 16);
+    }
   }
   auto load_tile = [&](int kt, int stage) {
     uint16_t* st = smem + stage * STAGE;
@@ -331,11 +352,21 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const u
       const int row = (i * kGemmLoadWaves + wave) * 8;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (gemm_lds_ptr)(st + row * GBK), 16, (aoff[i] + kb) | oob, 0, 0, 0);
     }
+    if constexpr (kBN) {
+      const uint32_t kr = (uint32_t)(kt * GBK * p.ldb * 2);
 #pragma unroll
-    for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
-      const int row = (i * kGemmLoadWaves + wave) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (gemm_lds_ptr)(st + (GBM + row) * GBK), 16, (boff[i] + kb) | oob,
-                                               0, 0, 0);
+      for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
+        const int krow = (i * kGemmLoadWaves + wave) * 2;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (gemm_lds_ptr)(st + GBM * GBK + krow * GBN), 16, boff[i] + kr, 0,
+                                                 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kGemmLoadsPerWave / 2; ++i) {
+        const int row = (i * kGemmLoadWaves + wave) * 8;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (gemm_lds_ptr)(st + (GBM + row) * GBK), 16,
+                                                 (boff[i] + kb) | oob, 0, 0, 0);
+      }
     }
   };
 
@@ -345,14 +376,45 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const u
   int loff[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) loff[s] = gswz(fr, 2 * s + fh);
+  // N-contiguous B: lane L (16-lane group g = L / 16, e = (L % 16) / 4,
+  // c = L % 4) of transposing read h addresses k row 16 s + 8 (g / 2) + 4 h +
+  // e, columns wn 64 + 32 j + 16 (g % 2) + 4 c .. + 3.
+  int troff[4][2][2];
+  if constexpr (kBN) {
+    const int g4 = lane >> 4, e4 = (lane >> 2) & 3, c4 = lane & 3;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int k = 16 * s + 8 * (g4 >> 1) + 4 * h + e4;
+          const int chunk = wn * 8 + 4 * j + 2 * (g4 & 1) + (c4 >> 1);
+          troff[s][h][j] = k * GBN + ((chunk ^ ((k & 3) << 2)) << 3) + 4 * (c4 & 1);
+        }
+  }
   u32x4 fa[2][4], fb[2][2];
+  auto read_b = [&](const uint16_t* stb, int s, int j) -> u32x4 {
+    if constexpr (kBN) {
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+      typedef __attribute__((address_space(3))) uint16_t lds_u16;
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)((lds_u16*)(stb + troff[s][0][j])));
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)((lds_u16*)(stb + troff[s][1][j])));
+      typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+      const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+      return u32x4{l2[0], l2[1], h2[0], h2[1]};
+    } else {
+      return *reinterpret_cast<const u32x4*>(stb + (wn * 64 + 32 * j) * GBK + loff[s]);
+    }
+  };
   auto read_slab = [&](int stage, int s, int buf) {
     const uint16_t* as = smem + stage * STAGE + (wm * 128) * GBK;
-    const uint16_t* bs = smem + stage * STAGE + (GBM + wn * 64) * GBK;
+    const uint16_t* stb = smem + stage * STAGE + GBM * GBK;
     // In the order the MFMAs first use them.
     fa[buf][0] = *reinterpret_cast<const u32x4*>(as + loff[s]);
-    fb[buf][0] = *reinterpret_cast<const u32x4*>(bs + loff[s]);
-    fb[buf][1] = *reinterpret_cast<const u32x4*>(bs + 32 * GBK + loff[s]);
+    fb[buf][0] = read_b(stb, s, 0);
+    fb[buf][1] = read_b(stb, s, 1);
 #pragma unroll
     for (int i = 1; i < 4; ++i) fa[buf][i] = *reinterpret_cast<const u32x4*>(as + i * 32 * GBK + loff[s]);
   };
@@ -369,14 +431,16 @@ __global__ void __launch_bounds__(GTHREADS, 1) gemm_nt_256(GemmParams p, const u
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<kF16>(fa[buf][i], fb[buf][j], acc[i][j]);
   };
-  // One MFMA, then one fragment read, six times; then the remaining MFMAs.
+  // One MFMA, then one fragment read, for each read of the slab; then the
+  // remaining MFMAs.
   auto interleave_reads = [&]() {
+    constexpr int kReads = kBN ? 8 : 6;
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < kReads; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if constexpr (kReads < 8) __builtin_amdgcn_sched_group_barrier(0x008, 8 - kReads, 0);
   };
 
   // Tile kt: slabs 0..2 read the next slab's fragments while multiplying;
@@ -825,17 +889,19 @@ void check(const char* what) {
 
 }  // namespace
 
-bool use_big_gemm(const GemmParams& p) {
+bool use_big_gemm(const GemmParams& p, bool b_kmajor) {
   // Below one tile per CU the 128 x 128 kernel's 4x more tiles fill the GPU
   // better (environment: PJRTX_BIG_GEMM_MIN_TILES).
   const int64_t min_tiles = env_int("PJRTX_BIG_GEMM_MIN_TILES", 256);
   const int64_t tiles = (int64_t)((p.M + GBM - 1) / GBM) * ((p.N + GBN - 1) / GBN) * p.batch;
-  // Every load offset (a 256-row panel) must stay below 2^31 bytes.
-  const int64_t panel_limit = int64_t(1) << 30;
+  // Every load offset (a 256-row panel of A, a panel or all K rows of B)
+  // must stay below 2^31 bytes.
+  const int64_t limit = int64_t(1) << 30;
+  const bool b_ok = b_kmajor ? (p.ldb >= p.K && (int64_t)GBN * p.ldb < limit)
+                             : (p.N % 8 == 0 && p.ldb >= p.N && (int64_t)p.K * p.ldb < limit);
   return p.M >= GBM && p.N >= GBN && p.K > 0 && p.K % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 &&
-         p.lda >= p.K && p.ldb >= p.K && p.a_batch_stride % 8 == 0 && p.b_batch_stride % 8 == 0 &&
-         tiles >= min_tiles && tiles < (int64_t(1) << 31) && (int64_t)GBM * p.lda < panel_limit &&
-         (int64_t)GBN * p.ldb < panel_limit;
+         p.lda >= p.K && b_ok && p.a_batch_stride % 8 == 0 && p.b_batch_stride % 8 == 0 && tiles >= min_tiles &&
+         tiles < (int64_t(1) << 31) && (int64_t)GBM * p.lda < limit;
 }
 
 void launch_transpose16(hipStream_t s, const void* in, void* out, int64_t batch, int64_t rows, int64_t cols,
@@ -850,18 +916,20 @@ void launch_transpose16(hipStream_t s, const void* in, void* out, int64_t batch,
 
 void launch_mfma_gemm(hipStream_t s, const GemmParams& p, const void* A, const void* B, void* C, bool f16, bool b_kmajor,
                       int out_bytes) {
-  if (b_kmajor && use_big_gemm(p)) {
+  if (use_big_gemm(p, b_kmajor)) {
     const int64_t tiles = (int64_t)((p.M + GBM - 1) / GBM) * ((p.N + GBN - 1) / GBN) * p.batch;
     const dim3 grid(static_cast<unsigned>(tiles)), block(GTHREADS);
     const uint16_t* a = static_cast<const uint16_t*>(A);
     const uint16_t* b = static_cast<const uint16_t*>(B);
+#define PJRTX_BIG(F16, OB, BN) hipLaunchKernelGGL((gemm_nt_256<F16, OB, BN>), grid, block, 0, s, p, a, b, C)
     if (out_bytes == 2) {
-      if (f16) hipLaunchKernelGGL((gemm_nt_256<true, 2>), grid, block, 0, s, p, a, b, C);
-      else hipLaunchKernelGGL((gemm_nt_256<false, 2>), grid, block, 0, s, p, a, b, C);
+      if (f16) { if (b_kmajor) PJRTX_BIG(true, 2, false); else PJRTX_BIG(true, 2, true); }
+      else { if (b_kmajor) PJRTX_BIG(false, 2, false); else PJRTX_BIG(false, 2, true); }
     } else {
-      if (f16) hipLaunchKernelGGL((gemm_nt_256<true, 4>), grid, block, 0, s, p, a, b, C);
-      else hipLaunchKernelGGL((gemm_nt_256<false, 4>), grid, block, 0, s, p, a, b, C);
+      if (f16) { if (b_kmajor) PJRTX_BIG(true, 4, false); else PJRTX_BIG(true, 4, true); }
+      else { if (b_kmajor) PJRTX_BIG(false, 4, false); else PJRTX_BIG(false, 4, true); }
     }
+#undef PJRTX_BIG
     check("gemm_nt_256");
     return;
   }

@@ -463,10 +463,13 @@ def test_concatenate_and_pad(client):
 
 
 _BIG_GEMM_SHAPES = [
-    ("bmk,bkn", (2, 300, 200), (2, 200, 520), "bf16", None),   # NN: transposed B, ragged M / N / K tail
+    ("bmk,bkn", (2, 300, 200), (2, 200, 520), "bf16", None),   # NN (B read N-contiguous), ragged M / N / K tail
     ("bmk,bnk", (3, 512, 136), (3, 264, 136), "bf16", None),   # NT, ragged N, K not a multiple of 64
     ("mk,kn", (256, 64), (64, 256), "f16", None),              # exactly one tile
     ("bmk,bnk", (2, 260, 72), (2, 300, 72), "bf16", "f32"),    # f32 output
+    ("bmk,bkn", (2, 264, 72), (2, 72, 300), "bf16", None),     # NN with N % 8 != 0: transposed copy of B
+    ("mk,kn", (520, 136), (136, 264), "bf16", "f32"),          # NN, f32 output, ragged M / N, K tail
+    ("bmk,bkn", (2, 256, 128), (2, 128, 512), "f16", None),    # NN, f16, whole tiles
 ]
 
 
