@@ -70,6 +70,32 @@ struct ScatterHotList {
   int64_t base[32] = {};
   int kmin = 0;                // lowest class that can hold a hot row
 };
+// Early rows: the longest rows, found from a sample of the keys, are folded
+// while the keys are still being sorted. `select` (one workgroup) sorts
+// kEarlySample keys taken at even strides and lists up to kEarlyRows rows
+// that fill at least kEarlyMinRun of them (longest first); the rows' update
+// indices are then listed in update order by a count / scan / write pass
+// over the keys, and their slices folded like hot rows. The sorted path
+// skips these rows (classify and the bulk fold read the list).
+constexpr int kEarlyRows = 4;
+constexpr int kEarlySample = 4096;
+constexpr int kEarlyMinRun = 64;
+constexpr int kEarlyBlockItems = 4096;  // keys per count / write workgroup
+struct ScatterEarly {
+  uint32_t* rows = nullptr;     // [1 + kEarlyRows]: count, then the rows
+  uint32_t* counts = nullptr;   // [kEarlyRows * blocks + 1]
+  uint32_t* offsets = nullptr;  // [kEarlyRows * blocks + 1]
+  uint32_t* list = nullptr;     // [n] update indices, row by row
+  uint32_t* scan_tmp = nullptr; // [2048]
+  int64_t blocks = 0;
+};
+inline int64_t scatter_early_blocks(int64_t n) { return (n + kEarlyBlockItems - 1) / kEarlyBlockItems; }
+// Queues the selection on `aux` (records `selected` after it, which the
+// sorted path's classify waits on), then the listing and the early folds.
+void launch_scatter_early(hipStream_t aux, hipEvent_t selected, const ScatterEarly& e, const uint32_t* keys, int64_t n,
+                          uint32_t invalid, int64_t row_elems, int op, DType t, const void* operand,
+                          const void* updates, void* out);
+
 struct ScatterRowsParams {
   int64_t rows = 0;
   int64_t row_elems = 0;
@@ -81,7 +107,8 @@ size_t scatter_hot_list_words(int64_t n);
 void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join, int64_t rows,
                          int64_t row_elems, int op, DType t, const void* operand, const void* updates,
                          const uint32_t* perm, const uint32_t* seg_start, const uint32_t* seg_end,
-                         const ScatterHotList& h, int64_t hot_wgs, void* out);
+                         const ScatterHotList& h, int64_t hot_wgs, void* out,
+                         const uint32_t* early_rows = nullptr);
 
 struct ScatterFoldParams {
   int64_t rows = 0;       // operand rows (element mode: operand elements)

@@ -365,14 +365,26 @@ struct alignas(sizeof(T) * VEC) VecOf {
 // Lists the hot rows by length class. With `init_src`, also copies each hot
 // row of the operand into the result (the integer chunk path accumulates
 // into it with atomics).
+// True when row r is one of the early rows (folded before the sort ends).
+__device__ __forceinline__ bool is_early_row(const uint32_t* __restrict__ early, int64_t r) {
+  if (!early) return false;
+  const uint32_t count = early[0];
+  bool hit = false;
+#pragma unroll
+  for (int j = 0; j < kEarlyRows; ++j) hit |= (uint32_t)j < count && early[1 + j] == (uint32_t)r;
+  return hit;
+}
+
 __global__ void __launch_bounds__(256) scatter_hot_classify(const uint32_t* __restrict__ seg_start,
                                                             const uint32_t* __restrict__ seg_end, int64_t rows,
                                                             ScatterHotList h, const uint4* __restrict__ init_src,
-                                                            uint4* __restrict__ init_dst, int64_t row_u4) {
+                                                            uint4* __restrict__ init_dst, int64_t row_u4,
+                                                            const uint32_t* __restrict__ early) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (r >= rows) return;
   const uint32_t len = seg_end[r] - seg_start[r];
   if (len <= (uint32_t)kHotMinUpdates) return;
+  if (is_early_row(early, r)) return;
   const int k = 31 - __clz(len);
   const uint32_t slot = atomicAdd(&h.counts[k], 1u);  // order inside a class does not change results
   h.rows[h.base[k] + slot] = (uint32_t)r;
@@ -692,12 +704,179 @@ __global__ void __launch_bounds__(256) scatter_hot_fold(
   }
 }
 
+// ---------------------------------------------------------------- early rows
+// Selection: kEarlySample keys at even strides sorted in LDS (bitonic); each
+// run of at least kEarlyMinRun equal keys (not the drop key) is a candidate;
+// the kEarlyRows longest (ties: smaller row) are listed, longest first.
+__global__ void __launch_bounds__(1024) scatter_early_select(const uint32_t* __restrict__ keys, int64_t n,
+                                                             uint32_t invalid, uint32_t* __restrict__ early) {
+  __shared__ uint32_t sk[kEarlySample];
+  __shared__ uint32_t cand_row[kEarlySample / kEarlyMinRun + 1], cand_len[kEarlySample / kEarlyMinRun + 1];
+  __shared__ uint32_t ncand;
+  const int tid = threadIdx.x;
+  if (tid == 0) ncand = 0;
+  for (int i = tid; i < kEarlySample; i += 1024) sk[i] = keys[(int64_t)i * n / kEarlySample];
+  __syncthreads();
+  for (int k = 2; k <= kEarlySample; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < kEarlySample; i += 1024) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint32_t a = sk[i], b = sk[l];
+          if ((a > b) == ((i & k) == 0)) {
+            sk[i] = b;
+            sk[l] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  for (int i = tid; i < kEarlySample; i += 1024) {
+    if (i > 0 && sk[i - 1] == sk[i]) continue;  // not a run start
+    int e = i + 1;
+    while (e < kEarlySample && sk[e] == sk[i]) ++e;
+    if (e - i >= kEarlyMinRun && sk[i] != invalid) {
+      const uint32_t slot = atomicAdd(&ncand, 1u);
+      cand_row[slot] = sk[i];
+      cand_len[slot] = (uint32_t)(e - i);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t count = 0;
+    bool taken[kEarlySample / kEarlyMinRun + 1] = {};
+    for (int j = 0; j < kEarlyRows; ++j) {
+      int best = -1;
+      for (uint32_t c = 0; c < ncand; ++c) {
+        if (taken[c]) continue;
+        if (best < 0 || cand_len[c] > cand_len[best] || (cand_len[c] == cand_len[best] && cand_row[c] < cand_row[best]))
+          best = (int)c;
+      }
+      if (best < 0) break;
+      taken[best] = true;
+      early[1 + count++] = cand_row[best];
+    }
+    early[0] = count;
+  }
+}
+
+// Per workgroup (kEarlyBlockItems consecutive keys, 16 a thread) and early
+// row j: how many keys name row j; counts[j * blocks + b]. The workgroup 0
+// also zeroes the trailing entry (the total after the scan).
+__global__ void __launch_bounds__(256) scatter_early_count(const uint32_t* __restrict__ keys, int64_t n,
+                                                           const uint32_t* __restrict__ early,
+                                                           uint32_t* __restrict__ counts, int64_t blocks) {
+  __shared__ uint32_t part[4][kEarlyRows];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t count = early[0];
+  uint32_t er[kEarlyRows];
+#pragma unroll
+  for (int j = 0; j < kEarlyRows; ++j) er[j] = (uint32_t)j < count ? early[1 + j] : 0xffffffffu;
+  uint32_t c[kEarlyRows] = {};
+  const int64_t base = (int64_t)blockIdx.x * kEarlyBlockItems + (int64_t)tid * 16;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t i = base + k;
+    const bool in = i < n;
+    const uint32_t key = in ? keys[i] : 0u;
+#pragma unroll
+    for (int j = 0; j < kEarlyRows; ++j) c[j] += in && (uint32_t)j < count && key == er[j] ? 1u : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kEarlyRows; ++j) {
+    uint32_t v = c[j];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) part[wave][j] = v;
+  }
+  __syncthreads();
+  if (tid < kEarlyRows) counts[(int64_t)tid * blocks + blockIdx.x] = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+  if (blockIdx.x == 0 && tid == 0) counts[(int64_t)kEarlyRows * blocks] = 0u;
+}
+
+// Writes each early row's update indices in update order: a thread's 16
+// keys, its exclusive rank among the workgroup's threads (wave scans plus
+// wave totals), and the workgroup's offset from the scanned counts.
+__global__ void __launch_bounds__(256) scatter_early_write(const uint32_t* __restrict__ keys, int64_t n,
+                                                           const uint32_t* __restrict__ early,
+                                                           const uint32_t* __restrict__ offsets, int64_t blocks,
+                                                           uint32_t* __restrict__ list) {
+  __shared__ uint32_t wtot[4][kEarlyRows];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t count = early[0];
+  uint32_t er[kEarlyRows];
+#pragma unroll
+  for (int j = 0; j < kEarlyRows; ++j) er[j] = (uint32_t)j < count ? early[1 + j] : 0xffffffffu;
+  const int64_t base = (int64_t)blockIdx.x * kEarlyBlockItems + (int64_t)tid * 16;
+  // match[k]: the early row (index + 1) key k names, 0 for none.
+  uint32_t match[16];
+  uint32_t c[kEarlyRows] = {};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t i = base + k;
+    const uint32_t key = i < n ? keys[i] : 0u;
+    match[k] = 0u;
+#pragma unroll
+    for (int j = 0; j < kEarlyRows; ++j)
+      if (i < n && (uint32_t)j < count && key == er[j]) {
+        match[k] = (uint32_t)j + 1u;
+        c[j] += 1u;
+      }
+  }
+  uint32_t incl[kEarlyRows];
+#pragma unroll
+  for (int j = 0; j < kEarlyRows; ++j) {
+    uint32_t v = c[j];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t u = __shfl_up(v, o);
+      if (lane >= o) v += u;
+    }
+    incl[j] = v;
+    if (lane == 63) wtot[wave][j] = v;
+  }
+  __syncthreads();
+  uint32_t pos[kEarlyRows];
+#pragma unroll
+  for (int j = 0; j < kEarlyRows; ++j) {
+    uint32_t wb = 0;
+    for (int w = 0; w < wave; ++w) wb += wtot[w][j];
+    pos[j] = offsets[(int64_t)j * blocks + blockIdx.x] + wb + incl[j] - c[j];
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+#pragma unroll
+    for (int j = 0; j < kEarlyRows; ++j)
+      if (match[k] == (uint32_t)j + 1u) list[pos[j]++] = (uint32_t)(base + k);
+  }
+}
+
+// Early row j's slices: workgroup j * slices + slice.
+template <typename Tag, ScatterOp OP>
+__global__ void __launch_bounds__(256) scatter_early_fold(int64_t row_elems,
+                                                          const typename StorageOf<Tag>::T* __restrict__ operand,
+                                                          const typename StorageOf<Tag>::T* updates,
+                                                          const uint32_t* __restrict__ early,
+                                                          const uint32_t* __restrict__ offsets, int64_t blocks,
+                                                          const uint32_t* list, typename StorageOf<Tag>::T* __restrict__ out) {
+  typedef typename StorageOf<Tag>::T T;
+  typedef HotShape<T> S;
+  __shared__ __align__(16) T lds[2 * S::BUF];
+  const int64_t slices = (row_elems + S::COLS - 1) / S::COLS;
+  const uint32_t j = (uint32_t)(blockIdx.x / slices);
+  const int slice = (int)(blockIdx.x % slices);
+  if (j >= early[0]) return;
+  const uint32_t lo = offsets[(int64_t)j * blocks], hi = offsets[(int64_t)(j + 1) * blocks];
+  if (hi <= lo) return;  // a selected row appears in the sample, so never empty
+  hot_slice_fold<Tag, OP>(row_elems, early[1 + j], slice, operand, updates, list, lo, hi - lo, out, lds);
+}
+
 template <typename Tag, ScatterOp OP, int VEC>
 __global__ void __launch_bounds__(256) scatter_rows_fold(
     ScatterRowsParams p, const typename StorageOf<Tag>::T* __restrict__ operand,
     const typename StorageOf<Tag>::T* __restrict__ updates, const uint32_t* __restrict__ perm,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ seg_end,
-    typename StorageOf<Tag>::T* __restrict__ out) {
+    typename StorageOf<Tag>::T* __restrict__ out, const uint32_t* __restrict__ early) {
   typedef Codec<Tag> K;
   typedef typename K::C C;
   typedef typename StorageOf<Tag>::T T;
@@ -706,6 +885,7 @@ __global__ void __launch_bounds__(256) scatter_rows_fold(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
   if (r >= p.rows) return;
+  if (is_early_row(early, r)) return;  // folded by the early path
   const uint32_t lo = seg_start[r], hi = seg_end[r];
   if (p.hot_wgs > 0 && hi - lo > (uint32_t)kHotMinUpdates) return;  // a hot row: folded by slices
   const T* xr = operand + r * p.row_elems;
@@ -862,7 +1042,7 @@ size_t scatter_hot_list_words(int64_t n) {
 void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join, int64_t rows,
                          int64_t row_elems, int op_i, DType t, const void* operand, const void* updates,
                          const uint32_t* perm, const uint32_t* seg_start, const uint32_t* seg_end,
-                         const ScatterHotList& h, int64_t hot_wgs, void* out) {
+                         const ScatterHotList& h, int64_t hot_wgs, void* out, const uint32_t* early_rows) {
   if (rows == 0 || row_elems == 0) return;
   const ScatterOp op = static_cast<ScatterOp>(op_i);
   const size_t es = dtype_size(t);
@@ -880,7 +1060,7 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
     const bool init = chunked && operand != out;
     hipLaunchKernelGGL(scatter_hot_classify, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, seg_end, rows, h,
                        init ? static_cast<const uint4*>(operand) : nullptr, init ? static_cast<uint4*>(out) : nullptr,
-                       row_elems * static_cast<int64_t>(es) / 16);
+                       row_elems * static_cast<int64_t>(es) / 16, early_rows);
     check("scatter_hot_classify");
   }
   if (p.hot_wgs > 0) {
@@ -905,7 +1085,8 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
       else PJRTX_HOT_OP(TAG, OPV);                                                                                    \
     }                                                                                                                 \
     hipLaunchKernelGGL((scatter_rows_fold<TAG, OPV, V>), gb, blk, 0, s, p, (const StorageOf<TAG>::T*)operand,        \
-                       (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, (StorageOf<TAG>::T*)out);        \
+                       (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, (StorageOf<TAG>::T*)out,         \
+                       early_rows);                                                                                   \
   } while (0)
 #define PJRTX_ROWS_V(TAG, V)                                              \
   switch (op) {                                                           \
@@ -941,6 +1122,47 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
     hcheck(hipEventRecord(join, aux), "hipEventRecord(scatter join)");
     hcheck(hipStreamWaitEvent(s, join, 0), "hipStreamWaitEvent(scatter join)");
   }
+}
+
+void launch_scatter_early(hipStream_t aux, hipEvent_t selected, const ScatterEarly& e, const uint32_t* keys, int64_t n,
+                          uint32_t invalid, int64_t row_elems, int op_i, DType t, const void* operand,
+                          const void* updates, void* out) {
+  PJRTX_CHECK(n >= kEarlySample && e.blocks == scatter_early_blocks(n), Code::kInternal, "scatter early: bad sizes");
+  const ScatterOp op = static_cast<ScatterOp>(op_i);
+  hipLaunchKernelGGL(scatter_early_select, dim3(1), dim3(1024), 0, aux, keys, n, invalid, e.rows);
+  check("scatter_early_select");
+  hcheck(hipEventRecord(selected, aux), "hipEventRecord(scatter early selected)");
+  const dim3 gb(static_cast<unsigned>(e.blocks)), blk(256);
+  hipLaunchKernelGGL(scatter_early_count, gb, blk, 0, aux, keys, n, e.rows, e.counts, e.blocks);
+  exclusive_scan(aux, e.counts, e.offsets, kEarlyRows * e.blocks + 1, e.scan_tmp);
+  hipLaunchKernelGGL(scatter_early_write, gb, blk, 0, aux, keys, n, e.rows, e.offsets, e.blocks, e.list);
+  const size_t es = dtype_size(t);
+  const int64_t cols = kHotSliceBytes / static_cast<int64_t>(es);
+  const dim3 gf(static_cast<unsigned>(kEarlyRows * ((row_elems + cols - 1) / cols)));
+#define PJRTX_EARLY(TAG, OPV)                                                                                        \
+  hipLaunchKernelGGL((scatter_early_fold<TAG, OPV>), gf, blk, 0, aux, row_elems, (const StorageOf<TAG>::T*)operand, \
+                     (const StorageOf<TAG>::T*)updates, e.rows, e.offsets, e.blocks, e.list, (StorageOf<TAG>::T*)out)
+#define PJRTX_EARLY_T(TAG)                                          \
+  switch (op) {                                                     \
+    case ScatterOp::kAdd: PJRTX_EARLY(TAG, ScatterOp::kAdd); break; \
+    case ScatterOp::kSet: PJRTX_EARLY(TAG, ScatterOp::kSet); break; \
+    case ScatterOp::kMax: PJRTX_EARLY(TAG, ScatterOp::kMax); break; \
+    case ScatterOp::kMin: PJRTX_EARLY(TAG, ScatterOp::kMin); break; \
+    case ScatterOp::kMul: PJRTX_EARLY(TAG, ScatterOp::kMul); break; \
+  }
+  switch (t) {
+    case DType::kF32: PJRTX_EARLY_T(float) break;
+    case DType::kF64: PJRTX_EARLY_T(double) break;
+    case DType::kBF16: PJRTX_EARLY_T(Bf16Tag) break;
+    case DType::kF16: PJRTX_EARLY_T(F16Tag) break;
+    case DType::kS32: PJRTX_EARLY_T(int32_t) break;
+    case DType::kU32: PJRTX_EARLY_T(uint32_t) break;
+    case DType::kS64: PJRTX_EARLY_T(int64_t) break;
+    default: fail(Code::kUnimplemented, std::string("scatter: element type not supported: ") + dtype_name(t));
+  }
+#undef PJRTX_EARLY_T
+#undef PJRTX_EARLY
+  check("scatter_early_fold");
 }
 
 void launch_scatter_fold(hipStream_t s, const ScatterFoldParams& p, DType t, const void* operand, const void* updates,

@@ -158,6 +158,42 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   uint32_t* K = static_cast<uint32_t*>(keys->ptr);
   uint32_t* V = static_cast<uint32_t*>(vals_a->ptr);
   launch_scatter_keys(s, p, I, K, V);
+  // Early rows (the longest, found from a sample of the keys) are folded on
+  // the second stream while the keys are sorted (environment:
+  // PJRTX_SCATTER_EARLY=0 disables). Only where the hot rows fold in update
+  // order by 16-byte slices (the integer add / max / min chunks are exact in
+  // any order and need no early start).
+  const bool int_type = xt.dtype == DType::kS32 || xt.dtype == DType::kU32 || xt.dtype == DType::kS64;
+  const bool chunked = int_type && (sop == ScatterOp::kAdd || sop == ScatterOp::kMax || sop == ScatterOp::kMin);
+  const bool vec16 = (p.row_elems * static_cast<int64_t>(esz)) % 16 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(U) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  ScatterEarly early;
+  MemRef early_mem;
+  const bool use_early = p.row_mode && !chunked && vec16 && n >= (int64_t(1) << 16) && n < (int64_t(1) << 31) &&
+                         env_int("PJRTX_SCATTER_EARLY", 1) != 0;
+  if (use_early) {
+    early.blocks = scatter_early_blocks(n);
+    const int64_t words = (1 + kEarlyRows) + 2 * (kEarlyRows * early.blocks + 1) + 2 * n + 2048;
+    early_mem = dev->allocate(static_cast<size_t>(words) * 4);
+    uint32_t* w = static_cast<uint32_t*>(early_mem->ptr);
+    early.rows = w;
+    early.counts = early.rows + (1 + kEarlyRows);
+    early.offsets = early.counts + (kEarlyRows * early.blocks + 1);
+    early.scan_tmp = early.offsets + (kEarlyRows * early.blocks + 1);
+    early.list = early.scan_tmp + 2048;
+    uint32_t* keys_copy = early.list + n;
+    // The sort rewrites K in place: the early path reads its own copy, and
+    // the sort starts once the copy is taken.
+    hipStream_t aux = dev->aux_stream();
+    hip_check(hipEventRecord(dev->fork_event(), s), "hipEventRecord(scatter early fork)");
+    hip_check(hipStreamWaitEvent(aux, dev->fork_event(), 0), "hipStreamWaitEvent(scatter early fork)");
+    hip_check(hipMemcpyAsync(keys_copy, K, static_cast<size_t>(n) * 4, hipMemcpyDeviceToDevice, aux),
+              "hipMemcpyAsync(scatter early keys)");
+    hip_check(hipEventRecord(dev->side2_event(), aux), "hipEventRecord(scatter early keys)");
+    hip_check(hipStreamWaitEvent(s, dev->side2_event(), 0), "hipStreamWaitEvent(scatter early keys)");
+    launch_scatter_early(aux, dev->side_event(), early, keys_copy, n, p.invalid, p.row_elems,
+                         static_cast<int>(sop), xt.dtype, X, U, out);
+  }
   int bits = 1;
   while ((int64_t(1) << bits) <= rows) ++bits;  // keys are in [0, rows]
   launch_radix_sort(s, K, V, static_cast<uint32_t*>(tkeys->ptr), static_cast<uint32_t*>(tvals->ptr), scratch->ptr, n, bits);
@@ -178,6 +214,15 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
       const int64_t slices = (p.row_elems + cols - 1) / cols;
       const int64_t max_items = (n / (kHotMinUpdates + 1)) * slices;
       hot_wgs = std::min<int64_t>(max_items, 2 * static_cast<int64_t>(dev->compute_units()));
+    }
+    if (use_early) {
+      // classify and the bulk fold skip the early rows: wait for the list.
+      hip_check(hipStreamWaitEvent(s, dev->side_event(), 0), "hipStreamWaitEvent(scatter early selected)");
+      launch_scatter_rows(s, dev->aux2_stream(), dev->fork2_event(), dev->join2_event(), rows, p.row_elems,
+                          static_cast<int>(sop), xt.dtype, X, U, V, seg_start, seg_end, h, hot_wgs, out, early.rows);
+      hip_check(hipEventRecord(dev->join_event(), dev->aux_stream()), "hipEventRecord(scatter early join)");
+      hip_check(hipStreamWaitEvent(s, dev->join_event(), 0), "hipStreamWaitEvent(scatter early join)");
+      return;
     }
     launch_scatter_rows(s, dev->aux_stream(), dev->fork_event(), dev->join_event(), rows, p.row_elems,
                         static_cast<int>(sop), xt.dtype, X, U, V, seg_start, seg_end, h,

@@ -209,6 +209,51 @@ def test_scatter_add_long_segments_other_types(client, dtype):
     np.testing.assert_array_equal(out, want)
 
 
+@pytest.mark.parametrize("case", ["bf16_add", "f64_add", "f32_set", "f32_one_row", "f32_mostly_dropped"])
+def test_scatter_early_rows(client, case):
+    """Scatters of at least 65,536 updates fold their longest rows (picked from
+    a sample of the keys) while the keys are sorted, and the sorted path skips
+    them: other element types and combiners, every update on one row, and a
+    majority of dropped (out-of-bounds) updates, whose key fills most of the
+    sample but is never picked. Bit-exact against the sequential loop."""
+    rows, n = 128, 70000
+    rng = np.random.default_rng(21)
+    idx = ops.zipf_indices(n, rows, seed=21)
+    if case == "f32_one_row":
+        idx = np.zeros(n, np.int32)
+    if case == "f32_mostly_dropped":
+        drop = rng.random(n) < 0.6
+        idx = np.where(drop, rows + 7, idx).astype(np.int32)
+    if case == "bf16_add":
+        dim = 64
+        x = ops.f32_to_bf16_bits(rng.standard_normal((rows, dim)).astype(np.float32))
+        u = ops.f32_to_bf16_bits((0.01 * rng.standard_normal((n, dim))).astype(np.float32))
+        (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "bf16"), x, idx, u, dtypes=["bf16", None, "bf16"])
+        np.testing.assert_array_equal(out, ops.scatter_rows_add_bf16_bits(x, idx, u))
+    elif case == "f64_add":
+        dim = 16
+        x = rng.standard_normal((rows, dim))
+        u = rng.standard_normal((n, dim))
+        (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "f64"), x, idx, u)
+        np.testing.assert_array_equal(out, ops.scatter_rows_add(x, idx, u))
+    elif case == "f32_set":
+        dim = 32
+        x = rng.standard_normal((rows, dim)).astype(np.float32)
+        u = rng.standard_normal((n, dim)).astype(np.float32)
+        (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "f32", combiner="set"), x, idx, u)
+        want = x.copy()
+        rev = idx[::-1]
+        r, first = np.unique(rev, return_index=True)
+        want[r] = u[n - 1 - first]
+        np.testing.assert_array_equal(out, want)
+    else:
+        dim = 32
+        x = rng.standard_normal((rows, dim)).astype(np.float32)
+        u = rng.standard_normal((n, dim)).astype(np.float32)
+        (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "f32"), x, idx, u)
+        np.testing.assert_array_equal(out, ops.scatter_rows_add(x, idx, u))
+
+
 @pytest.mark.parametrize("dtype,combiner", [("s32", "maximum"), ("s32", "minimum"), ("u32", "add"),
                                             ("s64", "maximum")])
 def test_scatter_integer_long_segments_any_order_ops(client, dtype, combiner):
