@@ -731,33 +731,32 @@ __global__ void __launch_bounds__(1024) scatter_early_select(const uint32_t* __r
       }
       __syncthreads();
     }
+  // Run starts: the run's end by binary search (upper bound of its key).
   for (int i = tid; i < kEarlySample; i += 1024) {
-    if (i > 0 && sk[i - 1] == sk[i]) continue;  // not a run start
-    int e = i + 1;
-    while (e < kEarlySample && sk[e] == sk[i]) ++e;
-    if (e - i >= kEarlyMinRun && sk[i] != invalid) {
+    const uint32_t k = sk[i];
+    if ((i > 0 && sk[i - 1] == k) || k == invalid) continue;
+    int lo = i, hi = kEarlySample;  // first index past the run in [lo, hi]
+    while (lo + 1 < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sk[mid] == k) lo = mid;
+      else hi = mid;
+    }
+    if (hi - i >= kEarlyMinRun) {
       const uint32_t slot = atomicAdd(&ncand, 1u);
-      cand_row[slot] = sk[i];
-      cand_len[slot] = (uint32_t)(e - i);
+      cand_row[slot] = k;
+      cand_len[slot] = (uint32_t)(hi - i);
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    uint32_t count = 0;
-    bool taken[kEarlySample / kEarlyMinRun + 1] = {};
-    for (int j = 0; j < kEarlyRows; ++j) {
-      int best = -1;
-      for (uint32_t c = 0; c < ncand; ++c) {
-        if (taken[c]) continue;
-        if (best < 0 || cand_len[c] > cand_len[best] || (cand_len[c] == cand_len[best] && cand_row[c] < cand_row[best]))
-          best = (int)c;
-      }
-      if (best < 0) break;
-      taken[best] = true;
-      early[1 + count++] = cand_row[best];
-    }
-    early[0] = count;
+  // Rank among the candidates: longer first, then the smaller row.
+  const uint32_t nc = ncand;
+  if ((uint32_t)tid < nc) {
+    const uint32_t r = cand_row[tid], l = cand_len[tid];
+    uint32_t rank = 0;
+    for (uint32_t c = 0; c < nc; ++c) rank += (cand_len[c] > l || (cand_len[c] == l && cand_row[c] < r)) ? 1u : 0u;
+    if (rank < (uint32_t)kEarlyRows) early[1 + rank] = r;
   }
+  if (tid == 0) early[0] = nc < (uint32_t)kEarlyRows ? nc : (uint32_t)kEarlyRows;
 }
 
 // Per workgroup (kEarlyBlockItems consecutive keys, 16 a thread) and early
