@@ -77,9 +77,9 @@ struct ScatterHotList {
 // indices are then listed in update order by a count / scan / write pass
 // over the keys, and their slices folded like hot rows. The sorted path
 // skips these rows (classify and the bulk fold read the list).
-constexpr int kEarlyRows = 4;
+constexpr int kEarlyRows = 8;
 constexpr int kEarlySample = 4096;
-constexpr int kEarlyMinRun = 64;
+constexpr int kEarlyMinRun = 32;
 constexpr int kEarlyBlockItems = 4096;  // keys per count / write workgroup
 struct ScatterEarly {
   uint32_t* rows = nullptr;     // [1 + kEarlyRows]: count, then the rows
@@ -117,8 +117,9 @@ struct ScatterFoldParams {
   ScatterOp op = ScatterOp::kAdd;
 };
 
+// keys2, when not null, receives a second copy of the keys.
 void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* indices, uint32_t* keys,
-                         uint32_t* vals);
+                         uint32_t* vals, uint32_t* keys2 = nullptr);
 // seg_start/seg_end: `rows` uint32 each; they and `extra_zero` words after
 // seg_end are zeroed by this launcher.
 void launch_scatter_segments(hipStream_t s, const uint32_t* sorted_keys, int64_t n, uint32_t invalid,

@@ -46,7 +46,8 @@ __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int byte
 
 // ------------------------------------------------------------------- keys
 __global__ void __launch_bounds__(256) scatter_keys(ScatterKeyParams p, const void* __restrict__ indices,
-                                                    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+                                                    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                                                    uint32_t* __restrict__ keys2) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= p.items) return;
   const int64_t s = t / p.window_items;
@@ -97,6 +98,7 @@ __global__ void __launch_bounds__(256) scatter_keys(ScatterKeyParams p, const vo
   }
   keys[t] = key;
   vals[t] = val;
+  if (keys2) keys2[t] = key;
 }
 
 // ------------------------------------------------------------- radix sort
@@ -705,50 +707,50 @@ __global__ void __launch_bounds__(256) scatter_hot_fold(
 }
 
 // ---------------------------------------------------------------- early rows
-// Selection: kEarlySample keys at even strides sorted in LDS (bitonic); each
-// run of at least kEarlyMinRun equal keys (not the drop key) is a candidate;
-// the kEarlyRows longest (ties: smaller row) are listed, longest first.
+// Selection: kEarlySample keys at even strides counted in an LDS hash table
+// (open addressing, at most half full); every key (not the drop key) seen at
+// least kEarlyMinRun times is a candidate; the kEarlyRows most frequent
+// (ties: smaller row) are listed, most frequent first.
+constexpr int kEarlyTable = 2 * kEarlySample;
 __global__ void __launch_bounds__(1024) scatter_early_select(const uint32_t* __restrict__ keys, int64_t n,
                                                              uint32_t invalid, uint32_t* __restrict__ early) {
-  __shared__ uint32_t sk[kEarlySample];
+  __shared__ uint32_t hkey[kEarlyTable], hcnt[kEarlyTable];
   __shared__ uint32_t cand_row[kEarlySample / kEarlyMinRun + 1], cand_len[kEarlySample / kEarlyMinRun + 1];
   __shared__ uint32_t ncand;
   const int tid = threadIdx.x;
   if (tid == 0) ncand = 0;
-  for (int i = tid; i < kEarlySample; i += 1024) sk[i] = keys[(int64_t)i * n / kEarlySample];
+  for (int i = tid; i < kEarlyTable; i += 1024) {
+    hkey[i] = 0xffffffffu;
+    hcnt[i] = 0u;
+  }
+  uint32_t sample[kEarlySample / 1024];
+#pragma unroll
+  for (int q = 0; q < kEarlySample / 1024; ++q) sample[q] = keys[(int64_t)(tid + q * 1024) * n / kEarlySample];
   __syncthreads();
-  for (int k = 2; k <= kEarlySample; k <<= 1)
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < kEarlySample; i += 1024) {
-        const int l = i ^ j;
-        if (l > i) {
-          const uint32_t a = sk[i], b = sk[l];
-          if ((a > b) == ((i & k) == 0)) {
-            sk[i] = b;
-            sk[l] = a;
-          }
-        }
+#pragma unroll
+  for (int q = 0; q < kEarlySample / 1024; ++q) {
+    const uint32_t k = sample[q];
+    if (k == invalid || k == 0xffffffffu) continue;
+    uint32_t h = (k * 2654435761u) & (kEarlyTable - 1);
+    for (;;) {  // the table never fills: at most kEarlySample keys in 2 kEarlySample slots
+      const uint32_t old = atomicCAS(&hkey[h], 0xffffffffu, k);
+      if (old == 0xffffffffu || old == k) {
+        atomicAdd(&hcnt[h], 1u);
+        break;
       }
-      __syncthreads();
-    }
-  // Run starts: the run's end by binary search (upper bound of its key).
-  for (int i = tid; i < kEarlySample; i += 1024) {
-    const uint32_t k = sk[i];
-    if ((i > 0 && sk[i - 1] == k) || k == invalid) continue;
-    int lo = i, hi = kEarlySample;  // first index past the run in [lo, hi]
-    while (lo + 1 < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (sk[mid] == k) lo = mid;
-      else hi = mid;
-    }
-    if (hi - i >= kEarlyMinRun) {
-      const uint32_t slot = atomicAdd(&ncand, 1u);
-      cand_row[slot] = k;
-      cand_len[slot] = (uint32_t)(hi - i);
+      h = (h + 1) & (kEarlyTable - 1);
     }
   }
   __syncthreads();
-  // Rank among the candidates: longer first, then the smaller row.
+  for (int i = tid; i < kEarlyTable; i += 1024) {
+    if (hcnt[i] >= (uint32_t)kEarlyMinRun) {
+      const uint32_t slot = atomicAdd(&ncand, 1u);
+      cand_row[slot] = hkey[i];
+      cand_len[slot] = hcnt[i];
+    }
+  }
+  __syncthreads();
+  // Rank among the candidates: more samples first, then the smaller row.
   const uint32_t nc = ncand;
   if ((uint32_t)tid < nc) {
     const uint32_t r = cand_row[tid], l = cand_len[tid];
@@ -995,9 +997,10 @@ void launch_radix_sort(hipStream_t s, uint32_t* keys, uint32_t* vals, uint32_t* 
   check("radix_sort");
 }
 
-void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* indices, uint32_t* keys, uint32_t* vals) {
+void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* indices, uint32_t* keys, uint32_t* vals,
+                         uint32_t* keys2) {
   if (p.items == 0) return;
-  hipLaunchKernelGGL(scatter_keys, dim3(blocks(p.items, 256)), dim3(256), 0, s, p, indices, keys, vals);
+  hipLaunchKernelGGL(scatter_keys, dim3(blocks(p.items, 256)), dim3(256), 0, s, p, indices, keys, vals, keys2);
   check("scatter_keys");
 }
 

@@ -109,7 +109,6 @@ Device::Device(int ordinal) : ordinal_(ordinal), alloc_(ordinal) {
   hip_check(hipEventCreateWithFlags(&fork2_ev_, hipEventDisableTiming), "hipEventCreate(fork2)");
   hip_check(hipEventCreateWithFlags(&join2_ev_, hipEventDisableTiming), "hipEventCreate(join2)");
   hip_check(hipEventCreateWithFlags(&side_ev_, hipEventDisableTiming), "hipEventCreate(side)");
-  hip_check(hipEventCreateWithFlags(&side2_ev_, hipEventDisableTiming), "hipEventCreate(side2)");
   xcd_round_robin_ = env_int("PJRTX_XCD_LOCAL", 1) != 0 && probe_xcd_round_robin(stream_);
   hip_check(hipMalloc(reinterpret_cast<void**>(&counters_), kArrivalCounterBytes), "hipMalloc(counters)");
   hip_check(hipMemsetAsync(counters_, 0, kArrivalCounterBytes, stream_), "hipMemsetAsync(counters)");

@@ -127,13 +127,12 @@ class Device {
   hipEvent_t join_event() const { return join_ev_; }
   // A third stream (default priority) with its own fork / join events, for a
   // step that keeps work on the second stream while forking more, and one
-  // two events a step may record on a side stream for the main stream to
+  // an event a step may record on a side stream for the main stream to
   // wait on.
   hipStream_t aux2_stream() const { return aux2_stream_; }
   hipEvent_t fork2_event() const { return fork2_ev_; }
   hipEvent_t join2_event() const { return join2_ev_; }
   hipEvent_t side_event() const { return side_ev_; }
-  hipEvent_t side2_event() const { return side2_ev_; }
 
  private:
   std::vector<MemRef>* capture_pins_ = nullptr;
@@ -144,7 +143,7 @@ class Device {
   hipStream_t aux_stream_ = nullptr;
   hipEvent_t fork_ev_ = nullptr, join_ev_ = nullptr;
   hipStream_t aux2_stream_ = nullptr;
-  hipEvent_t fork2_ev_ = nullptr, join2_ev_ = nullptr, side_ev_ = nullptr, side2_ev_ = nullptr;
+  hipEvent_t fork2_ev_ = nullptr, join2_ev_ = nullptr, side_ev_ = nullptr;
   bool xcd_round_robin_ = false;
   uint32_t* counters_ = nullptr;
   Allocator alloc_;

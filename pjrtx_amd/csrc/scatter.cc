@@ -157,7 +157,6 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   MemRef seg = dev->allocate(static_cast<size_t>(rows) * 8 + 32 * 4);
   uint32_t* K = static_cast<uint32_t*>(keys->ptr);
   uint32_t* V = static_cast<uint32_t*>(vals_a->ptr);
-  launch_scatter_keys(s, p, I, K, V);
   // Early rows (the longest, found from a sample of the keys) are folded on
   // the second stream while the keys are sorted (environment:
   // PJRTX_SCATTER_EARLY=0 disables). Only where the hot rows fold in update
@@ -181,18 +180,17 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
     early.offsets = early.counts + (kEarlyRows * early.blocks + 1);
     early.scan_tmp = early.offsets + (kEarlyRows * early.blocks + 1);
     early.list = early.scan_tmp + 2048;
+    // The sort rewrites K in place: the early path reads its own copy of
+    // the keys, written by the same key kernel.
     uint32_t* keys_copy = early.list + n;
-    // The sort rewrites K in place: the early path reads its own copy, and
-    // the sort starts once the copy is taken.
+    launch_scatter_keys(s, p, I, K, V, keys_copy);
     hipStream_t aux = dev->aux_stream();
     hip_check(hipEventRecord(dev->fork_event(), s), "hipEventRecord(scatter early fork)");
     hip_check(hipStreamWaitEvent(aux, dev->fork_event(), 0), "hipStreamWaitEvent(scatter early fork)");
-    hip_check(hipMemcpyAsync(keys_copy, K, static_cast<size_t>(n) * 4, hipMemcpyDeviceToDevice, aux),
-              "hipMemcpyAsync(scatter early keys)");
-    hip_check(hipEventRecord(dev->side2_event(), aux), "hipEventRecord(scatter early keys)");
-    hip_check(hipStreamWaitEvent(s, dev->side2_event(), 0), "hipStreamWaitEvent(scatter early keys)");
     launch_scatter_early(aux, dev->side_event(), early, keys_copy, n, p.invalid, p.row_elems,
                          static_cast<int>(sop), xt.dtype, X, U, out);
+  } else {
+    launch_scatter_keys(s, p, I, K, V);
   }
   int bits = 1;
   while ((int64_t(1) << bits) <= rows) ++bits;  // keys are in [0, rows]
