@@ -73,7 +73,7 @@ struct GemvSpec {
   std::vector<int> add;     // per member: residual addend (result = add + round(dot)) or -1
   std::vector<bool> store;  // per member: the result is written to memory
   int cols = 64;            // columns per tile (8 lanes of 8 elements per row at 64)
-  int depth = 8;            // weight rows in flight per lane
+  int depth = 4;            // weight rows in flight per lane
   int64_t ksplit = 1;       // K chunks (workgroups per tile)
   int64_t kchunk = 0;       // rows per K chunk
   // Segments: the unit whose last workgroup folds the partials. Joint
