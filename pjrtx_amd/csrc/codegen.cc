@@ -1262,7 +1262,11 @@ void KernelGen::reduce(Step& s) {
       // No device-scope fence (an L2 write-back on this GPU) is needed, and
       // no workgroup waits for another. Otherwise (fused_mode 0) the
       // partials stay for the `_combine` kernel launched next.
-      out_ << "__shared__ uint32_t last_arrival;\n";
+      // Only wavefront 0 takes part from here: the other wavefronts leave,
+      // and lane 0's arrival verdict reaches its wavefront by readfirstlane
+      // (no LDS round trip, no barrier).
+      out_ << "if (threadIdx.x >= 64) return;\n";
+      out_ << "uint32_t last = 0u;\n";
       out_ << "if (threadIdx.x == 0) {\n";
       for (size_t r = 0; r < accs.size(); ++r) {
         const Accum& a = accs[r];
@@ -1273,7 +1277,6 @@ void KernelGen::reduce(Step& s) {
           out_ << "slot[" << slots << "u + row * " << s.splits << "u + split] = (uint64_t)" << a.i << ";\n";
         out_ << "}\n";
       }
-      out_ << "uint32_t last = 0u;\n";
       out_ << "if (fused_mode) {\n";
       out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
       // one counter per 128-byte line: rows do not contend for a line
@@ -1282,9 +1285,8 @@ void KernelGen::reduce(Step& s) {
            << "u;\n";
       out_ << "if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n";
       out_ << "}\n";
-      out_ << "last_arrival = last;\n";
-      out_ << "}\n__syncthreads();\n";
-      out_ << "if (!last_arrival || threadIdx.x >= 64) return;\n";
+      out_ << "}\n";
+      out_ << "if (!__builtin_amdgcn_readfirstlane(last)) return;\n";
       out_ << "const uint32_t lane = threadIdx.x;\n";
       fold_partials(true);
       epilogue_then_combine = true;
