@@ -1087,22 +1087,26 @@ size_t Executable::execute_noalloc(Device* dev, const void* const* args, size_t 
                         num_outs));
   PJRTX_CHECK(loops_.empty(), Code::kUnimplemented,
               "execute_noalloc: programs with a while loop are not supported (their regions load on first use)");
-  Loaded* L = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(mu_);
-    auto it = loaded_.find(dev->ordinal());
-    PJRTX_CHECK(it != loaded_.end(), Code::kFailedPrecondition,
-                strformat("execute_noalloc: the executable is not loaded on device %d (loading allocates)",
-                          dev->ordinal()));
-    L = it->second.get();
-  }
   for (size_t i = 0; i < num_args; ++i)
     PJRTX_CHECK(args[i] || prog_.type(prog_.params[i]).bytes() == 0, Code::kInvalidArgument,
                 strformat("execute_noalloc: argument %zu is null", i));
   for (size_t i = 0; i < num_outs; ++i)
     PJRTX_CHECK(outs[i] || prog_.type(prog_.results[i]).bytes() == 0, Code::kInvalidArgument,
                 strformat("execute_noalloc: output %zu is null", i));
+  // Same order as execute(): the device's execute lock first, then busy (so
+  // no other thread's load can evict this executable while it runs; busy
+  // also refreshes its last use for the residency budget), then the lookup.
   std::lock_guard<std::mutex> lk(dev->exec_mutex());
+  BusyScope busy(this, dev->ordinal());
+  Loaded* L = nullptr;
+  {
+    std::lock_guard<std::mutex> lk2(mu_);
+    auto it = loaded_.find(dev->ordinal());
+    PJRTX_CHECK(it != loaded_.end(), Code::kFailedPrecondition,
+                strformat("execute_noalloc: the executable is not loaded on device %d (loading allocates)",
+                          dev->ordinal()));
+    L = it->second.get();
+  }
   dev->make_current();
   Arena arena;
   arena.dev = dev;
