@@ -1278,6 +1278,11 @@ void KernelGen::reduce(Step& s) {
         out_ << "}\n";
       }
       out_ << "if (fused_mode) {\n";
+      // The workgroup-scope release fence keeps the compiler from moving the
+      // slot stores past the counter RMW (it emits a wait for them, no cache
+      // write-back); s_waitcnt(0) then has every store acknowledged by the
+      // XCD's L2 before the RMW reaches that same L2.
+      out_ << "__builtin_amdgcn_fence(__ATOMIC_RELEASE, \"workgroup\");\n";
       out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
       // one counter per 128-byte line: rows do not contend for a line
       out_ << "uint32_t* ctr = reinterpret_cast<uint32_t*>(scratch + " << s.counter_offset << "u) + row * 32u;\n";
@@ -1287,6 +1292,8 @@ void KernelGen::reduce(Step& s) {
       out_ << "}\n";
       out_ << "}\n";
       out_ << "if (!__builtin_amdgcn_readfirstlane(last)) return;\n";
+      // Keeps the fold's slot loads after the RMW that decided `last`.
+      out_ << "__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"workgroup\");\n";
       out_ << "const uint32_t lane = threadIdx.x;\n";
       fold_partials(true);
       epilogue_then_combine = true;
@@ -1948,6 +1955,10 @@ void KernelGen::gemv(Step& s) {
     out_ << "gv_part[((size_t)(c_seg * " << g.wps << "u + c_w) * " << M << "u + m) * " << C
          << "u + c] = ((gv_red[0][m][c] + gv_red[1][m][c]) + gv_red[2][m][c]) + gv_red[3][m][c];\n";
     out_ << "}\n";
+    // Release fence at workgroup scope: a compiler barrier between the
+    // partial stores and the counter RMW (no cache write-back); s_waitcnt(0)
+    // has the stores acknowledged by the XCD's L2 first.
+    out_ << "__builtin_amdgcn_fence(__ATOMIC_RELEASE, \"workgroup\");\n";
     out_ << "__builtin_amdgcn_s_waitcnt(0);\n";
     out_ << "if (!fused_mode) __threadfence();\n";
     out_ << "if (gv_lane == 0u) {\n";
@@ -1959,6 +1970,7 @@ void KernelGen::gemv(Step& s) {
     out_ << "gv_last = last;\n}\n}\n";
     out_ << "__syncthreads();\n";
     out_ << "if (gv_last) {\n";
+    out_ << "__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"workgroup\");\n";
     out_ << "if (!fused_mode) __threadfence();\n";
     if (g.joint) {
       out_ << "for (uint32_t i = threadIdx.x; i < " << G * M * S << "u; i += 256u) {\n";
