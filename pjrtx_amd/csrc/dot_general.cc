@@ -134,11 +134,7 @@ void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector
   const bool low_precision = lt.dtype == DType::kBF16 || lt.dtype == DType::kF16;
   const bool out_ok = ot.dtype == lt.dtype || ot.dtype == DType::kF32;
   if (K == 0) {  // empty contraction: zeros
-    const uint64_t zero = 0;
-    MemRef z = dev->allocate(8);
-    hip_check(hipMemcpyAsync(z->ptr, &zero, 8, hipMemcpyHostToDevice, dev->stream()), "hipMemcpyAsync");
-    launch_fill(dev->stream(), out, z->ptr, ot.elements(), static_cast<int>(dtype_size(ot.dtype)));
-    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    launch_zero(dev->stream(), out, ot.elements() * static_cast<int64_t>(dtype_size(ot.dtype)));
     return;
   }
   if (low_precision && out_ok) {

@@ -36,6 +36,10 @@ void launch_box_copy(hipStream_t s, const BoxCopy& p, const void* src, void* dst
 // Fills `n` elements of `dst` with the element at `value` (device pointer).
 void launch_fill(hipStream_t s, void* dst, const void* value, int64_t n, int elem_bytes);
 
+// Zeroes `bytes` bytes of `dst` with a kernel (no memset node, no host value:
+// safe under graph capture and in the allocation-free execute).
+void launch_zero(hipStream_t s, void* dst, int64_t bytes);
+
 // True when workgroup b of a launch runs on the same XCD as workgroup
 // b % 8 (the round-robin placement that XCD-local cooperation between the
 // workgroups of one launch relies on). Runs a probe kernel and waits.

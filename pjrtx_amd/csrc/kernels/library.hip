@@ -86,6 +86,11 @@ __global__ void __launch_bounds__(256) fill_kernel(T* __restrict__ dst, const T*
   if (i < n) dst[i] = value[0];
 }
 
+__global__ void __launch_bounds__(256) zero_bytes_kernel(uint8_t* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = 0;
+}
+
 struct GatherUnits {
   GatherParams g;
   int64_t total;          // output units
@@ -239,6 +244,13 @@ void launch_fill(hipStream_t s, void* dst, const void* value, int64_t n, int ele
     default: fail(Code::kInternal, "fill: bad element size");
   }
   check_launch("fill");
+}
+
+void launch_zero(hipStream_t s, void* dst, int64_t bytes) {
+  if (bytes == 0) return;
+  hipLaunchKernelGGL(zero_bytes_kernel, dim3(static_cast<unsigned>(blocks_for(bytes))), dim3(256), 0, s,
+                     (uint8_t*)dst, bytes);
+  check_launch("zero");
 }
 
 void launch_add(hipStream_t s, const void* a, const void* y, void* out, int64_t n, DType t) {

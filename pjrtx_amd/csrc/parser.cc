@@ -1579,22 +1579,6 @@ Op Parser::parse_op(const std::vector<std::string>& result_names, int count_hint
     if (op.pad_low.empty()) op.pad_low.assign(r, 0);
     if (op.pad_high.empty()) op.pad_high.assign(r, 0);
   }
-  if (op.kind == OpKind::kReduceWindow && !op.operands.empty()) {
-    // Defaults of the optional window attributes, and a splat padding.
-    const size_t r = prog_.values[op.operands[0]].type.dims.size();
-    auto ones = [&](Dims* d) {
-      if (d->empty()) d->assign(r, 1);
-    };
-    ones(&op.strides);
-    ones(&op.base_dilations);
-    ones(&op.window_dilations);
-    if (op.pad_low.size() == 1 && op.pad_high.size() == 1 && op.pad_high[0] == -(op.pad_low[0] + 1)) {
-      op.pad_high.assign(r, op.pad_low[0]);
-      op.pad_low.assign(r, op.pad_low[0]);
-    }
-    if (op.pad_low.empty()) op.pad_low.assign(r, 0);
-    if (op.pad_high.empty()) op.pad_high.assign(r, 0);
-  }
 
   // Deferred pieces that need the result type.
   if (have_dense) {
