@@ -139,8 +139,10 @@ PJRTX_HIP_API int pjrtx_executable_run(struct PJRT_LoadedExecutable* exe, struct
                                        size_t num_args, int iters, double* ms_total);
 
 /* Allocation-free execute. No counterpart in the reference: it is for
- * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc). Runs a compiled,
+ * callers that cannot allocate device memory while they run (tight serving
+ * loops, harnesses that forbid hipMalloc). Its launches record no memset
+ * and make no host-synchronizing call, but capturing them into a HIP graph
+ * is not tested. Runs a compiled,
  * loaded executable (PJRT_Client_Compile loads it on device 0) on
  * caller-owned device memory: args[i] and outputs[i] are device addresses of
  * the i-th parameter / result, dense row-major, of the program's sizes.
@@ -155,9 +157,11 @@ PJRTX_HIP_API int pjrtx_executable_run(struct PJRT_LoadedExecutable* exe, struct
  * hipFree and no allocating library routine; the work is queued on the
  * device's stream and the call returns without waiting
  * (pjrtx_hip_synchronize waits). Every call on one GPU shares that GPU's
- * block and finds the previous call's contents in it: calls queued from one
- * thread are ordered on the device stream, but work that overlaps a call on
- * the same GPU from another stream or process races on the block.
+ * block (one per process) and finds the previous call's contents in it.
+ * Calls on one GPU, from any thread, take the device's execute lock and
+ * queue their work on the one device stream, so they run one after another
+ * and never overlap on the block; work the caller queues on other streams
+ * never touches it.
  * `scratch_used` (may be NULL) gets the bytes of the block the call used. */
 PJRTX_HIP_API int pjrtx_executable_execute_noalloc(struct PJRT_LoadedExecutable* exe, int device,
                                                    const void* const* args, size_t num_args,
