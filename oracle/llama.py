@@ -200,3 +200,65 @@ def forward_f64(cfg, W: dict, tokens: np.ndarray) -> np.ndarray:
         g = h @ w("w1")
         x = x + ((g / (1 + np.exp(-g))) * (h @ w("w3"))) @ w("w2")
     return norm(x[-1], Wd["final_norm"]) @ Wd["lm_head"]
+
+
+class DecoderF64:
+    """Incremental float64 decode with float64 KV caches and no bf16 rounding:
+    the exact model (the same arithmetic as `forward_f64`) evaluated one
+    program execution at a time, so that every step of a long decode can be
+    compared with the exact logits without recomputing the whole prefix.
+    `step(tokens)` runs tokens at the next positions (the prompt as one call,
+    then one token per call) and returns the last position's logits.
+
+    Pinned by tests/test_oracle_llama.py: after a prefill and each decode
+    step its logits equal `forward_f64` over the whole prefix (float64
+    rounding only)."""
+
+    def __init__(self, cfg, W: dict):
+        self.cfg = cfg
+        self.Wd = {k: v.astype(np.float64) for k, v in W.items()}
+        H, D = cfg.heads, cfg.head_dim
+        self.k = [np.zeros((cfg.max_len, H, D)) for _ in range(cfg.layers)]
+        self.v = [np.zeros((cfg.max_len, H, D)) for _ in range(cfg.layers)]
+        self.n = 0
+        half = D // 2
+        self.inv = cfg.theta ** (-np.arange(half) * 2.0 / D)
+
+    def step(self, tokens) -> np.ndarray:
+        cfg, Wd = self.cfg, self.Wd
+        tokens = np.asarray(tokens)
+        T = len(tokens)
+        H, D = cfg.heads, cfg.head_dim
+        half = D // 2
+        p0 = self.n
+        assert p0 + T <= cfg.max_len, "the exact decoder has no clamped positions"
+        pos = np.arange(p0, p0 + T)
+        rot = np.exp(1j * pos[:, None] * self.inv[None, :])                     # [T, half]
+        x = Wd["embed"][tokens % cfg.vocab]
+
+        def norm(v, g):
+            return v / np.sqrt(np.mean(v * v, axis=-1, keepdims=True) + cfg.eps) * g
+
+        def rope_c(a):
+            z = (a[..., :half] + 1j * a[..., half:]) * rot[:, None, :]
+            return np.concatenate([z.real, z.imag], -1)
+
+        L = p0 + T
+        allowed = np.arange(L)[None, :] <= pos[:, None]                          # [T, L]
+        for layer in range(cfg.layers):
+            w = lambda n: Wd[f"l{layer}.{n}"]  # noqa: E731
+            h = norm(x, w("attn_norm"))
+            q = rope_c((h @ w("wq")).reshape(T, H, D))
+            self.k[layer][p0:L] = rope_c((h @ w("wk")).reshape(T, H, D))
+            self.v[layer][p0:L] = (h @ w("wv")).reshape(T, H, D)
+            s = np.einsum("qhd,khd->hqk", q, self.k[layer][:L]) / np.sqrt(D)
+            s = np.where(allowed[None], s, -np.inf)
+            p = np.exp(s - s.max(-1, keepdims=True))
+            p /= p.sum(-1, keepdims=True)
+            ctx = np.einsum("hqk,khd->qhd", p, self.v[layer][:L]).reshape(T, H * D)
+            x = x + ctx @ w("wo")
+            h = norm(x, w("ffn_norm"))
+            g = h @ w("w1")
+            x = x + ((g / (1 + np.exp(-g))) * (h @ w("w3"))) @ w("w2")
+        self.n = L
+        return norm(x[-1], Wd["final_norm"]) @ Wd["lm_head"]

@@ -118,11 +118,12 @@ def test_c2_shape_winner_everywhere(client):
     check(client, bits, "max")
 
 
-@pytest.mark.parametrize("rows,n", [(64, 128256), (24, 50000)])
+@pytest.mark.parametrize("rows,n", [(64, 128256), (24, 50000), (5, 50000), (1, 128256), (13, 9000)])
 def test_fused_combine_matches_combine_kernel(client, monkeypatch, rows, n):
     """Split rows folded by the last-arriving workgroup of each row (the
-    default when the row count is a multiple of 8: every split of a row runs
-    on one XCD) give the same bits as the separate combine kernel
+    default: every split of a row runs on one XCD; a row count that is not a
+    multiple of 8 gets a padded grid whose extra workgroups leave at once)
+    give the same bits as the separate combine kernel
     (PJRTX_REDUCE_FUSED_COMBINE=0), on every one of several back-to-back
     executions (the per-row arrival counters are put back to zero by each
     launch), for the argmax, f16 sum, max and min of the benchmark's program."""
@@ -143,3 +144,20 @@ def test_fused_combine_matches_combine_kernel(client, monkeypatch, rows, n):
         assert len(got) == len(want)
         for g, w in zip(got, want):
             np.testing.assert_array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8))
+
+
+@pytest.mark.parametrize("rows,n", [(64, 128256), (5, 50000)])
+def test_combine_fallback_without_xcd_placement(client, run_fresh, rows, n):
+    """With the XCD placement probe disabled (PJRTX_XCD_LOCAL=0, read once per
+    process) split reductions run the main kernel plus the `_combine`
+    kernel; the C2 program's results are the same bits as the default
+    one-launch fold."""
+    from pjrtx_amd import programs
+    bits = ops.f32_to_bf16_bits(np.random.default_rng(23).standard_normal((rows, n)).astype(np.float32))
+    text = programs.c2_argmax_f16_reductions(rows, n)
+    want = client.compile(text)(bits, dtypes=["bf16"])
+    other = run_fresh(text, [bits], ["bf16"], {"PJRTX_XCD_LOCAL": "0"})
+    assert len(other) == len(want)
+    for g, w in zip(other, want):
+        np.testing.assert_array_equal(np.asarray(g).view(np.uint8), np.asarray(w).view(np.uint8))
+    np.testing.assert_array_equal(want[1], ops.argmax_rows(ops.bf16_bits_to_f32(bits))[1])

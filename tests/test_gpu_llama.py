@@ -146,12 +146,17 @@ def test_full_prefill_and_decode_match_oracle(full):
 
 
 def test_full_decode_128_steps_teacher_forced(full):
-    """All 128 decode steps of C5 at full size, teacher-forced: at every step
-    the GPU's logits are within twice the bar of the bf16 restatement fed the
-    same tokens, the GPU's token is the argmax of its own logits, and it
-    differs from the restatement's argmax only where the restatement's top-2
-    margin is within that bar. The steps where it differs are printed (and
-    recorded in the design notes)."""
+    """All 128 decode steps of C5 at full size, teacher-forced with the GPU's
+    tokens, each held to the bar against the exact model: the incremental
+    float64 decoder (float64 caches, no bf16 rounding; oracle.DecoderF64).
+    At every step the GPU's distance from the exact logits may exceed the
+    north_star bar (2e-2 of the logit range, and 2e-2 relative L2) only as
+    far as the faithful bf16 restatement's own distance does, by at most 20%
+    (the same rule as the prefill test above); the GPU stays within twice the
+    bar of the bf16 restatement; its token is the argmax of its own logits;
+    and it equals the exact model's argmax wherever the exact top-2 margin is
+    wider than twice the bar. The steps where the GPU's token differs from
+    the exact argmax are printed (all inside the margin)."""
     runner, wbits = full
     cfg = L.FULL
     W = O.weights_f32(cfg, wbits)
@@ -159,18 +164,27 @@ def test_full_decode_128_steps_teacher_forced(full):
     steps = cfg.new_tokens
     toks, _, logits = runner.generate(prompt, steps, keep_logits=True)
     _, ora_logits = O.generate(cfg, W, prompt, steps, forced=toks[:-1])
-    flips = []
+    dec = O.DecoderF64(cfg, W)
+    flips, worst = [], (0.0, 0.0)
     for i in range(steps):
+        exact = dec.step(prompt if i == 0 else [int(toks[i - 1])])
         g = O.bf16_bits_to_f32(logits[i])[0].astype(np.float64)
-        ref = np.asarray(ora_logits[i], np.float64)
-        scale = float(np.abs(ref).max())
-        assert np.abs(g - ref).max() <= 2 * TOL * scale, (i, np.abs(g - ref).max(), scale)
+        lg = np.asarray(ora_logits[i], np.float64)
+        scale = float(np.abs(exact).max())
+        norm = float(np.linalg.norm(exact))
+        gpu_max, ora_max = np.abs(g - exact).max(), np.abs(lg - exact).max()
+        gpu_l2, ora_l2 = np.linalg.norm(g - exact) / norm, np.linalg.norm(lg - exact) / norm
+        assert gpu_max <= max(TOL * scale, 1.2 * ora_max), (i, gpu_max, ora_max, scale)
+        assert gpu_l2 <= max(TOL, 1.2 * ora_l2), (i, gpu_l2, ora_l2)
+        assert np.abs(g - lg).max() <= 2 * TOL * scale, (i, np.abs(g - lg).max(), scale)
         assert int(toks[i]) == int(np.argmax(g))
-        if int(toks[i]) != int(np.argmax(ref)):
-            top = np.sort(ref)[::-1]
+        worst = (max(worst[0], gpu_max / scale), max(worst[1], gpu_l2))
+        if int(toks[i]) != int(np.argmax(exact)):
+            top = np.sort(exact)[::-1]
             assert top[0] - top[1] <= 2 * TOL * scale, (i, top[:2])
             flips.append(i)
-    print(f"C5 128-step teacher-forced greedy flips (margin-exempt): {flips}")
+    print(f"C5 128 steps vs float64: worst max error {worst[0]:.4f} of the logit range, worst relative L2 "
+          f"{worst[1]:.4f}; steps where the GPU's token is not the exact argmax (margin-exempt): {flips}")
 
 
 def test_full_decode_step_equals_longer_prefill(full, client):

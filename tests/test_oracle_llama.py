@@ -115,3 +115,23 @@ def test_greedy_generate_follows_argmax_and_teacher_forcing():
     np.testing.assert_array_equal(toks2, toks)
     for a, b in zip(logits, logits2):
         np.testing.assert_array_equal(a, b)
+
+
+def test_incremental_float64_decoder_equals_full_recompute():
+    """The incremental float64 decoder (caches in float64) gives, after the
+    prefill and after each decode step, the logits of `forward_f64` over the
+    whole prefix: an independent full recompute (float64 rounding only)."""
+    W = _weights()
+    prompt = L.prompt_tokens(CFG, seed=6)
+    dec = O.DecoderF64(CFG, W)
+    seen = list(prompt)
+    got = dec.step(prompt)
+    np.testing.assert_allclose(got, O.forward_f64(CFG, W, np.array(seen)), rtol=0, atol=1e-10)
+    rng = np.random.default_rng(8)
+    for _ in range(CFG.max_len - len(prompt)):
+        t = int(rng.integers(0, CFG.vocab))
+        got = dec.step([t])
+        seen.append(t)
+        want = O.forward_f64(CFG, W, np.array(seen))
+        np.testing.assert_allclose(got, want, rtol=0, atol=1e-10 * max(1.0, np.abs(want).max()))
+    assert dec.n == CFG.max_len
