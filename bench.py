@@ -4,7 +4,7 @@ A step is one PJRT execute of a workload's compiled StableHLO program on
 device-resident inputs (synthetic, seeded). Workloads (`--config`), after
 BASELINE.json's configs:
 
-  c2       (default, configs[1]) two-output max/index argmax over bf16
+  c2       (configs[1]) two-output max/index argmax over bf16
            logits [64,128256] plus f16 sum/max/min of logits.astype(f16)
   c1       configs[0]: f32 elementwise chain + row sum, [4096,4096]
   c3mm     configs[2]: plain bf16 matmul [8192,8192] x [8192,8192]
@@ -17,6 +17,10 @@ BASELINE.json's configs:
   topk     lax.top_k(logits, 50) over [64,128256] bf16 (sort row, not a
            BASELINE config)
   copy     counter calibration stream (not a bench line)
+
+With no --config (the driver's run) the line's value is c2's, and the c5
+decode (tokens/s, 128 greedy tokens) and c1 lines are measured in the same
+process and carried in it as "c5" and "c1" objects.
 
 Prints one JSON line: the whole-job rate, the dominant kernel's roofline
 (HIP-event timed per launch on the plugin's stream) and, unless
@@ -467,10 +471,12 @@ def bench_program(a, W: Workload) -> dict:
     return line
 
 
-def bench_c5(a) -> dict:
+def bench_c5(a, extras: bool = True) -> dict:
     """C5: greedy decode of the llama-like model. A step is one decode token
     (one PJRT execute of the decode program, caches donated). Prefill of the
-    512-token prompt is timed separately and reported in `config`."""
+    512-token prompt is timed separately and reported in `config`. `extras`
+    adds the forced-graph and one-execute (on-device loop) rates beside the
+    per-token one."""
     import numpy as np
     from pjrtx_amd import llama_like as L
     from pjrtx_amd.pjrt import Client
@@ -518,7 +524,7 @@ def bench_c5(a) -> dict:
     # plans, and this one runs eagerly. Skipped when the caller set
     # PJRTX_GRAPHS (profiling runs keep graphs off).
     graph_ms = None
-    if "PJRTX_GRAPHS" not in os.environ:
+    if extras and "PJRTX_GRAPHS" not in os.environ:
         os.environ["PJRTX_GRAPHS"] = "2"
         try:
             tok_e, _, caches_e = runner.start(prompt)
@@ -537,17 +543,19 @@ def bench_c5(a) -> dict:
 
     # All decode steps in one execute: the step inside an on-device while
     # loop over a constant count (compiled and warmed before timing).
-    looped = client.compile(L.generate_program(cfg, steps))
-    tok_l, _, caches_l = runner.start(prompt)
-    looped.execute_buffers(runner.weights + [tok_l, pos_bufs[0]] + caches_l)[0].block_until_ready()
-    tok_l, _, caches_l = runner.start(prompt)
-    tok_l.block_until_ready()
-    t0 = time.perf_counter()
-    outs_l = looped.execute_buffers(runner.weights + [tok_l, pos_bufs[0]] + caches_l)
-    outs_l[0].block_until_ready()
-    loop_ms = (time.perf_counter() - t0) * 1e3 / steps
-    loop_match = [int(x) for x in outs_l[0].to_numpy()] == tokens[1:]
-    del outs_l, caches_l
+    loop_ms, loop_match = None, None
+    if extras:
+        looped = client.compile(L.generate_program(cfg, steps))
+        tok_l, _, caches_l = runner.start(prompt)
+        looped.execute_buffers(runner.weights + [tok_l, pos_bufs[0]] + caches_l)[0].block_until_ready()
+        tok_l, _, caches_l = runner.start(prompt)
+        tok_l.block_until_ready()
+        t0 = time.perf_counter()
+        outs_l = looped.execute_buffers(runner.weights + [tok_l, pos_bufs[0]] + caches_l)
+        outs_l[0].block_until_ready()
+        loop_ms = round((time.perf_counter() - t0) * 1e3 / steps, 4)
+        loop_match = [int(x) for x in outs_l[0].to_numpy()] == tokens[1:]
+        del outs_l, caches_l
 
     plan = json.loads(runner.decode.optimized_program())
     units = launch_units(plan)
@@ -570,7 +578,7 @@ def bench_c5(a) -> dict:
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init bf16 weights 0.02*N(0,1) seed 0, random 512-token prompt seed 1)",
-        "config": {"workload": "llama_like_decode_8L_d2048_h16x128_ffn5632_v32000_prompt512",
+        "config": {"workload": C5_WORKLOAD,
                    "prefill_ms": round(prefill_s * 1e3, 3), "prefill_tokens_per_s": round(p / prefill_s, 1),
                    "setup_s": round(setup_s, 1), "weights_upload_ms": round(upload_s * 1e3, 1),
                    "weights_upload_gbps": round(upload_bytes / upload_s / 1e9, 1), "decode_step_hbm_bytes": step_bytes,
@@ -579,16 +587,44 @@ def bench_c5(a) -> dict:
                    "gpu_us_per_step_by_kind": {kk: round(v, 2) for kk, v in sorted(by_kind.items())},
                    "gpu_us_per_step": round(sum(unit_ms) * 1e3, 2), "first_tokens": tokens[:8],
                    "graph": graph_stats, "all_graphs_ms_per_step": graph_ms,
-                   "one_execute_ms_per_step": round(loop_ms, 4), "one_execute_tokens_match": loop_match},
-        "roofline": roofline(units, unit_ms, names, "bf16",
-                             "llama_like_decode_8L_d2048_h16x128_ffn5632_v32000_prompt512"),
+                   "one_execute_ms_per_step": loop_ms, "one_execute_tokens_match": loop_match},
+        "roofline": roofline(units, unit_ms, names, "bf16", C5_WORKLOAD),
     }
+    line["roofline"]["traffic"] = traffic_from_profiles(C5_WORKLOAD, line["roofline"]["kernel"])
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_c5(cfg, weights, prompt, tokens)
     return line
 
 
-def cpu_baseline_c5(cfg, weights, prompt, tokens, budget_s: float = 15.0) -> dict:
+C5_WORKLOAD = "llama_like_decode_8L_d2048_h16x128_ffn5632_v32000_prompt512"
+
+# Keys of a secondary workload's line carried into the default run's line.
+SUB_KEYS = ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "higher_is_better", "dtype", "data",
+            "config", "roofline", "cpu_baseline")
+
+
+def bench_default(a) -> dict:
+    """The driver's run (no --config): the headline C2 line (BASELINE.json
+    configs[1], the fused-reduction half of the metric) with two more
+    workloads measured in the same process and carried in the same JSON line:
+    `c5`, the llama-like decode tokens/s (the metric's other half; always the
+    config's 128 greedy tokens after the 512-token prompt, whatever --steps
+    says), and `c1` (configs[0], the fused elementwise chain + row sum, timed
+    over --steps executes). Each carries its own roofline (with the committed
+    rocprof figure and HBM traffic) and CPU baseline."""
+    import copy
+    line = bench_program(a, WORKLOADS["c2"])
+    sub1 = bench_program(copy.copy(a), WORKLOADS["c1"])
+    line["c1"] = {k: sub1[k] for k in SUB_KEYS if k in sub1}
+    a5 = copy.copy(a)
+    a5.steps = 128
+    a5.warmup = min(a.warmup, 10)
+    sub5 = bench_c5(a5, extras=False)
+    line["c5"] = {k: sub5[k] for k in SUB_KEYS if k in sub5}
+    return line
+
+
+def cpu_baseline_c5(cfg, weights, prompt, tokens, budget_s: float = 10.0) -> dict:
     """The numpy oracle decoding the same prompt (teacher-forced with the GPU's
     tokens) on this host, for about `budget_s` seconds of decode steps."""
     import numpy as np
@@ -613,19 +649,23 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; c3/c4 20; c5 128 tokens)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", choices=sorted(WORKLOADS) + ["c5"], default="c2")
+    ap.add_argument("--config", choices=sorted(WORKLOADS) + ["c5"], default=None,
+                    help="one workload; default: c2 as the line's value, with c5 and c1 carried in the same line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); "
               "multi-GPU sharding is design-only", file=sys.stderr)
         return 2
-    heavy = a.config.startswith(("c3", "c4"))
+    heavy = (a.config or "").startswith(("c3", "c4"))
     if a.steps is None:
         a.steps = 128 if a.config == "c5" else (20 if heavy else 200)
     if a.warmup is None:
         a.warmup = 10
-    line = bench_c5(a) if a.config == "c5" else bench_program(a, WORKLOADS[a.config])
+    if a.config is None:
+        line = bench_default(a)
+    else:
+        line = bench_c5(a) if a.config == "c5" else bench_program(a, WORKLOADS[a.config])
     print(json.dumps(line))
     return 0
 
