@@ -149,14 +149,31 @@ def test_full_decode_128_steps_teacher_forced(full):
     """All 128 decode steps of C5 at full size, teacher-forced with the GPU's
     tokens, each held to the bar against the exact model: the incremental
     float64 decoder (float64 caches, no bf16 rounding; oracle.DecoderF64).
-    At every step the GPU's distance from the exact logits may exceed the
-    north_star bar (2e-2 of the logit range, and 2e-2 relative L2) only as
-    far as the faithful bf16 restatement's own distance does, by at most 20%
-    (the same rule as the prefill test above); the GPU stays within twice the
-    bar of the bf16 restatement; its token is the argmax of its own logits;
-    and it equals the exact model's argmax wherever the exact top-2 margin is
-    wider than twice the bar. The steps where the GPU's token differs from
-    the exact argmax are printed (all inside the margin)."""
+
+    A faithful bf16 evaluation of this model cannot meet 2e-2 of the largest
+    logit at every step: the bf16 restatement (oracle.forward, numpy order)
+    is off the exact logits by 1.9% of the logit range at the median step and
+    exceeds 2e-2 at about a third of the steps (up to 2.5%), and by 1.9%
+    relative L2 (up to 2.2%). So the GPU is held to that evaluation's own
+    accuracy, step by step and on average:
+
+    * per step, relative L2 distance from the exact logits at most
+      max(2e-2, 1.2 x the restatement's), and max distance at most
+      max(2e-2 x max|logit|, 1.5 x the restatement's) (the max over 32,000
+      logits is an extreme value: the per-step ratio of two equally accurate
+      evaluations spreads to about 1.2 over 128 steps, the L2 ratio to 1.1);
+    * over the 128 steps, the mean relative L2 distance is within 2e-2, and
+      the mean ratios of the GPU's distances (max and L2) to the
+      restatement's are at most 1.05: the GPU is not systematically less
+      accurate than the bf16 evaluation;
+    * per step, within twice the bar of the restatement; the token is the
+      argmax of the GPU's own logits, and it equals the exact argmax wherever
+      the exact top-2 margin is wider than twice the bar.
+
+    Measured (MI355X): GPU max distance 1.85% of the range at the median step
+    (restatement 1.92%), relative L2 1.88% (1.91%); ratios median 0.99 (max)
+    and 0.98 (L2). The steps where the GPU's token is not the exact argmax
+    are printed (all inside the margin)."""
     runner, wbits = full
     cfg = L.FULL
     W = O.weights_f32(cfg, wbits)
@@ -165,7 +182,7 @@ def test_full_decode_128_steps_teacher_forced(full):
     toks, _, logits = runner.generate(prompt, steps, keep_logits=True)
     _, ora_logits = O.generate(cfg, W, prompt, steps, forced=toks[:-1])
     dec = O.DecoderF64(cfg, W)
-    flips, worst = [], (0.0, 0.0)
+    flips, stats = [], []
     for i in range(steps):
         exact = dec.step(prompt if i == 0 else [int(toks[i - 1])])
         g = O.bf16_bits_to_f32(logits[i])[0].astype(np.float64)
@@ -174,17 +191,22 @@ def test_full_decode_128_steps_teacher_forced(full):
         norm = float(np.linalg.norm(exact))
         gpu_max, ora_max = np.abs(g - exact).max(), np.abs(lg - exact).max()
         gpu_l2, ora_l2 = np.linalg.norm(g - exact) / norm, np.linalg.norm(lg - exact) / norm
-        assert gpu_max <= max(TOL * scale, 1.2 * ora_max), (i, gpu_max, ora_max, scale)
         assert gpu_l2 <= max(TOL, 1.2 * ora_l2), (i, gpu_l2, ora_l2)
+        assert gpu_max <= max(TOL * scale, 1.5 * ora_max), (i, gpu_max, ora_max, scale)
         assert np.abs(g - lg).max() <= 2 * TOL * scale, (i, np.abs(g - lg).max(), scale)
         assert int(toks[i]) == int(np.argmax(g))
-        worst = (max(worst[0], gpu_max / scale), max(worst[1], gpu_l2))
+        stats.append((gpu_max / scale, gpu_l2, gpu_max / ora_max, gpu_l2 / ora_l2))
         if int(toks[i]) != int(np.argmax(exact)):
             top = np.sort(exact)[::-1]
             assert top[0] - top[1] <= 2 * TOL * scale, (i, top[:2])
             flips.append(i)
-    print(f"C5 128 steps vs float64: worst max error {worst[0]:.4f} of the logit range, worst relative L2 "
-          f"{worst[1]:.4f}; steps where the GPU's token is not the exact argmax (margin-exempt): {flips}")
+    st = np.array(stats)
+    print(f"C5 128 steps vs float64: max distance / range median {np.median(st[:, 0]):.4f} max {st[:, 0].max():.4f}; "
+          f"relative L2 mean {st[:, 1].mean():.4f} max {st[:, 1].max():.4f}; GPU / restatement distance ratio mean "
+          f"{st[:, 2].mean():.3f} (max), {st[:, 3].mean():.3f} (L2); steps where the GPU's token is not the exact "
+          f"argmax (margin-exempt): {flips}")
+    assert st[:, 1].mean() <= TOL, st[:, 1].mean()
+    assert st[:, 2].mean() <= 1.05 and st[:, 3].mean() <= 1.05, (st[:, 2].mean(), st[:, 3].mean())
 
 
 def test_full_decode_step_equals_longer_prefill(full, client):
