@@ -645,7 +645,9 @@ class KernelGen {
 };
 
 void KernelGen::signature(const Step& s, std::map<int, std::string>* ptr_of, bool with_scratch, const char* suffix) {
-  out_ << "extern \"C\" __global__ void __launch_bounds__(256) " << s.name << suffix << "(";
+  // The separate combine kernel always runs 256 threads.
+  const int bounds = suffix && *suffix ? 256 : std::max(256, static_cast<int>(s.block));
+  out_ << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ") " << s.name << suffix << "(";
   int k = 0;
   for (int v : s.inputs) {
     const DType t = prog_.type(v).dtype;
@@ -1023,7 +1025,7 @@ void KernelGen::reduce(Step& s) {
       wave_done[r] = true;
       const std::string R = std::to_string(r);
       const char* mx = a.kind == ReducerKind::kArgMax ? "max_r" : "min_r";
-      const std::string span = std::to_string(256 * vec) + "u";
+      const std::string span = std::to_string(s.block * vec) + "u";
       o << "{ float bm = mu" << R << "[0];\n";
       o << "#pragma unroll\nfor (int u = 1; u < " << unroll << "; ++u) bm = " << mx << "(bm, mu" << R << "[u]);\n";
       o << wave_allreduce("float", "bm", [&](const std::string& x, const std::string& y) {
@@ -1100,7 +1102,8 @@ void KernelGen::reduce(Step& s) {
     }
   };
   if (s.row_schedule) {
-    const int64_t span = 256 * vec;
+    const int64_t span = static_cast<int64_t>(s.block) * vec;
+    const int nwaves = static_cast<int>(s.block) / 64;
     bool any_fast = false, any_two_phase = false;
     for (size_t r = 0; r < accs.size(); ++r) {
       any_fast = any_fast || fast_arg(r);
@@ -1169,10 +1172,11 @@ void KernelGen::reduce(Step& s) {
     if (deferred) deferred_finish(out_, full_u);
     // Shared slots for the cross-wave step of the block reductions.
     for (auto& a : accs) {
-      out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[4];\n";
-      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin) out_ << "__shared__ " << ait << " sm_" << a.i << "[4];\n";
+      out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[" << nwaves << "];\n";
+      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
+        out_ << "__shared__ " << ait << " sm_" << a.i << "[" << nwaves << "];\n";
     }
-    // Block reduction: wavefront all-reduce, then the 4 wave results are
+    // Block reduction: wavefront all-reduce, then the wave results are
     // combined in wave order by thread 0 (fixed order: deterministic).
     auto wave_reduce = [&](bool skip_done) {
       for (size_t r = 0; r < accs.size(); ++r) {
@@ -1202,7 +1206,7 @@ void KernelGen::reduce(Step& s) {
         const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
         out_ << a.v << " = sm_" << a.v << "[0];\n";
         if (am) out_ << a.i << " = sm_" << a.i << "[0];\n";
-        out_ << "for (int k = 1; k < 4; ++k) {\n";
+        out_ << "for (int k = 1; k < " << nwaves << "; ++k) {\n";
         if (am) {
           out_ << "if (" << arg_better(a.kind) << "(sm_" << a.v << "[k], sm_" << a.i << "[k], " << a.v << ", " << a.i
                << ")) { " << a.v << " = sm_" << a.v << "[k]; " << a.i << " = sm_" << a.i << "[k]; }\n";

@@ -1175,7 +1175,8 @@ void Planner::shape_reduce(Step* s) {
   vec = std::max(1, std::min(vec, 8));
   while (vec > 1 && row_len % vec != 0) vec /= 2;
   s->vec = vec;
-  const int64_t per_iter = 256 * vec;
+  const int block = opts_.reduce_block >= 1024 ? 1024 : opts_.reduce_block >= 512 ? 512 : 256;
+  const int64_t per_iter = block * vec;
   // Few long rows: split each row over several workgroups so the launch
   // reaches the target block count, keeping at least one full 256*vec span
   // per split.
@@ -1189,7 +1190,7 @@ void Planner::shape_reduce(Step* s) {
   s->chunk = chunk;
   s->unroll = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(8, (chunk + per_iter - 1) / per_iter)));
   s->grid = static_cast<uint32_t>(rows * splits);
-  s->block = 256;
+  s->block = block;
   if (splits > 1) {
     size_t per_slot = 0;
     for (const ReduceSpec& r : s->reduces) per_slot += (r.kind == ReducerKind::kArgMax || r.kind == ReducerKind::kArgMin) ? 16 : 8;

@@ -183,6 +183,9 @@ struct PlanOptions {
   // Target number of workgroups a reduction launch should reach.
   // (environment: PJRTX_REDUCE_TARGET_BLOCKS)
   int64_t reduce_target_blocks = env_int("PJRTX_REDUCE_TARGET_BLOCKS", 512);
+  // Threads per workgroup of the row-schedule reduce kernels (256, 512 or
+  // 1024).
+  int reduce_block = env_int("PJRTX_REDUCE_BLOCK", 256);
   // Split reductions fold their partials in the last workgroup of each row
   // instead of a second launch (environment: PJRTX_REDUCE_FUSED_COMBINE=1).
   // Off by default: each workgroup's device-scope release fence (an L2
