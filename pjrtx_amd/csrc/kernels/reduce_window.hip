@@ -1,13 +1,18 @@
 // stablehlo.reduce_window: one thread per output element folds its window in
 // row-major window order, starting from the init value, with padding
-// positions contributing the init value (StableHLO's padded-input
-// definition). Float windows fold sequentially in that order, the order a
-// sequential CPU evaluation uses, so f32 sums equal it bit for bit; 16-bit
-// floats accumulate in f32 and round once.
+// positions and base-dilation holes contributing the init value (StableHLO's
+// padded, dilated-input definition). Float windows fold sequentially in
+// that order, the order a sequential CPU evaluation uses, so f32 sums equal
+// it bit for bit; 16-bit floats accumulate in f32 and round once. The
+// two-operand (value, index) form folds with the argmax / argmin pair rule,
+// a selection, so its result does not depend on the order.
 //
 // Replaces the reference's pjrtx_mlx_metal_buffer_reduce_window
-// (reference: src/backend/mlx_metal/api.cc:4324-4437: sum or max over a
-// strided window view of the padded input, base dilation 1).
+// (reference: src/backend/mlx_metal/api.cc:4324-4435: sum or max over a
+// strided window view of the padded input, base dilation 1) and
+// pjrtx_mlx_metal_buffer_reduce_window_max_with_indices (api.cc:4437-4620:
+// the (max, index) pair of each window, found there by an argsort of the
+// window's values).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -56,6 +61,34 @@ __device__ __forceinline__ A fold(int op, A a, A b) {
   }
 }
 
+// Output o's coordinates.
+__device__ __forceinline__ void out_coords(const ReduceWindowParams& p, int64_t o, int64_t* oc) {
+  for (int d = p.rank - 1; d >= 0; --d) {
+    oc[d] = o % p.out_dims[d];
+    o /= p.out_dims[d];
+  }
+}
+
+// Input element read by window position w of the output at oc, or -1 for a
+// padding position or a base-dilation hole.
+__device__ __forceinline__ int64_t window_source(const ReduceWindowParams& p, const int64_t* oc, int64_t w) {
+  int64_t wc[kReduceWindowMaxRank];
+  for (int d = p.rank - 1; d >= 0; --d) {
+    wc[d] = w % p.window[d];
+    w /= p.window[d];
+  }
+  int64_t lin = 0;
+  bool inside = true;
+  for (int d = 0; d < p.rank; ++d) {
+    const int64_t c = oc[d] * p.stride[d] + wc[d] * p.dilation[d] - p.pad_low[d];
+    const int64_t b = p.base_dilation[d];
+    const int64_t q = c >= 0 ? c / b : -1;
+    inside &= c >= 0 && q * b == c && q < p.in_dims[d];
+    lin = lin * p.in_dims[d] + (q >= 0 ? q : 0);
+  }
+  return inside ? lin : -1;
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) reduce_window_kernel(ReduceWindowParams p, const T* __restrict__ in,
                                                             const T* __restrict__ init, T* __restrict__ out,
@@ -64,31 +97,79 @@ __global__ void __launch_bounds__(256) reduce_window_kernel(ReduceWindowParams p
   const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (o >= n_out) return;
   int64_t oc[kReduceWindowMaxRank];
-  {
-    int64_t r = o;
-    for (int d = p.rank - 1; d >= 0; --d) {
-      oc[d] = r % p.out_dims[d];
-      r /= p.out_dims[d];
-    }
-  }
+  out_coords(p, o, oc);
   const A iv = Acc<T>::in(init[0]);
   A acc = iv;
   for (int64_t w = 0; w < n_win; ++w) {
-    int64_t r = w, lin = 0;
-    bool inside = true;
-    int64_t wc[kReduceWindowMaxRank];
-    for (int d = p.rank - 1; d >= 0; --d) {
-      wc[d] = r % p.window[d];
-      r /= p.window[d];
-    }
-    for (int d = 0; d < p.rank; ++d) {
-      const int64_t c = oc[d] * p.stride[d] + wc[d] * p.dilation[d] - p.pad_low[d];
-      inside &= c >= 0 && c < p.in_dims[d];
-      lin = lin * p.in_dims[d] + c;
-    }
-    acc = fold<A>(p.op, acc, inside ? Acc<T>::in(in[lin]) : iv);
+    const int64_t src = window_source(p, oc, w);
+    acc = fold<A>(p.op, acc, src >= 0 ? Acc<T>::in(in[src]) : iv);
   }
   out[o] = Acc<T>::out(acc);
+}
+
+// (value, index) candidate x replaces the running pair a under the argmax
+// (kMax) or argmin rule: NaN first, then the larger (smaller) value, ties to
+// the lower index. Values compare as floats (so -0 == +0).
+template <bool kMax, typename A, typename I>
+__device__ __forceinline__ bool arg_takes(A xv, I xi, A av, I ai) {
+  const bool xn = xv != xv, an = av != av;
+  if (xn || an) return xn && (!an || xi < ai);
+  if (xv == av) return xi < ai;
+  return kMax ? xv > av : xv < av;
+}
+
+template <typename T, typename I, bool kMax>
+__global__ void __launch_bounds__(256) reduce_window_arg_kernel(ReduceWindowParams p, const T* __restrict__ vals,
+                                                                const I* __restrict__ idx, const T* __restrict__ init_v,
+                                                                const I* __restrict__ init_i, T* __restrict__ out_v,
+                                                                I* __restrict__ out_i, int64_t n_out, int64_t n_win) {
+  typedef typename Acc<T>::type A;
+  const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= n_out) return;
+  int64_t oc[kReduceWindowMaxRank];
+  out_coords(p, o, oc);
+  const T ivb = init_v[0];
+  const I ii = init_i[0];
+  T bv = ivb;  // the winner's own bits
+  A av = Acc<T>::in(ivb);
+  I ai = ii;
+  for (int64_t w = 0; w < n_win; ++w) {
+    const int64_t src = window_source(p, oc, w);
+    const T xb = src >= 0 ? vals[src] : ivb;
+    const I xi = src >= 0 ? idx[src] : ii;
+    const A xv = Acc<T>::in(xb);
+    if (arg_takes<kMax>(xv, xi, av, ai)) {
+      bv = xb;
+      av = xv;
+      ai = xi;
+    }
+  }
+  out_v[o] = bv;
+  out_i[o] = ai;
+}
+
+template <typename T, typename I>
+void launch_arg_typed(hipStream_t s, const ReduceWindowParams& p, const void* v, const void* i, const void* iv,
+                      const void* ii, void* ov, void* oi, int64_t n_out, int64_t n_win) {
+  const dim3 grid(static_cast<uint32_t>((n_out + 255) / 256)), block(256);
+  if (p.op == 4)
+    hipLaunchKernelGGL((reduce_window_arg_kernel<T, I, true>), grid, block, 0, s, p, (const T*)v, (const I*)i,
+                       (const T*)iv, (const I*)ii, (T*)ov, (I*)oi, n_out, n_win);
+  else
+    hipLaunchKernelGGL((reduce_window_arg_kernel<T, I, false>), grid, block, 0, s, p, (const T*)v, (const I*)i,
+                       (const T*)iv, (const I*)ii, (T*)ov, (I*)oi, n_out, n_win);
+}
+
+template <typename T>
+void launch_arg_index(hipStream_t s, const ReduceWindowParams& p, DType it, const void* v, const void* i,
+                      const void* iv, const void* ii, void* ov, void* oi, int64_t n_out, int64_t n_win) {
+  switch (it) {
+    case DType::kS32: launch_arg_typed<T, int32_t>(s, p, v, i, iv, ii, ov, oi, n_out, n_win); break;
+    case DType::kU32: launch_arg_typed<T, uint32_t>(s, p, v, i, iv, ii, ov, oi, n_out, n_win); break;
+    case DType::kS64: launch_arg_typed<T, int64_t>(s, p, v, i, iv, ii, ov, oi, n_out, n_win); break;
+    default:
+      fail(Code::kUnimplemented, std::string("reduce_window: index type ") + dtype_name(it) + " is not supported");
+  }
 }
 
 }  // namespace
@@ -130,6 +211,38 @@ void launch_reduce_window(hipStream_t s, const ReduceWindowParams& p, DType t, c
       break;
     default:
       fail(Code::kUnimplemented, std::string("reduce_window: element type ") + dtype_name(t) + " is not supported");
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(Code::kInternal, strformat("reduce_window launch failed: %s", hipGetErrorString(e)));
+}
+
+void launch_reduce_window_arg(hipStream_t s, const ReduceWindowParams& p, DType vt, DType it, const void* values,
+                              const void* indices, const void* init_value, const void* init_index, void* out_values,
+                              void* out_indices) {
+  PJRTX_CHECK(p.rank >= 1 && p.rank <= kReduceWindowMaxRank, Code::kUnimplemented, "reduce_window: rank 1..8");
+  PJRTX_CHECK(p.op == 4 || p.op == 5, Code::kInternal, "reduce_window: two-operand form needs argmax or argmin");
+  int64_t n_out = 1, n_win = 1;
+  for (int d = 0; d < p.rank; ++d) {
+    n_out *= p.out_dims[d];
+    n_win *= p.window[d];
+  }
+  if (n_out == 0) return;
+  switch (vt) {
+    case DType::kF32:
+      launch_arg_index<float>(s, p, it, values, indices, init_value, init_index, out_values, out_indices, n_out, n_win);
+      break;
+    case DType::kF64:
+      launch_arg_index<double>(s, p, it, values, indices, init_value, init_index, out_values, out_indices, n_out, n_win);
+      break;
+    case DType::kBF16:
+      launch_arg_index<__bf16>(s, p, it, values, indices, init_value, init_index, out_values, out_indices, n_out, n_win);
+      break;
+    case DType::kF16:
+      launch_arg_index<_Float16>(s, p, it, values, indices, init_value, init_index, out_values, out_indices, n_out,
+                                 n_win);
+      break;
+    default:
+      fail(Code::kUnimplemented, std::string("reduce_window: value type ") + dtype_name(vt) + " is not supported");
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(Code::kInternal, strformat("reduce_window launch failed: %s", hipGetErrorString(e)));

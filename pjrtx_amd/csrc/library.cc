@@ -190,8 +190,9 @@ void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops
 void run_dot_residual(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, int add, int out);
 
 // stablehlo.reduce_window (the planner checked the supported forms).
-// Replaces pjrtx_mlx_metal_buffer_reduce_window (reference:
-// src/backend/mlx_metal/api.cc:4324-4437).
+// Replaces pjrtx_mlx_metal_buffer_reduce_window and
+// pjrtx_mlx_metal_buffer_reduce_window_max_with_indices (reference:
+// src/backend/mlx_metal/api.cc:4324-4620).
 void run_reduce_window(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
   ReduceWindowParams p;
   const TensorType& in = prog.type(op.operands[0]);
@@ -201,6 +202,8 @@ void run_reduce_window(Device* dev, const Program& prog, const Op& op, std::vect
     case ReducerKind::kProd: p.op = 1; break;
     case ReducerKind::kMax: p.op = 2; break;
     case ReducerKind::kMin: p.op = 3; break;
+    case ReducerKind::kArgMax: p.op = 4; break;
+    case ReducerKind::kArgMin: p.op = 5; break;
     default: p.op = 0; break;
   }
   for (int d = 0; d < p.rank; ++d) {
@@ -209,7 +212,14 @@ void run_reduce_window(Device* dev, const Program& prog, const Op& op, std::vect
     p.window[d] = op.sizes[d];
     p.stride[d] = op.strides[d];
     p.dilation[d] = op.window_dilations[d];
+    p.base_dilation[d] = op.base_dilations[d];
     p.pad_low[d] = op.pad_low[d];
+  }
+  if (op.results.size() == 2) {
+    launch_reduce_window_arg(dev->stream(), p, in.dtype, prog.type(op.operands[1]).dtype, ptr(vals, op.operands[0]),
+                             ptr(vals, op.operands[1]), ptr(vals, op.operands[2]), ptr(vals, op.operands[3]),
+                             ptr(vals, op.results[0]), ptr(vals, op.results[1]));
+    return;
   }
   launch_reduce_window(dev->stream(), p, in.dtype, ptr(vals, op.operands[0]), ptr(vals, op.operands[1]),
                        ptr(vals, op.results[0]));

@@ -97,16 +97,24 @@ ReducerKind classify_reducer(const Program& prog, const Op& op) {
 }
 
 // reduce_window forms the library kernel runs (kernels/reduce_window.hip):
-// one operand, a sum / product / max / min region, base dilation 1,
-// non-negative padding, positive strides and window dilations, rank <= 8.
-// Anything else fails closed at compile time (the reference accepts sum and
-// max with base dilation 1, api.cc:4324-4360).
+// one operand with a sum / product / max / min region, or two operands
+// (values, indices) with an argmax / argmin pair region (the reference's
+// max-pool-with-indices form, lowering_reduction.zig:96-140); any base
+// dilation, window dilation and stride >= 1, padding of either sign, rank
+// <= 8. Anything else fails closed at compile time (the reference accepts
+// sum and max, and the max pair, with base dilation 1, api.cc:4324-4360,
+// 4437-4480).
 void check_reduce_window_supported(const Program& prog, const Op& op) {
-  PJRTX_CHECK(op.operands.size() == 2 && op.results.size() == 1, Code::kUnimplemented,
-              "reduce_window: only single-operand windows are supported");
+  const size_t n = op.results.size();
+  PJRTX_CHECK((n == 1 || n == 2) && op.operands.size() == 2 * n, Code::kUnimplemented,
+              "reduce_window: one operand, or two (values and indices), are supported");
   const ReducerKind k = classify_reducer(prog, op);
-  PJRTX_CHECK(k == ReducerKind::kSum || k == ReducerKind::kProd || k == ReducerKind::kMax || k == ReducerKind::kMin,
-              Code::kUnimplemented, "reduce_window: the region must be add, multiply, maximum or minimum");
+  if (n == 1)
+    PJRTX_CHECK(k == ReducerKind::kSum || k == ReducerKind::kProd || k == ReducerKind::kMax || k == ReducerKind::kMin,
+                Code::kUnimplemented, "reduce_window: the region must be add, multiply, maximum or minimum");
+  else
+    PJRTX_CHECK(k == ReducerKind::kArgMax || k == ReducerKind::kArgMin, Code::kUnimplemented,
+                "reduce_window: a two-operand region must be an argmax / argmin pair selection");
   const TensorType& in = prog.type(op.operands[0]);
   const TensorType& out = prog.type(op.results[0]);
   const size_t r = in.dims.size();
@@ -115,15 +123,26 @@ void check_reduce_window_supported(const Program& prog, const Op& op) {
                   op.window_dilations.size() == r && op.pad_low.size() == r && op.pad_high.size() == r,
               Code::kInvalidArgument, "reduce_window: window attributes do not match the operand rank");
   const DType t = in.dtype;
-  PJRTX_CHECK(t == DType::kF32 || t == DType::kF64 || t == DType::kBF16 || t == DType::kF16 || t == DType::kS32 ||
-                  t == DType::kS64,
-              Code::kUnimplemented, std::string("reduce_window: element type ") + dtype_name(t) + " is not supported");
+  if (n == 1) {
+    PJRTX_CHECK(t == DType::kF32 || t == DType::kF64 || t == DType::kBF16 || t == DType::kF16 || t == DType::kS32 ||
+                    t == DType::kS64,
+                Code::kUnimplemented, std::string("reduce_window: element type ") + dtype_name(t) + " is not supported");
+  } else {
+    const TensorType& ix = prog.type(op.operands[1]);
+    const TensorType& oi = prog.type(op.results[1]);
+    PJRTX_CHECK(t == DType::kF32 || t == DType::kF64 || t == DType::kBF16 || t == DType::kF16, Code::kUnimplemented,
+                std::string("reduce_window: value type ") + dtype_name(t) + " is not supported");
+    PJRTX_CHECK(ix.dtype == DType::kS32 || ix.dtype == DType::kU32 || ix.dtype == DType::kS64, Code::kUnimplemented,
+                std::string("reduce_window: index type ") + dtype_name(ix.dtype) + " is not supported");
+    PJRTX_CHECK(ix.dims == in.dims && oi.dims == out.dims && oi.dtype == ix.dtype && out.dtype == t &&
+                    prog.type(op.operands[2]).dtype == t && prog.type(op.operands[3]).dtype == ix.dtype,
+                Code::kInvalidArgument, "reduce_window: values and indices must have matching shapes and types");
+  }
   for (size_t d = 0; d < r; ++d) {
-    PJRTX_CHECK(op.base_dilations[d] == 1, Code::kUnimplemented, "reduce_window: base dilation must be 1");
-    PJRTX_CHECK(op.sizes[d] >= 1 && op.strides[d] >= 1 && op.window_dilations[d] >= 1 && op.pad_low[d] >= 0 &&
-                    op.pad_high[d] >= 0,
-                Code::kUnimplemented, "reduce_window: windows, strides and dilations must be positive, padding >= 0");
-    const int64_t padded = op.pad_low[d] + in.dims[d] + op.pad_high[d];
+    PJRTX_CHECK(op.sizes[d] >= 1 && op.strides[d] >= 1 && op.window_dilations[d] >= 1 && op.base_dilations[d] >= 1,
+                Code::kUnimplemented, "reduce_window: windows, strides and dilations must be positive");
+    const int64_t dilated = in.dims[d] == 0 ? 0 : (in.dims[d] - 1) * op.base_dilations[d] + 1;
+    const int64_t padded = op.pad_low[d] + dilated + op.pad_high[d];
     const int64_t span = (op.sizes[d] - 1) * op.window_dilations[d] + 1;
     const int64_t want = padded < span ? 0 : (padded - span) / op.strides[d] + 1;
     PJRTX_CHECK(out.dims[d] == want, Code::kInvalidArgument, "reduce_window: result shape does not match the window");

@@ -238,6 +238,48 @@ class Builder:
         ]
         return T(name, tuple(shape), x.dtype)
 
+    def reduce_window_arg(self, x: T, idx: T, init_v: T, init_i: T, window, strides=None, window_dilations=None,
+                          padding=None, base_dilations=None, kind: str = "max") -> tuple[T, T]:
+        """Two-operand stablehlo.reduce_window over (values, indices) in the
+        generic form, with the pair region jax.lax.reduce_window prints for
+        the reference op suite's comparator (jax_op_suite.py:294-310):
+        keep_left = (v_l > v_r) | ((v_l == v_r) & (i_l < i_r)), then a
+        select of each operand (LT for kind "min")."""
+        r = len(x.shape)
+        strides = list(strides or [1] * r)
+        wd = list(window_dilations or [1] * r)
+        bd = list(base_dilations or [1] * r)
+        pad = [list(p) for p in (padding or [(0, 0)] * r)]
+        shape = []
+        for d in range(r):
+            padded = pad[d][0] + (x.shape[d] - 1) * bd[d] + 1 + pad[d][1] if x.shape[d] else pad[d][0] + pad[d][1]
+            span = (window[d] - 1) * wd[d] + 1
+            shape.append(0 if padded < span else (padded - span) // strides[d] + 1)
+        name = self._fresh()
+        b = name[1:]
+        sv, si, pred = tensor_type((), x.dtype), tensor_type((), idx.dtype), tensor_type((), "pred")
+        ik = "SIGNED" if idx.dtype.startswith("s") else "UNSIGNED"
+        cmp = "GT" if kind == "max" else "LT"
+        arr = lambda v: "array<i64: " + ", ".join(str(int(e)) for e in v) + ">"  # noqa: E731
+        pads = ", ".join(f"[{lo}, {hi}]" for lo, hi in pad)
+        self.lines += [
+            f'    {name}:2 = "stablehlo.reduce_window"({x.name}, {idx.name}, {init_v.name}, {init_i.name}) ({{',
+            f"    ^bb0(%w{b}_a: {sv}, %w{b}_b: {si}, %w{b}_c: {sv}, %w{b}_d: {si}):",
+            f"      %w{b}_1 = stablehlo.compare  {cmp}, %w{b}_a, %w{b}_c,  FLOAT : ({sv}, {sv}) -> {pred}",
+            f"      %w{b}_2 = stablehlo.compare  EQ, %w{b}_a, %w{b}_c,  FLOAT : ({sv}, {sv}) -> {pred}",
+            f"      %w{b}_3 = stablehlo.compare  LT, %w{b}_b, %w{b}_d,  {ik} : ({si}, {si}) -> {pred}",
+            f"      %w{b}_4 = stablehlo.and %w{b}_2, %w{b}_3 : {pred}",
+            f"      %w{b}_5 = stablehlo.or %w{b}_1, %w{b}_4 : {pred}",
+            f"      %w{b}_6 = stablehlo.select %w{b}_5, %w{b}_a, %w{b}_c : {pred}, {sv}",
+            f"      %w{b}_7 = stablehlo.select %w{b}_5, %w{b}_b, %w{b}_d : {pred}, {si}",
+            f"      stablehlo.return %w{b}_6, %w{b}_7 : {sv}, {si}",
+            f"    }}) {{base_dilations = {arr(bd)}, padding = dense<[{pads}]> : tensor<{r}x2xi64>, "
+            f"window_dimensions = {arr(window)}, window_dilations = {arr(wd)}, window_strides = {arr(strides)}}} : "
+            f"({x.type}, {idx.type}, {init_v.type}, {init_i.type}) -> ({tensor_type(shape, x.dtype)}, "
+            f"{tensor_type(shape, idx.dtype)})",
+        ]
+        return T(f"{name}#0", tuple(shape), x.dtype), T(f"{name}#1", tuple(shape), idx.dtype)
+
     def convert(self, x: T, dtype: str) -> T:
         return self._emit(f"stablehlo.convert {x.name} : ({x.type}) -> {tensor_type(x.shape, dtype)}", x.shape, dtype)
 

@@ -136,6 +136,86 @@ func.func @main(%arg0: tensor<4xf32>, %arg1: tensor<4xf32>) -> (tensor<4xf32>, t
 def test_unsupported_reduce_window_fails_closed(plugin):
     b = Builder()
     x = b.param((8,), "f32")
-    y = b.reduce_window(x, b.constant(0.0, "f32"), "add", [2], base_dilations=[2])
-    with pytest.raises(Exception, match="base dilation"):
+    y = b.reduce_window(x, b.constant(0.0, "f32"), "add", [2], window_dilations=[0])
+    with pytest.raises(Exception, match="positive"):
         _plan(plugin, b.build([y]))
+    b = Builder()
+    x = b.param((8,), "s32")
+    i = b.param((8,), "s32")
+    v, k = b.reduce_window_arg(x, i, b.constant(0, "s32"), b.constant(0, "s32"), [2])
+    with pytest.raises(Exception, match="argmax|value type"):
+        _plan(plugin, b.build([v, k]))
+
+
+def test_reduce_window_base_dilation_closed_forms():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(7).astype(np.float32)
+    # window 1: the input placed every b-th position of a zero array
+    for bd in (2, 3):
+        got = F.reduce_window(x, 0.0, "add", [1], base_dilations=[bd])
+        want = np.zeros((len(x) - 1) * bd + 1, np.float32)
+        want[::bd] = x
+        np.testing.assert_array_equal(got, want)
+    # window 2, base dilation 2: [x0, x1, x1, x2, x2, ...]
+    got = F.reduce_window(x, 0.0, "add", [2], base_dilations=[2])
+    np.testing.assert_array_equal(got, x[(np.arange(2 * len(x) - 2) + 1) // 2])
+    # 2-D, with padding: every window of the dilated, padded array
+    y = rng.integers(-9, 9, (4, 5)).astype(np.int32)
+    dil = np.zeros((7, 13), np.int32)
+    dil[::2, ::3] = y
+    padded = np.pad(dil, ((1, 2), (0, 1)))
+    want = np.lib.stride_tricks.sliding_window_view(padded, (3, 2)).sum(axis=(2, 3))[::1, ::2]
+    got = F.reduce_window(y, 0, "add", [3, 2], strides=[1, 2], padding=[(1, 2), (0, 1)], base_dilations=[2, 3])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_reduce_window_negative_padding_crops():
+    x = np.arange(10, dtype=np.float32)
+    got = F.reduce_window(x, 0.0, "add", [1], padding=[(-2, -3)])
+    np.testing.assert_array_equal(got, x[2:-3])
+    got = F.reduce_window(x, -np.inf, "maximum", [3], padding=[(-1, 2)])
+    want = np.lib.stride_tricks.sliding_window_view(np.pad(x[1:], (0, 2), constant_values=-np.inf), 3).max(-1)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_reduce_window_arg_matches_numpy_argmax():
+    rng = np.random.default_rng(6)
+    x = rng.integers(-3, 4, (5, 12)).astype(np.float32)   # many ties
+    x[1, 4] = np.nan
+    x[3, 7] = np.nan
+    x[3, 9] = np.nan
+    idx = np.broadcast_to(np.arange(12, dtype=np.int32), x.shape).copy()
+    for kind in ("max", "min"):
+        v, i = F.reduce_window_arg(x, idx, -np.inf if kind == "max" else np.inf, 0, kind, [1, 4], strides=[1, 2])
+        win = np.lib.stride_tricks.sliding_window_view(x, (1, 4))[:, ::2, 0, :]
+        # numpy: first extreme (NaN counts as the extreme); the index is the
+        # window start plus the position in the window
+        pos = np.argmax(win, -1) if kind == "max" else np.argmin(win, -1)
+        start = np.arange(win.shape[1]) * 2
+        np.testing.assert_array_equal(i, start[None, :] + pos)
+        np.testing.assert_array_equal(v, np.take_along_axis(win, pos[..., None], -1)[..., 0])
+    # padding contributes (-inf, 0): an all-padding window returns it
+    v, i = F.reduce_window_arg(x[:1, :3], idx[:1, :3], -np.inf, 0, "max", [1, 2], padding=[(0, 0), (2, 0)])
+    np.testing.assert_array_equal(i[0, 0], 0)
+    assert v[0, 0] == -np.inf
+
+
+def test_reduce_window_arg_reference_op_suite_case():
+    # jax_op_suite.py:122 (f32_a) and 294-310: window (1, 2), stride 1, VALID,
+    # indices = arange(4) per row; f32_a has no ties, so every rule agrees
+    x = (np.arange(12, dtype=np.float32).reshape(3, 4) - np.float32(3.0)) / np.float32(7.0)
+    idx = np.broadcast_to(np.arange(4, dtype=np.int32), x.shape).copy()
+    v, i = F.reduce_window_arg(x, idx, -np.inf, 0, "max", [1, 2])
+    np.testing.assert_array_equal(v, x[:, 1:])
+    np.testing.assert_array_equal(i, np.broadcast_to(np.arange(1, 4, dtype=np.int32), (3, 3)))
+
+
+def test_reduce_window_new_forms_plan(plugin):
+    b = Builder()
+    x = b.param((6, 8), "f32")
+    i = b.param((6, 8), "s32")
+    v, k = b.reduce_window_arg(x, i, b.constant(float("-inf"), "f32"), b.constant(0, "s32"), [2, 2],
+                               strides=[2, 2], padding=[(1, -1), (0, 0)], base_dilations=[1, 2])
+    y = b.reduce_window(x, b.constant(0.0, "f32"), "add", [3, 1], base_dilations=[2, 1], padding=[(-1, 0), (0, 0)])
+    steps = _plan(plugin, b.build([v, k, y]))
+    assert [s.get("library") for s in steps] == ["reduce_window", "reduce_window"]
