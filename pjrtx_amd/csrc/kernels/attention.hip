@@ -803,6 +803,36 @@ __device__ __forceinline__ void merge_splits(const float* pr, int nact, int D, T
     else return *a;
   };
   const int tid = threadIdx.x;
+  if (nact <= 16) {
+    // Up to 16 splits: every (m, l, value) of the thread's column requested
+    // at once (clamped, unconditional loads: one L2 round trip instead of
+    // three), then the same fold in split order as below, so the same bits.
+    if (tid >= D) return;
+    float ms[16], ls[16], vs[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int64_t sp = (int64_t)(u < nact ? u : nact - 1) * (D + 2);
+      ms[u] = ld(pr + sp);
+      ls[u] = ld(pr + sp + 1);
+      vs[u] = ld(pr + sp + 2 + tid);
+    }
+    float mall = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (u < nact) mall = fmaxf(mall, ms[u]);
+    const float mref = mall == -INFINITY ? 0.f : mall;
+    float lsum = 0.f, acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u < nact) {
+        const float f = expf(ms[u] - mref);
+        lsum += ls[u] * f;
+        acc += vs[u] * f;
+      }
+    }
+    out[tid] = Elem<T>::put(acc / lsum);
+    return;
+  }
   if (tid < nact) {
     msh[tid] = ld(pr + (int64_t)tid * (D + 2));
     lsh[tid] = ld(pr + (int64_t)tid * (D + 2) + 1);
@@ -857,41 +887,67 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
   const int bh = row / p.Sq;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
-  const int nkeys = key_limit(p, read_offset(p), q) + 1;
-  const int nact = nkeys <= 0 ? 1 : (nkeys + keys_per_split - 1) / keys_per_split;
-  if (split >= nact) return;
   const T* Kp = K + (int64_t)b * p.k_b + (int64_t)hk * p.k_h;
   const T* Vp = V + (int64_t)b * p.v_b + (int64_t)hk * p.v_h;
   const T* Qp = Q + (int64_t)b * p.q_b + (int64_t)h * p.q_h + (int64_t)q * p.q_s;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int quarter = tid % LPK, kslot = tid / LPK;  // scores: key slot, share of the row
   const int c = tid % NCH, g = tid / NCH;             // P.V: head-dim piece, key group
+  const int k0 = split * keys_per_split;
+  // The query and the split's first pass of K and V rows are requested
+  // before the position is read (it only decides which keys count): one
+  // memory round trip for all of them. Rows are clamped to the cache; keys
+  // past the allowed ones are masked below whatever those rows hold.
+  u32x4 qraw[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) qraw[i] = *reinterpret_cast<const u32x4*>(Qp + (quarter * CPT + i) * EPC);
+  u32x4 kv0[CPT], vv0[KG];
+  const int slast = p.Skv > 0 ? p.Skv - 1 : 0;
+  if (p.Skv > 0) {
+    const int kst = std::min(k0 + kslot, slast);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      kv0[i] = *reinterpret_cast<const u32x4*>(Kp + (int64_t)kst * p.k_s + (quarter * CPT + i) * EPC);
+#pragma unroll
+    for (int i = 0; i < KG; ++i) {
+      const int kk = std::min(k0 + g * KG + i, slast);
+      vv0[i] = *reinterpret_cast<const u32x4*>(Vp + (int64_t)kk * p.v_s + c * EPC);
+    }
+  }
+  const int nkeys = key_limit(p, read_offset(p), q) + 1;
+  const int nact = nkeys <= 0 ? 1 : (nkeys + keys_per_split - 1) / keys_per_split;
+  if (split >= nact) return;
   float qv[CPT * EPC];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(Qp + (quarter * CPT + i) * EPC);
-    const T* e8 = reinterpret_cast<const T*>(&w);
+    const T* e8 = reinterpret_cast<const T*>(&qraw[i]);
 #pragma unroll
     for (int e = 0; e < EPC; ++e) qv[i * EPC + e] = Elem<T>::get(e8[e]);
   }
-  const int k0 = split * keys_per_split;
   const int k1 = std::min(nkeys, k0 + keys_per_split);
   float m = -INFINITY, l = 0.f, o[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) o[e] = 0.f;
   for (int kb = k0; kb < k1; kb += DKT) {
     const int key = kb + kslot;
-    u32x4 kv[CPT];
+    u32x4 kv[CPT], vv[KG];
+    if (kb == k0) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i)
-      kv[i] = key < k1 ? *reinterpret_cast<const u32x4*>(Kp + (int64_t)key * p.k_s + (quarter * CPT + i) * EPC)
-                       : u32x4{0u, 0u, 0u, 0u};
-    // keys past k1 weigh 0 and read the last allowed row instead
-    u32x4 vv[KG];
+      for (int i = 0; i < CPT; ++i) kv[i] = kv0[i];
 #pragma unroll
-    for (int i = 0; i < KG; ++i) {
-      const int kk = std::min(kb + g * KG + i, k1 - 1);
-      vv[i] = *reinterpret_cast<const u32x4*>(Vp + (int64_t)kk * p.v_s + c * EPC);
+      for (int i = 0; i < KG; ++i) vv[i] = vv0[i];
+    } else {
+      // later passes (splits of more than one pass): K and V requested
+      // together, rows past k1 read the last allowed row
+      const int kcl = std::min(key, k1 - 1);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i)
+        kv[i] = *reinterpret_cast<const u32x4*>(Kp + (int64_t)kcl * p.k_s + (quarter * CPT + i) * EPC);
+#pragma unroll
+      for (int i = 0; i < KG; ++i) {
+        const int kk = std::min(kb + g * KG + i, k1 - 1);
+        vv[i] = *reinterpret_cast<const u32x4*>(Vp + (int64_t)kk * p.v_s + c * EPC);
+      }
     }
     float acc = 0.f;
 #pragma unroll
@@ -925,10 +981,12 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
     for (int e = 0; e < EPC; ++e) o[e] *= alpha;
 #pragma unroll
     for (int i = 0; i < KG; ++i) {
+      // a key past k1 adds nothing (its row may hold anything)
+      const bool in = kb + g * KG + i < k1;
       const float pj = ps[g * KG + i];
       const T* e8 = reinterpret_cast<const T*>(&vv[i]);
 #pragma unroll
-      for (int e = 0; e < EPC; ++e) o[e] += pj * Elem<T>::get(e8[e]);
+      for (int e = 0; e < EPC; ++e) o[e] += in ? pj * Elem<T>::get(e8[e]) : 0.f;
     }
     __syncthreads();  // ps and wred are rewritten by the next pass
   }
