@@ -571,25 +571,41 @@ std::string combine_stmt(ReducerKind k, DType t, const std::string& a, const std
 
 std::string arg_better(ReducerKind k) { return k == ReducerKind::kArgMax ? "argmax_better" : "argmin_better"; }
 
+// DPP exchange steps that fold lanes [0, width) into each of those lanes:
+// xor 1 and xor 2 within quads, then the mirror within 8 lanes, then the
+// mirror within the 16-lane row.
+int dpp_steps_for(int width) { return width <= 2 ? 1 : width <= 4 ? 2 : width <= 8 ? 3 : 4; }
+
 // Wavefront all-reduce of `v` (type `ty`) with the fold `comb(a, b)` (a
 // statement updating a): four DPP exchange steps within rows of 16 lanes,
 // then the four row values read from lanes 0, 16, 32, 48 and folded in a
 // fixed tree. Every lane ends with the same value; the order is fixed, so
-// the result is deterministic.
+// the result is deterministic. With `width` <= 16 only lanes [0, width)
+// carry values (the others hold the fold's identity): the first
+// dpp_steps_for(width) steps leave the fold of those lanes in each of them,
+// the same value the full form gives (identities change no result), and the
+// later steps are not emitted.
 std::string wave_allreduce(const std::string& ty, const std::string& v,
-                           const std::function<std::string(const std::string&, const std::string&)>& comb) {
+                           const std::function<std::string(const std::string&, const std::string&)>& comb, int width = 64) {
+  static const char* const kSteps[4] = {"kDppXor1", "kDppXor2", "kDppHalfMirror", "kDppMirror"};
+  const int steps = width <= 16 ? dpp_steps_for(width) : 4;
   std::ostringstream o;
   o << "{ " << ty << " o_;\n";
-  for (const char* c : {"kDppXor1", "kDppXor2", "kDppHalfMirror", "kDppMirror"})
-    o << "o_ = dpp_move<" << c << ">(" << v << "); " << comb(v, "o_") << "\n";
-  o << ty << " w1_ = lane_value(" << v << ", 16), w2_ = lane_value(" << v << ", 32), w3_ = lane_value(" << v << ", 48);\n";
-  o << v << " = lane_value(" << v << ", 0);\n";
-  o << comb(v, "w1_") << " " << comb("w2_", "w3_") << " " << comb(v, "w2_") << "\n}\n";
+  for (int k = 0; k < steps; ++k) o << "o_ = dpp_move<" << kSteps[k] << ">(" << v << "); " << comb(v, "o_") << "\n";
+  if (width > 16) {
+    o << ty << " w1_ = lane_value(" << v << ", 16), w2_ = lane_value(" << v << ", 32), w3_ = lane_value(" << v << ", 48);\n";
+    o << v << " = lane_value(" << v << ", 0);\n";
+    o << comb(v, "w1_") << " " << comb("w2_", "w3_") << " " << comb(v, "w2_") << "\n";
+  }
+  o << "}\n";
   return o.str();
 }
 
 // The same for an argmax/argmin (value, index) pair under its comparator.
-std::string wave_allreduce_arg(ReducerKind k, const std::string& ity, const std::string& v, const std::string& i) {
+std::string wave_allreduce_arg(ReducerKind k, const std::string& ity, const std::string& v, const std::string& i,
+                               int width = 64) {
+  static const char* const kSteps[4] = {"kDppXor1", "kDppXor2", "kDppHalfMirror", "kDppMirror"};
+  const int steps = width <= 16 ? dpp_steps_for(width) : 4;
   const std::string better = arg_better(k);
   std::ostringstream o;
   auto take = [&](const std::string& av, const std::string& ai, const std::string& bv, const std::string& bi) {
@@ -597,13 +613,16 @@ std::string wave_allreduce_arg(ReducerKind k, const std::string& ity, const std:
            "; }";
   };
   o << "{ float ov_; " << ity << " oi_;\n";
-  for (const char* c : {"kDppXor1", "kDppXor2", "kDppHalfMirror", "kDppMirror"})
-    o << "ov_ = dpp_move<" << c << ">(" << v << "); oi_ = dpp_move<" << c << ">(" << i << "); " << take(v, i, "ov_", "oi_")
-      << "\n";
-  o << "float w1v_ = lane_value(" << v << ", 16), w2v_ = lane_value(" << v << ", 32), w3v_ = lane_value(" << v << ", 48);\n";
-  o << ity << " w1i_ = lane_value(" << i << ", 16), w2i_ = lane_value(" << i << ", 32), w3i_ = lane_value(" << i << ", 48);\n";
-  o << v << " = lane_value(" << v << ", 0); " << i << " = lane_value(" << i << ", 0);\n";
-  o << take(v, i, "w1v_", "w1i_") << " " << take("w2v_", "w2i_", "w3v_", "w3i_") << " " << take(v, i, "w2v_", "w2i_") << "\n}\n";
+  for (int s = 0; s < steps; ++s)
+    o << "ov_ = dpp_move<" << kSteps[s] << ">(" << v << "); oi_ = dpp_move<" << kSteps[s] << ">(" << i << "); "
+      << take(v, i, "ov_", "oi_") << "\n";
+  if (width > 16) {
+    o << "float w1v_ = lane_value(" << v << ", 16), w2v_ = lane_value(" << v << ", 32), w3v_ = lane_value(" << v << ", 48);\n";
+    o << ity << " w1i_ = lane_value(" << i << ", 16), w2i_ = lane_value(" << i << ", 32), w3i_ = lane_value(" << i << ", 48);\n";
+    o << v << " = lane_value(" << v << ", 0); " << i << " = lane_value(" << i << ", 0);\n";
+    o << take(v, i, "w1v_", "w1i_") << " " << take("w2v_", "w2i_", "w3v_", "w3i_") << " " << take(v, i, "w2v_", "w2i_") << "\n";
+  }
+  o << "}\n";
   return o.str();
 }
 
@@ -1178,22 +1197,25 @@ void KernelGen::reduce(Step& s) {
     }
     // Block reduction: wavefront all-reduce, then the wave results are
     // combined in wave order by thread 0 (fixed order: deterministic).
-    auto wave_reduce = [&](bool skip_done) {
+    // width: lanes that hold values (the fold of the split partials: one
+    // lane per split).
+    auto wave_reduce = [&](bool skip_done, int width) {
       for (size_t r = 0; r < accs.size(); ++r) {
         const Accum& a = accs[r];
         if (skip_done && wave_done[r]) continue;
         const bool am = a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin;
         if (am) {
-          out_ << wave_allreduce_arg(a.kind, ait, a.v, a.i);
+          out_ << wave_allreduce_arg(a.kind, ait, a.v, a.i, width);
         } else {
           const ReducerKind k = a.kind;
           const DType vt = a.vt;
-          out_ << wave_allreduce(a.acc_t, a.v, [&](const std::string& x, const std::string& y) { return combine_stmt(k, vt, x, y); });
+          out_ << wave_allreduce(a.acc_t, a.v, [&](const std::string& x, const std::string& y) { return combine_stmt(k, vt, x, y); },
+                                 width);
         }
       }
     };
     auto block_reduce = [&]() {
-      wave_reduce(true);
+      wave_reduce(true, 64);
       out_ << "if ((threadIdx.x & 63) == 0) {\n";
       for (auto& a : accs) {
         out_ << "sm_" << a.v << "[threadIdx.x >> 6] = " << a.v << ";\n";
@@ -1253,7 +1275,9 @@ void KernelGen::reduce(Step& s) {
                << ld("slot[" + std::to_string(slots) + "u + row * " + std::to_string(s.splits) + "u + lane]") << ";\n";
         out_ << "}\n";
       }
-      wave_reduce(false);
+      // Lanes at or past the split count hold identities: only the first
+      // splits lanes need folding (lane 0 keeps the result).
+      wave_reduce(false, static_cast<int>(s.splits));
       out_ << "if (lane != 0) return;\n";
     };
     if (split && s.fused_combine) {
