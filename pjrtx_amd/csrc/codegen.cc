@@ -1053,21 +1053,31 @@ void KernelGen::reduce(Step& s) {
       o << "const bool bn = bm != bm;\n";
       o << "const idx_t c = c0 + threadIdx.x * " << vec << "u;\n";
       if (idx_is_col[r]) {
+        // bm is the same in every lane, so the NaN and the ordinary case are
+        // separate uniform branches: each ballot is then one compare.
         o << "int fu = -1; unsigned long long fm = 0ull;\n";
-        o << "#pragma unroll\nfor (int u = " << unroll - 1 << "; u >= 0; --u) {\n";
-        o << "const bool ok = u < " << full_u << " || c + (idx_t)u * " << span << " < c1;\n";
-        o << "const unsigned long long m = __ballot(ok && (bn ? mu" << R << "[u] != mu" << R << "[u] : mu" << R
-          << "[u] == bm));\n";
-        o << "if (m) { fu = u; fm = m; }\n}\n";
+        for (int nan_case = 0; nan_case < 2; ++nan_case) {
+          o << (nan_case ? "} else {\n" : "if (!bn) {\n");
+          o << "#pragma unroll\nfor (int u = " << unroll - 1 << "; u >= 0; --u) {\n";
+          o << "const bool ok = u < " << full_u << " || c + (idx_t)u * " << span << " < c1;\n";
+          o << "const unsigned long long m = __ballot(ok && "
+            << (nan_case ? "mu" + R + "[u] != mu" + R + "[u]" : "mu" + R + "[u] == bm") << ");\n";
+          o << "if (m) { fu = u; fm = m; }\n}\n";
+        }
+        o << "}\n";
         o << a.v << " = bm; " << a.i << " = " << aimax << ";\n";
         o << "if (fm) {\n";
         o << "const int L = __ffsll(fm) - 1;\n";
         o << "float sv = bm; int sj = 0;\n";
         o << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
         o << "if (u == fu) {\n";
-        o << "#pragma unroll\nfor (int j = " << vec - 1 << "; j >= 0; --j) {\n";
-        o << "const float x = xa" << R << "[u][j]; const bool hit = bn ? x != x : x == bm;\n";
-        o << "sv = hit ? x : sv; sj = hit ? j : sj;\n}\n}\n}\n";
+        for (int nan_case = 0; nan_case < 2; ++nan_case) {
+          o << (nan_case ? "} else {\n" : "if (!bn) {\n");
+          o << "#pragma unroll\nfor (int j = " << vec - 1 << "; j >= 0; --j) {\n";
+          o << "const float x = xa" << R << "[u][j]; const bool hit = " << (nan_case ? "x != x" : "x == bm") << ";\n";
+          o << "sv = hit ? x : sv; sj = hit ? j : sj;\n}\n";
+        }
+        o << "}\n}\n}\n";
         o << a.v << " = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), L));\n";
         o << a.i << " = (" << ait << ")(c0 + ((threadIdx.x & ~63u) + (idx_t)L) * " << vec << "u + (idx_t)fu * " << span
           << " + (idx_t)__builtin_amdgcn_readlane(sj, L));\n";
