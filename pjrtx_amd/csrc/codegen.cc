@@ -916,8 +916,11 @@ void KernelGen::reduce(Step& s) {
       fail(Code::kInternal, "reduce kernel: row length and chunk must be multiples of the vector width");
   }
   // f32 sums of f16 values (JAX's f16 sum: convert f16->f32, add) fold each
-  // element with one mixed-precision FMA on the f16 value (add_f16v).
+  // element with one mixed-precision FMA on the f16 value (add_f16v), or, in
+  // the row schedule's vectorised loop, each pair of elements with one packed
+  // convert and one dot2 (add2_f16v).
   std::vector<bool> f16_sum(s.reduces.size(), false);
+  std::vector<std::string> f16_pre(s.reduces.size());
   for (size_t r = 0; r < s.reduces.size(); ++r) {
     const ReduceSpec& rs = s.reduces[r];
     for (int v : rs.inputs) {
@@ -938,6 +941,14 @@ void KernelGen::reduce(Step& s) {
         }
       }
       xs[r].push_back(w.value(src, rid));
+      // The f16 value's own source when it is a convert from f32 or bf16:
+      // add2_f16v rounds that value to f16 itself (one packed convert for two
+      // elements), which is the same rounding (bf16 widens to f32 exactly).
+      if (f16_sum[r])
+        for (const Op& op : prog_.ops)
+          if (!op.results.empty() && op.results[0] == src && op.kind == OpKind::kConvert &&
+              (prog_.type(op.operands[0]).dtype == DType::kF32 || prog_.type(op.operands[0]).dtype == DType::kBF16))
+            f16_pre[r] = "(float)(" + w.value(op.operands[0], rid) + ")";
     }
   }
   std::string elem_body = w.body.str();
@@ -1051,6 +1062,14 @@ void KernelGen::reduce(Step& s) {
         return x + " = " + mx + "(" + x + ", " + y + ");";
       });
       o << "const bool bn = bm != bm;\n";
+      // A max (min) over the same values as this argmax (argmin) folds the
+      // same sub-chunk maxima (minima) in the same total order (IEEE
+      // maximum/minimum): its wavefront result is bm.
+      for (size_t r2 = 0; r2 < accs.size(); ++r2)
+        if (shares[r2] == static_cast<int>(r)) {
+          o << accs[r2].v << " = bm;\n";
+          wave_done[r2] = true;
+        }
       o << "const idx_t c = c0 + threadIdx.x * " << vec << "u;\n";
       if (idx_is_col[r]) {
         // bm is the same in every lane, so the NaN and the ordinary case are
@@ -1099,7 +1118,10 @@ void KernelGen::reduce(Step& s) {
     }
   };
   // mode 0: element-wise fold; 1: per-sub-chunk two-phase argmax; 2: deferred argmax.
-  auto combine_elem = [&](std::ostream& o, int mode) {
+  // pairs: the caller's unrolled loop over j = 0..vec-1 (vec even) lets an
+  // f16 sum hold element j's value when j is even and add the pair at the
+  // odd j (add2_f16v).
+  auto combine_elem = [&](std::ostream& o, int mode, bool pairs = false) {
     for (size_t r = 0; r < accs.size(); ++r) {
       const Accum& a = accs[r];
       const char* mx = a.kind == ReducerKind::kArgMax ? "max_r(" : "min_r(";
@@ -1123,6 +1145,10 @@ void KernelGen::reduce(Step& s) {
       } else if ((a.kind == ReducerKind::kMax || a.kind == ReducerKind::kMin) && a.acc_t == "float") {
         o << a.v << " = " << (a.kind == ReducerKind::kMax ? "max_seq(" : "min_seq(") << a.v << ", (float)(" << xs[r][0]
           << "));\n";
+      } else if (f16_sum[r] && a.acc_t == "float" && pairs) {
+        const std::string x = f16_pre[r].empty() ? xs[r][0] : f16_pre[r];
+        o << "if (j & 1) " << a.v << " = add2_f16v(" << a.v << ", f16p" << r << ", " << x << "); else f16p" << r << " = " << x
+          << ";\n";
       } else if (f16_sum[r] && a.acc_t == "float") {
         o << a.v << " = add_f16v(" << a.v << ", " << xs[r][0] << ");\n";
       } else {
@@ -1171,10 +1197,14 @@ void KernelGen::reduce(Step& s) {
     if (deferred)
       for (size_t r = 0; r < accs.size(); ++r)
         if (fast_arg(r)) out_ << "mu" << r << "[u] = " << ident(r) << ";\n";
+    const bool pairs = vec % 2 == 0;
+    if (pairs)
+      for (size_t r = 0; r < accs.size(); ++r)
+        if (f16_sum[r] && accs[r].acc_t == "float") out_ << "float f16p" << r << " = 0.f;\n";
     out_ << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) {\n";
     out_ << "const idx_t col = cu + j;\nconst idx_t lin = row * " << s.row_len << "u + col;\n";
     out_ << col_digits.str() << elem_body;
-    combine_elem(out_, deferred ? 2 : two_phase ? 1 : 0);
+    combine_elem(out_, deferred ? 2 : two_phase ? 1 : 0, pairs);
     out_ << "}\n";
     if (two_phase) two_phase_finish(out_);
     if (deferred)

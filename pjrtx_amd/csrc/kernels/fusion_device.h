@@ -50,6 +50,18 @@ PJRTX_DEV float add_f16v(float acc, float x) {
   asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(acc));
   return r;
 }
+// acc + x + y for x, y holding f16 values (or f32 values to be rounded to
+// f16): one packed round-to-nearest convert (v_cvt_pk_f16_f32) and one
+// v_dot2 with the pair (1, 1), x * 1 + y * 1 + acc accumulated in f32. Two
+// instructions per pair instead of four; the pair is added as one step, so
+// the sum's rounding differs from two sequential f32 adds (an f32 sum of
+// f16 values either way).
+PJRTX_DEV float add2_f16v(float acc, float x, float y) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const h2_t h = __builtin_convertvector((f2_t){x, y}, h2_t);
+  return __builtin_amdgcn_fdot2(h, (h2_t){(_Float16)1, (_Float16)1}, acc, false);
+}
 
 // stablehlo.reduce_precision on the bits of a float with E exponent and Mn
 // mantissa bits: the mantissa rounds to m bits (to nearest, ties to even;
