@@ -1085,21 +1085,30 @@ void KernelGen::reduce(Step& s) {
         }
         o << "}\n";
         o << a.v << " = bm; " << a.i << " = " << aimax << ";\n";
+        // Lane L's first hit in sub-chunk fu: one ballot per element (all
+        // independent), then bit L of each, picked in scalar code. The value
+        // bits are bm's except for a zero maximum (the sign of the first
+        // zero) or a NaN (its payload): those read lane L's elements.
         o << "if (fm) {\n";
         o << "const int L = __ffsll(fm) - 1;\n";
-        o << "float sv = bm; int sj = 0;\n";
+        o << "int sj = " << vec - 1 << "; int svb = __builtin_bit_cast(int, bm);\n";
         o << "#pragma unroll\nfor (int u = 0; u < " << unroll << "; ++u) {\n";
         o << "if (u == fu) {\n";
+        o << "unsigned long long hj[" << vec << "];\n";
         for (int nan_case = 0; nan_case < 2; ++nan_case) {
           o << (nan_case ? "} else {\n" : "if (!bn) {\n");
-          o << "#pragma unroll\nfor (int j = " << vec - 1 << "; j >= 0; --j) {\n";
-          o << "const float x = xa" << R << "[u][j]; const bool hit = " << (nan_case ? "x != x" : "x == bm") << ";\n";
-          o << "sv = hit ? x : sv; sj = hit ? j : sj;\n}\n";
+          o << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) { const float x = xa" << R << "[u][j]; hj[j] = __ballot("
+            << (nan_case ? "x != x" : "x == bm") << "); }\n";
         }
+        o << "}\n";
+        o << "#pragma unroll\nfor (int j = " << vec - 2 << "; j >= 0; --j) if ((hj[j] >> L) & 1ull) sj = j;\n";
+        o << "if (bn || bm == 0.f) {\n";
+        o << "#pragma unroll\nfor (int j = 0; j < " << vec << "; ++j) { const int b = __builtin_amdgcn_readlane(__builtin_bit_cast(int, xa"
+          << R << "[u][j]), L); svb = j == sj ? b : svb; }\n";
         o << "}\n}\n}\n";
-        o << a.v << " = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), L));\n";
+        o << a.v << " = __builtin_bit_cast(float, svb);\n";
         o << a.i << " = (" << ait << ")(c0 + ((threadIdx.x & ~63u) + (idx_t)L) * " << vec << "u + (idx_t)fu * " << span
-          << " + (idx_t)__builtin_amdgcn_readlane(sj, L));\n";
+          << " + (idx_t)sj);\n";
         o << "}\n}\n";
       } else {
         o << "float sv = bm; " << ait << " si = " << aimax << ";\n";
@@ -1228,13 +1237,6 @@ void KernelGen::reduce(Step& s) {
       out_ << "}\n";
     }
     out_ << "}\n";
-    if (deferred) deferred_finish(out_, full_u);
-    // Shared slots for the cross-wave step of the block reductions.
-    for (auto& a : accs) {
-      out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[" << nwaves << "];\n";
-      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
-        out_ << "__shared__ " << ait << " sm_" << a.i << "[" << nwaves << "];\n";
-    }
     // Block reduction: wavefront all-reduce, then the wave results are
     // combined in wave order by thread 0 (fixed order: deterministic).
     // width: lanes that hold values (the fold of the split partials: one
@@ -1254,6 +1256,13 @@ void KernelGen::reduce(Step& s) {
         }
       }
     };
+    if (deferred) deferred_finish(out_, full_u);
+    // Shared slots for the cross-wave step of the block reductions.
+    for (auto& a : accs) {
+      out_ << "__shared__ " << a.acc_t << " sm_" << a.v << "[" << nwaves << "];\n";
+      if (a.kind == ReducerKind::kArgMax || a.kind == ReducerKind::kArgMin)
+        out_ << "__shared__ " << ait << " sm_" << a.i << "[" << nwaves << "];\n";
+    }
     auto block_reduce = [&]() {
       wave_reduce(true, 64);
       out_ << "if ((threadIdx.x & 63) == 0) {\n";
