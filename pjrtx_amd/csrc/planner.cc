@@ -1413,6 +1413,7 @@ Plan make_plan(const Program& prog, const PlanOptions& opts) {
   Planner p(prog, opts);
   Plan plan = p.run();
   if (env_flag("PJRTX_PLAN_DEBUG")) std::fprintf(stderr, "pjrtx plan: %s\n", plan.describe(prog).c_str());
+  plan.nt_min_bytes = opts.nt_min_bytes;
   plan.kernel_source = generate_kernels(prog, plan);
   return plan;
 }

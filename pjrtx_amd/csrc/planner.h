@@ -172,6 +172,7 @@ struct Plan {
   std::vector<int> written_params;
   std::map<int, int> producer;       // value -> op index
   std::string kernel_source;         // hiprtc source for all generated steps
+  int64_t nt_min_bytes = 0;          // PlanOptions::nt_min_bytes
   int num_fusion_kernels = 0;
   std::string describe(const Program& prog) const;  // JSON summary
 };
@@ -187,12 +188,15 @@ struct PlanOptions {
   // 1024).
   int reduce_block = env_int("PJRTX_REDUCE_BLOCK", 256);
   // Split reductions fold their partials in the last workgroup of each row
-  // instead of a second launch (environment: PJRTX_REDUCE_FUSED_COMBINE=1).
-  // Off by default: each workgroup's device-scope release fence (an L2
-  // write-back, needed because the XCDs' L2s are not coherent) costs more
-  // than the launch it saves (64x128256 bf16 argmax + f16 reductions:
-  // 16.0 us fused vs 4.3 + 2.6 us with the combine kernel).
+  // instead of a second launch (environment: PJRTX_REDUCE_FUSED_COMBINE,
+  // default 1). The fold needs no device-scope fence: every split of a row
+  // runs on one XCD (when the device places workgroups round-robin over the
+  // XCDs; otherwise the runtime launches the `_combine` kernel instead).
   bool reduce_fused_combine = env_int("PJRTX_REDUCE_FUSED_COMBINE", 1) != 0;
+  // Inputs of reduce kernels of at least this many bytes are read with
+  // non-temporal loads (environment: PJRTX_NT_MIN_BYTES; 0 never). C2's
+  // 16 MB logits stay below it (non-temporal: 5.06 -> 5.11 us).
+  int64_t nt_min_bytes = env_int("PJRTX_NT_MIN_BYTES", 32 << 20);
   bool fuse_siblings = true;
   bool fuse_epilogues = true;
   // Row chains (reduce -> reduce/loop over the same rows) become one kernel
