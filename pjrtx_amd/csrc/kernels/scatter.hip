@@ -364,6 +364,19 @@ struct alignas(sizeof(T) * VEC) VecOf {
   T v[VEC];
 };
 
+// A piece of an update row (16 bytes, or one element for narrow rows), which
+// the fold reads once: a non-temporal load (streams faster, and leaves the memory-side cache to
+// the operand rows and the keys).
+template <typename V>
+__device__ __forceinline__ V load_once(const V* p) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  if constexpr (sizeof(V) == 16) return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const u4*>(p)));
+  else if constexpr (sizeof(V) == 8) return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const u2*>(p)));
+  else if constexpr (sizeof(V) == 4) return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p)));
+  else return *p;
+}
+
 // Lists the hot rows by length class. With `init_src`, also copies each hot
 // row of the operand into the result (the integer chunk path accumulates
 // into it with atomics).
@@ -470,7 +483,7 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
 #pragma unroll
         for (int q = 0; q < kFoldDepth; ++q) {
           const int j = min(base + 4 * q, n - 1);  // clamped: a repeat of the last row is never folded
-          u[q] = col_ok ? *reinterpret_cast<const V*>(updates + (int64_t)pidx[j] * row_elems + c0) : V();
+          u[q] = col_ok ? load_once(reinterpret_cast<const V*>(updates + (int64_t)pidx[j] * row_elems + c0)) : V();
         }
       };
       auto fold = [&](const V (&u)[kFoldDepth], int base) {
@@ -907,14 +920,14 @@ __global__ void __launch_bounds__(256) scatter_rows_fold(
       V u[kFoldDepth];
 #pragma unroll
       for (int d = 0; d < kFoldDepth; ++d)
-        u[d] = *reinterpret_cast<const V*>(updates + (int64_t)perm[i + d] * p.row_elems + c0);
+        u[d] = load_once(reinterpret_cast<const V*>(updates + (int64_t)perm[i + d] * p.row_elems + c0));
 #pragma unroll
       for (int d = 0; d < kFoldDepth; ++d)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] = fold1<Tag, OP>(acc[e], K::ld(u[d].v[e]));
     }
     for (; i < hi; ++i) {
-      const V u = *reinterpret_cast<const V*>(updates + (int64_t)perm[i] * p.row_elems + c0);
+      const V u = load_once(reinterpret_cast<const V*>(updates + (int64_t)perm[i] * p.row_elems + c0));
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[e] = fold1<Tag, OP>(acc[e], K::ld(u.v[e]));
     }
