@@ -1897,7 +1897,7 @@ void KernelGen::gemv(Step& s) {
     out_ << "#pragma unroll\nfor (int i = 0; i < " << D << "; ++i) {\n";
     out_ << "const uint32_t r = " << p << "r0 + ((" << b << ") * " << D << "u + (uint32_t)i) * " << RS << "u;\n";
     out_ << "const uint32_t rr = r < " << p << "k1 ? r : " << p << "k1 - 1u;\n";
-    out_ << dst << "[i] = gv_load16(wp + (size_t)rr * " << p << "N);\n";
+    out_ << dst << "[i] = gv_load16<" << (g.weights_nt ? "true" : "false") << ">(wp + (size_t)rr * " << p << "N);\n";
     out_ << "}\n}\n";
   };
   assign_item("c_", "gv_lb");

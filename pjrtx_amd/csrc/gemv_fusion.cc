@@ -204,6 +204,7 @@ class GemvFuser {
       s.name = strformat("pjrtx_gemv_%d", id++);
     }
     plan_.num_fusion_kernels += id;
+    keep_weights_in_mall();
     releases();
   }
 
@@ -493,6 +494,28 @@ class GemvFuser {
     }
     s->grid = static_cast<uint32_t>(g.wgs);
     s->block = 256;
+  }
+
+  // The smallest GEMV weights, up to opts_.gemv_mall_mb in all, keep plain
+  // loads (they may stay in the MALL between executes); the others stream
+  // with non-temporal loads, which do not displace them.
+  void keep_weights_in_mall() {
+    const int64_t budget = opts_.gemv_mall_mb << 20;
+    if (budget <= 0) return;
+    std::vector<std::pair<int64_t, size_t>> by_size;
+    for (size_t i = 0; i < steps_.size(); ++i) {
+      if (steps_[i].kind != StepKind::kGemv) continue;
+      int64_t bytes = 0;
+      for (int d : steps_[i].gemv.dots) bytes += prog_.type(prog_.ops[d].operands[1]).bytes();
+      by_size.push_back({bytes, i});
+    }
+    std::stable_sort(by_size.begin(), by_size.end(), [](const auto& a, const auto& b) { return a.first < b.first; });
+    int64_t used = 0;
+    for (auto& [bytes, i] : by_size) {
+      if (used + bytes > budget) break;
+      used += bytes;
+      steps_[i].gemv.weights_nt = false;
+    }
   }
 
   void releases() {

@@ -335,8 +335,9 @@ PJRTX_DEV float min_seq(float acc, float x) { return min_r(acc, x); }
 // ------------------------------------------------------------ decode GEMV
 typedef uint32_t gv_u32x4 __attribute__((ext_vector_type(4)));
 // Decode weights are read once per token, more of them than the MALL holds:
-// non-temporal loads (the C5 decode step: 2370 -> 2580 tokens/s).
-PJRTX_DEV gv_u32x4 gv_load16(const uint16_t* p) { return ld16<true>(p); }
+// non-temporal loads by default (the C5 decode step: 2370 -> 2580 tokens/s).
+template <bool NT = true>
+PJRTX_DEV gv_u32x4 gv_load16(const uint16_t* p) { return ld16<NT>(p); }
 // acc[e] += x * w[e] for the eight 16-bit weights of one 16-byte piece, in
 // element order (bf16: the high half of each 32-bit word is the odd element).
 template <bool kF16>

@@ -86,6 +86,7 @@ struct GemvSpec {
   size_t partial_bytes = 0;                 // partial slots before the counters in scratch
   int64_t wgs = 0;                          // workgroups launched (8 per XCD round)
   bool stage_all_x = false;                 // whole X in LDS (else each workgroup's one chunk)
+  bool weights_nt = true;                   // weights read with non-temporal loads
 };
 
 struct Step {
@@ -215,6 +216,12 @@ struct PlanOptions {
   bool gemv_fusion = env_int("PJRTX_GEMV_FUSION", 1) != 0;
   // Target workgroups per GEMV launch (environment: PJRTX_GEMV_WGS).
   int64_t gemv_target_wgs = env_int("PJRTX_GEMV_WGS", 768);
+  // GEMV weights read with plain loads, smallest first, up to this many MB
+  // per program; the rest use non-temporal loads (environment:
+  // PJRTX_GEMV_MALL_MB). Plain-loaded weights may stay in the memory-side
+  // cache (MALL, 256 MB) from one execute to the next. C5 decode, tokens/s:
+  // 0 MB 2581, 64 MB 2594, 100 MB 2598, 160 MB 2553, 200 MB 2545.
+  int64_t gemv_mall_mb = env_int("PJRTX_GEMV_MALL_MB", 96);
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
