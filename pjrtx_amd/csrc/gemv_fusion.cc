@@ -437,9 +437,10 @@ class GemvFuser {
     if (g.joint) {
       while (g.cols > 32 && g.seg_cols % g.cols != 0) g.cols /= 2;
     }
-    // Weight rows in flight per lane: 4, 8 or 16 (PJRTX_GEMV_DEPTH); 4 is
-    // the fastest on the C5 decode step (2360 vs 2310 tokens/s at 8).
-    const int64_t d = env_int("PJRTX_GEMV_DEPTH", 4);
+    // Weight rows in flight per lane: 4, 8 or 16 (PJRTX_GEMV_DEPTH); by
+    // default 4, or 8 below when that puts a whole K chunk of a GEMV without
+    // prologue in flight at once.
+    const int64_t d = env_int("PJRTX_GEMV_DEPTH", 0);
     g.depth = (d == 8 || d == 16) ? static_cast<int>(d) : 4;
     const int64_t rows_per_step = 4 * (64 / (g.cols / 8));  // 256 threads
     const int members = static_cast<int>(g.dots.size());
@@ -477,6 +478,11 @@ class GemvFuser {
     const int64_t xs_cap = kMaxLdsFloats / g.M / rows_per_step * rows_per_step;
     if (s->prologue.empty()) kchunk = std::min(kchunk, xs_cap);
     g.kchunk = kchunk;
+    // Depth 8 when it makes the chunk one batch and there is no prologue to
+    // wait for first (C5 down projection, K 5632: 7.47 -> 6.72 us per call;
+    // GEMVs with an RMSNorm prologue were slower at 8).
+    if (d == 0 && !persist && s->prologue.empty() && kchunk > rows_per_step * 4 && kchunk <= rows_per_step * 8)
+      g.depth = 8;
     g.ksplit = (g.K + kchunk - 1) / kchunk;
     g.wps = (g.joint ? members * (g.seg_cols / g.cols) : 1) * g.ksplit;
     g.direct = g.ksplit == 1 && !g.joint;
