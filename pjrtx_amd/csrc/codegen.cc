@@ -333,6 +333,24 @@ std::string Writer::emit_op(const Op& op, int v, int id) {
       const std::vector<std::string> m = multi_of(id);
       const int64_t cd = op.dim;
       const std::string c = m[cd];
+      // Copies of one value (RoPE's [cos, cos] table): the coordinate is
+      // wrapped into the operand and the operand evaluated once, instead of
+      // once per copy and a select.
+      bool copies = op.operands.size() > 1 && prog_.type(op.operands[0]).dims[cd] > 0;
+      for (int o : op.operands) copies &= o == op.operands[0];
+      if (copies) {
+        const int64_t sz = prog_.type(op.operands[0]).dims[cd];
+        const int64_t n = static_cast<int64_t>(op.operands.size());
+        std::string e = "(" + c + " - " + std::to_string((n - 1) * sz) + "u)";
+        for (int64_t k = n - 2; k >= 0; --k)
+          e = "(" + c + " < " + std::to_string((k + 1) * sz) + "u ? " + c + " - " + std::to_string(k * sz) + "u : " + e + ")";
+        Idx I;
+        I.key = "cc" + std::to_string(v) + "(" + idxs_[id].key + ")";
+        I.shape = prog_.type(op.operands[0]).dims;
+        I.multi = m;
+        I.multi[cd] = e;
+        return define(R, value(op.operands[0], add_index(I)));
+      }
       std::vector<std::string> vals;
       std::vector<int64_t> ends;
       int64_t off = 0;
@@ -2060,16 +2078,36 @@ void KernelGen::gemv(Step& s) {
     out_ << "__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"workgroup\");\n";
     out_ << "if (!fused_mode) __threadfence();\n";
     if (g.joint) {
-      out_ << "for (uint32_t i = threadIdx.x; i < " << G * M * S << "u; i += 256u) {\n";
-      out_ << "const uint32_t gv_g = i / " << M * S << "u, rem = i % " << M * S << "u;\n";
-      out_ << "const uint32_t m = rem / " << S << "u, c = rem % " << S << "u;\n";
-      out_ << "const size_t base = (size_t)c_seg * " << g.wps << "u + ((size_t)gv_g * " << tps << "u + c / " << C
-           << "u) * " << g.ksplit << "u;\n";
-      out_ << "float sum = 0.0f;\n";
-      out_ << "#pragma unroll\nfor (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += "
-           << ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) + "u + c % " +
-                 std::to_string(C) + "u]")
-           << ";\n";
+      // Up to Q passes of 256 threads over the segment's elements. When the
+      // partials of every pass fit in registers, all of them are requested
+      // first (one L2 round trip instead of one per pass), then summed in
+      // the same K-chunk order.
+      const int64_t n_el = G * M * S, Q = (n_el + 255) / 256;
+      const bool batched = Q > 1 && Q * g.ksplit <= 64;
+      const std::string decode = "const uint32_t gv_g = i / " + std::to_string(M * S) + "u, rem = i % " +
+                                 std::to_string(M * S) + "u;\nconst uint32_t m = rem / " + std::to_string(S) +
+                                 "u, c = rem % " + std::to_string(S) + "u;\nconst size_t base = (size_t)c_seg * " +
+                                 std::to_string(g.wps) + "u + ((size_t)gv_g * " + std::to_string(tps) + "u + c / " +
+                                 std::to_string(C) + "u) * " + std::to_string(g.ksplit) + "u;\n";
+      const std::string part = ld("gv_part[((base + k) * " + std::to_string(M) + "u + m) * " + std::to_string(C) +
+                                  "u + c % " + std::to_string(C) + "u]");
+      if (batched) {
+        out_ << "float gv_pv[" << Q << "][" << g.ksplit << "];\n";
+        out_ << "#pragma unroll\nfor (int q = 0; q < " << Q << "; ++q) {\n";
+        out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)q;\n";
+        out_ << "if (i < " << n_el << "u) {\n" << decode;
+        out_ << "#pragma unroll\nfor (uint32_t k = 0; k < " << g.ksplit << "u; ++k) gv_pv[q][k] = " << part << ";\n";
+        out_ << "}\n}\n";
+        out_ << "#pragma unroll\nfor (int q = 0; q < " << Q << "; ++q) {\n";
+        out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)q;\n";
+        out_ << "if (i >= " << n_el << "u) continue;\n" << decode;
+        out_ << "float sum = 0.0f;\n";
+        out_ << "#pragma unroll\nfor (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += gv_pv[q][k];\n";
+      } else {
+        out_ << "for (uint32_t i = threadIdx.x; i < " << n_el << "u; i += 256u) {\n" << decode;
+        out_ << "float sum = 0.0f;\n";
+        out_ << "#pragma unroll\nfor (uint32_t k = 0; k < " << g.ksplit << "u; ++k) sum += " << part << ";\n";
+      }
       out_ << "const uint32_t col = c_seg * " << S << "u + c;\n";
       out_ << "float y = 0.0f;\n";
       for (int m = 0; m < G; ++m) {
