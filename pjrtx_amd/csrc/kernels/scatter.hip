@@ -396,15 +396,24 @@ __global__ void __launch_bounds__(256) scatter_hot_classify(const uint32_t* __re
                                                             uint4* __restrict__ init_dst, int64_t row_u4,
                                                             const uint32_t* __restrict__ early) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
-  const uint32_t len = seg_end[r] - seg_start[r];
-  if (len <= (uint32_t)kHotMinUpdates) return;
-  if (is_early_row(early, r)) return;
-  const int k = 31 - __clz(len);
-  const uint32_t slot = atomicAdd(&h.counts[k], 1u);  // order inside a class does not change results
-  h.rows[h.base[k] + slot] = (uint32_t)r;
-  if (init_src)
-    for (int64_t j = 0; j < row_u4; ++j) init_dst[r * row_u4 + j] = init_src[r * row_u4 + j];
+  const uint32_t len = r < rows ? seg_end[r] - seg_start[r] : 0u;
+  const bool hot = len > (uint32_t)kHotMinUpdates && !is_early_row(early, r);
+  if (hot) {
+    const int k = 31 - __clz(len);
+    const uint32_t slot = atomicAdd(&h.counts[k], 1u);  // order inside a class does not change results
+    h.rows[h.base[k] + slot] = (uint32_t)r;
+  }
+  if (!init_src) return;
+  // The wave copies its hot rows one after the other, 16 bytes a lane (one
+  // thread copying a whole row serialised the row's loads).
+  const int lane = threadIdx.x & 63;
+  uint64_t m = __ballot(hot);
+  while (m) {
+    const int l = __ffsll((unsigned long long)m) - 1;
+    m &= m - 1;
+    const int64_t rr = (int64_t)blockIdx.x * 256 + (threadIdx.x & ~63) + l;
+    for (int64_t j = lane; j < row_u4; j += 64) init_dst[rr * row_u4 + j] = init_src[rr * row_u4 + j];
+  }
 }
 
 // Integer add / max / min on hot rows: exact in any order, so a row's updates
