@@ -377,9 +377,6 @@ __device__ __forceinline__ V load_once(const V* p) {
   else return *p;
 }
 
-// Lists the hot rows by length class. With `init_src`, also copies each hot
-// row of the operand into the result (the integer chunk path accumulates
-// into it with atomics).
 // True when row r is one of the early rows (folded before the sort ends).
 __device__ __forceinline__ bool is_early_row(const uint32_t* __restrict__ early, int64_t r) {
   if (!early) return false;
@@ -390,9 +387,13 @@ __device__ __forceinline__ bool is_early_row(const uint32_t* __restrict__ early,
   return hit;
 }
 
+// Lists the hot rows by length class. With `init_dst` (the integer chunk
+// path, which merges into the result with atomics, when the result is not
+// the operand's own buffer), also fills each hot row of the result with the
+// reduction's identity; the row's first chunk folds the operand row in.
 __global__ void __launch_bounds__(256) scatter_hot_classify(const uint32_t* __restrict__ seg_start,
                                                             const uint32_t* __restrict__ seg_end, int64_t rows,
-                                                            ScatterHotList h, const uint4* __restrict__ init_src,
+                                                            ScatterHotList h, uint4 identity,
                                                             uint4* __restrict__ init_dst, int64_t row_u4,
                                                             const uint32_t* __restrict__ early) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -403,16 +404,16 @@ __global__ void __launch_bounds__(256) scatter_hot_classify(const uint32_t* __re
     const uint32_t slot = atomicAdd(&h.counts[k], 1u);  // order inside a class does not change results
     h.rows[h.base[k] + slot] = (uint32_t)r;
   }
-  if (!init_src) return;
-  // The wave copies its hot rows one after the other, 16 bytes a lane (one
-  // thread copying a whole row serialised the row's loads).
+  if (!init_dst) return;
+  // The wave fills its hot rows, 16 bytes a lane (stores only: nothing to
+  // wait for, where copying the operand rows waited on each row's loads).
   const int lane = threadIdx.x & 63;
   uint64_t m = __ballot(hot);
   while (m) {
     const int l = __ffsll((unsigned long long)m) - 1;
     m &= m - 1;
     const int64_t rr = (int64_t)blockIdx.x * 256 + (threadIdx.x & ~63) + l;
-    for (int64_t j = lane; j < row_u4; j += 64) init_dst[rr * row_u4 + j] = init_src[rr * row_u4 + j];
+    for (int64_t j = lane; j < row_u4; j += 64) init_dst[rr * row_u4 + j] = identity;
   }
 }
 
@@ -452,7 +453,7 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
                                                           const uint32_t* __restrict__ perm,
                                                           const uint32_t* __restrict__ seg_start,
                                                           const uint32_t* __restrict__ seg_end, ScatterHotList h,
-                                                          T* __restrict__ out) {
+                                                          const T* __restrict__ operand_init, T* __restrict__ out) {
   constexpr int VEC = 16 / (int)sizeof(T);
   typedef VecOf<T, VEC> V;
   __shared__ V part[3][64];
@@ -485,6 +486,12 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
       const bool col_ok = c0 < row_elems;
       V acc;
       bool any = false;
+      // With operand_init (the result rows hold the identity), wave 0 of
+      // the row's first chunk starts from the operand row.
+      if (operand_init && chunk == 0 && wave == 0 && col_ok) {
+        acc = *reinterpret_cast<const V*>(operand_init + (int64_t)row * row_elems + c0);
+        any = true;
+      }
       // Wave w folds rows w, w + 4, ...; kFoldDepth of them per batch, the
       // next batch's loads issued before the current batch is folded.
       V ua[kFoldDepth], ub[kFoldDepth];
@@ -1080,11 +1087,21 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
   // chunks merged with atomics instead of sequential column chains.
   const bool int_type = t == DType::kS32 || t == DType::kU32 || t == DType::kS64;
   const bool chunked = int_type && (op == ScatterOp::kAdd || op == ScatterOp::kMax || op == ScatterOp::kMin);
+  const bool init = chunked && operand != out;
   if (p.hot_wgs > 0) {
-    const bool init = chunked && operand != out;
+    // The identity of the chunks' reduction, as 16 bytes of the element type.
+    uint4 identity = {0u, 0u, 0u, 0u};
+    if (op != ScatterOp::kAdd) {
+      const bool mx = op == ScatterOp::kMax;
+      uint32_t w[4];
+      if (t == DType::kS32) w[0] = w[1] = w[2] = w[3] = mx ? 0x80000000u : 0x7fffffffu;
+      else if (t == DType::kU32) w[0] = w[1] = w[2] = w[3] = mx ? 0u : 0xffffffffu;
+      else w[0] = w[2] = mx ? 0u : 0xffffffffu, w[1] = w[3] = mx ? 0x80000000u : 0x7fffffffu;  // s64, little-endian
+      identity = uint4{w[0], w[1], w[2], w[3]};
+    }
     hipLaunchKernelGGL(scatter_hot_classify, dim3(blocks(rows, 256)), dim3(256), 0, s, seg_start, seg_end, rows, h,
-                       init ? static_cast<const uint4*>(operand) : nullptr, init ? static_cast<uint4*>(out) : nullptr,
-                       row_elems * static_cast<int64_t>(es) / 16, early_rows);
+                       identity, init ? static_cast<uint4*>(out) : nullptr, row_elems * static_cast<int64_t>(es) / 16,
+                       early_rows);
     check("scatter_hot_classify");
   }
   if (p.hot_wgs > 0) {
@@ -1100,7 +1117,8 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
   do {                                                                                                                \
     if constexpr (std::is_integral<StorageOf<TAG>::T>::value && OPV != ScatterOp::kSet && OPV != ScatterOp::kMul)     \
       hipLaunchKernelGGL((scatter_hot_chunks<StorageOf<TAG>::T, OPV>), gh, blk, 0, aux, row_elems,                    \
-                         (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, h, (StorageOf<TAG>::T*)out);   \
+                         (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, h,                              \
+                         init ? (const StorageOf<TAG>::T*)operand : nullptr, (StorageOf<TAG>::T*)out);               \
   } while (0)
 #define PJRTX_ROWS_OP(TAG, V, OPV)                                                                                    \
   do {                                                                                                                \
