@@ -118,12 +118,14 @@ struct ScatterFoldParams {
 };
 
 // keys2, when not null, receives a second copy of the keys.
+// `zero`: zero_n words the key kernel also zeroes (may be null).
 void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* indices, uint32_t* keys,
-                         uint32_t* vals, uint32_t* keys2 = nullptr);
+                         uint32_t* vals, uint32_t* keys2 = nullptr, uint32_t* zero = nullptr, int64_t zero_n = 0);
 // seg_start/seg_end: `rows` uint32 each; they and `extra_zero` words after
-// seg_end are zeroed by this launcher.
+// seg_end are zeroed by this launcher unless `zeroed` (the key kernel did).
 void launch_scatter_segments(hipStream_t s, const uint32_t* sorted_keys, int64_t n, uint32_t invalid,
-                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows, int64_t extra_zero = 0);
+                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows, int64_t extra_zero = 0,
+                             bool zeroed = false);
 // out = fold(operand, updates in order) per target; `operand` may equal `out`.
 void launch_scatter_fold(hipStream_t s, const ScatterFoldParams& p, DType t, const void* operand,
                          const void* updates, const uint32_t* perm, const uint32_t* seg_start,

@@ -45,10 +45,14 @@ __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int byte
 }
 
 // ------------------------------------------------------------------- keys
+// Also zeroes zero[0 .. zero_n) (the segment bounds and counters the later
+// steps fill), saving a launch.
 __global__ void __launch_bounds__(256) scatter_keys(ScatterKeyParams p, const void* __restrict__ indices,
                                                     uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
-                                                    uint32_t* __restrict__ keys2) {
+                                                    uint32_t* __restrict__ keys2, uint32_t* __restrict__ zero,
+                                                    int64_t zero_n) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t < zero_n) zero[t] = 0u;
   if (t >= p.items) return;
   const int64_t s = t / p.window_items;
   const int64_t wpos = t - s * p.window_items;
@@ -175,35 +179,23 @@ __global__ void __launch_bounds__(256) scan_tile_sums(const uint32_t* __restrict
   if (threadIdx.x == 0) sums[blockIdx.x] = red[0];
 }
 
-// In-place exclusive scan of up to 2048 values in one workgroup.
-__global__ void __launch_bounds__(256) scan_small(uint32_t* __restrict__ a, int64_t n) {
-  __shared__ uint32_t t[256];
-  uint32_t v[8];
-  uint32_t local = 0;
-  for (int j = 0; j < 8; ++j) {
-    const int64_t e = threadIdx.x * 8 + j;
-    v[j] = e < n ? a[e] : 0u;
-    local += v[j];
-  }
-  t[threadIdx.x] = local;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    const uint32_t x = threadIdx.x >= o ? t[threadIdx.x - o] : 0u;
-    __syncthreads();
-    t[threadIdx.x] += x;
-    __syncthreads();
-  }
-  uint32_t run = t[threadIdx.x] - local;
-  for (int j = 0; j < 8; ++j) {
-    const int64_t e = threadIdx.x * 8 + j;
-    if (e < n) a[e] = run;
-    run += v[j];
-  }
-}
-
+// Exclusive scan of one tile, offset by the sum of the tile sums before it
+// (at most kScanTile of them, summed by the workgroup: integers, so the
+// order does not matter).
 __global__ void __launch_bounds__(256) scan_apply(const uint32_t* __restrict__ in, uint32_t* __restrict__ out, int64_t n,
-                                                  const uint32_t* __restrict__ tile_offsets) {
+                                                  const uint32_t* __restrict__ tile_sums) {
   __shared__ uint32_t t[256];
+  __shared__ uint32_t tile_offset;
+  {
+    uint32_t pre = 0;
+    for (int64_t i = threadIdx.x; i < (int64_t)blockIdx.x; i += 256) pre += tile_sums[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) pre += __shfl_xor(pre, o);
+    if ((threadIdx.x & 63) == 0) t[threadIdx.x >> 6] = pre;
+    __syncthreads();
+    if (threadIdx.x == 0) tile_offset = t[0] + t[1] + t[2] + t[3];
+    __syncthreads();
+  }
   const int64_t base = (int64_t)blockIdx.x * kScanTile + threadIdx.x * 8;
   uint32_t v[8];
   uint32_t local = 0;
@@ -219,7 +211,7 @@ __global__ void __launch_bounds__(256) scan_apply(const uint32_t* __restrict__ i
     t[threadIdx.x] += x;
     __syncthreads();
   }
-  uint32_t run = tile_offsets[blockIdx.x] + t[threadIdx.x] - local;
+  uint32_t run = tile_offset + t[threadIdx.x] - local;
   for (int j = 0; j < 8; ++j) {
     if (base + j < n) out[base + j] = run;
     run += v[j];
@@ -975,7 +967,6 @@ void exclusive_scan(hipStream_t s, const uint32_t* in, uint32_t* out, int64_t n,
   const int64_t tiles = (n + kScanTile - 1) / kScanTile;
   PJRTX_CHECK(tiles <= kScanTile, Code::kUnimplemented, "scan too large");
   hipLaunchKernelGGL(scan_tile_sums, dim3(blocks(n, kScanTile)), dim3(256), 0, s, in, n, tmp);
-  hipLaunchKernelGGL(scan_small, dim3(1), dim3(256), 0, s, tmp, tiles);
   hipLaunchKernelGGL(scan_apply, dim3(blocks(n, kScanTile)), dim3(256), 0, s, in, out, n, tmp);
 }
 
@@ -1027,16 +1018,18 @@ void launch_radix_sort(hipStream_t s, uint32_t* keys, uint32_t* vals, uint32_t* 
 }
 
 void launch_scatter_keys(hipStream_t s, const ScatterKeyParams& p, const void* indices, uint32_t* keys, uint32_t* vals,
-                         uint32_t* keys2) {
-  if (p.items == 0) return;
-  hipLaunchKernelGGL(scatter_keys, dim3(blocks(p.items, 256)), dim3(256), 0, s, p, indices, keys, vals, keys2);
+                         uint32_t* keys2, uint32_t* zero, int64_t zero_n) {
+  if (p.items == 0 && zero_n == 0) return;
+  hipLaunchKernelGGL(scatter_keys, dim3(blocks(std::max<int64_t>(p.items, zero_n), 256)), dim3(256), 0, s, p, indices,
+                     keys, vals, keys2, zero, zero_n);
   check("scatter_keys");
 }
 
 void launch_scatter_segments(hipStream_t s, const uint32_t* sorted_keys, int64_t n, uint32_t invalid,
-                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows, int64_t extra_zero) {
+                             uint32_t* seg_start, uint32_t* seg_end, int64_t rows, int64_t extra_zero, bool zeroed) {
   // Zero with a kernel (not a memset node), so the sequence stays capturable.
-  if (seg_end == seg_start + rows) {
+  if (zeroed) {
+  } else if (seg_end == seg_start + rows) {
     hipLaunchKernelGGL(zero_u32, dim3(blocks(2 * rows + extra_zero, 256)), dim3(256), 0, s, seg_start,
                        2 * rows + extra_zero);
   } else {

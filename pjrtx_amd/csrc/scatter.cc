@@ -183,14 +183,14 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
     // The sort rewrites K in place: the early path reads its own copy of
     // the keys, written by the same key kernel.
     uint32_t* keys_copy = early.list + n;
-    launch_scatter_keys(s, p, I, K, V, keys_copy);
+    launch_scatter_keys(s, p, I, K, V, keys_copy, static_cast<uint32_t*>(seg->ptr), 2 * rows + 32);
     hipStream_t aux = dev->aux_stream();
     hip_check(hipEventRecord(dev->fork_event(), s), "hipEventRecord(scatter early fork)");
     hip_check(hipStreamWaitEvent(aux, dev->fork_event(), 0), "hipStreamWaitEvent(scatter early fork)");
     launch_scatter_early(aux, dev->side_event(), early, keys_copy, n, p.invalid, p.row_elems,
                          static_cast<int>(sop), xt.dtype, X, U, out);
   } else {
-    launch_scatter_keys(s, p, I, K, V);
+    launch_scatter_keys(s, p, I, K, V, nullptr, static_cast<uint32_t*>(seg->ptr), 2 * rows + 32);
   }
   int bits = 1;
   while ((int64_t(1) << bits) <= rows) ++bits;  // keys are in [0, rows]
@@ -198,7 +198,7 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   uint32_t* seg_start = static_cast<uint32_t*>(seg->ptr);
   uint32_t* seg_end = seg_start + rows;
   uint32_t* hot_counts = seg_end + rows;
-  launch_scatter_segments(s, K, n, p.invalid, seg_start, seg_end, rows, 32);
+  launch_scatter_segments(s, K, n, p.invalid, seg_start, seg_end, rows, 32, /*zeroed=*/true);
   if (p.row_mode) {
     // Segments longer than kHotMinUpdates fold by column slices on
     // persistent workgroups (two per CU) on the device's second stream; the
