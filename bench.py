@@ -430,6 +430,9 @@ def bench_program(a, W: Workload) -> dict:
     # client's per-call cost is left out; the Python-loop figure is reported
     # beside it.
     ms_per_step = exe.run_loop(bufs, a.steps) / a.steps
+    # The same loop through the PJRT C API (one PJRT_LoadedExecutable_Execute
+    # per step, its event and outputs destroyed), beside it.
+    pjrt_ms_per_step = exe.run_loop_pjrt(bufs, a.steps) / a.steps
     t0 = time.perf_counter()
     last = None
     for _ in range(a.steps):
@@ -462,6 +465,7 @@ def bench_program(a, W: Workload) -> dict:
                    "pct_peak_end_to_end": round(pct, 2),
                    "hbm_gbps_end_to_end": round(W.bytes / sec / 1e9, 2),
                    "kernels_per_step": sum(1 for n in names if n != "-"),
+                   "pjrt_c_api_ms_per_step": round(pjrt_ms_per_step, 5),
                    "python_client_ms_per_step": round(py_ms_per_step, 5),
                    "kernel_us": unit_table(names, unit_ms)},
         "roofline": rf,

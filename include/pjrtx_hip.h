@@ -138,6 +138,18 @@ PJRTX_HIP_API int pjrtx_executable_time_steps(struct PJRT_LoadedExecutable* exe,
 PJRTX_HIP_API int pjrtx_executable_run(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
                                        size_t num_args, int iters, double* ms_total);
 
+/* The same loop through this plugin's PJRT C API table (GetPjrtApi): each
+ * iteration is one PJRT_LoadedExecutable_Execute with a completion event,
+ * followed by PJRT_Event_Destroy and PJRT_Buffer_Destroy of its outputs, as
+ * a C PJRT client does, so the figure includes the PJRT layer's host work
+ * per call (argument structs, output buffer and event objects). Writes the
+ * wall milliseconds from a synchronized start to the synchronized end of the
+ * last call to *ms_total. Replaces the reference's steady-execute
+ * measurement (src/plugin/jax/jax_llama_like_inference.py:291-296) at the
+ * C-API level. */
+PJRTX_HIP_API int pjrtx_executable_run_pjrt(struct PJRT_LoadedExecutable* exe, struct PJRT_Buffer* const* args,
+                                            size_t num_args, int iters, double* ms_total);
+
 /* Allocation-free execute. No counterpart in the reference: it is for
  * callers that cannot allocate device memory while they run (tight serving
  * loops, harnesses that forbid hipMalloc). Its launches record no memset

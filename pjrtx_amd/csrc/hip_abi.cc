@@ -59,6 +59,8 @@ void copy_out(const std::string& s, char* out, size_t cap, size_t* needed) {
 }
 }  // namespace
 
+extern "C" const PJRT_Api* GetPjrtApi(void);
+
 extern "C" {
 
 const char* pjrtx_hip_last_error(void) { return g_last_error.c_str(); }
@@ -222,6 +224,74 @@ int pjrtx_executable_run(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* args, s
     for (int i = 0; i < iters; ++i) {
       std::shared_ptr<Event> done;
       std::vector<BufferRef> outs = exe->exe->execute(dev, in, &done, nullptr);
+    }
+    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    *ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  });
+}
+
+int pjrtx_executable_run_pjrt(PJRT_LoadedExecutable* exe, PJRT_Buffer* const* args, size_t num_args, int iters,
+                              double* ms_total) {
+  return guarded([&] {
+    PJRTX_CHECK(exe && iters > 0 && ms_total, Code::kInvalidArgument, "run_pjrt: bad arguments");
+    PJRTX_CHECK(!exe->deleted, Code::kFailedPrecondition, "run_pjrt: executable was deleted");
+    PJRTX_CHECK(args || num_args == 0, Code::kInvalidArgument, "run_pjrt: null argument array");
+    const PJRT_Api* api = GetPjrtApi();
+    Device* dev = num_args ? args[0]->buf->dev : exe->devices.at(0)->dev;
+    const size_t nout = exe->exe->program().results.size();
+    std::vector<PJRT_Buffer*> outs(std::max<size_t>(1, nout));
+    PJRT_Buffer** out_lists[1] = {outs.data()};
+    PJRT_Buffer* const* arg_lists[1] = {args};
+    PJRT_Event* events[1] = {nullptr};
+    PJRT_ExecuteOptions opts;
+    std::memset(&opts, 0, sizeof(opts));
+    opts.struct_size = PJRT_ExecuteOptions_STRUCT_SIZE;
+    PJRT_LoadedExecutable_Execute_Args a;
+    std::memset(&a, 0, sizeof(a));
+    a.struct_size = PJRT_LoadedExecutable_Execute_Args_STRUCT_SIZE;
+    a.executable = exe;
+    a.options = &opts;
+    a.argument_lists = arg_lists;
+    a.num_devices = 1;
+    a.num_args = num_args;
+    a.output_lists = out_lists;
+    a.device_complete_events = events;
+    // A PJRT error from the loop is returned as this call's status.
+    auto call = [&](PJRT_Error* e) {
+      if (!e) return;
+      PJRT_Error_Message_Args m;
+      std::memset(&m, 0, sizeof(m));
+      m.struct_size = PJRT_Error_Message_Args_STRUCT_SIZE;
+      m.error = e;
+      api->PJRT_Error_Message(&m);
+      const std::string msg(m.message, m.message_size);
+      PJRT_Error_Destroy_Args d;
+      std::memset(&d, 0, sizeof(d));
+      d.struct_size = PJRT_Error_Destroy_Args_STRUCT_SIZE;
+      d.error = e;
+      api->PJRT_Error_Destroy(&d);
+      fail(Code::kInternal, "run_pjrt: " + msg);
+    };
+    dev->make_current();
+    hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < iters; ++i) {
+      call(api->PJRT_LoadedExecutable_Execute(&a));
+      if (events[0]) {
+        PJRT_Event_Destroy_Args ed;
+        std::memset(&ed, 0, sizeof(ed));
+        ed.struct_size = PJRT_Event_Destroy_Args_STRUCT_SIZE;
+        ed.event = events[0];
+        call(api->PJRT_Event_Destroy(&ed));
+        events[0] = nullptr;
+      }
+      for (size_t k = 0; k < nout; ++k) {
+        PJRT_Buffer_Destroy_Args bd;
+        std::memset(&bd, 0, sizeof(bd));
+        bd.struct_size = PJRT_Buffer_Destroy_Args_STRUCT_SIZE;
+        bd.buffer = outs[k];
+        call(api->PJRT_Buffer_Destroy(&bd));
+      }
     }
     hip_check(hipStreamSynchronize(dev->stream()), "hipStreamSynchronize");
     *ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();

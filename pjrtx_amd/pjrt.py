@@ -230,6 +230,7 @@ class Plugin:
             "pjrtx_executable_step_names": [c_void_p, c_char_p, c_size_t, POINTER(c_size_t)],
             "pjrtx_executable_graph_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_executable_run": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double)],
+            "pjrtx_executable_run_pjrt": [c_void_p, POINTER(c_void_p), c_size_t, c_int, POINTER(c_double)],
             "pjrtx_executable_stats": [c_void_p, POINTER(c_int64)],
             "pjrtx_compile_cache_stats": [POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)],
             "pjrtx_compile_cache_usage": [POINTER(c_int64), POINTER(c_int64)],
@@ -535,6 +536,17 @@ class Executable:
         arr = (c_void_p * max(1, len(args)))(*[b.handle for b in args])
         ms = c_double(0.0)
         self.client.p.hip_check(L.pjrtx_executable_run(self.handle, arr, len(args), iters, ctypes.byref(ms)))
+        return ms.value
+
+    def run_loop_pjrt(self, args: list[Buffer], iters: int) -> float:
+        """Wall ms of `iters` executions, each a PJRT_LoadedExecutable_Execute
+        through the plugin's C API table with its event and output buffers
+        destroyed after it (pjrtx_executable_run_pjrt), synchronized on both
+        sides."""
+        L = self.client.p.lib
+        arr = (c_void_p * max(1, len(args)))(*[b.handle for b in args])
+        ms = c_double(0.0)
+        self.client.p.hip_check(L.pjrtx_executable_run_pjrt(self.handle, arr, len(args), iters, ctypes.byref(ms)))
         return ms.value
 
     def execute_noalloc(self, arg_ptrs: list[int], out_ptrs: list[int], device: int = 0) -> int:

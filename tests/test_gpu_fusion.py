@@ -168,3 +168,17 @@ def test_execute_rejects_wrong_argument(client):
     assert e.value.code == 3
     with pytest.raises(PjrtError):
         exe(np.zeros((8, 255), np.float32), np.zeros((8, 255), np.float32))
+
+
+def test_execute_loops_through_plugin_and_pjrt_c_api(client):
+    """The plugin's own execute loop and the loop through the PJRT C API table
+    (one PJRT_LoadedExecutable_Execute per step, its event and outputs
+    destroyed) both run, leave the arguments usable and time a positive
+    interval; an execute afterwards still gives the oracle's rows."""
+    x, y = ops.c1_inputs(64, 1000, seed=5)
+    exe = client.compile(programs.c1_elementwise_rowsum(64, 1000))
+    bufs = [client.buffer(x), client.buffer(y)]
+    assert exe.run_loop(bufs, 4) > 0
+    assert exe.run_loop_pjrt(bufs, 4) > 0
+    (out,) = exe.execute_buffers(bufs)
+    np.testing.assert_allclose(out.to_numpy(), ops.c1_rowsum(x, y), rtol=1e-5, atol=1e-6)
