@@ -487,16 +487,24 @@ AttnParams attention_params(const Program& prog, const Op& op) {
 
 static_assert(Device::kArrivalCounterBytes / 128 >= kAttnCounterRows, "one counter line per decode query row");
 
-void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals) {
+size_t attention_partials_bytes(const Program& prog, const Op& op) {
+  return attention_scratch_bytes(attention_params(prog, op), prog.type(op.operands[0]).dtype);
+}
+
+void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, bool partials_out) {
   AttnParams p = attention_params(prog, op);
   auto ptr = [&](int v) -> void* { return vals[v] ? vals[v]->ptr : nullptr; };
   if (op.attn.has_offset_operand) p.offset_ptr = ptr(op.operands[3]);
   const DType t = prog.type(op.operands[0]).dtype;
-  const size_t scratch_bytes = attention_scratch_bytes(p, t);
+  const size_t scratch_bytes = partials_out ? 0 : attention_scratch_bytes(p, t);
+  if (partials_out) {
+    PJRTX_CHECK(vals[op.results[0]] && vals[op.results[0]]->bytes >= attention_scratch_bytes(p, t), Code::kInternal,
+                "attention: partials output buffer too small");
+  }
   MemRef scratch = scratch_bytes ? dev->allocate(scratch_bytes) : nullptr;
   launch_attention(dev->stream(), p, t, ptr(op.operands[0]), ptr(op.operands[1]), ptr(op.operands[2]),
                    ptr(op.results[0]), scratch ? static_cast<float*>(scratch->ptr) : nullptr, dev->arrival_counters(),
-                   dev->xcd_round_robin());
+                   dev->xcd_round_robin(), partials_out);
 }
 
 }  // namespace pjrtx

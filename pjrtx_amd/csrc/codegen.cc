@@ -1983,20 +1983,42 @@ void KernelGen::gemv(Step& s) {
     const std::string X = ptr_of.at(g.x);
     const int64_t nx = all_x ? M * K : M * g.kchunk;
     const int64_t per = (nx + 255) / 256;
+    // X element i: read as is, or merged from a decode attention's split
+    // partials (M == 1). A merged element's partials are requested before
+    // the weight rows and folded after them when they fit in 96 registers a
+    // lane; otherwise each element is merged before the weight rows are
+    // requested.
+    const std::string NS = std::to_string(g.attn_splits);
+    const bool attn_late = g.attn_splits > 0 && per * g.attn_splits * 3 <= 96;
+    auto x_elem = [&](const std::string& i) {
+      if (g.attn_splits == 0) return load_expr(wt, X, i);
+      return "gv_attn_merge<" + NS + ", " + std::to_string(g.attn_dim) + ", " + (f16 ? "true" : "false") +
+             ">(reinterpret_cast<const float*>(" + X + "), " + i + ")";
+    };
+    const std::string valid = all_x ? "i < " + std::to_string(nx) + "u"
+                                    : "i < " + std::to_string(nx) + "u && k < " + std::to_string(K) + "u";
+    const std::string idx = all_x ? "i" : "m * " + std::to_string(K) + "u + k";
     out_ << "float gv_xr[" << per << "];\n";
+    if (attn_late) out_ << "float gv_am[" << per << "][" << NS << "], gv_al[" << per << "][" << NS << "], gv_av[" << per
+                        << "][" << NS << "];\n";
     out_ << "#pragma unroll\nfor (int j = 0; j < " << per << "; ++j) {\n";
     out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)j;\n";
-    if (all_x) {
-      out_ << "gv_xr[j] = i < " << nx << "u ? " << load_expr(wt, X, "i") << " : 0.0f;\n";
+    if (!all_x) out_ << "const uint32_t m = i / " << g.kchunk << "u, k = c_k0 + i % " << g.kchunk << "u;\n";
+    if (attn_late) {
+      out_ << "if (" << valid << ") gv_attn_load<" << NS << ", " << g.attn_dim << ">(reinterpret_cast<const float*>(" << X
+           << "), " << idx << ", gv_am[j], gv_al[j], gv_av[j]);\n";
     } else {
-      out_ << "const uint32_t m = i / " << g.kchunk << "u, k = c_k0 + i % " << g.kchunk << "u;\n";
-      out_ << "gv_xr[j] = (i < " << nx << "u && k < " << K << "u) ? "
-           << load_expr(wt, X, "m * " + std::to_string(K) + "u + k") << " : 0.0f;\n";
+      out_ << "gv_xr[j] = (" << valid << ") ? " << x_elem(idx) << " : 0.0f;\n";
     }
     out_ << "}\n";
     load_batch("c_", "0u", "gv_wv");
     out_ << "#pragma unroll\nfor (int j = 0; j < " << per << "; ++j) {\n";
     out_ << "const uint32_t i = threadIdx.x + 256u * (uint32_t)j;\n";
+    if (attn_late) {
+      if (!all_x) out_ << "const uint32_t k = c_k0 + i % " << g.kchunk << "u;\n";
+      out_ << "gv_xr[j] = (" << valid << ") ? gv_attn_fold<" << NS << ", " << (f16 ? "true" : "false")
+           << ">(gv_am[j], gv_al[j], gv_av[j]) : 0.0f;\n";
+    }
     out_ << "if (i < " << nx << "u) gv_xs[i] = gv_xr[j];\n}\n";
     out_ << "__syncthreads();\n";
   }

@@ -19,8 +19,12 @@
 #include <set>
 
 #include "planner.h"
+#include "kernels/attention.h"
 
 namespace pjrtx {
+
+AttnParams attention_params(const Program& prog, const Op& op);  // attention.cc
+
 namespace {
 
 std::map<int, int> producers_of(const std::vector<Step>& steps) {
@@ -204,6 +208,10 @@ class GemvFuser {
       s.name = strformat("pjrtx_gemv_%d", id++);
     }
     plan_.num_fusion_kernels += id;
+    if (opts_.attn_merge_in_gemv) {
+      for (Step& s : steps_)
+        if (s.kind == StepKind::kGemv) merge_attention_splits(&s);
+    }
     keep_weights_in_mall();
     releases();
   }
@@ -500,6 +508,46 @@ class GemvFuser {
     }
     s->grid = static_cast<uint32_t>(g.wgs);
     s->block = 256;
+  }
+
+  // A GEMV without prologue whose LHS is, through layout-preserving aliases
+  // only, the output of a split decode attention with one query row per head
+  // (the o-projection of a decode step), and the only reader of each value on
+  // the way: the attention writes its split partials instead of the rows and
+  // the GEMV merges them while staging X. The attention launch then ends with
+  // its partial stores (no arrival count, no merge round trips), and the
+  // GEMV's X reads, issued before its weight rows as before, fetch the
+  // partials instead. Up to 16 splits (the merge keeps each split's m, l and
+  // value in registers).
+  void merge_attention_splits(Step* G) {
+    GemvSpec& g = G->gemv;
+    if (!G->prologue.empty() || g.M != 1) return;
+    auto v2s = producers_of(steps_);
+    int v = g.x;
+    for (;;) {
+      auto it = v2s.find(v);
+      if (it == v2s.end() || outputs_.count(v) || readers(v) != 1) return;
+      const Step& P = steps_[it->second];
+      if (P.kind == StepKind::kAlias) {
+        v = P.inputs[0];
+        continue;
+      }
+      if (P.kind != StepKind::kLibrary || P.lib != LibKind::kAttention || P.outputs != std::vector<int>{v}) return;
+      const Op& op = prog_.ops[P.lib_op];
+      const AttnParams ap = attention_params(prog_, op);
+      const DType t = prog_.type(op.operands[0]).dtype;
+      int nsplit = 1, per = 0;
+      if (attention_path(ap, t, &nsplit, &per) != AttnPath::kDecode || nsplit < 2 || nsplit > 16) return;
+      // Row r = head r (one batch, one query); X's flat element k is output
+      // element (head k / D, column k % D), the rows D apart.
+      if (ap.B != 1 || ap.Sq != 1 || ap.o_h != ap.D || static_cast<int64_t>(ap.Hq) * ap.D != g.K) return;
+      if (prog_.type(op.results[0]).dtype != prog_.type(g.x).dtype) return;
+      if (t != DType::kBF16 && t != DType::kF16) return;
+      steps_[it->second].attn_partials = true;
+      g.attn_splits = nsplit;
+      g.attn_dim = ap.D;
+      return;
+    }
   }
 
   // The smallest GEMV weights, up to opts_.gemv_mall_mb in all, keep plain

@@ -51,8 +51,14 @@ size_t attention_scratch_bytes(const AttnParams& p, DType t);
 // device runs workgroup b on XCD b % 8) and `counters` (arrival counters, one
 // per 128 bytes, zero on entry and left zero) covers the query rows (at most
 // kAttnCounterRows); otherwise a second kernel merges them.
+//
+// `partials_out` (split decode path only, attention_scratch_bytes > 0): `out`
+// receives the split partials instead of the output rows, as floats [row]
+// [split][m, l, D unnormalized outputs] with l = -1 for a split past the
+// row's last allowed key, for a reader that merges them itself (a decode
+// GEMV whose input is this output); `scratch` is not used.
 constexpr int64_t kAttnCounterRows = 8192;
 void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
-                      void* out, float* scratch, uint32_t* counters, bool xcd_local);
+                      void* out, float* scratch, uint32_t* counters, bool xcd_local, bool partials_out = false);
 
 }  // namespace pjrtx

@@ -774,14 +774,22 @@ __global__ void __launch_bounds__(256) attn_rows(AttnParams p, const T* __restri
 // key exit at once.
 //
 // One split: the workgroup writes the row. Otherwise each split writes
-// (m, l, unnormalized O) to `part`; with `fused` (workgroup b runs on XCD
+// (m, l, unnormalized O) to `part`; in fused mode (workgroup b runs on XCD
 // b % 8 and the row's splits were placed on one XCD) the split counts its
 // arrival on the row's L2 counter once its stores are acknowledged by that
 // L2, and the last to arrive merges the splits in split order (reading past
 // its L1) and puts the counter back to zero; without it attn_combine, launched
 // next, merges them the same way. The merge order is fixed, so the result
 // does not depend on which split arrives last.
+//
+// Partials mode (`mode` kDecodePartials): `part` is the step's output. Every
+// split writes its (m, l, unnormalized O), one split included, and the
+// splits past the row's last allowed key write l = -1 (a sum of exponentials
+// is never negative) and exit, so the reader (a decode GEMV staging its
+// input) merges the splits whose l is not -1, in split order, with the same
+// arithmetic as merge_splits.
 constexpr int DK = 64;
+constexpr int kDecodeCombine = 0, kDecodeFused = 1, kDecodePartials = 2;
 constexpr int kCounterStride = 32;  // uint32 per arrival counter: one 128-byte line each
 
 template <typename T>
@@ -863,7 +871,7 @@ template <typename T, int NCH, int DKT>
 __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __restrict__ Q, const T* __restrict__ K,
                                                    const T* __restrict__ V, T* __restrict__ O, float* __restrict__ part,
                                                    int keys_per_split, int nsplit, uint32_t* __restrict__ counters,
-                                                   int fused) {
+                                                   int mode) {
   constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte piece
   constexpr int D = NCH * EPC;
   constexpr int LPK = 256 / DKT;       // lanes per key in the scores (4 for 64-key passes, 8 for 32)
@@ -916,7 +924,10 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
   }
   const int nkeys = key_limit(p, read_offset(p), q) + 1;
   const int nact = nkeys <= 0 ? 1 : (nkeys + keys_per_split - 1) / keys_per_split;
-  if (split >= nact) return;
+  if (split >= nact) {
+    if (mode == kDecodePartials && tid == 0) part[((int64_t)row * nsplit + split) * (D + 2) + 1] = -1.f;
+    return;
+  }
   float qv[CPT * EPC];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
@@ -999,7 +1010,7 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
     for (int gg = 0; gg < G; ++gg) acc += ow[gg][tid];
   }
   T* orow = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s;
-  if (nact == 1) {
+  if (nact == 1 && mode != kDecodePartials) {
     if (tid < D) orow[tid] = Elem<T>::put(acc / l);
     return;
   }
@@ -1009,7 +1020,7 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
     pr[(int64_t)split * (D + 2)] = m;
     pr[(int64_t)split * (D + 2) + 1] = l;
   }
-  if (!fused) return;
+  if (mode != kDecodeFused) return;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are in the L2
   __syncthreads();
   if (tid == 0) {
@@ -1051,16 +1062,15 @@ bool decode_fits(const AttnParams& p) {
 
 template <typename T>
 void launch_decode(hipStream_t s, const AttnParams& p, const T* q, const T* k, const T* v, T* o, float* part,
-                   int nsplit, int keys_per_split, uint32_t* counters, bool fused) {
+                   int nsplit, int keys_per_split, uint32_t* counters, int mode) {
   constexpr int EPC = 16 / sizeof(T);
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
   const dim3 grid(static_cast<uint32_t>(8 * ((rows + 7) / 8) * nsplit)), block(256);
-  const int f = fused ? 1 : 0;
   // 32-key passes for splits that are not whole 64-key passes (K rows of at
   // least 8 pieces, so a key's 8 lanes each take whole pieces).
   const bool half = keys_per_split % DK != 0;
 #define PJRTX_DEC(NC, DKT) \
-  hipLaunchKernelGGL((attn_decode<T, NC, DKT>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, f)
+  hipLaunchKernelGGL((attn_decode<T, NC, DKT>), grid, block, 0, s, p, q, k, v, o, part, keys_per_split, nsplit, counters, mode)
   switch (p.D / EPC) {
     case 4: PJRTX_DEC(4, 64); break;
     case 8: if (half) PJRTX_DEC(8, 32); else PJRTX_DEC(8, 64); break;
@@ -1068,7 +1078,7 @@ void launch_decode(hipStream_t s, const AttnParams& p, const T* q, const T* k, c
     default: if (half) PJRTX_DEC(32, 32); else PJRTX_DEC(32, 64); break;
   }
 #undef PJRTX_DEC
-  if (nsplit > 1 && !fused)
+  if (nsplit > 1 && mode == kDecodeCombine)
     hipLaunchKernelGGL((attn_combine<T>), dim3(static_cast<uint32_t>(rows)), dim3(std::max(64, p.D)), 0, s, p, part,
                        nsplit, keys_per_split, o);
 }
@@ -1133,7 +1143,7 @@ size_t attention_scratch_bytes(const AttnParams& p, DType t) {
 }
 
 void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q, const void* K, const void* V,
-                      void* out, float* scratch, uint32_t* counters, bool xcd_local) {
+                      void* out, float* scratch, uint32_t* counters, bool xcd_local, bool partials_out) {
   PJRTX_CHECK(p.B >= 1 && p.Hq >= 1 && p.Hkv >= 1 && p.Hq % p.Hkv == 0 && p.D >= 1 && p.Sq >= 0 && p.Skv >= 0,
               Code::kInvalidArgument, "attention: bad shape");
   PJRTX_CHECK(p.D <= 512, Code::kUnimplemented, "attention: head dim above 512");
@@ -1144,20 +1154,24 @@ void launch_attention(hipStream_t s, const AttnParams& p, DType t, const void* Q
   if (path == AttnPath::kDecode) {
     PJRTX_CHECK(static_cast<int64_t>(p.B) * p.Hq * p.Sq < (int64_t(1) << 31), Code::kUnimplemented,
                 "attention: too many query rows");
+    PJRTX_CHECK(!partials_out || nsplit > 1, Code::kInternal, "attention: partials output without key splits");
+    if (partials_out) scratch = static_cast<float*>(out);
     PJRTX_CHECK(nsplit == 1 || scratch != nullptr, Code::kInternal, "attention: split decode needs scratch");
     const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-    const bool fused = xcd_local && counters != nullptr && rows <= kAttnCounterRows;
+    const int mode = partials_out ? kDecodePartials
+                      : xcd_local && counters != nullptr && rows <= kAttnCounterRows ? kDecodeFused
+                                                                                      : kDecodeCombine;
     if (t == DType::kF32)
       launch_decode<float>(s, p, static_cast<const float*>(Q), static_cast<const float*>(K),
-                           static_cast<const float*>(V), static_cast<float*>(out), scratch, nsplit, per, counters, fused);
+                           static_cast<const float*>(V), static_cast<float*>(out), scratch, nsplit, per, counters, mode);
     else if (t == DType::kBF16)
       launch_decode<uint16_t>(s, p, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
                               static_cast<const uint16_t*>(V), static_cast<uint16_t*>(out), scratch, nsplit, per,
-                              counters, fused);
+                              counters, mode);
     else
       launch_decode<_Float16>(s, p, static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
                               static_cast<const _Float16*>(V), static_cast<_Float16*>(out), scratch, nsplit, per,
-                              counters, fused);
+                              counters, mode);
   } else if (path == AttnPath::kTiles) {
     const int64_t grid = static_cast<int64_t>(p.B) * p.Hq * ((p.Sq + FQ - 1) / FQ);
     PJRTX_CHECK(grid < (int64_t(1) << 31), Code::kUnimplemented, "attention: too many query tiles");

@@ -357,6 +357,50 @@ PJRTX_DEV void gv_fma8(float* acc, float x, const gv_u32x4& w) {
     acc[2 * q + 1] = __builtin_fmaf(x, hi, acc[2 * q + 1]);
   }
 }
+// X element k of a decode GEMV whose input is a split decode attention's
+// partials (floats [head][split][m, l, D unnormalized values]; l = -1 marks
+// a split past the row's last allowed key): gv_attn_load requests the
+// element's m, l and value of every split (so a kernel can issue its weight
+// loads before waiting for them); gv_attn_fold merges the splits in split
+// order with the attention kernel's own merge arithmetic (max of m; weights
+// exp(m - max); sums of l and of the values times the weights; one
+// division) and rounds to the 16-bit input type.
+template <int NS, int D>
+PJRTX_DEV void gv_attn_load(const float* __restrict__ part, uint32_t k, float (&ms)[NS], float (&ls)[NS],
+                            float (&vs)[NS]) {
+  const float* pr = part + (size_t)(k / D) * NS * (D + 2);
+  const uint32_t d = k % D;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    ms[u] = pr[u * (D + 2)];
+    ls[u] = pr[u * (D + 2) + 1];
+    vs[u] = pr[u * (D + 2) + 2 + d];
+  }
+}
+template <int NS, bool kF16>
+PJRTX_DEV float gv_attn_fold(const float (&ms)[NS], const float (&ls)[NS], const float (&vs)[NS]) {
+  float mall = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+    if (ls[u] != -1.f) mall = fmaxf(mall, ms[u]);
+  const float mref = mall == -__builtin_inff() ? 0.f : mall;
+  float lsum = 0.f, acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    if (ls[u] != -1.f) {
+      const float f = expf(ms[u] - mref);
+      lsum += ls[u] * f;
+      acc += vs[u] * f;
+    }
+  }
+  return kF16 ? round_f16(acc / lsum) : round_bf16(acc / lsum);
+}
+template <int NS, int D, bool kF16>
+PJRTX_DEV float gv_attn_merge(const float* __restrict__ part, uint32_t k) {
+  float ms[NS], ls[NS], vs[NS];
+  gv_attn_load<NS, D>(part, k, ms, ls, vs);
+  return gv_attn_fold<NS, kF16>(ms, ls, vs);
+}
 
 // ------------------------------------------------------ wavefront reductions
 // 64-lane wavefronts: xor-butterfly over lane offsets 32..1. Every lane ends

@@ -185,7 +185,7 @@ GatherParams make_gather_params(const Program& prog, const Op& op) {
 
 void run_dot_general(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
 void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
-void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals);
+void run_attention(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, bool partials_out);
 void run_dot_group(Device* dev, const Program& prog, const std::vector<int>& ops, std::vector<MemRef>& vals);
 void run_dot_residual(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>& vals, int add, int out);
 
@@ -254,7 +254,7 @@ void run_library_step(Device* dev, const Program& prog, const Step& step, std::v
       run_scatter(dev, prog, op, vals);
       return;
     case LibKind::kAttention:
-      run_attention(dev, prog, op, vals);
+      run_attention(dev, prog, op, vals, step.attn_partials);
       return;
     case LibKind::kDotGroup:
       run_dot_group(dev, prog, step.group_ops, vals);

@@ -1356,6 +1356,7 @@ std::string Plan::describe(const Program& prog) const {
       o << "]";
       for (size_t m = 0; m < g.add.size(); ++m)
         if (g.add[m] >= 0) o << ",\"residual_add\":" << g.add[m];
+      if (g.attn_splits) o << ",\"attention_splits_merged\":" << g.attn_splits;
     }
     if (s.kind == StepKind::kReduce) {
       o << ",\"reducers\":[";
@@ -1397,6 +1398,7 @@ std::string Plan::describe(const Program& prog) const {
         o << ",\"flops\":" << 4 * q.elements() * skv << ",\"effective_flops\":" << 4 * (q.elements() / sq) * pairs
           << ",\"causal\":" << (d.attn.causal ? "true" : "false")
           << ",\"q_coef\":" << d.attn.q_coef << ",\"offset\":" << d.attn.offset
+          << ",\"partials_out\":" << (s.attn_partials ? "true" : "false")
           << ",\"offset_operand\":" << (d.attn.has_offset_operand ? "true" : "false") << ",\"scale\":" << strformat("%.17g", d.attn.scale)
           << ",\"layout\":" << d.attn.layout;
       }

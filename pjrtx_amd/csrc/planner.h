@@ -87,6 +87,11 @@ struct GemvSpec {
   int64_t wgs = 0;                          // workgroups launched (8 per XCD round)
   bool stage_all_x = false;                 // whole X in LDS (else each workgroup's one chunk)
   bool weights_nt = true;                   // weights read with non-temporal loads
+  // x is a split decode attention's partials output (M == 1, one query
+  // row per head): element k is head k / attn_dim, column k % attn_dim,
+  // merged over attn_splits splits while X is staged. 0: x is read as is.
+  int attn_splits = 0;
+  int attn_dim = 0;
 };
 
 struct Step {
@@ -124,6 +129,10 @@ struct Step {
   // dynamic_update_slice whose operand dies here: the update is written into
   // the operand's buffer, which becomes the result (no copy).
   bool in_place = false;
+  // kAttention on the split decode path whose only reader is a kGemv that
+  // merges the splits: the output buffer holds the split partials
+  // (attention_partials_bytes), not the output rows.
+  bool attn_partials = false;
 
   // launch geometry of generated kernels
   uint32_t grid = 1;
@@ -222,6 +231,11 @@ struct PlanOptions {
   // cache (MALL, 256 MB) from one execute to the next. C5 decode, tokens/s:
   // 0 MB 2581, 64 MB 2594, 100 MB 2598, 160 MB 2553, 200 MB 2545.
   int64_t gemv_mall_mb = env_int("PJRTX_GEMV_MALL_MB", 96);
+  // A decode GEMV whose input is a split decode attention's output merges
+  // the attention's splits itself while staging its input, so the attention
+  // launch ends after its partial stores (environment:
+  // PJRTX_ATTN_MERGE_GEMV, 0 keeps the merge in the attention launch).
+  bool attn_merge_in_gemv = env_int("PJRTX_ATTN_MERGE_GEMV", 1) != 0;
 };
 
 Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
@@ -237,6 +251,10 @@ void rewrite_program(Program* prog);
 // (gemv_fusion.cc). Runs on a finished plan (after liveness); recomputes the
 // releases. `outputs` are the program's result values.
 void fuse_gemv_steps(const Program& prog, Plan* plan, const std::set<int>& outputs, const PlanOptions& opts);
+
+// Bytes of the split partials a kAttention op writes on the split decode
+// path (0 on the other paths) (attention.cc).
+size_t attention_partials_bytes(const Program& prog, const Op& op);
 
 // Emits the HIP source of every generated step (codegen.cc).
 std::string generate_kernels(const Program& prog, Plan& plan);

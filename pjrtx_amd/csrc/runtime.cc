@@ -927,6 +927,8 @@ void Executable::run_step(Loaded* L, size_t si, std::vector<MemRef>& vals, int p
       }
       if (s.in_place) {
         vals[s.outputs[0]] = vals[prog_.ops[s.lib_op].operands[0]];
+      } else if (s.attn_partials) {
+        vals[s.outputs[0]] = dev->allocate(attention_partials_bytes(prog_, prog_.ops[s.lib_op]));
       } else {
         for (int v : s.outputs) vals[v] = dev->allocate(prog_.type(v).bytes());
       }

@@ -245,3 +245,61 @@ def test_full_decode_loop_in_one_execute_matches_per_step(full):
     per_step, _, _ = runner.generate(prompt, 16)
     looped, _ = runner.generate_in_one_execute(prompt, 16)
     np.testing.assert_array_equal(looped, per_step)
+
+
+# Caches of 200 slots: the decode attention splits each head's keys over 4
+# workgroups of 64 keys, so the o-projection GEMV merges the attention's
+# split partials (positions 60..69 go from one active split to two).
+SPLIT = L.LlamaConfig(layers=2, d_model=128, heads=4, head_dim=32, ffn=320, vocab=512, max_len=200, prompt=60,
+                      new_tokens=10)
+
+
+def test_split_decode_attention_merged_in_gemv_matches_oracle(client):
+    import json
+    plan = json.loads(client.compile(L.decode_program(SPLIT)).optimized_program())
+    assert sum(bool(s.get("partials_out")) for s in plan["steps"]) == SPLIT.layers
+    assert sum(s.get("attention_splits_merged") == 4 for s in plan["steps"]) == SPLIT.layers
+    w = L.init_weights(SPLIT, seed=0)
+    runner = L.LlamaRunner(client, SPLIT, w)
+    W = O.weights_f32(SPLIT, w)
+    for seed in (1, 2):
+        prompt = L.prompt_tokens(SPLIT, seed=seed)
+        toks, _, logits = runner.generate(prompt, SPLIT.new_tokens, keep_logits=True)
+        _, forced_logits = O.generate(SPLIT, W, prompt, SPLIT.new_tokens, forced=toks[:-1])
+        for i in range(SPLIT.new_tokens):
+            _check_step(O.bf16_bits_to_f32(logits[i])[0], forced_logits[i], int(toks[i]))
+
+
+@pytest.mark.parametrize("env", [{}, {"PJRTX_GEMV_PERSIST": "1", "PJRTX_GEMV_PWGS": "256"}],
+                         ids=["chunk_x", "whole_x"])
+def test_full_decode_attention_merge_in_gemv_is_bit_exact(full, client, monkeypatch, env):
+    """The o-projection GEMV's merge of the attention's split partials gives
+    the same bits as the attention launch's own merge: every output of a
+    decode step (token, logits, caches) at positions with one split active
+    (0, 5, 63), with two (64, 65), with several (300) and with all ten (639),
+    over random caches. `whole_x` stages all of X per workgroup (persistent
+    GEMV items) instead of the workgroup's K chunk."""
+    import json
+    runner, _ = full
+    cfg = L.FULL
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    merged = client.compile(L.decode_program(cfg))
+    plan = json.loads(merged.optimized_program())
+    oproj = [s for s in plan["steps"] if s.get("attention_splits_merged")]
+    assert len(oproj) == cfg.layers and all(s["attention_splits_merged"] == 10 for s in oproj)
+    assert all(s["stage_all_x"] == bool(env) for s in oproj)
+    monkeypatch.setenv("PJRTX_ATTN_MERGE_GEMV", "0")
+    own = client.compile(L.decode_program(cfg))
+    assert not any(s.get("partials_out") for s in json.loads(own.optimized_program())["steps"])
+    rng = np.random.default_rng(11)
+    caches = [client.buffer(L.f32_to_bf16_bits(rng.standard_normal(L.cache_shape(cfg)).astype(np.float32)), "bf16")
+              for _ in range(2 * cfg.layers)]
+    tok = client.buffer(np.array([17], np.int32))
+    for pos in (0, 5, 63, 64, 65, 300, 639):
+        args = runner.weights + [tok, client.buffer(np.array(pos, np.int32))] + caches
+        keep = list(range(len(args)))
+        a = merged.execute_buffers(args, non_donatable=keep)
+        b = own.execute_buffers(args, non_donatable=keep)
+        for i, (x, y) in enumerate(zip(a, b)):
+            np.testing.assert_array_equal(x.to_numpy(), y.to_numpy(), err_msg=f"position {pos}, output {i}")

@@ -238,6 +238,25 @@ def test_decode_layer_is_five_launches(plugin):
     assert len(units) <= 5 * L.FULL.layers + 5
     # Every split GEMV folds in-launch (no combine kernel).
     assert all(s["direct"] or s["fused_combine"] for s in gemv)
+    # The attention writes its 10 key splits' partials and the o-projection
+    # merges them while staging its input.
+    attn = [s for s in steps if s.get("library") == "attention"]
+    assert len(attn) == L.FULL.layers and all(s["partials_out"] for s in attn)
+    oproj = [s for s in gemv if s.get("attention_splits_merged")]
+    assert len(oproj) == L.FULL.layers
+    assert all(s["attention_splits_merged"] == 10 and s["members"] == 1 and "residual_add" in s for s in oproj)
+
+
+def test_attention_merge_stays_in_attention_without_splits_or_when_off(plugin, monkeypatch):
+    """40-slot caches give one key split: nothing to merge, the attention
+    writes its rows. PJRTX_ATTN_MERGE_GEMV=0 keeps the merge in the attention
+    launch."""
+    from pjrtx_amd import llama_like as L
+    steps = plan(plugin, L.decode_program(L.TINY))["steps"]
+    assert not any(s.get("partials_out") or s.get("attention_splits_merged") for s in steps)
+    monkeypatch.setenv("PJRTX_ATTN_MERGE_GEMV", "0")
+    steps = plan(plugin, L.decode_program(L.FULL))["steps"]
+    assert not any(s.get("partials_out") or s.get("attention_splits_merged") for s in steps)
 
 
 def test_gemv_epilogue_must_stay_inside_segments(plugin):
