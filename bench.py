@@ -322,9 +322,9 @@ def profile_unit_us(workload: str, unit: str):
     of this workload records (its `rocprof_unit_us <unit> <us> [route]` line:
     the unit's kernels' total duration over the run divided by the unit's
     calls), so that `frac` can be recomputed from the profile. A plain GEMM
-    has two routes (hipBLASLt unless PJRTX_BLASLT=0, else the own kernels),
+    has two routes (the own kernels, or hipBLASLt with PJRTX_BLASLT=1),
     each with its own summary."""
-    route = "own" if os.environ.get("PJRTX_BLASLT", "1") == "0" else "blaslt"
+    route = "blaslt" if os.environ.get("PJRTX_BLASLT", "0") == "1" else "own"
     for p in sorted((ROOT / "profiles").glob(f"*.{workload}.kernel_stats.md")):
         for ln in p.read_text().splitlines():
             parts = ln.strip().strip("`").split()
@@ -399,15 +399,21 @@ def unit_table(names, unit_ms) -> dict:
 
 def traffic_from_profiles(workload: str, kernel: str):
     """HBM bytes per launch of `kernel`, from the counter summary committed
-    under profiles/ (null when that kernel was not profiled)."""
-    p = ROOT / "profiles" / f"{workload}_traffic.json"
-    if p.exists():
+    under profiles/ (null when that kernel was not profiled). A plain GEMM on
+    the hipBLASLt route (PJRTX_BLASLT=1) reads its own summary."""
+    names = [f"{workload}_traffic.json"]
+    if os.environ.get("PJRTX_BLASLT", "0") == "1":
+        names.insert(0, f"{workload}_blaslt_traffic.json")
+    for name in names:
+        p = ROOT / "profiles" / name
+        if not p.exists():
+            continue
         try:
             d = json.loads(p.read_text())
-            if d.get("kernel") == kernel:
-                return d.get("hbm_bytes_per_launch")
         except Exception:
             return None
+        if d.get("kernel") == kernel:
+            return d.get("hbm_bytes_per_launch")
     return None
 
 

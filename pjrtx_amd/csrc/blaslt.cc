@@ -89,7 +89,9 @@ LtPlan make_plan(hipblasLtHandle_t h, const GemmParams& g, bool f16, bool b_kmaj
 }  // namespace
 
 bool blaslt_wanted(const GemmParams& g) {
-  if (env_int("PJRTX_BLASLT", 1) == 0) return false;
+  // Opt-in (PJRTX_BLASLT=1): by default every product runs on the own MFMA
+  // kernels; the library route stays for A/B measurements.
+  if (env_int("PJRTX_BLASLT", 0) == 0) return false;
   // The allocation-free execute never enters the library (its handle and
   // heuristics allocate).
   if (thread_arena()) return false;

@@ -395,27 +395,29 @@ def test_dot_f32_fallback_and_rank3_rank2(client):
 
 
 def test_matmul_8192_sampled_rows(client):
-    """C3d at full size; rows sampled for the float64 reference."""
-    n = 8192
-    rng = np.random.default_rng(8)
-    a = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
-    b_ = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
-    (out,) = run(client, programs.c3_matmul(n, n, n), a, b_, dtypes=["bf16", "bf16"])
-    rows = np.array([0, 1, 127, 128, 4095, 8191])
-    want = fb(a[rows]).astype(np.float64) @ fb(b_).astype(np.float64)
-    assert_bf16_close(out[rows], want)
-
-
-def test_matmul_8192_own_kernel_sampled_rows(client, monkeypatch):
-    """C3d at full size on the hand-written MFMA kernel (library GEMM off);
-    sampled rows against float64, both ends and tile boundaries."""
-    monkeypatch.setenv("PJRTX_BLASLT", "0")
+    """C3d at full size on the default route, the hand-written MFMA kernel
+    (gemm_nt_256, B read N-contiguous); sampled rows against float64, both
+    ends and tile boundaries."""
     n = 8192
     rng = np.random.default_rng(9)
     a = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
     b_ = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
     (out,) = run(client, programs.c3_matmul(n, n, n), a, b_, dtypes=["bf16", "bf16"])
     rows = np.array([0, 1, 255, 256, 4095, 4096, 8190, 8191])
+    want = fb(a[rows]).astype(np.float64) @ fb(b_).astype(np.float64)
+    assert_bf16_close(out[rows], want)
+
+
+def test_matmul_8192_library_route_sampled_rows(client, monkeypatch):
+    """C3d at full size on the opt-in hipBLASLt route (PJRTX_BLASLT=1); rows
+    sampled for the float64 reference."""
+    monkeypatch.setenv("PJRTX_BLASLT", "1")
+    n = 8192
+    rng = np.random.default_rng(8)
+    a = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
+    b_ = bf((rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n))))
+    (out,) = run(client, programs.c3_matmul(n, n, n), a, b_, dtypes=["bf16", "bf16"])
+    rows = np.array([0, 1, 127, 128, 4095, 8191])
     want = fb(a[rows]).astype(np.float64) @ fb(b_).astype(np.float64)
     assert_bf16_close(out[rows], want)
 
@@ -562,9 +564,9 @@ _LIBRARY_GEMM_SHAPES = [
 
 @pytest.mark.parametrize("shape", _LIBRARY_GEMM_SHAPES)
 def test_dot_library_gemm_matches_own_kernels(client, shape, monkeypatch):
-    """Plain products that fill the GPU go to hipBLASLt: same tolerance to the
-    float64 product as the own MFMA kernels (PJRTX_BLASLT=0), and the same
-    bits on every call."""
+    """Plain products that fill the GPU on the opt-in hipBLASLt route
+    (PJRTX_BLASLT=1): same tolerance to the float64 product as the own MFMA
+    kernels (the default route), and the same bits on every call."""
     spec, sa, sb, out_dt = shape
     rng = np.random.default_rng(sum(sa) + sum(sb))
     a = bf(rng.standard_normal(sa).astype(np.float32))
@@ -577,6 +579,7 @@ def test_dot_library_gemm_matches_own_kernels(client, shape, monkeypatch):
     x, y = bld.param(sa, "bf16"), bld.param(sb, "bf16")
     t = bld.build([bld.dot_general(x, y, batch=(lb, rb), contract=(lc, rc), out_dtype=out_dt)])
     want = ops.dot_general_f64(fb(a), fb(b_), lb, rb, lc, rc)
+    monkeypatch.setenv("PJRTX_BLASLT", "1")
     exe = client.compile(t)
     (lib1,) = exe(a, b_, dtypes=["bf16", "bf16"])
     (lib2,) = exe(a, b_, dtypes=["bf16", "bf16"])
