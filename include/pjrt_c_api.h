@@ -1389,6 +1389,33 @@ typedef struct PJRT_Api {
  * Replaces reference src/plugin/plugin.zig:11 (`export fn GetPjrtApi`). */
 const PJRT_Api* GetPjrtApi(void);
 
+/* ------------------------ GPU custom-call extension ---------------------- */
+/* The first (and only) entry of PJRT_Api.extension_start's chain: registers a
+ * custom-call target by handler (the public PJRT GPU extension layout; the
+ * reference installs the same extension, src/plugin/custom_call.zig:143-156,
+ * api.zig:66). api_version 0 (untyped) only; the handler_execute pointer
+ * names a pjrtx built-in by address (PjRTx_CustomCall_* in pjrtx_hip.h). */
+typedef struct PJRT_Gpu_Register_Custom_Call_Args {
+  size_t struct_size;
+  const char* function_name;
+  size_t function_name_size;
+  int api_version;
+  void* handler_instantiate;
+  void* handler_prepare;
+  void* handler_initialize;
+  void* handler_execute;
+} PJRT_Gpu_Register_Custom_Call_Args;
+#define PJRT_Gpu_Register_Custom_Call_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_Gpu_Register_Custom_Call_Args, handler_execute)
+
+typedef PJRT_Error* PJRT_Gpu_Register_Custom_Call(PJRT_Gpu_Register_Custom_Call_Args* args);
+
+typedef struct PJRT_Gpu_Custom_Call {
+  PJRT_Extension_Base base;
+  PJRT_Gpu_Register_Custom_Call* custom_call;
+} PJRT_Gpu_Custom_Call;
+#define PJRT_Gpu_Custom_Call_STRUCT_SIZE PJRT_STRUCT_SIZE(PJRT_Gpu_Custom_Call, custom_call)
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,7 @@
 #include <map>
 #include <set>
 
+#include "custom_call.h"
 #include "kernels/attention.h"
 #include "planner.h"
 #include "runtime.h"
@@ -36,8 +37,11 @@ constexpr const char* kSdpaTarget = "pjrtx.mlx_metal.scaled_dot_product_attentio
 bool is_attention_float(DType t) { return t == DType::kF32 || t == DType::kF16 || t == DType::kBF16; }
 
 void lower_custom_call(Program* prog, Op* op) {
-  PJRTX_CHECK(op->target == kSdpaTarget, Code::kUnimplemented,
-              "custom_call target '" + op->target + "' is not supported by pjrtx");
+  if (op->target != kSdpaTarget) {
+    // Registered identity / unary / binary targets (custom_call.cc).
+    lower_registered_custom_call(*prog, op);
+    return;
+  }
   // reference: lowering_custom_call.zig:216-300
   PJRTX_CHECK(op->operands.size() == 4 && op->results.size() == 1, Code::kInvalidArgument,
               "scaled-dot-product-attention custom_call requires q, k, v, and token_index inputs with one output");

@@ -483,8 +483,9 @@ std::string Writer::emit_op(const Op& op, int v, int id) {
       return define(R, std::string("sign_i<") + ct + ">(" + a[0] + ")");
     case OpKind::kIsFinite: return define(R, "__builtin_isfinite(" + a[0] + ")");
     case OpKind::kPopcnt:
-      return define(R, std::string("(") + ct + ")" + (dtype_size(A) == 8 ? "__popcll((uint64_t)" : "__popc((uint32_t)(") +
-                           std::string(unsigned_of(A)) + ")" + a[0] + (dtype_size(A) == 8 ? ")" : "))"));
+      // zero-extended through the unsigned type of the operand's width
+      return define(R, std::string("(") + ct + ")" + (dtype_size(A) == 8 ? "__popcll((uint64_t)(" : "__popc((uint32_t)(") +
+                           std::string(unsigned_of(A)) + ")" + a[0] + ")");
     case OpKind::kClz: {
       const size_t bits = dtype_size(A) * 8;
       if (bits == 64) return define(R, std::string("(") + ct + ")__clzll((int64_t)" + a[0] + ")");

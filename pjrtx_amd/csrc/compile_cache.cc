@@ -20,6 +20,7 @@
 #include <mutex>
 #include <unordered_map>
 
+#include "custom_call.h"
 #include "planner.h"
 #include "runtime.h"
 
@@ -79,6 +80,8 @@ std::string env_key() {
   std::string k;
   for (char** e = environ; e && *e; ++e)
     if (std::strncmp(*e, "PJRTX_", 6) == 0) k += std::string(*e) + '\n';
+  // Registered custom-call targets change how a program lowers.
+  k += "custom_call_registry " + std::to_string(custom_call_registry_version()) + '\n';
   return k;
 }
 

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/pjrt_c_api.h"
+#include "custom_call.h"
 #include "pjrt_handles.h"
 #include "runtime.h"
 
@@ -1215,6 +1216,82 @@ static PJRT_Error* Unimplemented(A*) {
   return make_error(Code::kUnimplemented, "pjrtx: this PJRT function is not implemented by the ROCm backend");
 }
 
+// ------------------------------------------------------ custom-call targets
+// The PJRT GPU custom-call extension and the PjRTx_* registration exports
+// (reference: src/plugin/custom_call.zig:35-185). A handler registered
+// through the extension is recognised by its address: one of the three
+// marker functions below; any other handler is UNIMPLEMENTED (this plugin
+// runs no host or device code of the caller's).
+
+extern "C" {
+__attribute__((visibility("default"))) void PjRTx_CustomCall_Identity(void) {}
+__attribute__((visibility("default"))) void PjRTx_CustomCall_UnarySqrt(void) {}
+__attribute__((visibility("default"))) void PjRTx_CustomCall_BinaryAdd(void) {}
+}
+
+static std::string name_of(const char* p, size_t n, const char* what) {
+  PJRTX_CHECK(p != nullptr, Code::kInvalidArgument, std::string("custom call ") + what + " is null");
+  return std::string(p, n);
+}
+
+static PJRT_Error* Gpu_Register_Custom_Call(PJRT_Gpu_Register_Custom_Call_Args* args) {
+  return guarded("PJRT_Gpu_Register_Custom_Call", [&] {
+    PJRTX_CHECK(args != nullptr, Code::kInvalidArgument, "custom call registration args are null");
+    PJRTX_CHECK(args->struct_size >= PJRT_Gpu_Register_Custom_Call_Args_STRUCT_SIZE, Code::kInvalidArgument,
+                "custom call registration args struct is too small");
+    const std::string target = name_of(args->function_name, args->function_name_size, "target");
+    PJRTX_CHECK(args->api_version == 0, Code::kUnimplemented,
+                "pjrtx custom calls support the PJRT GPU untyped API version 0 only");
+    PJRTX_CHECK(args->handler_execute != nullptr, Code::kInvalidArgument, "custom call handler_execute is null");
+    const void* h = args->handler_execute;
+    if (h == reinterpret_cast<const void*>(&PjRTx_CustomCall_Identity)) {
+      register_custom_call_identity(target);
+    } else if (h == reinterpret_cast<const void*>(&PjRTx_CustomCall_UnarySqrt)) {
+      register_custom_call_unary(target, "sqrt");
+    } else if (h == reinterpret_cast<const void*>(&PjRTx_CustomCall_BinaryAdd)) {
+      register_custom_call_binary(target, "add");
+    } else {
+      fail(Code::kUnimplemented, "custom call handler is not a pjrtx handler (PjRTx_CustomCall_*)");
+    }
+  });
+}
+
+static PJRT_Gpu_Custom_Call g_gpu_custom_call = {
+    {PJRT_Gpu_Custom_Call_STRUCT_SIZE, PJRT_Extension_Type_Gpu_Custom_Call, nullptr}, Gpu_Register_Custom_Call};
+
+extern "C" {
+__attribute__((visibility("default"))) PJRT_Error* PjRTx_RegisterCustomCallIdentity(const char* function_name,
+                                                                                   size_t function_name_size) {
+  return guarded("PjRTx_RegisterCustomCallIdentity",
+                 [&] { register_custom_call_identity(name_of(function_name, function_name_size, "target")); });
+}
+
+__attribute__((visibility("default"))) PJRT_Error* PjRTx_RegisterCustomCallUnary(const char* function_name,
+                                                                                size_t function_name_size,
+                                                                                const char* op_name,
+                                                                                size_t op_name_size) {
+  return guarded("PjRTx_RegisterCustomCallUnary", [&] {
+    register_custom_call_unary(name_of(function_name, function_name_size, "target"),
+                               name_of(op_name, op_name_size, "op name"));
+  });
+}
+
+__attribute__((visibility("default"))) PJRT_Error* PjRTx_RegisterCustomCallBinary(const char* function_name,
+                                                                                 size_t function_name_size,
+                                                                                 const char* op_name,
+                                                                                 size_t op_name_size) {
+  return guarded("PjRTx_RegisterCustomCallBinary", [&] {
+    register_custom_call_binary(name_of(function_name, function_name_size, "target"),
+                                name_of(op_name, op_name_size, "op name"));
+  });
+}
+
+__attribute__((visibility("default"))) void PjRTx_UnregisterCustomCall(const char* function_name,
+                                                                      size_t function_name_size) {
+  if (function_name != nullptr) unregister_custom_call(std::string(function_name, function_name_size));
+}
+}
+
 // ----------------------------------------------------------------- the table
 
 extern "C" __attribute__((visibility("default"))) const PJRT_Api* GetPjrtApi(void) {
@@ -1222,7 +1299,7 @@ extern "C" __attribute__((visibility("default"))) const PJRT_Api* GetPjrtApi(voi
     PJRT_Api a;
     std::memset(&a, 0, sizeof(a));
     a.struct_size = PJRT_Api_STRUCT_SIZE;
-    a.extension_start = nullptr;
+    a.extension_start = &g_gpu_custom_call.base;
     a.pjrt_api_version.struct_size = PJRT_Api_Version_STRUCT_SIZE;
     a.pjrt_api_version.extension_start = nullptr;
     a.pjrt_api_version.major_version = PJRT_API_MAJOR;

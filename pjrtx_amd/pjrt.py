@@ -55,6 +55,19 @@ class ExtBase(Structure):
 ExtBase._fields_ = [("struct_size", c_size_t), ("type", c_uint), ("next", POINTER(ExtBase))]
 
 
+class GpuRegisterCustomCallArgs(Structure):
+    """PJRT_Gpu_Register_Custom_Call_Args (include/pjrt_c_api.h)."""
+    _fields_ = [("struct_size", c_size_t), ("function_name", c_char_p), ("function_name_size", c_size_t),
+                ("api_version", c_int), ("handler_instantiate", c_void_p), ("handler_prepare", c_void_p),
+                ("handler_initialize", c_void_p), ("handler_execute", c_void_p)]
+
+
+class GpuCustomCallExtension(Structure):
+    """PJRT_Gpu_Custom_Call: the extension header and its registration function."""
+    _fields_ = [("base", ExtBase),
+                ("custom_call", ctypes.CFUNCTYPE(c_void_p, POINTER(GpuRegisterCustomCallArgs)))]
+
+
 def _args(name: str, fields: list[tuple[str, object]]):
     return type(name, (Structure,), {"_fields_": [("struct_size", c_size_t), ("extension_start", c_void_p)] + fields})
 
@@ -281,6 +294,60 @@ class Plugin:
         d.error = err
         ctypes.CFUNCTYPE(None, POINTER(ErrorDestroyArgs))(self.api.PJRT_Error_Destroy)(ctypes.byref(d))
         return PjrtError(c.code, msg)
+
+    # Custom-call targets (include/pjrtx_custom_call.h; host only).
+    def _cc_call(self, fn, *names: bytes) -> None:
+        argv = []
+        for n in names:
+            argv += [n, len(n) if n is not None else 0]
+        fn.restype = c_void_p
+        err = fn(*argv)
+        if err:
+            raise self._error(err)
+
+    def register_custom_call_identity(self, target: str) -> None:
+        self._cc_call(self.lib.PjRTx_RegisterCustomCallIdentity, target.encode())
+
+    def register_custom_call_unary(self, target: str, op: str) -> None:
+        self._cc_call(self.lib.PjRTx_RegisterCustomCallUnary, target.encode(), op.encode())
+
+    def register_custom_call_binary(self, target: str, op: str) -> None:
+        self._cc_call(self.lib.PjRTx_RegisterCustomCallBinary, target.encode(), op.encode())
+
+    def unregister_custom_call(self, target: str) -> None:
+        b = target.encode()
+        self.lib.PjRTx_UnregisterCustomCall.argtypes = [c_char_p, c_size_t]
+        self.lib.PjRTx_UnregisterCustomCall.restype = None
+        self.lib.PjRTx_UnregisterCustomCall(b, len(b))
+
+    def gpu_custom_call_extension(self):
+        """The PJRT GPU custom-call extension from PJRT_Api.extension_start's
+        chain (type 0), or None."""
+        ext = ctypes.cast(self.api.extension_start, POINTER(ExtBase)) if self.api.extension_start else None
+        while ext:
+            if ext.contents.type == 0:
+                return ctypes.cast(ext, POINTER(GpuCustomCallExtension)).contents
+            ext = ext.contents.next
+        return None
+
+    def register_custom_call_handler(self, target: str, handler: int, api_version: int = 0,
+                                     struct_size: int | None = None) -> None:
+        """PJRT_Gpu_Register_Custom_Call through the extension; `handler` is the
+        handler_execute address (a PjRTx_CustomCall_* marker)."""
+        ext = self.gpu_custom_call_extension()
+        if ext is None:
+            raise PjrtError(12, "PJRT GPU custom-call extension not found")
+        b = target.encode()
+        a = GpuRegisterCustomCallArgs(struct_size=struct_size or ctypes.sizeof(GpuRegisterCustomCallArgs),
+                                      function_name=b, function_name_size=len(b), api_version=api_version,
+                                      handler_execute=handler)
+        err = ext.custom_call(ctypes.byref(a))
+        if err:
+            raise self._error(err)
+
+    def marker(self, name: str) -> int:
+        """Address of a PjRTx_CustomCall_* marker handler."""
+        return ctypes.cast(getattr(self.lib, name), c_void_p).value
 
     # Host-only compiler entry points (no GPU needed).
     def plan_json(self, text: str) -> str:

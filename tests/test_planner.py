@@ -290,3 +290,12 @@ def test_window_write_not_absorbed_into_kernel_reading_operand(plugin):
     assert not any(s.get("window_outputs") for s in steps)
     dus = [s for s in steps if s.get("library") == "dynamic_update_slice"]
     assert len(dus) == 1
+
+
+@pytest.mark.parametrize("dt", ["s8", "u8", "s16", "u16", "s32", "u32", "s64", "u64"])
+def test_popcnt_and_clz_kernels_compile_at_every_width(plugin, dt):
+    """Generated popcnt / count_leading_zeros code compiles (hiprtc, no GPU)
+    for every integer width (the 32-bit popcnt once emitted an extra ')')."""
+    b = Builder()
+    x = b.param((4, 8), dt)
+    assert plugin.compile_check(b.build([b.popcnt(x), b.clz(x)])) > 0
