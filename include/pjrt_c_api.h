@@ -1215,7 +1215,18 @@ typedef struct PJRT_TopologyDescription_GetDeviceDescriptions_Args {
   size_t num_descriptions;                     /* out */
 } PJRT_TopologyDescription_GetDeviceDescriptions_Args;
 typedef PJRT_Error* PJRT_TopologyDescription_GetDeviceDescriptions(PJRT_TopologyDescription_GetDeviceDescriptions_Args* args);
-typedef struct PJRT_TopologyDescription_Serialize_Args PJRT_TopologyDescription_Serialize_Args;
+typedef struct PJRT_SerializedTopology PJRT_SerializedTopology;
+typedef struct PJRT_TopologyDescription_Serialize_Args {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  PJRT_TopologyDescription* topology;
+  const char* serialized_bytes;                   /* out; lives as long as serialized_topology */
+  size_t serialized_bytes_size;                   /* out */
+  PJRT_SerializedTopology* serialized_topology;   /* out */
+  void (*serialized_topology_deleter)(PJRT_SerializedTopology* serialized_topology); /* out; call once */
+} PJRT_TopologyDescription_Serialize_Args;
+#define PJRT_TopologyDescription_Serialize_Args_STRUCT_SIZE \
+  PJRT_STRUCT_SIZE(PJRT_TopologyDescription_Serialize_Args, serialized_topology_deleter)
 typedef PJRT_Error* PJRT_TopologyDescription_Serialize(PJRT_TopologyDescription_Serialize_Args* args);
 typedef struct PJRT_TopologyDescription_Attributes_Args {
   size_t struct_size;

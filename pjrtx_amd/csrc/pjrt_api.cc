@@ -1202,6 +1202,30 @@ static PJRT_Error* TopologyDescription_GetDeviceDescriptions(PJRT_TopologyDescri
   });
 }
 
+// "platform=<name>;version=<version>;devices=<n>" and one
+// ";device=<id>:<local hardware id>:<process index>:<kind>" per device
+// (reference: topology.zig:85-108, the same fields in the same order).
+static void SerializedTopology_Delete(PJRT_SerializedTopology* t) { delete t; }
+
+static PJRT_Error* TopologyDescription_Serialize(PJRT_TopologyDescription_Serialize_Args* args) {
+  return guarded("PJRT_TopologyDescription_Serialize", [&] {
+    PJRTX_ARGS_CHECK(args, PJRT_TopologyDescription_Serialize_Args, serialized_topology_deleter);
+    PJRTX_CHECK(args->topology != nullptr && args->topology->client != nullptr, Code::kInvalidArgument,
+                "PJRT_TopologyDescription_Serialize: topology is null");
+    const PJRT_Client* client = args->topology->client;
+    auto t = std::make_unique<PJRT_SerializedTopology>();
+    std::string& s = t->bytes;
+    s = "platform=" + kPlatformName + ";version=" + client->platform_version +
+        ";devices=" + std::to_string(client->devices.size());
+    for (const PJRT_Device* d : client->devices)
+      s += ";device=" + std::to_string(d->desc.id) + ":" + std::to_string(d->desc.id) + ":0:" + d->desc.kind;
+    args->serialized_bytes = s.data();
+    args->serialized_bytes_size = s.size();
+    args->serialized_topology = t.release();
+    args->serialized_topology_deleter = SerializedTopology_Delete;
+  });
+}
+
 static PJRT_Error* TopologyDescription_Attributes(PJRT_TopologyDescription_Attributes_Args* args) {
   return guarded("PJRT_TopologyDescription_Attributes", [&] {
     args->attributes = nullptr;
@@ -1392,7 +1416,7 @@ extern "C" __attribute__((visibility("default"))) const PJRT_Api* GetPjrtApi(voi
     a.PJRT_TopologyDescription_PlatformName = TopologyDescription_PlatformName;
     a.PJRT_TopologyDescription_PlatformVersion = TopologyDescription_PlatformVersion;
     a.PJRT_TopologyDescription_GetDeviceDescriptions = TopologyDescription_GetDeviceDescriptions;
-    a.PJRT_TopologyDescription_Serialize = Unimplemented<PJRT_TopologyDescription_Serialize_Args>;
+    a.PJRT_TopologyDescription_Serialize = TopologyDescription_Serialize;
     a.PJRT_TopologyDescription_Attributes = TopologyDescription_Attributes;
     a.PJRT_Compile = Unimplemented<PJRT_Compile_Args>;
     a.PJRT_Executable_OutputElementTypes = Executable_OutputElementTypes;

@@ -46,6 +46,11 @@ struct PJRT_TopologyDescription {
   PJRT_Client* client = nullptr;
 };
 
+// PJRT_TopologyDescription_Serialize's result, freed by its deleter.
+struct PJRT_SerializedTopology {
+  std::string bytes;
+};
+
 struct PJRT_Client {
   std::vector<std::unique_ptr<PJRT_Device>> device_storage;
   std::vector<std::unique_ptr<PJRT_Memory>> memory_storage;

@@ -98,6 +98,10 @@ ClientCreateArgs = _args("ClientCreateArgs", [
     ("kv_put_callback", c_void_p), ("kv_put_user_arg", c_void_p),
     ("client", c_void_p), ("kv_try_get_callback", c_void_p), ("kv_try_get_user_arg", c_void_p)])
 ClientDestroyArgs = _args("ClientDestroyArgs", [("client", c_void_p)])
+ClientTopologyDescriptionArgs = _args("ClientTopologyDescriptionArgs", [("client", c_void_p), ("topology", c_void_p)])
+TopologySerializeArgs = _args("TopologySerializeArgs", [
+    ("topology", c_void_p), ("serialized_bytes", c_void_p), ("serialized_bytes_size", c_size_t),
+    ("serialized_topology", c_void_p), ("serialized_topology_deleter", ctypes.CFUNCTYPE(None, c_void_p))])
 ClientPlatformNameArgs = _args("ClientPlatformNameArgs", [("client", c_void_p), ("platform_name", c_void_p),
                                                           ("platform_name_size", c_size_t)])
 ClientDevicesArgs = _args("ClientDevicesArgs", [("client", c_void_p), ("devices", POINTER(c_void_p)),
@@ -683,6 +687,19 @@ class Client:
         d.client = self.handle
         self.p.call("Client_Devices", d)
         self.devices = [d.devices[i] for i in range(d.num_devices)]
+
+    def topology_serialized(self) -> str:
+        """PJRT_Client_TopologyDescription, then PJRT_TopologyDescription_Serialize
+        (the bytes copied, the serialized topology freed by its deleter)."""
+        t = _mk(ClientTopologyDescriptionArgs())
+        t.client = self.handle
+        self.p.call("Client_TopologyDescription", t)
+        a = _mk(TopologySerializeArgs())
+        a.topology = t.topology
+        self.p.call("TopologyDescription_Serialize", a)
+        out = ctypes.string_at(a.serialized_bytes, a.serialized_bytes_size).decode()
+        a.serialized_topology_deleter(a.serialized_topology)
+        return out
 
     @property
     def platform_name(self) -> str:
