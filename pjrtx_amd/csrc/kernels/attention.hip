@@ -999,7 +999,9 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
 #pragma unroll
       for (int e = 0; e < EPC; ++e) o[e] += in ? pj * Elem<T>::get(e8[e]) : 0.f;
     }
-    __syncthreads();  // ps and wred are rewritten by the next pass
+    // ps and wred are rewritten by the next pass (nothing after the last
+    // pass touches them; the block's k-range is uniform, so is the branch)
+    if (kb + DKT < k1) __syncthreads();
   }
 #pragma unroll
   for (int e = 0; e < EPC; ++e) ow[g][c * EPC + e] = o[e];
