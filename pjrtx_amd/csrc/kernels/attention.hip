@@ -768,10 +768,13 @@ __global__ void __launch_bounds__(256) attn_rows(AttnParams p, const T* __restri
 // walks its chunk 64 keys per pass with both loads in flight at once: for
 // the scores 4 lanes share a key (each a quarter of its K row, folded by two
 // xor shuffles), for P.V a lane owns one 16-byte head-dim piece of a group of
-// keys (each V row read as one coalesced span). The pass max and sum fold
-// over the waves through LDS in wave order (online softmax). The key groups
-// of P.V fold through LDS in group order. Splits past the row's last allowed
-// key exit at once.
+// keys (each V row read as one coalesced span). Each wave scores a quarter
+// of a pass's keys and its P.V lanes read the same keys, so it runs an
+// online softmax of its own (max and sum by xor shuffles, P handed to the
+// P.V lanes by shuffles) with no barrier between passes; after the last
+// pass the four waves' (max, sum, output) meet through LDS, the key groups
+// of P.V folded in group order, each scaled by its wave's exp(m_w - max).
+// Splits past the row's last allowed key exit at once.
 //
 // One split: the workgroup writes the row. Otherwise each split writes
 // (m, l, unnormalized O) to `part`; in fused mode (workgroup b runs on XCD
@@ -880,7 +883,6 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
   constexpr int G = 256 / NCH;         // key groups in P.V
   constexpr int KG = DKT / G;          // keys per group
   static_assert(KG >= 1, "at least one key per P.V group");
-  __shared__ float ps[DKT];
   __shared__ float wred[2][4];
   __shared__ float ow[G][D];
   __shared__ float msh[64], lsh[64];
@@ -936,6 +938,13 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
     for (int e = 0; e < EPC; ++e) qv[i * EPC + e] = Elem<T>::get(e8[e]);
   }
   const int k1 = std::min(nkeys, k0 + keys_per_split);
+  // Wave w scores keys w DKT/4 .. (w+1) DKT/4 - 1 of every pass, and its P.V
+  // lanes read exactly those keys' V rows (group g's keys start at g KG, and
+  // a wave's groups start at w DKT/4), so each wave keeps an online softmax
+  // of its own (max, sum and output over its keys) and the passes need no
+  // barrier: P moves from the scoring lanes to the P.V lanes by shuffles.
+  // The four waves' states meet once, after the last pass.
+  const int wk0 = wave * (DKT / 4);
   float m = -INFINITY, l = 0.f, o[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) o[e] = 0.f;
@@ -971,45 +980,55 @@ __global__ void __launch_bounds__(256) attn_decode(AttnParams p, const T* __rest
     for (int k = 1; k < LPK; k <<= 1) acc += __shfl_xor(acc, k);
     if (p.round_scores) acc = Elem<T>::get(Elem<T>::put(acc));
     const float sc = key < k1 ? acc * p.scale : -INFINITY;
+    // the wave's max and sum over its keys (xor butterflies over the key
+    // bits of the lane index: every lane ends with them)
     float mx = sc;
 #pragma unroll
     for (int k = 32; k >= LPK; k >>= 1) mx = fmaxf(mx, __shfl_xor(mx, k));
-    if (lane == 0) wred[0][wave] = mx;
-    __syncthreads();
-    const float mnew = fmaxf(m, fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3])));
+    const float mnew = fmaxf(m, mx);
     const float mref = mnew == -INFINITY ? 0.f : mnew;
     const float alpha = expf(m - mref);
     const float pe = expf(sc - mref);
-    if (quarter == 0) ps[kslot] = pe;
     float sum = quarter == 0 ? pe : 0.f;
 #pragma unroll
     for (int k = 32; k >= LPK; k >>= 1) sum += __shfl_xor(sum, k);
-    if (lane == 0) wred[1][wave] = sum;
-    __syncthreads();
-    l = l * alpha + (((wred[1][0] + wred[1][1]) + wred[1][2]) + wred[1][3]);
+    l = l * alpha + sum;
     m = mnew;
 #pragma unroll
     for (int e = 0; e < EPC; ++e) o[e] *= alpha;
 #pragma unroll
     for (int i = 0; i < KG; ++i) {
-      // a key past k1 adds nothing (its row may hold anything)
-      const bool in = kb + g * KG + i < k1;
-      const float pj = ps[g * KG + i];
+      // a key past k1 adds nothing (its row may hold anything); its
+      // exponential sits in lane (key - wk0) LPK of this wave
+      const int kk = g * KG + i;
+      const bool in = kb + kk < k1;
+      const float pj = __shfl(pe, (kk - wk0) * LPK);
       const T* e8 = reinterpret_cast<const T*>(&vv[i]);
 #pragma unroll
       for (int e = 0; e < EPC; ++e) o[e] += in ? pj * Elem<T>::get(e8[e]) : 0.f;
     }
-    // ps and wred are rewritten by the next pass (nothing after the last
-    // pass touches them; the block's k-range is uniform, so is the branch)
-    if (kb + DKT < k1) __syncthreads();
   }
+  // The waves meet: each wave's (l, O) scaled by exp(m_w - max m_w).
 #pragma unroll
   for (int e = 0; e < EPC; ++e) ow[g][c * EPC + e] = o[e];
+  if (lane == 0) {
+    wred[0][wave] = m;
+    wred[1][wave] = l;
+  }
   __syncthreads();
+  float fw[4];
+  {
+    const float mall = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
+    const float mr = mall == -INFINITY ? 0.f : mall;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) fw[w] = expf(wred[0][w] - mr);
+    l = ((wred[1][0] * fw[0] + wred[1][1] * fw[1]) + wred[1][2] * fw[2]) + wred[1][3] * fw[3];
+    m = mall;
+  }
   float acc = 0.f;
   if (tid < D) {
 #pragma unroll
-    for (int gg = 0; gg < G; ++gg) acc += ow[gg][tid];
+    for (int gg = 0; gg < G; ++gg) acc += ow[gg][tid] * fw[gg / (G / 4)];
   }
   T* orow = O + (int64_t)b * p.o_b + (int64_t)h * p.o_h + (int64_t)q * p.o_s;
   if (nact == 1 && mode != kDecodePartials) {
