@@ -194,7 +194,7 @@ void lower_registered_custom_call(const Program& prog, Op* op) {
           break;
       }
       op->kind = spec.op;
-      op->name = "stablehlo." + op_name_of(spec.op);
+      op->name = std::string("stablehlo.") + op_kind_name(spec.op);
       break;
     case CustomCallKind::kBinary: {
       const TensorType& rhs = prog.type(op->operands[1]);
@@ -220,7 +220,7 @@ void lower_registered_custom_call(const Program& prog, Op* op) {
           break;
       }
       op->kind = spec.op;
-      op->name = "stablehlo." + op_name_of(spec.op);
+      op->name = std::string("stablehlo.") + op_kind_name(spec.op);
       break;
     }
   }
