@@ -423,6 +423,7 @@ void rewrite_program(Program* prog) {
       changed = true;
     }
   }
+  changed |= fold_gather_index_wrap(prog);
   const char* env = std::getenv("PJRTX_FUSED_ATTENTION");
   if (!(env && std::string(env) == "0")) {
     remove_dead_ops(prog);  // use counts below must not see dead users

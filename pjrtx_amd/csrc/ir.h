@@ -120,6 +120,11 @@ struct Op {
   Dims input_batching_dims, scatter_indices_batching_dims;
   bool indices_are_sorted = false;
   bool unique_indices = false;
+  // gather: a negative start index i is read as i + index_wrap (in the
+  // index type's width, wrapping) before the clamp: JAX's negative-index
+  // normalization (select(i < 0, i + N, i)) folded into the gather by
+  // fold_gather_index_wrap. 0: indices are read as they are.
+  int64_t index_wrap = 0;
 
   // constant literal: raw little-endian element bytes of the result type,
   // or one element when `splat`.

@@ -66,6 +66,9 @@ struct GatherParams {
   int idx_batch_dim[kMaxRank] = {};  // matching start_indices_batching_dims
   int idx_bytes = 4;
   int idx_signed = 1;
+  // > 0: a negative start index i becomes i + wrap (wrapping in idx_bytes)
+  // before the clamp (Op::index_wrap).
+  int64_t wrap = 0;
 };
 void launch_gather(hipStream_t s, const GatherParams& p, const void* operand, const void* indices, void* out,
                    int elem_bytes);

@@ -46,6 +46,18 @@ __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int byte
   return is_signed ? (int64_t)(int8_t)u : (int64_t)u;
 }
 
+// A gather start index after JAX's negative-index normalization folded into
+// the gather: i < 0 reads as i + wrap, the add wrapping in the index type's
+// width as the program's own add does; then sign-extended as before.
+__device__ __forceinline__ int64_t wrap_index(int64_t i, int64_t wrap, int bytes) {
+  if (wrap == 0 || i >= 0) return i;
+  const uint64_t s = (uint64_t)i + (uint64_t)wrap;
+  if (bytes == 8) return (int64_t)s;
+  if (bytes == 4) return (int64_t)(int32_t)(uint32_t)s;
+  if (bytes == 2) return (int64_t)(int16_t)(uint16_t)s;
+  return (int64_t)(int8_t)(uint8_t)s;
+}
+
 __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // Box copy in units. `p` dims/strides/offsets are in units; dyn starts are in
@@ -126,7 +138,7 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherUnits p, const T* __r
   for (int d = 0; d < g.op_rank; ++d) start[d] = 0;
   for (int k = 0; k < g.n_index; ++k) {
     const int64_t off = (g.ivd < g.idx_rank) ? (int64_t)k * g.idx_stride[g.ivd] : 0;
-    start[g.start_map[k]] = load_index(indices, idx_base + off, g.idx_bytes, g.idx_signed);
+    start[g.start_map[k]] = wrap_index(load_index(indices, idx_base + off, g.idx_bytes, g.idx_signed), g.wrap, g.idx_bytes);
   }
   for (int k = 0; k < g.n_batching; ++k) start[g.op_batch_dim[k]] = batch_coord[g.idx_batch_dim[k]];
   int64_t src = 0;
@@ -146,11 +158,12 @@ constexpr int64_t kGatherRowChunk = 1024;
 
 __global__ void __launch_bounds__(256) gather_rows_kernel(const u32x4* __restrict__ operand,
                                                           const void* __restrict__ indices, int idx_bytes,
-                                                          int idx_signed, int64_t op_rows, int64_t units_per_row,
-                                                          int64_t nchunks, u32x4* __restrict__ out) {
+                                                          int idx_signed, int64_t wrap, int64_t op_rows,
+                                                          int64_t units_per_row, int64_t nchunks,
+                                                          u32x4* __restrict__ out) {
   const int64_t bid = blockIdx.x;
   const int64_t r = bid / nchunks, chunk = bid - r * nchunks;
-  const int64_t src = clamp64(load_index(indices, r, idx_bytes, idx_signed), 0, op_rows - 1);
+  const int64_t src = clamp64(wrap_index(load_index(indices, r, idx_bytes, idx_signed), wrap, idx_bytes), 0, op_rows - 1);
   const u32x4* srow = operand + src * units_per_row;
   u32x4* drow = out + r * units_per_row;
   const int64_t u0 = chunk * kGatherRowChunk + threadIdx.x;
@@ -286,7 +299,7 @@ void launch_gather(hipStream_t s, const GatherParams& g, const void* operand, co
       const int64_t nchunks = (upr + kGatherRowChunk - 1) / kGatherRowChunk;
       PJRTX_CHECK(out_rows * nchunks < (int64_t(1) << 31), Code::kUnimplemented, "gather: too many rows");
       hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(out_rows * nchunks)), dim3(256), 0, s,
-                         static_cast<const u32x4*>(operand), indices, g.idx_bytes, g.idx_signed, g.op_dims[0], upr,
+                         static_cast<const u32x4*>(operand), indices, g.idx_bytes, g.idx_signed, g.wrap, g.op_dims[0], upr,
                          nchunks, static_cast<u32x4*>(out));
       check_launch("gather_rows");
       return;

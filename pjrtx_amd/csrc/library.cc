@@ -4,6 +4,7 @@
 #include "kernels/reduce_window.h"
 
 #include <cstring>
+#include <map>
 
 #include "runtime.h"
 #include "sort_op.h"
@@ -125,6 +126,107 @@ void run_pad(Device* dev, const Program& prog, const Op& op, std::vector<MemRef>
 // Translates StableHLO gather dimension numbers into the kernel's mapping
 // (semantics: StableHLO spec `gather`; start indices are clamped so the slice
 // stays in bounds, as reference executable_metal_graph_gather.zig:61-65).
+// JAX normalizes a negative gather index i to i + N before the gather
+// (select(compare(LT, i, 0), add(i, N), i), N the gathered dimension's size,
+// as `table[i]` lowers); the gather kernels apply the same rule while they
+// read the index (Op::index_wrap), so the normalization's elementwise launch
+// goes away (PJRTX_GATHER_WRAP=0 keeps it). Matched for a one-component
+// index vector whose value reaches the gather through reshapes and
+// broadcasts that only add unit dimensions (the flat order unchanged): the
+// gather then reads i through one reshape to its index shape.
+bool fold_gather_index_wrap(Program* prog) {
+  if (env_int("PJRTX_GATHER_WRAP", 1) == 0) return false;
+  std::map<int, size_t> producer;
+  for (size_t i = 0; i < prog->ops.size(); ++i)
+    for (int r : prog->ops[i].results) producer[r] = i;
+  auto op_of = [&](int v) -> const Op* {
+    auto it = producer.find(v);
+    return it == producer.end() ? nullptr : &prog->ops[it->second];
+  };
+  auto is_int = [](DType t) { return (dtype_is_signed_int(t) || dtype_is_unsigned_int(t)) && t != DType::kPred; };
+  // A splat integer constant, directly or broadcast from a one-element one.
+  auto splat_int = [&](int v, int64_t* out) {
+    const Op* o = op_of(v);
+    if (o && o->kind == OpKind::kBroadcastInDim && prog->type(o->operands[0]).elements() == 1) o = op_of(o->operands[0]);
+    if (!o || o->kind != OpKind::kConstant || o->results.size() != 1) return false;
+    const TensorType& t = prog->type(o->results[0]);
+    const size_t es = dtype_size(t.dtype);
+    if (!is_int(t.dtype) || !(o->splat || t.elements() == 1) || o->literal.size() < es) return false;
+    uint64_t u = 0;
+    std::memcpy(&u, o->literal.data(), es);
+    const int sh = 64 - 8 * static_cast<int>(es);
+    *out = dtype_is_signed_int(t.dtype) && sh > 0 ? static_cast<int64_t>(u << sh) >> sh : static_cast<int64_t>(u);
+    return true;
+  };
+  // Views that keep the flat element order.
+  auto order_view = [&](const Op* o) {
+    if (o->kind == OpKind::kReshape) return true;
+    if (o->kind != OpKind::kBroadcastInDim) return false;
+    const TensorType& in = prog->type(o->operands[0]);
+    const TensorType& out = prog->type(o->results[0]);
+    if (in.elements() != out.elements()) return false;
+    for (size_t k = 1; k < o->dims.size(); ++k)
+      if (o->dims[k] <= o->dims[k - 1]) return false;
+    return true;
+  };
+  // The reshapes to insert, each before its gather (ops are not moved while
+  // producers are still looked up).
+  std::vector<std::pair<size_t, Op>> inserts;
+  for (size_t gi = 0; gi < prog->ops.size(); ++gi) {
+    Op& g = prog->ops[gi];
+    if (g.kind == OpKind::kGather && g.index_wrap == 0 && g.start_index_map.size() == 1) {
+      const int idx = g.operands[1];
+      int v = idx;
+      const Op* o = op_of(v);
+      while (o && order_view(o)) {
+        v = o->operands[0];
+        o = op_of(v);
+      }
+      int64_t zero = -1, n = 0;
+      const int64_t N = prog->type(g.operands[0]).dims.at(g.start_index_map[0]);
+      if (o && o->kind == OpKind::kSelect) {
+        const int x = o->operands[2];
+        const Op* cmp = op_of(o->operands[0]);
+        const Op* add = op_of(o->operands[1]);
+        const bool cmp_ok = cmp && cmp->kind == OpKind::kCompare && cmp->cmp_dir == CmpDir::kLT &&
+                            cmp->cmp_type != CmpType::kUnsigned && cmp->cmp_type != CmpType::kFloat &&
+                            cmp->operands[0] == x && splat_int(cmp->operands[1], &zero) && zero == 0;
+        int other = -1;
+        if (add && add->kind == OpKind::kAdd) other = add->operands[0] == x ? add->operands[1] : add->operands[1] == x ? add->operands[0] : -1;
+        const bool add_ok = other >= 0 && splat_int(other, &n) && n == N;
+        const DType xt = prog->type(x).dtype;
+        if (cmp_ok && add_ok && dtype_is_signed_int(xt) && xt == prog->type(idx).dtype && N > 0 &&
+            prog->type(x).elements() == prog->type(idx).elements()) {
+          // the gather's index operand: x through one reshape to its shape
+          Value nv;
+          nv.type = prog->type(idx);
+          nv.name = prog->values[x].name + ".gather_index";
+          prog->values.push_back(nv);
+          const int r = static_cast<int>(prog->values.size()) - 1;
+          Op rs;
+          rs.kind = OpKind::kReshape;
+          rs.name = "stablehlo.reshape";
+          rs.operands = {x};
+          rs.results = {r};
+          g.operands[1] = r;
+          g.index_wrap = N;
+          inserts.emplace_back(gi, std::move(rs));
+        }
+      }
+    }
+  }
+  if (inserts.empty()) return false;
+  std::vector<Op> ops;
+  ops.reserve(prog->ops.size() + inserts.size());
+  size_t next = 0;
+  for (size_t i = 0; i < prog->ops.size(); ++i) {
+    while (next < inserts.size() && inserts[next].first == i) ops.push_back(std::move(inserts[next++].second));
+    ops.push_back(std::move(prog->ops[i]));
+  }
+  prog->ops = std::move(ops);
+  return true;
+}
+
 GatherParams make_gather_params(const Program& prog, const Op& op) {
   const TensorType& x = prog.type(op.operands[0]);
   const TensorType& idx = prog.type(op.operands[1]);
@@ -180,6 +282,7 @@ GatherParams make_gather_params(const Program& prog, const Op& op) {
   }
   g.idx_bytes = static_cast<int>(dtype_size(idx.dtype));
   g.idx_signed = dtype_is_signed_int(idx.dtype);
+  g.wrap = op.index_wrap;
   return g;
 }
 

@@ -246,6 +246,10 @@ Plan make_plan(const Program& prog, const PlanOptions& opts = PlanOptions());
 // Unsupported custom-call targets fail with kUnimplemented.
 void rewrite_program(Program* prog);
 
+// Folds JAX's negative-index normalization of gather indices into the
+// gathers (library.cc); true when a gather changed.
+bool fold_gather_index_wrap(Program* prog);
+
 // Turns decode-shaped dot and dot-group library steps into kGemv steps and
 // absorbs their row-fused prologues and elementwise epilogues
 // (gemv_fusion.cc). Runs on a finished plan (after liveness); recomputes the

@@ -86,6 +86,31 @@ def test_embedding_gather(client, vocab, dim, batch, seq):
     np.testing.assert_array_equal(out, ops.gather_rows(table, idx))
 
 
+@pytest.mark.parametrize("idx_dtype", ["s32", "s64"])
+@pytest.mark.parametrize("dim", [64, 5])
+def test_gather_folded_index_wrap_edges(client, idx_dtype, dim):
+    """JAX's negative-index normalization, folded into the gather, on the
+    indices where it matters: -1 and -rows wrap to the last and first rows,
+    indices still out of range after the wrap (and the type's extremes) are
+    clamped; dim 5 takes the generic gather kernel, 64 the row kernel."""
+    vocab, n = 1000, 64
+    np_t = np.int32 if idx_dtype == "s32" else np.int64
+    info = np.iinfo(np_t)
+    rng = np.random.default_rng(dim)
+    table = bf((0.02 * rng.standard_normal((vocab, dim))).astype(np.float32))
+    idx = rng.integers(-2 * vocab, 2 * vocab, n).astype(np_t)
+    idx[:10] = [-1, -vocab, -vocab - 1, -5000, 0, vocab - 1, vocab, vocab + 5, info.min, info.max]
+    b = Builder()
+    tp = b.param((vocab, dim), "bf16")
+    ip = b.param((n,), idx_dtype)
+    wrapped = b.select(b.compare("LT", ip, b.scalar_like(0, ip)), b.add(ip, b.scalar_like(vocab, ip)), ip)
+    iv = b.broadcast_in_dim(wrapped, (n, 1), [0])
+    t = b.build([b.gather(tp, iv, offset_dims=[1], collapsed_slice_dims=[0], start_index_map=[0],
+                          index_vector_dim=1, slice_sizes=[1, dim])])
+    (out,) = run(client, t, table, idx, dtypes=["bf16", None])
+    np.testing.assert_array_equal(out, ops.gather_rows(table, idx))
+
+
 # ----------------------------------------------------------------- scatter
 
 @pytest.mark.parametrize("mode", ["set", "add"])

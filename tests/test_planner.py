@@ -299,3 +299,36 @@ def test_popcnt_and_clz_kernels_compile_at_every_width(plugin, dt):
     b = Builder()
     x = b.param((4, 8), dt)
     assert plugin.compile_check(b.build([b.popcnt(x), b.clz(x)])) > 0
+
+
+def _wrapped_gather(vocab, dim, n, idx_dtype="s32", add_value=None):
+    """table[idx] as jnp indexing lowers it (select(i < 0, i + add, i)), with
+    `add` the table's row count unless given."""
+    b = Builder()
+    table = b.param((vocab, dim), "bf16")
+    idx = b.param((n,), idx_dtype)
+    add = vocab if add_value is None else add_value
+    wrapped = b.select(b.compare("LT", idx, b.scalar_like(0, idx)), b.add(idx, b.scalar_like(add, idx)), idx)
+    iv = b.broadcast_in_dim(wrapped, (n, 1), [0])
+    return b.build([b.gather(table, iv, offset_dims=[1], collapsed_slice_dims=[0], start_index_map=[0],
+                             index_vector_dim=1, slice_sizes=[1, dim])])
+
+
+@pytest.mark.parametrize("idx_dtype", ["s32", "s64"])
+def test_gather_index_wrap_folds_into_the_gather(plugin, monkeypatch, idx_dtype):
+    # the normalization's loop kernel goes away: the gather reads the raw
+    # indices through a view and applies i < 0 ? i + rows : i itself
+    p = plan(plugin, _wrapped_gather(1000, 64, 16, idx_dtype))
+    assert [st["kind"] for st in p["steps"]] == ["alias", "library"]
+    assert p["steps"][0]["inputs"] == [1]
+    monkeypatch.setenv("PJRTX_GATHER_WRAP", "0")
+    p = plan(plugin, _wrapped_gather(1000, 64, 16, idx_dtype))
+    kinds = [st["kind"] for st in p["steps"]]
+    assert kinds == ["loop", "library"] and "select" in p["steps"][0]["ops"]
+
+
+def test_gather_index_wrap_needs_the_row_count(plugin):
+    # a wrap by anything but the gathered dimension's size is not JAX's
+    # normalization and stays an elementwise kernel
+    p = plan(plugin, _wrapped_gather(1000, 64, 16, add_value=999))
+    assert [st["kind"] for st in p["steps"]] == ["loop", "library"]
