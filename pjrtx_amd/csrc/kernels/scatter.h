@@ -69,25 +69,38 @@ struct ScatterHotList {
   uint32_t* rows = nullptr;    // class k's rows at base[k] ..
   int64_t base[32] = {};
   int kmin = 0;                // lowest class that can hold a hot row
+  // 1 when workgroup b runs on XCD b % 8 and the grid is a multiple of 8:
+  // consecutive items (the slices of one row) then go to workgroups of one
+  // XCD, so the two 64-byte halves of an update row's 128-byte line are
+  // read through the same L2.
+  int xcd_group = 0;
 };
 // Early rows: the longest rows, found from a sample of the keys, are folded
 // while the keys are still being sorted. `select` (one workgroup) sorts
 // kEarlySample keys taken at even strides and lists up to kEarlyRows rows
 // that fill at least kEarlyMinRun of them (longest first); the rows' update
-// indices are then listed in update order by a count / scan / write pass
-// over the keys, and their slices folded like hot rows. The sorted path
+// indices are then listed in update order by a count / write pass over the
+// keys (a scan of the counts in between only for more than
+// kEarlyInlineBlocks blocks), and their slices folded like hot rows. The sorted path
 // skips these rows (classify and the bulk fold read the list).
 constexpr int kEarlyRows = 8;
 constexpr int kEarlySample = 4096;
 constexpr int kEarlyMinRun = 32;
 constexpr int kEarlyBlockItems = 4096;  // keys per count / write workgroup
+constexpr int kEarlyInlineBlocks = 1024;  // up to this many, the write kernel scans the counts itself
 struct ScatterEarly {
   uint32_t* rows = nullptr;     // [1 + kEarlyRows]: count, then the rows
   uint32_t* counts = nullptr;   // [kEarlyRows * blocks + 1]
-  uint32_t* offsets = nullptr;  // [kEarlyRows * blocks + 1]
+  // [kEarlyRows * blocks + 1]: the scan of `counts`, or (up to
+  // kEarlyInlineBlocks blocks) the rows' starts and the total in its first
+  // kEarlyRows + 1 words
+  uint32_t* offsets = nullptr;
   uint32_t* list = nullptr;     // [n] update indices, row by row
   uint32_t* scan_tmp = nullptr; // [2048]
   int64_t blocks = 0;
+  // 1 when workgroup b runs on XCD b % 8: all slices of one early row run on
+  // one XCD (ScatterHotList::xcd_group).
+  int xcd_group = 0;
 };
 inline int64_t scatter_early_blocks(int64_t n) { return (n + kEarlyBlockItems - 1) / kEarlyBlockItems; }
 // Queues the selection on `aux` (records `selected` after it, which the

@@ -453,7 +453,13 @@ __global__ void __launch_bounds__(256) scatter_hot_chunks(int64_t row_elems, con
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int64_t total = 0;
   for (int k = 31; k >= h.kmin; --k) total += (int64_t)h.counts[k] * (((int64_t(2) << k) + kHotChunk - 1) / kHotChunk);
-  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+  // With xcd_group, workgroup b (on XCD b % 8) takes item slot
+  // (b % 8) * (grid / 8) + b / 8 of each round: a bijection on the round's
+  // slots that puts consecutive items on one XCD.
+  const int64_t slot = h.xcd_group && gridDim.x % 8 == 0
+                           ? (int64_t)(blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8
+                           : (int64_t)blockIdx.x;
+  for (int64_t item = slot; item < total; item += gridDim.x) {
     int64_t it = item;
     uint32_t row = 0, chunk = 0;
     for (int k = 31; k >= h.kmin; --k) {
@@ -709,7 +715,13 @@ __global__ void __launch_bounds__(256) scatter_hot_fold(
   const int64_t slices = (row_elems + S::COLS - 1) / S::COLS;
   int64_t total = 0;
   for (int k = 31; k >= h.kmin; --k) total += (int64_t)h.counts[k] * slices;
-  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+  // With xcd_group, workgroup b (on XCD b % 8) takes item slot
+  // (b % 8) * (grid / 8) + b / 8 of each round: a bijection on the round's
+  // slots that puts consecutive items on one XCD.
+  const int64_t slot = h.xcd_group && gridDim.x % 8 == 0
+                           ? (int64_t)(blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8
+                           : (int64_t)blockIdx.x;
+  for (int64_t item = slot; item < total; item += gridDim.x) {
     int64_t it = item;
     uint32_t row = 0;
     int slice = 0;
@@ -819,13 +831,61 @@ __global__ void __launch_bounds__(256) scatter_early_count(const uint32_t* __res
 // Writes each early row's update indices in update order: a thread's 16
 // keys, its exclusive rank among the workgroup's threads (wave scans plus
 // wave totals), and the workgroup's offset from the scanned counts.
+// `offsets`: the exclusive scan of `counts` (row-major [row][block]), or
+// null for a grid of at most kEarlyInlineBlocks workgroups, which then
+// computes its own entries of that scan from `counts` (every workgroup sums
+// the rows' totals and its earlier blocks' counts) and whose workgroup 0
+// writes the rows' starts and the total to row_starts[0 .. kEarlyRows].
 __global__ void __launch_bounds__(256) scatter_early_write(const uint32_t* __restrict__ keys, int64_t n,
                                                            const uint32_t* __restrict__ early,
-                                                           const uint32_t* __restrict__ offsets, int64_t blocks,
+                                                           const uint32_t* __restrict__ offsets,
+                                                           const uint32_t* __restrict__ counts,
+                                                           uint32_t* __restrict__ row_starts, int64_t blocks,
                                                            uint32_t* __restrict__ list) {
   __shared__ uint32_t wtot[4][kEarlyRows];
+  __shared__ uint32_t wpre[4][2 * kEarlyRows];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t count = early[0];
+  uint32_t start[kEarlyRows];  // scan entry (j, this block)
+  if (offsets) {
+#pragma unroll
+    for (int j = 0; j < kEarlyRows; ++j) start[j] = offsets[(int64_t)j * blocks + blockIdx.x];
+  } else {
+    // tot[j]: row j's total; pre[j]: row j's counts in blocks before this one
+    uint32_t tot[kEarlyRows] = {}, pre[kEarlyRows] = {};
+    for (int64_t b = tid; b < blocks; b += 256) {
+#pragma unroll
+      for (int j = 0; j < kEarlyRows; ++j) {
+        const uint32_t c = counts[(int64_t)j * blocks + b];
+        tot[j] += c;
+        pre[j] += b < (int64_t)blockIdx.x ? c : 0u;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kEarlyRows; ++j) {
+      uint32_t t = tot[j], q = pre[j];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        t += __shfl_xor(t, o);
+        q += __shfl_xor(q, o);
+      }
+      if (lane == 0) {
+        wpre[wave][j] = t;
+        wpre[wave][kEarlyRows + j] = q;
+      }
+    }
+    __syncthreads();
+    uint32_t row0 = 0;
+#pragma unroll
+    for (int j = 0; j < kEarlyRows; ++j) {
+      const uint32_t t = wpre[0][j] + wpre[1][j] + wpre[2][j] + wpre[3][j];
+      start[j] = row0 + wpre[0][kEarlyRows + j] + wpre[1][kEarlyRows + j] + wpre[2][kEarlyRows + j] +
+                 wpre[3][kEarlyRows + j];
+      if (blockIdx.x == 0 && tid == 0) row_starts[j] = row0;
+      row0 += t;
+    }
+    if (blockIdx.x == 0 && tid == 0) row_starts[kEarlyRows] = row0;
+  }
   uint32_t er[kEarlyRows];
 #pragma unroll
   for (int j = 0; j < kEarlyRows; ++j) er[j] = (uint32_t)j < count ? early[1 + j] : 0xffffffffu;
@@ -863,7 +923,7 @@ __global__ void __launch_bounds__(256) scatter_early_write(const uint32_t* __res
   for (int j = 0; j < kEarlyRows; ++j) {
     uint32_t wb = 0;
     for (int w = 0; w < wave; ++w) wb += wtot[w][j];
-    pos[j] = offsets[(int64_t)j * blocks + blockIdx.x] + wb + incl[j] - c[j];
+    pos[j] = start[j] + wb + incl[j] - c[j];
   }
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
@@ -879,16 +939,21 @@ __global__ void __launch_bounds__(256) scatter_early_fold(int64_t row_elems,
                                                           const typename StorageOf<Tag>::T* __restrict__ operand,
                                                           const typename StorageOf<Tag>::T* updates,
                                                           const uint32_t* __restrict__ early,
-                                                          const uint32_t* __restrict__ offsets, int64_t blocks,
-                                                          const uint32_t* list, typename StorageOf<Tag>::T* __restrict__ out) {
+                                                          const uint32_t* __restrict__ row_starts, int64_t stride,
+                                                          const uint32_t* list, typename StorageOf<Tag>::T* __restrict__ out,
+                                                          int xcd_group) {
   typedef typename StorageOf<Tag>::T T;
   typedef HotShape<T> S;
   __shared__ __align__(16) T lds[2 * S::BUF];
   const int64_t slices = (row_elems + S::COLS - 1) / S::COLS;
-  const uint32_t j = (uint32_t)(blockIdx.x / slices);
-  const int slice = (int)(blockIdx.x % slices);
+  // xcd_group: workgroup b (XCD b % 8) takes slot (b % 8) * (grid / 8) + b / 8,
+  // so one row's slices share an XCD (ScatterHotList::xcd_group).
+  const int64_t b = xcd_group && gridDim.x % 8 == 0 ? (int64_t)(blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8
+                                                     : (int64_t)blockIdx.x;
+  const uint32_t j = (uint32_t)(b / slices);
+  const int slice = (int)(b % slices);
   if (j >= early[0]) return;
-  const uint32_t lo = offsets[(int64_t)j * blocks], hi = offsets[(int64_t)(j + 1) * blocks];
+  const uint32_t lo = row_starts[(int64_t)j * stride], hi = row_starts[(int64_t)(j + 1) * stride];
   if (hi <= lo) return;  // a selected row appears in the sample, so never empty
   hot_slice_fold<Tag, OP>(row_elems, early[1 + j], slice, operand, updates, list, lo, hi - lo, out, lds);
 }
@@ -1169,14 +1234,20 @@ void launch_scatter_early(hipStream_t aux, hipEvent_t selected, const ScatterEar
   hcheck(hipEventRecord(selected, aux), "hipEventRecord(scatter early selected)");
   const dim3 gb(static_cast<unsigned>(e.blocks)), blk(256);
   hipLaunchKernelGGL(scatter_early_count, gb, blk, 0, aux, keys, n, e.rows, e.counts, e.blocks);
-  exclusive_scan(aux, e.counts, e.offsets, kEarlyRows * e.blocks + 1, e.scan_tmp);
-  hipLaunchKernelGGL(scatter_early_write, gb, blk, 0, aux, keys, n, e.rows, e.offsets, e.blocks, e.list);
+  // Up to kEarlyInlineBlocks workgroups compute their own offsets (no scan
+  // launches on the early path); the fold then reads the rows' starts.
+  const bool inline_scan = e.blocks <= kEarlyInlineBlocks;
+  if (!inline_scan) exclusive_scan(aux, e.counts, e.offsets, kEarlyRows * e.blocks + 1, e.scan_tmp);
+  hipLaunchKernelGGL(scatter_early_write, gb, blk, 0, aux, keys, n, e.rows, inline_scan ? nullptr : e.offsets,
+                     e.counts, e.offsets, e.blocks, e.list);
+  const int64_t stride = inline_scan ? 1 : e.blocks;
   const size_t es = dtype_size(t);
   const int64_t cols = kHotSliceBytes / static_cast<int64_t>(es);
   const dim3 gf(static_cast<unsigned>(kEarlyRows * ((row_elems + cols - 1) / cols)));
 #define PJRTX_EARLY(TAG, OPV)                                                                                        \
   hipLaunchKernelGGL((scatter_early_fold<TAG, OPV>), gf, blk, 0, aux, row_elems, (const StorageOf<TAG>::T*)operand, \
-                     (const StorageOf<TAG>::T*)updates, e.rows, e.offsets, e.blocks, e.list, (StorageOf<TAG>::T*)out)
+                     (const StorageOf<TAG>::T*)updates, e.rows, e.offsets, stride, e.list, (StorageOf<TAG>::T*)out,       \
+                     e.xcd_group)
 #define PJRTX_EARLY_T(TAG)                                          \
   switch (op) {                                                     \
     case ScatterOp::kAdd: PJRTX_EARLY(TAG, ScatterOp::kAdd); break; \

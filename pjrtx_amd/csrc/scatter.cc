@@ -166,12 +166,16 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
   const bool chunked = int_type && (sop == ScatterOp::kAdd || sop == ScatterOp::kMax || sop == ScatterOp::kMin);
   const bool vec16 = (p.row_elems * static_cast<int64_t>(esz)) % 16 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(U) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  // Slices of one row on one XCD (PJRTX_SCATTER_XCD=0 turns it off): only
+  // where workgroup b is known to run on XCD b % 8.
+  const int xcd_group = dev->xcd_round_robin() && env_int("PJRTX_SCATTER_XCD", 1) != 0 ? 1 : 0;
   ScatterEarly early;
   MemRef early_mem;
   const bool use_early = p.row_mode && !chunked && vec16 && n >= (int64_t(1) << 16) && n < (int64_t(1) << 31) &&
                          env_int("PJRTX_SCATTER_EARLY", 1) != 0;
   if (use_early) {
     early.blocks = scatter_early_blocks(n);
+    early.xcd_group = xcd_group;
     const int64_t words = (1 + kEarlyRows) + 2 * (kEarlyRows * early.blocks + 1) + 2 * n + 2048;
     early_mem = dev->allocate(static_cast<size_t>(words) * 4);
     uint32_t* w = static_cast<uint32_t*>(early_mem->ptr);
@@ -208,6 +212,7 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
     ScatterHotList h;
     if (n > kHotMinUpdates && scatter_hot_list_words(n) <= static_cast<size_t>(n)) {
       h = scatter_hot_list(n, hot_counts, static_cast<uint32_t*>(tkeys->ptr));
+      h.xcd_group = xcd_group;
       const int64_t cols = kHotSliceBytes / static_cast<int64_t>(dtype_size(xt.dtype));
       const int64_t slices = (p.row_elems + cols - 1) / cols;
       const int64_t max_items = (n / (kHotMinUpdates + 1)) * slices;
