@@ -197,13 +197,17 @@ def _topk():
 # --------------------------------------------------------------- CPU legs
 
 def _cpu_c1(inputs):
-    from oracle import ops
-    return (lambda: ops.c1_rowsum(*inputs)), 1.0, "full workload, numpy oracle"
+    from oracle import cbaseline
+    t = cbaseline.host_threads()
+    return ((lambda: cbaseline.c1(*inputs, threads=t)), 1.0,
+            f"full workload, C restatement of the oracle (oracle/c/baseline.c, -O3 AVX2) on {t} host threads")
 
 
 def _cpu_c2(inputs):
-    from oracle import ops
-    return (lambda: ops.c2_reference(inputs[0])), 1.0, "full workload, numpy oracle"
+    from oracle import cbaseline
+    t = cbaseline.host_threads()
+    return ((lambda: cbaseline.c2(inputs[0], threads=t)), 1.0,
+            f"full workload, C restatement of the oracle (oracle/c/baseline.c, -O3 AVX2) on {t} host threads")
 
 
 def _cpu_copy(inputs):
@@ -288,7 +292,7 @@ def cpu_baseline(W: Workload, inputs, budget_s: float = 10.0) -> dict:
     out = {"unit": "TFLOP/s" if W.flops else "GB/s", "cores": host_threads(), "kind": "port",
            "sample": f"{sample}; {n} calls, {el / n * 1e3:.1f} ms/call"}
     out["value"] = round(W.flops / step_s / 1e12, 4) if W.flops else round(W.bytes / step_s / 1e9, 3)
-    if "BLAS" not in sample:
+    if "BLAS" not in sample and "host threads" not in sample:
         out["cores"] = 1  # numpy elementwise / indexing runs on one thread
     out["host"] = host_facts()
     return out
