@@ -1162,19 +1162,26 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
                        early_rows);
     check("scatter_hot_classify");
   }
+  // The hot rows and the bulk rows fold at once on two streams: the hot
+  // rows on the second stream, the bulk rows on `s` (PJRTX_SCATTER_HOT_MAIN=1
+  // swaps them, so the hot rows start first: slower, measured).
+  hipStream_t hot_s = aux, bulk_s = s;
   if (p.hot_wgs > 0) {
-    // The hot slices run on the second stream, beside the bulk rows.
     hcheck(hipEventRecord(fork, s), "hipEventRecord(scatter fork)");
     hcheck(hipStreamWaitEvent(aux, fork, 0), "hipStreamWaitEvent(scatter fork)");
+    if (env_int("PJRTX_SCATTER_HOT_MAIN", 0) != 0) {
+      hot_s = s;
+      bulk_s = aux;
+    }
   }
   const dim3 gh(static_cast<unsigned>(p.hot_wgs)), gb(static_cast<unsigned>(blocks(rows, 4))), blk(256);
 #define PJRTX_HOT_OP(TAG, OPV)                                                                                        \
-  hipLaunchKernelGGL((scatter_hot_fold<TAG, OPV>), gh, blk, 0, aux, row_elems, (const StorageOf<TAG>::T*)operand,   \
+  hipLaunchKernelGGL((scatter_hot_fold<TAG, OPV>), gh, blk, 0, hot_s, row_elems, (const StorageOf<TAG>::T*)operand, \
                      (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, h, (StorageOf<TAG>::T*)out)
 #define PJRTX_CHUNK_OP(TAG, OPV)                                                                                      \
   do {                                                                                                                \
     if constexpr (std::is_integral<StorageOf<TAG>::T>::value && OPV != ScatterOp::kSet && OPV != ScatterOp::kMul)     \
-      hipLaunchKernelGGL((scatter_hot_chunks<StorageOf<TAG>::T, OPV>), gh, blk, 0, aux, row_elems,                    \
+      hipLaunchKernelGGL((scatter_hot_chunks<StorageOf<TAG>::T, OPV>), gh, blk, 0, hot_s, row_elems,                  \
                          (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, h,                              \
                          init ? (const StorageOf<TAG>::T*)operand : nullptr, (StorageOf<TAG>::T*)out);               \
   } while (0)
@@ -1184,7 +1191,8 @@ void launch_scatter_rows(hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEve
       if (chunked) PJRTX_CHUNK_OP(TAG, OPV);                                                                         \
       else PJRTX_HOT_OP(TAG, OPV);                                                                                    \
     }                                                                                                                 \
-    hipLaunchKernelGGL((scatter_rows_fold<TAG, OPV, V>), gb, blk, 0, s, p, (const StorageOf<TAG>::T*)operand,        \
+    hipLaunchKernelGGL((scatter_rows_fold<TAG, OPV, V>), gb, blk, 0, p.hot_wgs > 0 ? bulk_s : s, p,                  \
+                       (const StorageOf<TAG>::T*)operand,                                                            \
                        (const StorageOf<TAG>::T*)updates, perm, seg_start, seg_end, (StorageOf<TAG>::T*)out,         \
                        early_rows);                                                                                   \
   } while (0)

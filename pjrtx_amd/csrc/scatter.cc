@@ -216,7 +216,8 @@ void run_scatter(Device* dev, const Program& prog, const Op& op, std::vector<Mem
       const int64_t cols = kHotSliceBytes / static_cast<int64_t>(dtype_size(xt.dtype));
       const int64_t slices = (p.row_elems + cols - 1) / cols;
       const int64_t max_items = (n / (kHotMinUpdates + 1)) * slices;
-      hot_wgs = std::min<int64_t>(max_items, 2 * static_cast<int64_t>(dev->compute_units()));
+      hot_wgs = std::min<int64_t>(max_items, env_int("PJRTX_SCATTER_HOT_PER_CU", 2) *
+                                                 static_cast<int64_t>(dev->compute_units()));
     }
     if (use_early) {
       // classify and the bulk fold skip the early rows: wait for the list.
