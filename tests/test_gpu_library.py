@@ -202,6 +202,22 @@ def test_scatter_add_full_size_zipf(client):
     assert ops.segment_lengths(idx, rows).max() > 90000
 
 
+def test_scatter_add_f32_many_updates_scanned_early_lists(client):
+    """More than 4M updates: the early rows' listing runs with a scan of the
+    per-block counts between its count and write kernels (up to 4M the write
+    kernel sums them itself). f32 bit-exact in update order; out-of-bounds
+    indices skipped."""
+    rows, dim, n = 2048, 4, 4_400_000
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    idx = ops.zipf_indices(n, rows, seed=31)
+    idx[:4] = [-1, rows, rows + 7, -rows]
+    upd = rng.standard_normal((n, dim)).astype(np.float32)
+    (out,) = run(client, programs.c4_scatter_add(rows, dim, n, "f32"), x, idx, upd)
+    np.testing.assert_array_equal(out, ops.scatter_rows_add(x, idx, upd))
+    assert ops.segment_lengths(idx, rows).max() > 256 * 64  # early rows picked
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f64", "s64"])
 def test_scatter_add_long_segments_other_types(client, dtype):
     """The sliced in-order fold for 2- and 8-byte elements: bf16/f16 round
