@@ -75,7 +75,8 @@ def test_batched_gather(client):
     np.testing.assert_array_equal(out, ops.gather_stablehlo(x, idx, [2], [1], [1], 2, [1, 1, 4], [0], [0]))
 
 
-@pytest.mark.parametrize("vocab,dim,batch,seq", [(100, 64, 2, 7), (1000, 4096, 2, 64), (128256, 4096, 8, 2048)])
+@pytest.mark.parametrize("vocab,dim,batch,seq", [(100, 64, 2, 7), (1000, 4096, 2, 64), (128256, 4096, 8, 2048),
+                                                  (300, 6144, 1, 9), (50, 16384, 1, 3)])
 def test_embedding_gather(client, vocab, dim, batch, seq):
     rng = np.random.default_rng(vocab)
     table = bf((0.02 * rng.standard_normal((vocab, dim))).astype(np.float32))
